@@ -1,0 +1,246 @@
+#!/usr/bin/env python3
+"""Benchmark of the LFM2-MoE Q8_0 MoE layer on one MI355X.
+
+Metric: MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0.
+
+A step is one pass of the MoE block (router, top-K, expert SwiGLU products,
+weighted combine, residual) over one batch of synthetic tokens.  Default
+workload: batch-1 decode through one MoE layer (H=2048, F=1792, E=32, K=4,
+Q8_0 experts), rotating over `--layers` independently seeded layer instances
+(16 x 374 MB = 6 GB resident) so that consecutive steps never find their
+expert weights in L2 or the 256 MB Infinity Cache.
+
+Inputs are generated on the device before the timed region.  Times come from
+HIP events on the stream the kernels run on; the per-kernel roofline figure
+comes from a second pass over the same steps with every launch bracketed by
+its own event pair (qq_profile_*).
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwenqwen3.js_amd"))
+
+METRIC = "MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0"
+HBM_PEAK_GBPS = 8000.0
+H, F, E, K = 2048, 1792, 32, 4
+QBLK = 34
+
+WORKLOADS = {
+    # name: (T tokens per step, bias kind, description)
+    "decode_b1": (1, "uniform", "moe_layer_decode_batch1"),
+    "decode_b64": (64, "uniform", "moe_layer_decode_batch64"),
+    "prefill_2048": (2048, "zipf", "moe_layer_prefill_2048_zipf"),
+}
+
+
+def expert_bytes():
+    gate = F * (H // 32) * QBLK
+    down = H * (F // 32) * QBLK
+    return gate, down
+
+
+def kernel_bytes(name, T, n_experts, n_pairs):
+    """Algorithmic HBM bytes of one launch of `name` (each weight byte once)."""
+    gate, down = expert_bytes()
+    if name == "router_logits":
+        return E * H * 4 + T * H * 4 + T * E * 4
+    if name == "router_topk":
+        return T * E * 4 + E * 4 + T * K * 12 + T * E * 4
+    if name == "expert_gateup":
+        return n_experts * 2 * gate + T * H * 4 + n_pairs * F * 4
+    if name == "expert_down_combine":
+        return n_experts * down + n_pairs * F * 4 + T * K * 12 + 2 * T * H * 4
+    return None
+
+
+def layer_bytes(T, n_experts):
+    gate, down = expert_bytes()
+    return n_experts * (2 * gate + down) + E * H * 4 + E * 4 + 2 * T * H * 4
+
+
+def make_layer(torch, ctx, seed, bias_kind):
+    """One layer's tensors: GGUF Q8_0 bytes made on the device, repacked by the library."""
+    import qq_hip
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    tensors = []
+    for in_dim, out_dim in ((H, F), (H, F), (F, H)):
+        nblk = E * out_dim * (in_dim // 32)
+        blocks = torch.empty((nblk, QBLK), dtype=torch.uint8, device="cuda")
+        qs = torch.randint(-127, 128, (nblk, 32), generator=g, device="cuda", dtype=torch.int8)
+        d = (torch.randn(nblk, generator=g, device="cuda").abs() * 0.002).to(torch.float16)
+        blocks[:, 2:] = qs.view(torch.uint8)
+        blocks[:, :2] = d.view(torch.uint8).view(nblk, 2)
+        torch.cuda.synchronize()
+        tensors.append(ctx.upload_q8_0_dev(blocks.data_ptr(), blocks.numel(), in_dim, out_dim, E))
+        del blocks, qs, d
+    rng = np.random.default_rng(seed)
+    router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    if bias_kind == "zipf":
+        k = np.arange(1, E + 1, dtype=np.float64)
+        pmf = k ** -1.1
+        pmf /= pmf.sum()
+        bias = (0.17 * np.log(pmf[rng.permutation(E)])).astype(np.float32)
+    else:
+        bias = rng.uniform(-0.01, 0.01, E).astype(np.float32)
+    return ctx.moe_create(router, qq_hip.TYPE_F32, bias, *tensors, H, F, E, K)
+
+
+def cpu_baseline(T_step, seconds):
+    """The oracle (C restatement of the reference's single-threaded JS path) timed on
+    this host: tokens/sec through one MoE layer on a bounded sample of tokens."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    import synth
+    L = synth.moe_layer(7)
+    x, hid = synth.activations(8, 256, H)
+    oracle.moe_ffn(L, x[:1], hid[:1])           # warm-up
+    n = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.moe_ffn(L, x[n % 256:n % 256 + 1], hid[n % 256:n % 256 + 1])
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return {
+        "value": n / el,
+        "unit": "tokens/s",
+        "cores": 1,
+        "kind": "port",
+        "sample": "%d single-token MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0) in %.1f s "
+                  "on 1 thread of %d host cores; tokens are independent, so tokens/s scales to "
+                  "batch %d" % (n, el, os.cpu_count() or 0, T_step),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--workload", choices=sorted(WORKLOADS), default="decode_b1")
+    ap.add_argument("--layers", type=int, default=16, help="distinct layer instances rotated over")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus %d refused)"
+              % args.gpus, file=sys.stderr)
+        return 2
+
+    import torch
+    import qq_hip
+
+    T, bias_kind, wname = WORKLOADS[args.workload]
+    torch.cuda.init()
+    ctx = qq_hip.Context(0)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+
+    n_layers = args.layers if T == 1 else min(args.layers, 4)
+    layers = [make_layer(torch, ctx, 1000 + i, bias_kind) for i in range(n_layers)]
+    S = 64 if T == 1 else 2
+    gx = torch.Generator(device="cuda")
+    gx.manual_seed(99)
+    X = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    HID = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    idx = torch.empty((S, T, K), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        s = i % S
+        layers[i % n_layers].forward_dev(X[s].data_ptr(), HID[s].data_ptr(), T,
+                                         idx_ptr=idx[s].data_ptr())
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = ev0.elapsed_time(ev1)
+    ms_per_step = total_ms / args.steps
+
+    # distinct experts per step (weights each step must read at least once)
+    used = idx.cpu().numpy()
+    n_exp = float(np.mean([len(np.unique(used[s])) for s in range(S)]))
+    n_pairs = T * K
+
+    # per-kernel pass: same steps, every launch bracketed by its own events
+    ctx.profile_enable(args.steps * 8)
+    for i in range(args.steps):
+        step(i)
+    prof = ctx.profile_read()
+    ctx.profile_enable(0)
+    kernels = {}
+    for name, (ms, cnt) in prof.items():
+        b = kernel_bytes(name, T, n_exp, n_pairs)
+        avg_us = 1000.0 * ms / cnt
+        kernels[name] = {"avg_us": round(avg_us, 3), "launches": cnt,
+                         "bytes": None if b is None else int(b),
+                         "gbps": None if b is None else round(b / (avg_us * 1e3), 1)}
+    dom = max(prof, key=lambda n: prof[n][0])
+    dom_k = kernels[dom]
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_%s.json" % args.workload)
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom)
+
+    lb = layer_bytes(T, n_exp)
+    tokens_per_s = T * args.steps / (total_ms / 1000.0)
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": wname, "H": H, "F": F, "E": E, "K": K, "T": T,
+                   "weights": "Q8_0", "activations": "f32", "router": "f32 (f64 accumulate)",
+                   "layer_instances": n_layers, "distinct_experts_per_step": round(n_exp, 2)},
+        "hbm_gbps_layer": round(lb / (ms_per_step * 1e6), 1),
+        "hbm_frac_layer": round(lb / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+        "roofline": {"kernel": dom, "bound": "hbm", "achieved": dom_k["gbps"],
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": None if dom_k["gbps"] is None else round(dom_k["gbps"] / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic},
+        "kernels": kernels,
+    }
+    for l in layers:
+        for t in l._keep:
+            t.release()
+        l.release()
+    ctx.close()
+
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(T, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,140 @@
+/*
+ * qq_moe.h -- C ABI of the MI355X (gfx950) LFM2-MoE Q8_0 MoE feed-forward path.
+ *
+ * Plain C: opaque handles, host or device pointers, sizes, int status codes.
+ * Every entry point returns QQ_OK (0) or a negative QQ_E* code; the message of
+ * the last failure on a context is qq_last_error(ctx) (qq_last_error(NULL)
+ * reports a failed qq_init).  A binding turns a non-zero status into an
+ * exception, as the reference does with `throw new Error(...)`
+ * (src/tensor.js:494).
+ *
+ * Entry points whose pointers are host memory (suffix-free names) are
+ * synchronous, like the JavaScript functions they replace.  The *_dev
+ * variants take device pointers, enqueue on the context's stream and return
+ * without waiting.
+ *
+ * Reference interfaces replaced (kishida/QwenQwen3.js):
+ *   matmulQ80xF32(meta, input)          src/tensor.js:26-53
+ *   matmulGeneric(meta, input)          src/tensor.js:485-496 (type 8 branch)
+ *   Lfm2Engine.prototype._moEFFN        src/lfm2-engine.js:413-487
+ *   Lfm2GPUEngine.prototype._moEFFNGPU  src/webgpu.js:1882-1917 (device-resident peer)
+ */
+#ifndef QQ_MOE_H
+#define QQ_MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QQ_OK            0
+#define QQ_E_ARG        -1   /* bad argument, shape or type            */
+#define QQ_E_HIP        -2   /* HIP runtime error                      */
+#define QQ_E_NODEV      -3   /* no usable gfx950 device                */
+#define QQ_E_NOMEM      -4   /* device or pinned allocation failed     */
+
+/* GGUF tensor type codes (src/gguf.js TENSOR_TYPES) accepted on this path. */
+#define QQ_TYPE_F32      0
+#define QQ_TYPE_Q8_0     8
+
+typedef struct qq_ctx qq_ctx;
+typedef struct qq_tensor qq_tensor;
+typedef struct qq_moe qq_moe;
+
+/* ---- context --------------------------------------------------------- */
+
+/* Open device `device` (HIP ordinal) and create a stream.  Fails with
+ * QQ_E_NODEV when the device is absent or not gfx950.  No reference
+ * counterpart: the reference's device setup is GPUDevice.init
+ * (src/webgpu.js:349-489). */
+int qq_init(int device, qq_ctx **out);
+void qq_destroy(qq_ctx *ctx);
+const char *qq_last_error(const qq_ctx *ctx);
+
+/* Use `hip_stream` (a hipStream_t, or NULL for the context's own stream) for
+ * every later launch on this context. */
+int qq_set_stream(qq_ctx *ctx, void *hip_stream);
+int qq_synchronize(qq_ctx *ctx);
+
+/* ---- Q8_0 tensors ---------------------------------------------------- */
+
+/* Repack `n_mats` GGUF Q8_0 matrices of shape [in_dim, out_dim] into device
+ * memory once.  `gguf_bytes` points at the first block (meta.buffer +
+ * meta.offset, src/gguf.js:235-261) and holds n_mats*out_dim*ceil(in_dim/32)
+ * 34-byte blocks; n_mats = 1 for a 2-D tensor and E for the 3-D expert
+ * tensors ffn_{gate,up,down}_exps (src/lfm2-engine.js:131-136), whose expert
+ * e is sliced by _expertSlice (src/lfm2-engine.js:489-505). */
+int qq_q8_0_upload(qq_ctx *ctx, const void *gguf_bytes, size_t nbytes, int in_dim,
+                   int out_dim, int n_mats, qq_tensor **out);
+/* Same, from GGUF bytes already in device memory. */
+int qq_q8_0_upload_dev(qq_ctx *ctx, const void *gguf_bytes_dev, size_t nbytes, int in_dim,
+                       int out_dim, int n_mats, qq_tensor **out);
+int qq_tensor_release(qq_ctx *ctx, qq_tensor *t);
+
+/* matmulQ80xF32 (src/tensor.js:26-53) for `rows` input vectors:
+ * y[r][c] = sum_k x[r][k] * W_mat[k][c], W_mat = matrix `mat` of t.
+ * x is rows*in_dim floats, y is rows*out_dim floats (host memory). */
+int qq_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, float *y,
+                   int rows);
+/* Device-pointer variant; enqueued, not waited for. */
+int qq_q8_0_matvec_dev(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x_dev,
+                       float *y_dev, int rows);
+
+/* ---- MoE layer ------------------------------------------------------- */
+
+/* Bind one LFM2-MoE MoE layer (src/lfm2-engine.js:129-137).
+ *   router_bytes  ffn_gate_inp.weight [H, E]: F32 (E columns of H floats) or Q8_0
+ *   bias          exp_probs_b.bias as E floats (_readWeightF32, src/tensor.js:80-100),
+ *                 or NULL when the layer has none
+ *   gate, up      ffn_gate_exps / ffn_up_exps tensors [H, F, E]
+ *   down          ffn_down_exps tensor [F, H, E]
+ * The router and bias are copied; gate/up/down are borrowed and must outlive
+ * the layer handle. */
+int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const float *bias,
+                  const qq_tensor *gate, const qq_tensor *up, const qq_tensor *down,
+                  int H, int F, int E, int K, qq_moe **out);
+int qq_moe_release(qq_ctx *ctx, qq_moe *m);
+
+/* Lfm2Engine._moEFFN (src/lfm2-engine.js:413-487) over T tokens, each row
+ * independent (the reference runs T sequential calls, src/lfm2-engine.js:550-555):
+ *   x       [T*H]  ffn_norm output (bufNormed), read only
+ *   hidden  [T*H]  residual stream (bufHidden), updated in place: hidden += MoE(x)
+ *   mask    [E]    expertMask membership (nonzero = skip that expert) or NULL;
+ *                  masked weights are not renormalised (src/lfm2-engine.js:464)
+ *   idx     [T*K]  selected experts in rank order, or NULL
+ *   w       [T*K]  normalised weights p_k/(1e-6 + sum p), binary64 as the
+ *                  onRouterUpdate payload carries them, or NULL
+ *   probs   [T*E]  sigmoid probabilities, or NULL
+ * Host pointers; synchronous. */
+int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                   const uint8_t *mask, int32_t *idx, double *w, float *probs);
+/* Device-pointer variant (mask stays a host array of E bytes or NULL;
+ * idx/w/probs device pointers or NULL); enqueued, not waited for. */
+int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev,
+                       int T, const uint8_t *mask, int32_t *idx_dev, double *w_dev,
+                       float *probs_dev);
+
+/* ---- measurement ------------------------------------------------------ */
+
+/* Record a HIP event pair around work enqueued between qq_timer_start and
+ * qq_timer_stop on the context's stream; qq_timer_stop waits and returns the
+ * elapsed milliseconds. */
+int qq_timer_start(qq_ctx *ctx);
+int qq_timer_stop(qq_ctx *ctx, float *ms);
+
+/* Per-kernel timing: while enabled, every kernel launch on the context is
+ * bracketed by a HIP event pair on the launch stream (up to max_launches
+ * launches; 0 disables).  qq_profile_read waits for the stream and returns,
+ * for each kernel id < n, the summed milliseconds and the launch count, then
+ * clears the record.  qq_profile_name(id) names the kernel. */
+int qq_profile_enable(qq_ctx *ctx, int max_launches);
+int qq_profile_read(qq_ctx *ctx, float *ms_sum, int *count, int n);
+const char *qq_profile_name(int id);
+int qq_profile_kernel_count(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* QQ_MOE_H */

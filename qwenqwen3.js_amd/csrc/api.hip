@@ -1,0 +1,547 @@
+// api.hip -- the extern "C" boundary declared in include/qq_moe.h.
+#include "qq_internal.h"
+
+#include <cstdlib>
+#include <new>
+
+namespace qq {
+
+static thread_local char g_init_err[512] = "";
+
+int set_error(qq_ctx *ctx, const char *fmt, ...)
+{
+    char *dst = ctx ? ctx->err : g_init_err;
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(dst, 512, fmt, ap);
+    va_end(ap);
+    return QQ_E_ARG;
+}
+
+int check_hip(qq_ctx *ctx, hipError_t e, const char *what)
+{
+    char *dst = ctx ? ctx->err : g_init_err;
+    snprintf(dst, 512, "HIP error %d (%s) in %s", (int)e, hipGetErrorString(e), what);
+    return (e == hipErrorOutOfMemory) ? QQ_E_NOMEM : QQ_E_HIP;
+}
+
+int ensure_scratch(qq_ctx *ctx, size_t bytes)
+{
+    if (bytes <= ctx->scratch_bytes) return QQ_OK;
+    // in-flight kernels may still use the old arena
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    ctx->scratch = nullptr;
+    ctx->scratch_bytes = 0;
+    const size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    QQ_HIP(ctx, hipMalloc(&ctx->scratch, sz));
+    ctx->scratch_bytes = sz;
+    return QQ_OK;
+}
+
+int ensure_pinned(qq_ctx *ctx, size_t bytes)
+{
+    if (bytes <= ctx->pinned_bytes) return QQ_OK;
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+    ctx->pinned = nullptr;
+    ctx->pinned_bytes = 0;
+    const size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
+    QQ_HIP(ctx, hipHostMalloc(&ctx->pinned, sz, hipHostMallocDefault));
+    ctx->pinned_bytes = sz;
+    return QQ_OK;
+}
+
+static const char *const kKernelNames[K_COUNT] = {
+    "repack_q8_0", "q8_0_matvec", "router_logits", "router_topk", "expert_gateup", "expert_down_combine",
+};
+
+void prof_begin(qq_ctx *ctx, int id)
+{
+    if (!ctx->prof_on || ctx->prof_n >= ctx->prof_cap) return;
+    const int i = ctx->prof_n;
+    ctx->prof_id[i] = id;
+    (void)hipEventRecord(ctx->prof_ev[2 * i], ctx->stream);
+}
+
+void prof_end(qq_ctx *ctx)
+{
+    if (!ctx->prof_on || ctx->prof_n >= ctx->prof_cap) return;
+    (void)hipEventRecord(ctx->prof_ev[2 * ctx->prof_n + 1], ctx->stream);
+    ctx->prof_n++;
+}
+
+static void prof_free(qq_ctx *ctx)
+{
+    for (int i = 0; i < 2 * ctx->prof_cap; i++) (void)hipEventDestroy(ctx->prof_ev[i]);
+    free(ctx->prof_ev);
+    free(ctx->prof_id);
+    ctx->prof_ev = nullptr;
+    ctx->prof_id = nullptr;
+    ctx->prof_cap = ctx->prof_n = 0;
+}
+
+static size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+static int mask_from_bytes(qq_ctx *ctx, const uint8_t *mask, int E, MaskBits *out)
+{
+    memset(out, 0, sizeof(*out));
+    if (!mask) return QQ_OK;
+    if (E > MAX_E) return set_error(ctx, "expert count %d exceeds %d", E, MAX_E);
+    for (int e = 0; e < E; e++)
+        if (mask[e]) out->w[e >> 5] |= 1u << (e & 31);
+    return QQ_OK;
+}
+
+static int tensor_alloc(qq_ctx *ctx, int in_dim, int out_dim, int n_mats, qq_tensor **out)
+{
+    if (in_dim <= 0 || out_dim <= 0 || n_mats <= 0)
+        return set_error(ctx, "bad Q8_0 shape [%d, %d, %d]", in_dim, out_dim, n_mats);
+    qq_tensor *t = new (std::nothrow) qq_tensor();
+    if (!t) return set_error(ctx, "host allocation failed");
+    t->in_dim = in_dim;
+    t->out_dim = out_dim;
+    t->n_mats = n_mats;
+    t->nb = (in_dim + QK - 1) / QK;
+    t->kp = t->nb * QK;
+    const size_t rows = (size_t)n_mats * out_dim;
+    t->qs_bytes = rows * t->kp;
+    t->d_bytes = rows * t->nb * sizeof(__half);
+    hipError_t e = hipMalloc(&t->qs, t->qs_bytes);
+    if (e == hipSuccess) e = hipMalloc(&t->d, t->d_bytes);
+    if (e != hipSuccess) {
+        if (t->qs) (void)hipFree(t->qs);
+        delete t;
+        return check_hip(ctx, e, "hipMalloc(Q8_0 tensor)");
+    }
+    *out = t;
+    return QQ_OK;
+}
+
+}  // namespace qq
+
+using namespace qq;
+
+extern "C" {
+
+int qq_init(int device, qq_ctx **out)
+{
+    if (!out) return set_error(nullptr, "qq_init: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        snprintf(g_init_err, sizeof g_init_err, "no HIP device available (%s)",
+                 e == hipSuccess ? "0 devices" : hipGetErrorString(e));
+        return QQ_E_NODEV;
+    }
+    if (device < 0 || device >= n) {
+        snprintf(g_init_err, sizeof g_init_err, "device %d out of range (%d devices)", device, n);
+        return QQ_E_NODEV;
+    }
+    hipDeviceProp_t prop;
+    if ((e = hipGetDeviceProperties(&prop, device)) != hipSuccess) return check_hip(nullptr, e, "hipGetDeviceProperties");
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        snprintf(g_init_err, sizeof g_init_err, "device %d is %s, this library is built for gfx950",
+                 device, prop.gcnArchName);
+        return QQ_E_NODEV;
+    }
+    if ((e = hipSetDevice(device)) != hipSuccess) return check_hip(nullptr, e, "hipSetDevice");
+    qq_ctx *ctx = new (std::nothrow) qq_ctx();
+    if (!ctx) return set_error(nullptr, "host allocation failed");
+    ctx->device = device;
+    ctx->num_cus = prop.multiProcessorCount;
+    if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
+        delete ctx;
+        return check_hip(nullptr, e, "hipStreamCreate");
+    }
+    ctx->own_stream = 1;
+    if ((e = hipEventCreate(&ctx->ev0)) != hipSuccess || (e = hipEventCreate(&ctx->ev1)) != hipSuccess) {
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return check_hip(nullptr, e, "hipEventCreate");
+    }
+    *out = ctx;
+    return QQ_OK;
+}
+
+void qq_destroy(qq_ctx *ctx)
+{
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->pinned) (void)hipHostFree(ctx->pinned);
+    (void)hipEventDestroy(ctx->ev0);
+    (void)hipEventDestroy(ctx->ev1);
+    prof_free(ctx);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    delete ctx;
+}
+
+const char *qq_last_error(const qq_ctx *ctx) { return ctx ? ctx->err : g_init_err; }
+
+int qq_set_stream(qq_ctx *ctx, void *hip_stream)
+{
+    if (!ctx) return QQ_E_ARG;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
+    if (hip_stream) {
+        ctx->stream = static_cast<hipStream_t>(hip_stream);
+        ctx->own_stream = 0;
+    } else {
+        QQ_HIP(ctx, hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking));
+        ctx->own_stream = 1;
+    }
+    return QQ_OK;
+}
+
+int qq_synchronize(qq_ctx *ctx)
+{
+    if (!ctx) return QQ_E_ARG;
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return QQ_OK;
+}
+
+// ---- Q8_0 tensors ---------------------------------------------------------
+
+static int upload_common(qq_ctx *ctx, const void *src, bool src_on_device, size_t nbytes,
+                         int in_dim, int out_dim, int n_mats, qq_tensor **out)
+{
+    if (!ctx || !out || !src) return set_error(ctx, "qq_q8_0_upload: NULL argument");
+    *out = nullptr;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    qq_tensor *t = nullptr;
+    int rc = tensor_alloc(ctx, in_dim, out_dim, n_mats, &t);
+    if (rc) return rc;
+    const size_t need = (size_t)n_mats * out_dim * t->nb * QBLK;
+    if (nbytes < need) {
+        qq_tensor_release(ctx, t);
+        return set_error(ctx, "Q8_0 tensor [%d, %d, %d] needs %zu bytes, got %zu", in_dim, out_dim,
+                         n_mats, need, nbytes);
+    }
+    const uint8_t *dev_src = static_cast<const uint8_t *>(src);
+    void *staging = nullptr;
+    if (!src_on_device) {
+        hipError_t e = hipMalloc(&staging, need);
+        if (e != hipSuccess) {
+            qq_tensor_release(ctx, t);
+            return check_hip(ctx, e, "hipMalloc(upload staging)");
+        }
+        e = hipMemcpyAsync(staging, src, need, hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) {
+            (void)hipFree(staging);
+            qq_tensor_release(ctx, t);
+            return check_hip(ctx, e, "hipMemcpy(upload)");
+        }
+        dev_src = static_cast<const uint8_t *>(staging);
+    }
+    rc = launch_repack_q8_0(ctx, dev_src, t);
+    hipError_t e = hipStreamSynchronize(ctx->stream);
+    if (staging) (void)hipFree(staging);
+    if (rc == QQ_OK && e != hipSuccess) rc = check_hip(ctx, e, "repack");
+    if (rc) {
+        qq_tensor_release(ctx, t);
+        return rc;
+    }
+    *out = t;
+    return QQ_OK;
+}
+
+int qq_q8_0_upload(qq_ctx *ctx, const void *gguf_bytes, size_t nbytes, int in_dim, int out_dim,
+                   int n_mats, qq_tensor **out)
+{
+    return upload_common(ctx, gguf_bytes, false, nbytes, in_dim, out_dim, n_mats, out);
+}
+
+int qq_q8_0_upload_dev(qq_ctx *ctx, const void *gguf_bytes_dev, size_t nbytes, int in_dim,
+                       int out_dim, int n_mats, qq_tensor **out)
+{
+    return upload_common(ctx, gguf_bytes_dev, true, nbytes, in_dim, out_dim, n_mats, out);
+}
+
+int qq_tensor_release(qq_ctx *ctx, qq_tensor *t)
+{
+    if (!t) return QQ_OK;
+    if (ctx) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    if (t->qs) (void)hipFree(t->qs);
+    if (t->d) (void)hipFree(t->d);
+    delete t;
+    return QQ_OK;
+}
+
+static int matvec_check(qq_ctx *ctx, const qq_tensor *t, int mat, int rows)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!t) return set_error(ctx, "matvec: NULL tensor");
+    if (mat < 0 || mat >= t->n_mats) return set_error(ctx, "matvec: matrix %d of %d", mat, t->n_mats);
+    if (rows < 0) return set_error(ctx, "matvec: rows %d", rows);
+    return QQ_OK;
+}
+
+int qq_q8_0_matvec_dev(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x_dev, float *y_dev,
+                       int rows)
+{
+    int rc = matvec_check(ctx, t, mat, rows);
+    if (rc) return rc;
+    if (rows == 0) return QQ_OK;
+    if (!x_dev || !y_dev) return set_error(ctx, "matvec: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    return launch_q8_0_matvec(ctx, t, mat, x_dev, t->in_dim, y_dev, t->out_dim, rows);
+}
+
+int qq_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, float *y, int rows)
+{
+    int rc = matvec_check(ctx, t, mat, rows);
+    if (rc) return rc;
+    if (rows == 0) return QQ_OK;
+    if (!x || !y) return set_error(ctx, "matvec: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t xb = (size_t)rows * t->in_dim * 4, yb = (size_t)rows * t->out_dim * 4;
+    if ((rc = ensure_scratch(ctx, align256(xb) + yb))) return rc;
+    float *dx = static_cast<float *>(ctx->scratch);
+    float *dy = reinterpret_cast<float *>(static_cast<char *>(ctx->scratch) + align256(xb));
+    QQ_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = launch_q8_0_matvec(ctx, t, mat, dx, t->in_dim, dy, t->out_dim, rows))) return rc;
+    QQ_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return QQ_OK;
+}
+
+// ---- MoE layer --------------------------------------------------------------
+
+int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const float *bias,
+                  const qq_tensor *gate, const qq_tensor *up, const qq_tensor *down, int H, int F,
+                  int E, int K, qq_moe **out)
+{
+    if (!ctx || !out) return QQ_E_ARG;
+    *out = nullptr;
+    if (!router_bytes || !gate || !up || !down) return set_error(ctx, "qq_moe_create: NULL tensor");
+    if (H <= 0 || F <= 0 || E <= 0 || K <= 0 || K > E || E > MAX_E || K > MAX_K)
+        return set_error(ctx, "qq_moe_create: bad dims H=%d F=%d E=%d K=%d (E<=%d, K<=%d)", H, F, E, K,
+                         MAX_E, MAX_K);
+    if (H > 4096 || F > 4096) return set_error(ctx, "qq_moe_create: H and F must be <= 4096");
+    if (gate->in_dim != H || gate->out_dim != F || gate->n_mats != E || up->in_dim != H ||
+        up->out_dim != F || up->n_mats != E)
+        return set_error(ctx, "qq_moe_create: gate/up must be [%d, %d, %d]", H, F, E);
+    if (down->in_dim != F || down->out_dim != H || down->n_mats != E)
+        return set_error(ctx, "qq_moe_create: down must be [%d, %d, %d]", F, H, E);
+    if (router_type != QQ_TYPE_F32 && router_type != QQ_TYPE_Q8_0)
+        return set_error(ctx, "Unsupported tensor type for matmul: %d", router_type);
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    qq_moe *m = new (std::nothrow) qq_moe();
+    if (!m) return set_error(ctx, "host allocation failed");
+    m->H = H;
+    m->F = F;
+    m->E = E;
+    m->K = K;
+    m->router_type = router_type;
+    m->gate = gate;
+    m->up = up;
+    m->down = down;
+    m->has_bias = bias != nullptr;
+    int rc = QQ_OK;
+    hipError_t e = hipMalloc(&m->bias, (size_t)E * 4);
+    if (e == hipSuccess) {
+        e = bias ? hipMemcpy(m->bias, bias, (size_t)E * 4, hipMemcpyHostToDevice)
+                 : hipMemset(m->bias, 0, (size_t)E * 4);
+    }
+    if (e != hipSuccess) rc = check_hip(ctx, e, "router bias");
+    if (rc == QQ_OK) {
+        if (router_type == QQ_TYPE_F32) {
+            e = hipMalloc(&m->router_f32, (size_t)E * H * 4);
+            if (e == hipSuccess) e = hipMemcpy(m->router_f32, router_bytes, (size_t)E * H * 4, hipMemcpyHostToDevice);
+            if (e != hipSuccess) rc = check_hip(ctx, e, "router upload");
+        } else {
+            const size_t nb = (size_t)(H + QK - 1) / QK;
+            rc = qq_q8_0_upload(ctx, router_bytes, (size_t)E * nb * QBLK, H, E, 1, &m->router_q8);
+        }
+    }
+    if (rc) {
+        qq_moe_release(ctx, m);
+        return rc;
+    }
+    *out = m;
+    return QQ_OK;
+}
+
+int qq_moe_release(qq_ctx *ctx, qq_moe *m)
+{
+    if (!m) return QQ_OK;
+    if (ctx) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    if (m->bias) (void)hipFree(m->bias);
+    if (m->router_f32) (void)hipFree(m->router_f32);
+    if (m->router_q8) qq_tensor_release(ctx, m->router_q8);
+    delete m;
+    return QQ_OK;
+}
+
+// Scratch layout of one forward: logits | idx | w | probs | g
+struct FwdLayout {
+    size_t logits, idx, w, probs, work, total, work_bytes;
+};
+
+static FwdLayout fwd_layout(const qq_moe *m, int T, size_t base)
+{
+    FwdLayout L;
+    size_t o = base;
+    L.logits = o; o += align256((size_t)T * m->E * 4);
+    L.idx = o;    o += align256((size_t)T * m->K * 4);
+    L.w = o;      o += align256((size_t)T * m->K * 8);
+    L.probs = o;  o += align256((size_t)T * m->E * 4);
+    L.work = o;
+    L.work_bytes = moe_work_bytes(m, T);
+    o += align256(L.work_bytes);
+    L.total = o;
+    return L;
+}
+
+static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                        const MaskBits &mask, int32_t *idx, double *w, float *probs, size_t base)
+{
+    FwdLayout L = fwd_layout(m, T, base);
+    int rc = ensure_scratch(ctx, L.total);
+    if (rc) return rc;
+    char *s = static_cast<char *>(ctx->scratch);
+    float *logits = reinterpret_cast<float *>(s + L.logits);
+    if (!idx) idx = reinterpret_cast<int32_t *>(s + L.idx);
+    if (!w) w = reinterpret_cast<double *>(s + L.w);
+    if ((rc = launch_router_topk(ctx, m, x, T, logits, idx, w, probs))) return rc;
+    return launch_moe_experts(ctx, m, x, hidden, T, mask, idx, w, s + L.work, L.work_bytes);
+}
+
+static int forward_check(qq_ctx *ctx, const qq_moe *m, int T)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!m) return set_error(ctx, "moe_forward: NULL layer");
+    if (T < 0) return set_error(ctx, "moe_forward: T=%d", T);
+    return QQ_OK;
+}
+
+int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev, int T,
+                       const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev)
+{
+    int rc = forward_check(ctx, m, T);
+    if (rc || T == 0) return rc;
+    if (!x_dev || !hidden_dev) return set_error(ctx, "moe_forward: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
+    return forward_impl(ctx, m, x_dev, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, 0);
+}
+
+int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                   const uint8_t *mask, int32_t *idx, double *w, float *probs)
+{
+    int rc = forward_check(ctx, m, T);
+    if (rc || T == 0) return rc;
+    if (!x || !hidden) return set_error(ctx, "moe_forward: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
+    // device copies of x and hidden sit in front of the forward's own scratch
+    const size_t xb = (size_t)T * m->H * 4;
+    const size_t io = 2 * align256(xb);
+    FwdLayout L = fwd_layout(m, T, io);
+    if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    char *s = static_cast<char *>(ctx->scratch);
+    float *dx = reinterpret_cast<float *>(s);
+    float *dh = reinterpret_cast<float *>(s + align256(xb));
+    int32_t *didx = reinterpret_cast<int32_t *>(s + L.idx);
+    double *dw = reinterpret_cast<double *>(s + L.w);
+    float *dp = probs ? reinterpret_cast<float *>(s + L.probs) : nullptr;
+    QQ_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    QQ_HIP(ctx, hipMemcpyAsync(dh, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+    if ((rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, dp, io))) return rc;
+    QQ_HIP(ctx, hipMemcpyAsync(hidden, dh, xb, hipMemcpyDeviceToHost, ctx->stream));
+    if (idx) QQ_HIP(ctx, hipMemcpyAsync(idx, didx, (size_t)T * m->K * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (w) QQ_HIP(ctx, hipMemcpyAsync(w, dw, (size_t)T * m->K * 8, hipMemcpyDeviceToHost, ctx->stream));
+    if (probs) QQ_HIP(ctx, hipMemcpyAsync(probs, dp, (size_t)T * m->E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return QQ_OK;
+}
+
+// ---- measurement ------------------------------------------------------------
+
+int qq_timer_start(qq_ctx *ctx)
+{
+    if (!ctx) return QQ_E_ARG;
+    QQ_HIP(ctx, hipEventRecord(ctx->ev0, ctx->stream));
+    return QQ_OK;
+}
+
+int qq_timer_stop(qq_ctx *ctx, float *ms)
+{
+    if (!ctx || !ms) return QQ_E_ARG;
+    QQ_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
+    QQ_HIP(ctx, hipEventSynchronize(ctx->ev1));
+    QQ_HIP(ctx, hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
+    return QQ_OK;
+}
+
+int qq_profile_enable(qq_ctx *ctx, int max_launches)
+{
+    if (!ctx) return QQ_E_ARG;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    ctx->prof_on = 0;
+    ctx->prof_n = 0;
+    if (max_launches <= 0) return QQ_OK;
+    if (max_launches > ctx->prof_cap) {
+        prof_free(ctx);
+        ctx->prof_ev = static_cast<hipEvent_t *>(calloc(2 * (size_t)max_launches, sizeof(hipEvent_t)));
+        ctx->prof_id = static_cast<int *>(calloc((size_t)max_launches, sizeof(int)));
+        if (!ctx->prof_ev || !ctx->prof_id) {
+            prof_free(ctx);
+            return set_error(ctx, "profile: host allocation failed");
+        }
+        for (int i = 0; i < 2 * max_launches; i++) {
+            hipError_t e = hipEventCreate(&ctx->prof_ev[i]);
+            if (e != hipSuccess) {
+                ctx->prof_cap = i / 2;
+                return check_hip(ctx, e, "hipEventCreate(profile)");
+            }
+            ctx->prof_cap = (i + 1) / 2;
+        }
+    }
+    ctx->prof_on = 1;
+    return QQ_OK;
+}
+
+int qq_profile_read(qq_ctx *ctx, float *ms_sum, int *count, int n)
+{
+    if (!ctx || !ms_sum || !count) return QQ_E_ARG;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    for (int i = 0; i < n; i++) {
+        ms_sum[i] = 0.0f;
+        count[i] = 0;
+    }
+    for (int i = 0; i < ctx->prof_n; i++) {
+        float ms = 0.0f;
+        QQ_HIP(ctx, hipEventElapsedTime(&ms, ctx->prof_ev[2 * i], ctx->prof_ev[2 * i + 1]));
+        const int id = ctx->prof_id[i];
+        if (id >= 0 && id < n) {
+            ms_sum[id] += ms;
+            count[id]++;
+        }
+    }
+    ctx->prof_n = 0;
+    return QQ_OK;
+}
+
+const char *qq_profile_name(int id)
+{
+    return (id >= 0 && id < K_COUNT) ? kKernelNames[id] : "";
+}
+
+int qq_profile_kernel_count(void) { return K_COUNT; }
+
+}  // extern "C"

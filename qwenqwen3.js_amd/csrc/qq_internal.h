@@ -1,0 +1,121 @@
+// qq_internal.h -- shared definitions of the gfx950 MoE library (not installed).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <cstddef>
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+#include <cstring>
+
+#include "../../include/qq_moe.h"
+
+namespace qq {
+
+constexpr int QK = 32;        // weights per Q8_0 block
+constexpr int QBLK = 34;      // bytes per GGUF Q8_0 block {fp16 d, int8 qs[32]}
+constexpr int WAVE = 64;      // CDNA wavefront width
+constexpr int MAX_E = 256;    // experts supported by the router and the mask bitset
+constexpr int MAX_K = 16;     // experts used per token
+
+// Expert mask passed by value to kernels (bit e set = expert e skipped).
+struct MaskBits {
+    uint32_t w[MAX_E / 32];
+};
+
+__host__ __device__ inline bool mask_has(const MaskBits &m, int e)
+{
+    return (m.w[e >> 5] >> (e & 31)) & 1u;
+}
+
+}  // namespace qq
+
+// Device-resident Q8_0 matrices after the one-time repack.
+//   qs: int8 [n_mats][rows][kp]   (row r = GGUF column r, kp = nb*32, k contiguous)
+//   d : fp16 [n_mats][rows][nb]   (scale of block b of row r)
+// The repack keeps 34 bytes per 32 weights (the GGUF byte count) but splits
+// the 2-byte scale out of each block so that every row of qs is 32-byte
+// aligned and a wavefront reads it as 64 lanes x 16 contiguous bytes.
+struct qq_tensor {
+    int in_dim;     // k (GGUF shape[0])
+    int out_dim;    // rows (GGUF shape[1])
+    int n_mats;     // experts (GGUF shape[2], 1 for a 2-D tensor)
+    int nb;         // blocks per row = ceil(in_dim/32)
+    int kp;         // nb*32
+    int8_t *qs;
+    __half *d;
+    size_t qs_bytes, d_bytes;
+};
+
+struct qq_moe {
+    int H, F, E, K;
+    int router_type;           // QQ_TYPE_F32 or QQ_TYPE_Q8_0
+    float *router_f32;         // [E][H] (F32 router; GGUF column e = expert e)
+    qq_tensor *router_q8;      // owned copy when the router is Q8_0
+    float *bias;               // [E] selection bias (zeros when absent)
+    int has_bias;
+    const qq_tensor *gate, *up, *down;   // borrowed; the caller keeps them alive
+};
+
+struct qq_ctx {
+    int device;
+    int num_cus;
+    hipStream_t stream;
+    int own_stream;
+    char err[512];
+    // device scratch arena (grown on demand; one arena per context)
+    void *scratch;
+    size_t scratch_bytes;
+    // pinned host staging for the host-pointer entry points
+    void *pinned;
+    size_t pinned_bytes;
+    // timing events of the bench entry points
+    hipEvent_t ev0, ev1;
+    // per-kernel event pairs (qq_profile_*): pool of 2*prof_cap events
+    int prof_on;
+    int prof_n, prof_cap;
+    hipEvent_t *prof_ev;
+    int *prof_id;
+};
+
+namespace qq {
+
+// Kernel ids reported by qq_profile_read (names in api.hip).
+enum KernelId {
+    K_REPACK = 0,
+    K_MATVEC,
+    K_ROUTER_LOGITS,
+    K_ROUTER_TOPK,
+    K_GATEUP,
+    K_DOWN_COMBINE,
+    K_COUNT
+};
+
+// Bracket one launch with an event pair when profiling is on.
+void prof_begin(qq_ctx *ctx, int id);
+void prof_end(qq_ctx *ctx);
+
+int set_error(qq_ctx *ctx, const char *fmt, ...);
+int check_hip(qq_ctx *ctx, hipError_t e, const char *what);
+int ensure_scratch(qq_ctx *ctx, size_t bytes);
+int ensure_pinned(qq_ctx *ctx, size_t bytes);
+
+#define QQ_HIP(ctx, call)                                          \
+    do {                                                           \
+        hipError_t e_ = (call);                                    \
+        if (e_ != hipSuccess) return ::qq::check_hip(ctx, e_, #call); \
+    } while (0)
+
+// kernel entry wrappers (defined in the .hip files)
+int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t);
+int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, int ldx,
+                       float *y, int ldy, int rows);
+int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, float *logits,
+                       int32_t *idx, double *w, float *probs);
+int launch_moe_experts(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                       const MaskBits &mask, const int32_t *idx, const double *w,
+                       void *work, size_t work_bytes);
+size_t moe_work_bytes(const qq_moe *m, int T);
+
+}  // namespace qq
