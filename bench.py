@@ -49,16 +49,23 @@ def expert_bytes():
 
 
 def kernel_bytes(name, T, n_experts, n_pairs):
-    """Algorithmic HBM bytes of one launch of `name` (each weight byte once)."""
+    """Algorithmic HBM bytes of one launch of `name`: every weight, router and
+    activation byte the math needs, once; intermediate buffers the kernels
+    exchange (partial sums, grouped rows) are not counted."""
     gate, down = expert_bytes()
+    router = E * H * 4 + E * 4
+    if name == "decode_experts":
+        return n_experts * (2 * gate + down) + router + T * H * 4
+    if name == "decode_combine":
+        return 2 * T * H * 4
     if name == "router_logits":
-        return E * H * 4 + T * H * 4 + T * E * 4
-    if name == "router_topk":
-        return T * E * 4 + E * 4 + T * K * 12 + T * E * 4
-    if name == "expert_gateup":
-        return n_experts * 2 * gate + T * H * 4 + n_pairs * F * 4
-    if name == "expert_down_combine":
-        return n_experts * down + n_pairs * F * 4 + T * K * 12 + 2 * T * H * 4
+        return E * H * 4 + T * H * 4
+    if name == "grouped_gateup":
+        return n_experts * 2 * gate + T * H * 4
+    if name == "grouped_down":
+        return n_experts * down
+    if name == "combine":
+        return 2 * T * H * 4
     return None
 
 
@@ -145,7 +152,9 @@ def main():
     T, bias_kind, wname = WORKLOADS[args.workload]
     torch.cuda.init()
     ctx = qq_hip.Context(0)
-    stream = torch.cuda.current_stream()
+    # the library launches on this stream; every event below is recorded on it
+    stream = torch.cuda.Stream()
+    torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
 
     n_layers = args.layers if T == 1 else min(args.layers, 4)
@@ -174,6 +183,7 @@ def main():
         step(i)
     ev1.record(stream)
     torch.cuda.synchronize()
+    ctx.synchronize()          # raises if a device-side wait expired
     total_ms = ev0.elapsed_time(ev1)
     ms_per_step = total_ms / args.steps
 
@@ -188,6 +198,7 @@ def main():
         step(i)
     prof = ctx.profile_read()
     ctx.profile_enable(0)
+    ctx.synchronize()
     kernels = {}
     for name, (ms, cnt) in prof.items():
         b = kernel_bytes(name, T, n_exp, n_pairs)

@@ -53,8 +53,25 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes)
 }
 
 static const char *const kKernelNames[K_COUNT] = {
-    "repack_q8_0", "q8_0_matvec", "router_logits", "router_topk", "expert_gateup", "expert_down_combine",
+    "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
+    "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
 };
+
+// Read and clear the device error word; non-zero means a bounded device-side
+// wait expired (the results of that call are not valid).
+static int check_device_error(qq_ctx *ctx)
+{
+    uint32_t e = 0;
+    QQ_HIP(ctx, hipMemcpyAsync(&e, ctx->sync_err, 4, hipMemcpyDeviceToHost, ctx->stream));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (e) {
+        QQ_HIP(ctx, hipMemsetAsync(ctx->sync_err, 0, 4, ctx->stream));
+        QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        snprintf(ctx->err, sizeof ctx->err, "device-side wait for the router timed out (code %u)", e);
+        return QQ_E_HIP;
+    }
+    return QQ_OK;
+}
 
 void prof_begin(qq_ctx *ctx, int id)
 {
@@ -161,6 +178,19 @@ int qq_init(int device, qq_ctx **out)
         delete ctx;
         return check_hip(nullptr, e, "hipEventCreate");
     }
+    void *sync = nullptr;
+    const size_t sync_bytes = 2 * MAX_E * sizeof(uint64_t) + 256;
+    if ((e = hipMalloc(&sync, sync_bytes)) != hipSuccess || (e = hipMemset(sync, 0, sync_bytes)) != hipSuccess) {
+        if (sync) (void)hipFree(sync);
+        (void)hipEventDestroy(ctx->ev0);
+        (void)hipEventDestroy(ctx->ev1);
+        (void)hipStreamDestroy(ctx->stream);
+        delete ctx;
+        return check_hip(nullptr, e, "sync area");
+    }
+    ctx->sync_slots = static_cast<uint64_t *>(sync);
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_slots + 2 * MAX_E);
+    ctx->epoch = 0;
     *out = ctx;
     return QQ_OK;
 }
@@ -174,6 +204,7 @@ void qq_destroy(qq_ctx *ctx)
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
     (void)hipEventDestroy(ctx->ev0);
     (void)hipEventDestroy(ctx->ev1);
+    if (ctx->sync_slots) (void)hipFree(ctx->sync_slots);
     prof_free(ctx);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
     delete ctx;
@@ -200,8 +231,9 @@ int qq_set_stream(qq_ctx *ctx, void *hip_stream)
 int qq_synchronize(qq_ctx *ctx)
 {
     if (!ctx) return QQ_E_ARG;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return QQ_OK;
+    return check_device_error(ctx);
 }
 
 // ---- Q8_0 tensors ---------------------------------------------------------
@@ -383,38 +415,42 @@ int qq_moe_release(qq_ctx *ctx, qq_moe *m)
     return QQ_OK;
 }
 
-// Scratch layout of one forward: logits | idx | w | probs | g
-struct FwdLayout {
-    size_t logits, idx, w, probs, work, total, work_bytes;
-};
+// Scratch of one forward.  Decode (T == 1): the decode kernels' own area.
+// Token batches: logits | idx | w | grouped work, per chunk of tokens.
+constexpr int T_CHUNK = 4096;
 
-static FwdLayout fwd_layout(const qq_moe *m, int T, size_t base)
+static size_t forward_scratch(const qq_moe *m, int T)
 {
-    FwdLayout L;
-    size_t o = base;
-    L.logits = o; o += align256((size_t)T * m->E * 4);
-    L.idx = o;    o += align256((size_t)T * m->K * 4);
-    L.w = o;      o += align256((size_t)T * m->K * 8);
-    L.probs = o;  o += align256((size_t)T * m->E * 4);
-    L.work = o;
-    L.work_bytes = moe_work_bytes(m, T);
-    o += align256(L.work_bytes);
-    L.total = o;
-    return L;
+    if (decode_supported(m, T)) return align256(decode_work_bytes(m));
+    const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
+    return align256(Tc * m->E * 4) + align256(Tc * m->K * 4) + align256(Tc * m->K * 8) +
+           align256(grouped_work_bytes(m, (int)Tc));
 }
 
+// x, hidden (and the optional outputs) are device pointers; scratch starts at `base`.
 static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                         const MaskBits &mask, int32_t *idx, double *w, float *probs, size_t base)
 {
-    FwdLayout L = fwd_layout(m, T, base);
-    int rc = ensure_scratch(ctx, L.total);
+    int rc = ensure_scratch(ctx, base + forward_scratch(m, T));
     if (rc) return rc;
-    char *s = static_cast<char *>(ctx->scratch);
-    float *logits = reinterpret_cast<float *>(s + L.logits);
-    if (!idx) idx = reinterpret_cast<int32_t *>(s + L.idx);
-    if (!w) w = reinterpret_cast<double *>(s + L.w);
-    if ((rc = launch_router_topk(ctx, m, x, T, logits, idx, w, probs))) return rc;
-    return launch_moe_experts(ctx, m, x, hidden, T, mask, idx, w, s + L.work, L.work_bytes);
+    char *s = static_cast<char *>(ctx->scratch) + base;
+    if (decode_supported(m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs, s);
+    const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
+    float *logits = reinterpret_cast<float *>(s);
+    int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(Tc * m->E * 4));
+    double *sw = reinterpret_cast<double *>(reinterpret_cast<char *>(sidx) + align256(Tc * m->K * 4));
+    char *work = reinterpret_cast<char *>(sw) + align256(Tc * m->K * 8);
+    for (int t0 = 0; t0 < T; t0 += T_CHUNK) {
+        const int tn = (T - t0 < T_CHUNK) ? T - t0 : T_CHUNK;
+        int32_t *ci = idx ? idx + (size_t)t0 * m->K : sidx;
+        double *cw = w ? w + (size_t)t0 * m->K : sw;
+        float *cp = probs ? probs + (size_t)t0 * m->E : nullptr;
+        const float *cx = x + (size_t)t0 * m->H;
+        float *ch = hidden + (size_t)t0 * m->H;
+        if ((rc = launch_router_topk(ctx, m, cx, tn, logits, ci, cw, cp))) return rc;
+        if ((rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work))) return rc;
+    }
+    return QQ_OK;
 }
 
 static int forward_check(qq_ctx *ctx, const qq_moe *m, int T)
@@ -446,26 +482,26 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     MaskBits mb;
     if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
-    // device copies of x and hidden sit in front of the forward's own scratch
+    // device copies: x | hidden | idx | w | probs, then the forward's scratch
     const size_t xb = (size_t)T * m->H * 4;
-    const size_t io = 2 * align256(xb);
-    FwdLayout L = fwd_layout(m, T, io);
-    if ((rc = ensure_scratch(ctx, L.total))) return rc;
+    const size_t ib = (size_t)T * m->K * 4, wb = (size_t)T * m->K * 8, pb = (size_t)T * m->E * 4;
+    const size_t io = 2 * align256(xb) + align256(ib) + align256(wb) + align256(pb);
+    if ((rc = ensure_scratch(ctx, io + forward_scratch(m, T)))) return rc;
     char *s = static_cast<char *>(ctx->scratch);
     float *dx = reinterpret_cast<float *>(s);
     float *dh = reinterpret_cast<float *>(s + align256(xb));
-    int32_t *didx = reinterpret_cast<int32_t *>(s + L.idx);
-    double *dw = reinterpret_cast<double *>(s + L.w);
-    float *dp = probs ? reinterpret_cast<float *>(s + L.probs) : nullptr;
+    int32_t *didx = reinterpret_cast<int32_t *>(s + 2 * align256(xb));
+    double *dw = reinterpret_cast<double *>(reinterpret_cast<char *>(didx) + align256(ib));
+    float *dp = reinterpret_cast<float *>(reinterpret_cast<char *>(dw) + align256(wb));
     QQ_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
     QQ_HIP(ctx, hipMemcpyAsync(dh, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
-    if ((rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, dp, io))) return rc;
+    if ((rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, probs ? dp : nullptr, io))) return rc;
     QQ_HIP(ctx, hipMemcpyAsync(hidden, dh, xb, hipMemcpyDeviceToHost, ctx->stream));
-    if (idx) QQ_HIP(ctx, hipMemcpyAsync(idx, didx, (size_t)T * m->K * 4, hipMemcpyDeviceToHost, ctx->stream));
-    if (w) QQ_HIP(ctx, hipMemcpyAsync(w, dw, (size_t)T * m->K * 8, hipMemcpyDeviceToHost, ctx->stream));
-    if (probs) QQ_HIP(ctx, hipMemcpyAsync(probs, dp, (size_t)T * m->E * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (idx) QQ_HIP(ctx, hipMemcpyAsync(idx, didx, ib, hipMemcpyDeviceToHost, ctx->stream));
+    if (w) QQ_HIP(ctx, hipMemcpyAsync(w, dw, wb, hipMemcpyDeviceToHost, ctx->stream));
+    if (probs) QQ_HIP(ctx, hipMemcpyAsync(probs, dp, pb, hipMemcpyDeviceToHost, ctx->stream));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return QQ_OK;
+    return check_device_error(ctx);
 }
 
 // ---- measurement ------------------------------------------------------------

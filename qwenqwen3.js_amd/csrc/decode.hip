@@ -1,0 +1,461 @@
+// decode.hip -- batch-1 decode of one LFM2-MoE MoE layer in two launches.
+//
+// Reference: Lfm2Engine._moEFFN, src/lfm2-engine.js:413-487, for one token.
+//
+// Launch 1 (moe_decode_experts): E router workgroups + K*NS expert-unit
+// workgroups (NS = ceil(F/32)).
+//   * router workgroup e: binary64 dot of x with router column e, fp32 logit,
+//     p_e = fp32 sigmoid (binary64 math) and selection score s_e = fp32(p_e +
+//     bias_e), published as two 64-bit words slot_s[e] = (epoch << 32) | s_e
+//     and slot_p[e] = (epoch << 32) | p_e with relaxed device-scope stores.
+//     Value and epoch travel together, so no fence (and no cache write-back or
+//     invalidate) is needed on either side, and every expert has its own
+//     words, so nothing is contended.
+//   * expert-unit workgroup (k, s): stages x in LDS (and, in waves 1-7, its
+//     3-level int8 decomposition), waits in wave 0 (bounded) until all E score
+//     slots carry this call's epoch, ranks the experts itself (rank of e =
+//     number of experts ordered before it by (score desc, index asc): the
+//     order of a stable descending sort; identical in every workgroup), then
+//     streams one F-slice of the rank-k expert: gate and up rows f in
+//     [32s, 32s+32) (2 x 32 rows x H), SwiGLU, and the matching down block
+//     column s (H rows x 32), writing the partial down product
+//     partial[k][s][0..H).  Every weight load is issued before any
+//     arithmetic; dot products use v_dot4_i32_i8.
+//   Workgroup (0, 0) also writes the routing outputs.
+// Launch 2 (moe_decode_combine): y_k = sum_s partial[k][s] in a fixed order,
+//   acc = fp32(acc + w_k * y_k) in rank order, hidden += acc.
+//
+// Nothing waits on another workgroup except on the router slots, and the
+// router workgroups have the lowest ids, so they are dispatched first and never
+// wait themselves.  The wait is bounded by the wall clock; on expiry the
+// workgroup sets the context's error word and returns.
+#include "qq_device.h"
+
+namespace qq {
+
+constexpr int DEC_WAVES = 8;
+constexpr int DEC_THREADS = DEC_WAVES * WAVE;
+constexpr uint64_t DEC_WAIT_TICKS = 5000000;   // 50 ms at the 100 MHz wall clock
+
+struct DecodeArgs {
+    const float *x;
+    int H, F, E, K;
+    int nbH, nbF, NS;
+    const float *rf32;
+    const int8_t *rq;
+    const __half *rd;
+    int router_q8;
+    const float *bias;
+    const int8_t *gq;
+    const __half *gd;
+    const int8_t *uq;
+    const __half *ud;
+    const int8_t *dq;
+    const __half *dd;
+    MaskBits mask;
+    uint32_t epoch;
+    uint64_t *slot_s;     // [E] (epoch << 32 | selection score bits), persist across calls
+    uint64_t *slot_p;     // [E] (epoch << 32 | sigmoid probability bits)
+    float *partial;       // [K][NS][H]
+    int32_t *route_idx;   // [K]
+    double *route_w;      // [K]
+    int32_t *out_idx;     // optional outputs
+    double *out_w;
+    float *out_probs;
+    uint32_t *err;
+};
+
+// Bounded wait until lanes < E of `slots` carry `epoch`; returns the word.
+__device__ __forceinline__ uint64_t wait_slots(const uint64_t *slots, int E, uint32_t epoch, int lane,
+                                               int &ok)
+{
+    const uint64_t t0 = wall_clock64();
+    uint64_t v;
+    while (true) {
+        v = (lane < E) ? __hip_atomic_load(&slots[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                       : ((uint64_t)epoch << 32);
+        if (__all((uint32_t)(v >> 32) == epoch)) break;
+        if (wall_clock64() - t0 > DEC_WAIT_TICKS) {
+            ok = 0;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+    return v;
+}
+
+// NBW = blocks of H per wave (and 32-row chunks of H per wave) = ceil(ceil(H/32)/8).
+template <int NBW>
+__global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeArgs a)
+{
+    constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
+    constexpr int NHB = XN / 16;                // 16-value chunks
+    __shared__ __align__(16) float xl[XN];
+    __shared__ __align__(16) int4 xq1[NHB], xq2[NHB], xq3[NHB];
+    __shared__ float xsig[NHB];
+    __shared__ __align__(16) float gl[QK];
+    __shared__ __align__(16) int4 gq1[2], gq2[2], gq3[2];
+    __shared__ float gsig[2];
+    __shared__ float redg[DEC_WAVES][QK];
+    __shared__ float redu[DEC_WAVES][QK];
+    __shared__ double rsum[DEC_WAVES];
+    __shared__ int sh_e, sh_ok;
+    __shared__ int sh_rank_e[MAX_K];
+    __shared__ float sh_rank_p[MAX_K];
+    __shared__ __align__(16) float sh_score[WAVE];
+
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = threadIdx.x / WAVE;
+
+    if ((int)blockIdx.x < a.E) {
+        // ---- router workgroup: logit, sigmoid, score of expert e ----
+        const int e = blockIdx.x;
+        double acc = 0.0;
+        if (!a.router_q8 && (a.H & 3) == 0) {
+            const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+            const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32 + (size_t)e * a.H);
+            for (int k4 = threadIdx.x; k4 < a.H / 4; k4 += DEC_THREADS) {
+                const float4 xv = x4[k4], wv = w4[k4];
+                acc = fma((double)xv.x, (double)wv.x, acc);
+                acc = fma((double)xv.y, (double)wv.y, acc);
+                acc = fma((double)xv.z, (double)wv.z, acc);
+                acc = fma((double)xv.w, (double)wv.w, acc);
+            }
+        } else {
+            for (int k = threadIdx.x; k < a.H; k += DEC_THREADS) {
+                double wv;
+                if (a.router_q8) {
+                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e);
+                    wv = (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]);
+                } else {
+                    wv = (double)a.rf32[(size_t)e * a.H + k];
+                }
+                acc = fma((double)a.x[k], wv, acc);
+            }
+        }
+        acc = wave_sum(acc);
+        if (lane == 0) rsum[wave] = acc;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double s = rsum[0];
+#pragma unroll
+            for (int w = 1; w < DEC_WAVES; w++) s = s + rsum[w];
+            // lfm2-engine.js:420-431
+            const float logit = (float)s;
+            const float p = (float)(1.0 / (1.0 + exp(-(double)logit)));
+            const float sc = p + a.bias[e];
+            const uint64_t ep = (uint64_t)a.epoch << 32;
+            __hip_atomic_store(&a.slot_p[e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(&a.slot_s[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+    }
+
+    const int unit = blockIdx.x - a.E;
+    const int kslot = unit / a.NS;
+    const int s = unit - kslot * a.NS;
+
+    // ---- x -> LDS ----
+    for (int i = threadIdx.x; i < XN; i += DEC_THREADS) xl[i] = (i < a.H) ? a.x[i] : 0.0f;
+    __syncthreads();
+
+    // ---- routing (lfm2-engine.js:433-447) in wave 0; waves 1-7 decompose x ----
+    if (wave == 0) {
+        int ok = 1;
+        const uint64_t v = wait_slots(a.slot_s, a.E, a.epoch, lane, ok);
+        const float sc = (lane < a.E) ? __uint_as_float((uint32_t)v) : -INFINITY;
+        sh_score[lane] = sc;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        // rank: experts ordered before this one by (score desc, index asc);
+        // the rank-k expert is the k-th element of a stable descending sort
+        int rank = 0;
+        for (int i0 = 0; i0 < a.E; i0 += 4) {
+            const float4 q = *reinterpret_cast<const float4 *>(&sh_score[i0]);
+            const float qq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int i = i0 + u;
+                rank += (i < a.E && (qq[u] > sc || (qq[u] == sc && i < lane))) ? 1 : 0;
+            }
+        }
+        if (lane >= a.E) rank = INT_MAX;
+        const uint64_t hit = __ballot(rank == kslot);
+        if (lane == 0) {
+            sh_e = hit ? (int)__builtin_ctzll(hit) : 0;
+            sh_ok = ok && hit != 0;
+            if (!ok) atomicOr(a.err, 1u);
+        }
+        if (unit == 0 && ok) {
+            // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457)
+            int okp = 1;
+            const uint64_t pv = wait_slots(a.slot_p, a.E, a.epoch, lane, okp);
+            if (!okp && lane == 0) atomicOr(a.err, 2u);
+            const float p = __uint_as_float((uint32_t)pv);
+            if (a.out_probs && lane < a.E) a.out_probs[lane] = p;
+            if (rank < a.K) {
+                sh_rank_e[rank] = lane;
+                sh_rank_p[rank] = p;
+            }
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+            if (lane == 0) {
+                double sumW = 1e-6;
+                for (int k = 0; k < a.K; k++) sumW = sumW + (double)sh_rank_p[k];
+                const double inv = 1.0 / sumW;
+                for (int k = 0; k < a.K; k++) {
+                    const double wk = (double)sh_rank_p[k] * inv;
+                    a.route_idx[k] = sh_rank_e[k];
+                    a.route_w[k] = wk;
+                    if (a.out_idx) a.out_idx[k] = sh_rank_e[k];
+                    if (a.out_w) a.out_w[k] = wk;
+                }
+            }
+        }
+    } else {
+        for (int c = threadIdx.x - WAVE; c < NHB; c += DEC_THREADS - WAVE) {
+            Lev3 L;
+            decompose16(&xl[16 * c], L);
+            xq1[c] = L.l1;
+            xq2[c] = L.l2;
+            xq3[c] = L.l3;
+            xsig[c] = L.sig;
+        }
+    }
+    __syncthreads();
+    if (!sh_ok) return;
+    const int e = sh_e;
+    if (mask_has(a.mask, e)) return;   // the combine skips masked ranks
+
+    const int h = lane & 1;
+    const int f = s * QK + lane / 2;
+    const bool f_ok = f < a.F;
+
+    // ---- issue every weight load of this workgroup ----
+    // All addresses are clamped in bounds so every load is unconditional and
+    // the compiler issues them back to back; out-of-range rows / blocks get a
+    // zero scale afterwards.  One 64-bit base per tensor, uniform strides.
+    int4 gq[NBW], uq[NBW], dq[NBW];
+    __half gdh[NBW], udh[NBW], ddh[NBW];
+    {
+        const int fc = min(f, a.F - 1);
+        const int ilast = (a.nbH - 1 - wave) >= 0 ? (a.nbH - 1 - wave) / DEC_WAVES : 0;
+        const size_t row0 = ((size_t)e * a.nbH + min(wave, a.nbH - 1)) * a.F + fc;
+        const size_t rstride = (size_t)DEC_WAVES * a.F;
+        const int8_t *gp = a.gq + row0 * QK + 16 * h;
+        const int8_t *up = a.uq + row0 * QK + 16 * h;
+#pragma unroll
+        for (int i = 0; i < NBW; i++) {
+            const size_t o = (size_t)min(i, ilast) * rstride;
+            gq[i] = *reinterpret_cast<const int4 *>(gp + o * QK);
+            uq[i] = *reinterpret_cast<const int4 *>(up + o * QK);
+            gdh[i] = a.gd[row0 + o];
+            udh[i] = a.ud[row0 + o];
+        }
+        // down rows j = (wave + 8i)*32 + lane/2 of block column s
+        const size_t dsbase = ((size_t)e * a.nbF + s) * a.H;
+#pragma unroll
+        for (int i = 0; i < NBW; i++) {
+            const int j = min((wave + DEC_WAVES * i) * QK + lane / 2, a.H - 1);
+            dq[i] = *reinterpret_cast<const int4 *>(a.dq + (dsbase + j) * QK + 16 * h);
+            ddh[i] = a.dd[dsbase + j];
+        }
+    }
+    // every load above is issued before any of the work below
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- gate / up rows, SwiGLU (tensor.js:167-178) ----
+    float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NBW; i++) {
+        // blocks past nbH: zero scale and zero activations (x is padded)
+        const int b = wave + DEC_WAVES * i;
+        const int c = 2 * b + h;
+        const bool bok = f_ok && b < a.nbH;
+        const float sg = bok ? __half2float(gdh[i]) : 0.0f;
+        const float su = bok ? __half2float(udh[i]) : 0.0f;
+        const int4 l1 = xq1[c], l2 = xq2[c], l3 = xq3[c];
+        const float sig = xsig[c];
+        ga = fmaf(dot16_lev3(gq[i], l1, l2, l3, sig), sg, ga);
+        ua = fmaf(dot16_lev3(uq[i], l1, l2, l3, sig), su, ua);
+    }
+    ga += __shfl_xor(ga, 1, WAVE);
+    ua += __shfl_xor(ua, 1, WAVE);
+    if (h == 0) {
+        redg[wave][lane / 2] = ga;
+        redu[wave][lane / 2] = ua;
+    }
+    __syncthreads();
+    if (threadIdx.x < QK) {
+        const int r = threadIdx.x;
+        float G = redg[0][r], U = redu[0][r];
+#pragma unroll
+        for (int w = 1; w < DEC_WAVES; w++) {
+            G += redg[w][r];
+            U += redu[w][r];
+        }
+        float gv = 0.0f;
+        if (s * QK + r < a.F) {
+            const double g64 = (double)G;
+            const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
+            gv = sg * U;
+        }
+        gl[r] = gv;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        Lev3 L;
+        decompose16(&gl[16 * threadIdx.x], L);
+        gq1[threadIdx.x] = L.l1;
+        gq2[threadIdx.x] = L.l2;
+        gq3[threadIdx.x] = L.l3;
+        gsig[threadIdx.x] = L.sig;
+    }
+    __syncthreads();
+
+    // ---- partial down product over this slice ----
+    float *part = a.partial + ((size_t)kslot * a.NS + s) * a.H;
+    const int4 m1 = gq1[h], m2 = gq2[h], m3 = gq3[h];
+    const float msig = gsig[h];
+#pragma unroll
+    for (int i = 0; i < NBW; i++) {
+        const int j = (wave + DEC_WAVES * i) * QK + lane / 2;
+        const float sdd = (j < a.H) ? __half2float(ddh[i]) : 0.0f;
+        float y = dot16_lev3(dq[i], m1, m2, m3, msig) * sdd;
+        y += __shfl_xor(y, 1, WAVE);
+        if (h == 0 && j < a.H) part[j] = y;
+    }
+}
+
+// 256 threads per 32 outputs: thread (group q, output jl) sums the slices
+// s = q, q+8, ... (NSP of them, NSP = ceil(NS/8)) of up to 4 ranks, with all
+// its loads in flight at once; the 8 groups are then summed in a fixed order.
+template <int NSP>
+__global__ __launch_bounds__(256) void moe_decode_combine_kernel(
+    const float *__restrict__ partial, int H, int NS, int K, const int32_t *__restrict__ route_idx,
+    const double *__restrict__ route_w, MaskBits mask, float *__restrict__ hidden)
+{
+    __shared__ float red[MAX_K][8][32];
+    const int jl = threadIdx.x & 31;
+    const int q = threadIdx.x >> 5;
+    const int j = blockIdx.x * 32 + jl;
+    const int jc = min(j, H - 1);
+    for (int k0 = 0; k0 < K; k0 += 4) {
+        float v[4][NSP];
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            const int k = min(k0 + kk, K - 1);
+#pragma unroll
+            for (int i = 0; i < NSP; i++) {
+                const int s = min(q + 8 * i, NS - 1);
+                v[kk][i] = partial[((size_t)k * NS + s) * H + jc];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kk = 0; kk < 4; kk++) {
+            float y = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NSP; i++)
+                if (q + 8 * i < NS) y += v[kk][i];
+            if (k0 + kk < K) red[k0 + kk][q][jl] = y;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 32 && j < H) {
+        float acc = 0.0f;
+        for (int k = 0; k < K; k++) {
+            const int e = route_idx[k];
+            if ((unsigned)e >= (unsigned)MAX_E || mask_has(mask, e)) continue;
+            float y = red[k][0][jl];
+#pragma unroll
+            for (int p = 1; p < 8; p++) y += red[k][p][jl];
+            acc = (float)((double)acc + route_w[k] * (double)y);
+        }
+        hidden[j] = hidden[j] + acc;
+    }
+}
+
+bool decode_supported(const qq_moe *m, int T)
+{
+    return T == 1 && m->E <= WAVE && m->H <= 8 * DEC_WAVES * QK;
+}
+
+size_t decode_work_bytes(const qq_moe *m)
+{
+    const int NS = (m->F + QK - 1) / QK;
+    return (size_t)m->K * NS * m->H * 4 + 256 + 256 + (size_t)m->K * 4 + 256;
+}
+
+template <int NBW>
+static void launch_experts(const DecodeArgs &a, dim3 grid, hipStream_t st)
+{
+    hipLaunchKernelGGL(moe_decode_experts_kernel<NBW>, grid, dim3(DEC_THREADS), 0, st, a);
+}
+
+int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
+                      const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
+                      char *work)
+{
+    DecodeArgs a;
+    a.x = x;
+    a.H = m->H;
+    a.F = m->F;
+    a.E = m->E;
+    a.K = m->K;
+    a.nbH = (m->H + QK - 1) / QK;
+    a.nbF = (m->F + QK - 1) / QK;
+    a.NS = a.nbF;
+    a.router_q8 = m->router_type == QQ_TYPE_Q8_0;
+    a.rf32 = m->router_f32;
+    a.rq = a.router_q8 ? m->router_q8->qs : nullptr;
+    a.rd = a.router_q8 ? m->router_q8->d : nullptr;
+    a.bias = m->bias;
+    a.gq = m->gate->qs;
+    a.gd = m->gate->d;
+    a.uq = m->up->qs;
+    a.ud = m->up->d;
+    a.dq = m->down->qs;
+    a.dd = m->down->d;
+    a.mask = mask;
+    if (++ctx->epoch == 0) ctx->epoch = 1;
+    a.epoch = ctx->epoch;
+    a.slot_s = ctx->sync_slots;
+    a.slot_p = ctx->sync_slots + MAX_E;
+    a.err = ctx->sync_err;
+    const size_t part_b = ((size_t)m->K * a.NS * m->H * 4 + 255) & ~(size_t)255;
+    a.partial = reinterpret_cast<float *>(work);
+    a.route_w = reinterpret_cast<double *>(work + part_b);
+    a.route_idx = reinterpret_cast<int32_t *>(reinterpret_cast<char *>(a.route_w) + 256);
+    a.out_idx = out_idx;
+    a.out_w = out_w;
+    a.out_probs = out_probs;
+
+    const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
+    const dim3 grid(m->E + m->K * a.NS);
+    prof_begin(ctx, K_DECODE_EXPERTS);
+    if (nbw <= 1) launch_experts<1>(a, grid, ctx->stream);
+    else if (nbw <= 2) launch_experts<2>(a, grid, ctx->stream);
+    else if (nbw <= 4) launch_experts<4>(a, grid, ctx->stream);
+    else launch_experts<8>(a, grid, ctx->stream);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+
+    const int nsp = (a.NS + 7) / 8;
+    const dim3 cgrid((m->H + 31) / 32);
+#define QQ_CB(N)                                                                                 \
+    hipLaunchKernelGGL(moe_decode_combine_kernel<N>, cgrid, dim3(256), 0, ctx->stream, a.partial, \
+                       m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden)
+    prof_begin(ctx, K_DECODE_COMBINE);
+    if (nsp <= 1) QQ_CB(1);
+    else if (nsp <= 2) QQ_CB(2);
+    else if (nsp <= 4) QQ_CB(4);
+    else if (nsp <= 8) QQ_CB(8);
+    else QQ_CB(16);
+    prof_end(ctx);
+#undef QQ_CB
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+}  // namespace qq

@@ -1,7 +1,9 @@
-// qq_device.h -- device helpers shared by the kernels (wave reductions, Q8_0 dot).
+// qq_device.h -- device helpers shared by the kernels.
 #pragma once
 
 #include "qq_internal.h"
+
+#include <climits>
 
 namespace qq {
 
@@ -40,9 +42,200 @@ __device__ __forceinline__ float dot16_q8(const int4 q, const float *x, float xs
     return fmaf(-128.0f, xsum, acc);
 }
 
-__device__ __forceinline__ float half_bits_to_float(uint16_t h)
+// Same, activations read from LDS as four float4.
+__device__ __forceinline__ float dot16_q8_lds(const int4 q, const float *xl, float xsum)
 {
-    return __half2float(__ushort_as_half(h));
+    float xr[16];
+    const float4 *p = reinterpret_cast<const float4 *>(xl);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = p[i];
+        xr[4 * i] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    return dot16_q8(q, xr, xsum);
+}
+
+// Hide a register value from loop-invariant code motion: without it the
+// compiler hoists the int8->float conversion of every weight out of a token
+// loop and runs out of registers.
+__device__ __forceinline__ void opaque(int4 &q)
+{
+    asm volatile("" : "+v"(q.x), "+v"(q.y), "+v"(q.z), "+v"(q.w));
+}
+
+// 16 int8 weights -> 16 floats in offset binary (q + 128), one
+// v_cvt_f32_ubyteN each; pair with dot16_off.
+__device__ __forceinline__ void cvt16_off(const int4 q, float *w)
+{
+    const uint32_t d[4] = {(uint32_t)q.x ^ 0x80808080u, (uint32_t)q.y ^ 0x80808080u,
+                           (uint32_t)q.z ^ 0x80808080u, (uint32_t)q.w ^ 0x80808080u};
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int b = 0; b < 4; b++) w[4 * i + b] = (float)((d[i] >> (8 * b)) & 0xffu);
+}
+
+// sum_i (q_i + 128) * x_i - 128 * sum_i x_i, x from LDS.
+__device__ __forceinline__ float dot16_off(const float *w, const float *xl, float xsum)
+{
+    const float4 *p = reinterpret_cast<const float4 *>(xl);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float4 v = p[i];
+        acc = fmaf(w[4 * i], v.x, acc);
+        acc = fmaf(w[4 * i + 1], v.y, acc);
+        acc = fmaf(w[4 * i + 2], v.z, acc);
+        acc = fmaf(w[4 * i + 3], v.w, acc);
+    }
+    return fmaf(-128.0f, xsum, acc);
+}
+
+// ---- int8 dot products on a 3-level decomposition of fp32 activations ----
+// A chunk of 16 activations with sigma = max|x|/127 is written as
+//   x ~= sigma * (a1 + a2/254 + a3/254^2),  a1, a2, a3 in [-127, 127],
+// each level a rounded residual of the previous one.  The representation
+// error is below sigma * 2^-15 + |x| * 2^-23 per value, about 1e-7 of the
+// chunk's largest value, so a dot product against int8 weights keeps fp32
+// accuracy while each group of 4 weights costs one v_dot4 per level.
+struct Lev3 {
+    int4 l1, l2, l3;
+    float sig;
+};
+
+__device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
+{
+    return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+           ((uint32_t)(d & 0xff) << 24);
+}
+
+__device__ __forceinline__ void decompose16(const float *v, Lev3 &o)
+{
+    float m = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
+    int q1[16], q2[16], q3[16];
+    const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const float t = v[i] * inv;
+        const float a1 = fminf(fmaxf(rintf(t), -127.0f), 127.0f);
+        const float t2 = (t - a1) * 254.0f;
+        const float a2 = fminf(fmaxf(rintf(t2), -127.0f), 127.0f);
+        const float t3 = (t2 - a2) * 254.0f;
+        const float a3 = fminf(fmaxf(rintf(t3), -127.0f), 127.0f);
+        q1[i] = (int)a1;
+        q2[i] = (int)a2;
+        q3[i] = (int)a3;
+    }
+    o.sig = m * (1.0f / 127.0f);
+    o.l1 = make_int4((int)pack4_i8(q1[0], q1[1], q1[2], q1[3]), (int)pack4_i8(q1[4], q1[5], q1[6], q1[7]),
+                     (int)pack4_i8(q1[8], q1[9], q1[10], q1[11]), (int)pack4_i8(q1[12], q1[13], q1[14], q1[15]));
+    o.l2 = make_int4((int)pack4_i8(q2[0], q2[1], q2[2], q2[3]), (int)pack4_i8(q2[4], q2[5], q2[6], q2[7]),
+                     (int)pack4_i8(q2[8], q2[9], q2[10], q2[11]), (int)pack4_i8(q2[12], q2[13], q2[14], q2[15]));
+    o.l3 = make_int4((int)pack4_i8(q3[0], q3[1], q3[2], q3[3]), (int)pack4_i8(q3[4], q3[5], q3[6], q3[7]),
+                     (int)pack4_i8(q3[8], q3[9], q3[10], q3[11]), (int)pack4_i8(q3[12], q3[13], q3[14], q3[15]));
+}
+
+__device__ __forceinline__ int sdot16(const int4 q, const int4 a)
+{
+    int s = __builtin_amdgcn_sdot4(q.x, a.x, 0, false);
+    s = __builtin_amdgcn_sdot4(q.y, a.y, s, false);
+    s = __builtin_amdgcn_sdot4(q.z, a.z, s, false);
+    return __builtin_amdgcn_sdot4(q.w, a.w, s, false);
+}
+
+// sum_i q_i * x_i for 16 int8 weights against a decomposed chunk.
+__device__ __forceinline__ float dot16_lev3(const int4 q, const int4 l1, const int4 l2, const int4 l3,
+                                            float sig)
+{
+    const float s1 = (float)sdot16(q, l1);
+    const float s2 = (float)sdot16(q, l2);
+    const float s3 = (float)sdot16(q, l3);
+    return fmaf(fmaf(s3, 1.0f / 254.0f, s2), 1.0f / 254.0f, s1) * sig;
+}
+
+// Offsets in the block-major device layout of a qq_tensor:
+//   qs[(mat*nb + b)*rows + r][32],  d[(mat*nb + b)*rows + r]
+__device__ __forceinline__ size_t bm_index(int mat, int nb, int b, int rows, int r)
+{
+    return ((size_t)mat * nb + b) * rows + r;
+}
+
+// Sigmoid routing for one token in one wavefront (lfm2-engine.js:420-447).
+// Lane e (+64*i) holds the fp32 logit of expert e.  Every lane returns the
+// same ranked selection: idx[k], unbiased probability p[k] and 1/S with
+// S = 1e-6 + sum_k p[k] accumulated in rank order in binary64.  The argmax
+// order (score desc, index asc) is the order of a stable descending sort.
+template <int EPL>
+struct WaveRoute {
+    int idx[MAX_K];
+    float p[MAX_K];
+    double inv;
+    float prob[EPL];   // this lane's sigmoid probabilities (expert lane + 64*i)
+};
+
+__device__ __forceinline__ bool rank_before(float av, int ai, float bv, int bi)
+{
+    if (ai == INT_MAX) return false;
+    if (bi == INT_MAX) return true;
+    return (av > bv) || (av == bv && ai < bi);
+}
+
+template <int EPL>
+__device__ __forceinline__ void wave_route(const float (&logit)[EPL], int E, int K,
+                                           const float *__restrict__ bias, WaveRoute<EPL> &out)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    float s[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane + WAVE * i;
+        out.prob[i] = 0.0f;
+        s[i] = 0.0f;
+        if (e < E) {
+            out.prob[i] = (float)(1.0 / (1.0 + exp(-(double)logit[i])));
+            s[i] = out.prob[i] + bias[e];
+        }
+    }
+    uint32_t taken = 0;
+    double sumW = 1e-6;
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++) {   // fully unrolled: idx/p stay in registers
+        out.idx[k] = INT_MAX;
+        out.p[k] = 0.0f;
+        if (k >= K) continue;
+        float bv = 0.0f, bp = 0.0f;
+        int bi = INT_MAX;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int e = lane + WAVE * i;
+            if (e < E && !((taken >> i) & 1u) && (bi == INT_MAX || s[i] > bv)) {
+                bv = s[i];
+                bi = e;
+                bp = out.prob[i];
+            }
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, WAVE);
+            const int oi = __shfl_xor(bi, o, WAVE);
+            const float op = __shfl_xor(bp, o, WAVE);
+            if (rank_before(ov, oi, bv, bi)) {
+                bv = ov;
+                bi = oi;
+                bp = op;
+            }
+        }
+        if ((bi & (WAVE - 1)) == lane) taken |= 1u << (bi / WAVE);
+        out.idx[k] = bi;
+        out.p[k] = bp;
+        sumW = sumW + (double)bp;
+    }
+    out.inv = 1.0 / sumW;
 }
 
 }  // namespace qq

@@ -72,6 +72,12 @@ struct qq_ctx {
     size_t pinned_bytes;
     // timing events of the bench entry points
     hipEvent_t ev0, ev1;
+    // device words shared by the kernels of this context: the decode router's
+    // per-expert (epoch, score) and (epoch, probability) slots (2*MAX_E) and
+    // the error word
+    uint64_t *sync_slots;
+    uint32_t *sync_err;
+    uint32_t epoch;
     // per-kernel event pairs (qq_profile_*): pool of 2*prof_cap events
     int prof_on;
     int prof_n, prof_cap;
@@ -87,8 +93,12 @@ enum KernelId {
     K_MATVEC,
     K_ROUTER_LOGITS,
     K_ROUTER_TOPK,
-    K_GATEUP,
-    K_DOWN_COMBINE,
+    K_DECODE_EXPERTS,
+    K_DECODE_COMBINE,
+    K_DISPATCH,
+    K_GROUPED_GATEUP,
+    K_GROUPED_DOWN,
+    K_COMBINE,
     K_COUNT
 };
 
@@ -113,9 +123,13 @@ int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x,
                        float *y, int ldy, int rows);
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, float *logits,
                        int32_t *idx, double *w, float *probs);
-int launch_moe_experts(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                       const MaskBits &mask, const int32_t *idx, const double *w,
-                       void *work, size_t work_bytes);
-size_t moe_work_bytes(const qq_moe *m, int T);
+bool decode_supported(const qq_moe *m, int T);
+size_t decode_work_bytes(const qq_moe *m);
+int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
+                      const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
+                      char *work);
+size_t grouped_work_bytes(const qq_moe *m, int T);
+int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                       const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 
 }  // namespace qq

@@ -110,6 +110,10 @@ def _check_moe(L, x, hid, mask=None, tol=TOL_GEMV, rows=None):
 
 
 @pytest.mark.parametrize("case", [
+    dict(H=64, F=64, E=8, K=2, T=1),
+    dict(H=100, F=50, E=5, K=5, T=1),        # ragged dims on the batch-1 path
+    dict(H=2048, F=1792, E=64, K=8, T=1),    # 64 experts, 8 used
+    dict(H=4096, F=96, E=16, K=2, T=1),      # widest hidden size
     dict(H=64, F=64, E=8, K=2, T=5),
     dict(H=96, F=160, E=6, K=3, T=4),
     dict(H=2048, F=64, E=32, K=4, T=3),
@@ -156,11 +160,28 @@ def test_moe_ties_lower_index():
 
 
 def test_moe_decode_batch1_full():
-    """One LFM2-8B-A1B MoE layer at batch-1 decode (H=2048, F=1792, E=32, K=4)."""
+    """One LFM2-8B-A1B MoE layer at batch-1 decode (H=2048, F=1792, E=32, K=4),
+    several calls in a row on one layer handle (the router flags are reused)."""
     L = full_layer(1)
-    x, hid = synth.activations(101, 4, 2048)
-    for t in range(4):
-        _check_moe(L, x[t:t + 1], hid[t:t + 1])
+    x, hid = synth.activations(101, 6, 2048)
+    ctx = gpu_context()
+    m = upload_layer(ctx, L)
+    try:
+        for t in range(6):
+            mask = {int(oracle.moe_route(L, x[t:t + 1])[0][0, 1])} if t == 5 else None
+            out, idx, w, probs = m.forward(x[t:t + 1], hid[t:t + 1], mask=mask)
+            r_out, r_idx, r_w, r_probs = oracle.moe_ffn(L, x[t:t + 1], hid[t:t + 1], mask=mask)
+            np.testing.assert_array_equal(idx, r_idx)
+            np.testing.assert_array_equal(w, r_w)
+            np.testing.assert_array_equal(probs, r_probs)
+            err = rel_l2(moe_delta(out, hid[t:t + 1]), moe_delta(r_out, hid[t:t + 1]))
+            _say("decode token", t, "rel_l2", err)
+            assert err < TOL_GEMV
+        ctx.synchronize()
+    finally:
+        for t in m._keep:
+            t.release()
+        m.release()
 
 
 def test_moe_decode_batch64_full():
