@@ -1,0 +1,173 @@
+'use strict';
+// MI355X drop-in for the LFM2-MoE MoE feed-forward path of QwenQwen3.js.
+//
+// Keeps the reference's JavaScript call surface and runs it on the gfx950 HIP
+// library through the Node-API addon (qq_napi.node -> libqqmoe.so):
+//   matmulQ80xF32(meta, input)      src/tensor.js:26-53
+//   matmulGeneric(meta, input)      src/tensor.js:485-496 (type 8; other types are
+//                                   delegated to the matmulGeneric being replaced)
+//   Lfm2Engine.prototype._moEFFN    src/lfm2-engine.js:413-487
+// plus a batched entry point with no reference counterpart:
+//   device.moeForward(layer, X, hidden, T, {mask, wantProbs})
+//
+// There is no CPU fallback: when the addon or the device is missing, the
+// constructor and install() throw.  Written for Node 12 (no `?.`, no `??`).
+
+const path = require('path');
+
+const ADDON_PATH = path.join(__dirname, '..', 'qq_napi.node');
+let addon = null;
+
+function native() {
+    if (!addon) addon = require(ADDON_PATH);
+    return addon;
+}
+
+function halfToNumber(bits) {
+    const sign = (bits & 0x8000) ? -1 : 1;
+    const exp = (bits >>> 10) & 0x1f;
+    const man = bits & 0x3ff;
+    if (exp === 0) return sign * man * Math.pow(2, -24);
+    if (exp === 31) return man ? NaN : sign * Infinity;
+    return sign * (1024 + man) * Math.pow(2, exp - 25);
+}
+
+// _readWeightF32 (src/tensor.js:80-100) for the expert-bias vector.
+function readWeightF32(meta, n) {
+    if (meta.type === 0) return new Float32Array(meta.buffer, meta.offset, n).slice();
+    if (meta.type === 8) {
+        const u8 = new Uint8Array(meta.buffer), i8 = new Int8Array(meta.buffer);
+        const out = new Float32Array(n);
+        for (let b = 0; b < Math.ceil(n / 32); b++) {
+            const p = meta.offset + b * 34;
+            const d = halfToNumber(u8[p] | (u8[p + 1] << 8));
+            for (let i = 0; i < 32 && b * 32 + i < n; i++) out[b * 32 + i] = i8[p + 2 + i] * d;
+        }
+        return out;
+    }
+    throw new Error('Unsupported weight type for norm: ' + meta.type);
+}
+
+function asFloat32(a) {
+    return (a instanceof Float32Array) ? a : Float32Array.from(a);
+}
+
+class MoEDevice {
+    constructor(device) {
+        this.native = native();
+        this.ctx = this.native.init(device === undefined ? 0 : (device | 0));
+        this._tensors = new WeakMap();   // ArrayBuffer -> Map(key -> device tensor)
+        this.fallbackMatmul = null;
+    }
+
+    // Device copy of a GGUF Q8_0 tensor, uploaded (and repacked) once per
+    // (buffer, offset, shape).  _expertSlice makes a new meta per call
+    // (src/lfm2-engine.js:498-504), so the cache keys on the bytes, not the meta.
+    tensorFor(meta, inDim, outDim, nMats) {
+        let byKey = this._tensors.get(meta.buffer);
+        if (!byKey) {
+            byKey = new Map();
+            this._tensors.set(meta.buffer, byKey);
+        }
+        const key = meta.offset + ':' + inDim + ':' + outDim + ':' + nMats;
+        let t = byKey.get(key);
+        if (!t) {
+            t = this.native.uploadQ80(this.ctx, meta.buffer, meta.offset, inDim, outDim, nMats);
+            byKey.set(key, t);
+        }
+        return t;
+    }
+
+    matmulQ80xF32(meta, input) {
+        if (meta.type !== 8) throw new Error('matmulQ80xF32: tensor type ' + meta.type + ' is not Q8_0');
+        const t = this.tensorFor(meta, meta.shape[0], meta.shape[1], 1);
+        return this.native.matvec(this.ctx, t, 0, asFloat32(input), 1);
+    }
+
+    matmulGeneric(meta, input) {
+        if (meta.type === 8) return this.matmulQ80xF32(meta, input);
+        if (this.fallbackMatmul) return this.fallbackMatmul(meta, input);
+        throw new Error('Unsupported tensor type for matmul: ' + meta.type);
+    }
+
+    // One device MoE handle per layer object (src/lfm2-engine.js:129-137).
+    layerHandle(layer, E, K) {
+        if (layer._qqMoe) return layer._qqMoe;
+        const g = layer.ffnGateExps, u = layer.ffnUpExps, d = layer.ffnDownExps;
+        const H = g.shape[0], F = g.shape[1];
+        if (g.type !== 8 || u.type !== 8 || d.type !== 8)
+            throw new Error('MoE expert tensors must be Q8_0 (type 8)');
+        if (g.shape[2] !== E || d.shape[0] !== F || d.shape[1] !== H)
+            throw new Error('MoE expert tensor shapes do not match [H, F, E] / [F, H, E]');
+        const gt = this.tensorFor(g, H, F, E);
+        const ut = this.tensorFor(u, H, F, E);
+        const dt = this.tensorFor(d, F, H, E);
+        const r = layer.routerWeight;
+        const bias = layer.expProbsBias ? readWeightF32(layer.expProbsBias, E) : null;
+        const moe = this.native.moeCreate(this.ctx, r.buffer, r.offset, r.type, bias, gt, ut, dt, H, F, E, K);
+        const handle = { moe: moe, H: H, F: F, E: E, K: K };
+        Object.defineProperty(layer, '_qqMoe', { value: handle, enumerable: false, configurable: true });
+        return handle;
+    }
+
+    // T tokens, each row independent (the reference runs T sequential calls,
+    // src/lfm2-engine.js:550-555).  hidden is updated in place.
+    moeForward(layer, X, hidden, T, opts) {
+        const o = opts || {};
+        const K = o.K !== undefined ? o.K : 4;
+        const E = layer.ffnGateExps.shape[2];
+        const h = this.layerHandle(layer, E, K);
+        let mask = null;
+        if (o.mask && o.mask.size) {
+            mask = new Uint8Array(h.E);
+            o.mask.forEach(function (e) { if (e >= 0 && e < h.E) mask[e] = 1; });
+        }
+        return this.native.moeForward(this.ctx, h.moe, asFloat32(X), hidden, T, mask, !!o.wantProbs);
+    }
+
+    // Lfm2Engine._moEFFN (src/lfm2-engine.js:413-487) on `eng` (an Lfm2Engine).
+    // The routing telemetry carries the same payload; it is delivered after the
+    // block has run.  bufMoEOut is not written (the sum goes straight into
+    // bufHidden on the device).
+    moEFFN(eng, layerIdx, layer) {
+        const want = !!eng.onRouterUpdate;
+        const r = this.moeForward(layer, eng.bufNormed, eng.bufHidden, 1,
+                                  { K: eng.nExpertsUsed, mask: eng.expertMask, wantProbs: want });
+        if (want) {
+            eng.onRouterUpdate({
+                layer: layerIdx,
+                probs: Array.from(r.probs),
+                selected: Array.from(r.idx),
+                weights: Array.from(r.w),
+            });
+        }
+    }
+
+    release() {
+        if (this.ctx) {
+            this.native.release(this.ctx);
+            this.ctx = null;
+        }
+    }
+}
+
+// Rebind the reference's globals (or any object holding them) to the device:
+// matmulQ80xF32, matmulGeneric (type 8 here, other types to the previous
+// function) and Lfm2Engine.prototype._moEFFN.  Throws when the device is
+// unavailable; nothing is rebound in that case.
+function install(scope, opts) {
+    const o = opts || {};
+    const dev = new MoEDevice(o.device);
+    if (typeof scope.matmulGeneric === 'function') dev.fallbackMatmul = scope.matmulGeneric;
+    scope.matmulQ80xF32 = function (meta, input) { return dev.matmulQ80xF32(meta, input); };
+    scope.matmulGeneric = function (meta, input) { return dev.matmulGeneric(meta, input); };
+    if (scope.Lfm2Engine && scope.Lfm2Engine.prototype) {
+        scope.Lfm2Engine.prototype._moEFFN = function (layerIdx, layer) {
+            return dev.moEFFN(this, layerIdx, layer);
+        };
+    }
+    return dev;
+}
+
+module.exports = { MoEDevice: MoEDevice, install: install, readWeightF32: readWeightF32,
+                   halfToNumber: halfToNumber, ADDON_PATH: ADDON_PATH };

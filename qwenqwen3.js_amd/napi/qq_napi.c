@@ -1,0 +1,432 @@
+/*
+ * qq_napi.c -- Node-API binding of the C ABI in include/qq_moe.h.
+ *
+ * A thin layer: typed arrays and ArrayBuffers are passed to the library by
+ * pointer (no copies on the JS side), handles are napi externals whose
+ * finalizers release the device objects, and every non-zero status becomes a
+ * thrown Error carrying qq_last_error(), as the reference throws from
+ * matmulGeneric (src/tensor.js:494).
+ *
+ * Exports (all synchronous, like the JavaScript they replace):
+ *   init(device) -> ctx
+ *   lastError(ctx | null) -> string
+ *   uploadQ80(ctx, bytes, byteOffset, inDim, outDim, nMats) -> tensor
+ *       bytes: ArrayBuffer or typed array holding GGUF Q8_0 blocks
+ *   matvec(ctx, tensor, mat, x: Float32Array, rows) -> Float32Array(rows*outDim)
+ *   moeCreate(ctx, routerBytes, routerOffset, routerType, bias: Float32Array|null,
+ *             gate, up, down, H, F, E, K) -> moe
+ *   moeForward(ctx, moe, x: Float32Array, hidden: Float32Array, T,
+ *              mask: Uint8Array|null, wantProbs) -> {idx, w, probs}
+ *       hidden is updated in place; idx Int32Array(T*K), w Float64Array(T*K),
+ *       probs Float32Array(T*E) or null
+ *   release(handle)    frees a tensor / moe / ctx now instead of at GC
+ */
+#include <node_api.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "../../include/qq_moe.h"
+
+enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3 };
+
+typedef struct handle {
+    int kind;
+    void *ptr;           /* qq_ctx*, qq_tensor* or qq_moe* (NULL once released) */
+    struct handle *ctx;  /* owning context handle (tensor, moe) */
+    napi_ref ctx_ref;    /* keeps the context alive while this handle lives */
+    napi_ref keep[3];    /* moe: keeps gate/up/down tensors alive */
+    int in_dim, out_dim, n_mats;
+    int H, E, K;
+} handle;
+
+#define CHECK_NAPI(env, call)                                                        \
+    do {                                                                             \
+        if ((call) != napi_ok) {                                                     \
+            napi_throw_error((env), NULL, "qq_napi: N-API call failed: " #call);     \
+            return NULL;                                                             \
+        }                                                                            \
+    } while (0)
+
+static napi_value throw_qq(napi_env env, const char *what, int rc, qq_ctx *ctx)
+{
+    char msg[640];
+    snprintf(msg, sizeof msg, "%s failed (%d): %s", what, rc, qq_last_error(ctx));
+    napi_throw_error(env, NULL, msg);
+    return NULL;
+}
+
+static void release_handle(napi_env env, handle *h)
+{
+    if (!h->ptr) return;
+    qq_ctx *ctx = h->ctx ? (qq_ctx *)h->ctx->ptr : NULL;
+    switch (h->kind) {
+    case H_TENSOR: qq_tensor_release(ctx, (qq_tensor *)h->ptr); break;
+    case H_MOE: qq_moe_release(ctx, (qq_moe *)h->ptr); break;
+    case H_CTX: qq_destroy((qq_ctx *)h->ptr); break;
+    }
+    h->ptr = NULL;
+    for (int i = 0; i < 3; i++)
+        if (h->keep[i]) {
+            napi_delete_reference(env, h->keep[i]);
+            h->keep[i] = NULL;
+        }
+    if (h->ctx_ref) {
+        napi_delete_reference(env, h->ctx_ref);
+        h->ctx_ref = NULL;
+    }
+}
+
+static void finalize_handle(napi_env env, void *data, void *hint)
+{
+    (void)hint;
+    handle *h = (handle *)data;
+    release_handle(env, h);
+    free(h);
+}
+
+static handle *get_handle(napi_env env, napi_value v, int kind)
+{
+    void *data = NULL;
+    napi_valuetype t;
+    if (napi_typeof(env, v, &t) != napi_ok || t != napi_external ||
+        napi_get_value_external(env, v, &data) != napi_ok || !data) {
+        napi_throw_type_error(env, NULL, "qq_napi: expected a handle");
+        return NULL;
+    }
+    handle *h = (handle *)data;
+    if (h->kind != kind) {
+        napi_throw_type_error(env, NULL, "qq_napi: wrong handle kind");
+        return NULL;
+    }
+    if (!h->ptr) {
+        napi_throw_error(env, NULL, "qq_napi: handle already released");
+        return NULL;
+    }
+    return h;
+}
+
+static napi_value new_handle(napi_env env, handle *h)
+{
+    napi_value v;
+    if (napi_create_external(env, h, finalize_handle, NULL, &v) != napi_ok) {
+        free(h);
+        napi_throw_error(env, NULL, "qq_napi: cannot create handle");
+        return NULL;
+    }
+    return v;
+}
+
+/* Raw bytes of an ArrayBuffer or of any typed array (its viewed range). */
+static int get_bytes(napi_env env, napi_value v, uint8_t **data, size_t *len)
+{
+    bool is_ab = false, is_ta = false;
+    napi_is_arraybuffer(env, v, &is_ab);
+    if (is_ab) {
+        void *p;
+        if (napi_get_arraybuffer_info(env, v, &p, len) != napi_ok) return -1;
+        *data = (uint8_t *)p;
+        return 0;
+    }
+    napi_is_typedarray(env, v, &is_ta);
+    if (is_ta) {
+        napi_typedarray_type tt;
+        size_t n, off;
+        void *p;
+        napi_value ab;
+        if (napi_get_typedarray_info(env, v, &tt, &n, &p, &ab, &off) != napi_ok) return -1;
+        size_t es = 1;
+        switch (tt) {
+        case napi_int16_array: case napi_uint16_array: es = 2; break;
+        case napi_int32_array: case napi_uint32_array: case napi_float32_array: es = 4; break;
+        case napi_float64_array: case napi_bigint64_array: case napi_biguint64_array: es = 8; break;
+        default: es = 1;
+        }
+        *data = (uint8_t *)p;
+        *len = n * es;
+        return 0;
+    }
+    return -1;
+}
+
+static int get_typed(napi_env env, napi_value v, napi_typedarray_type want, void **data, size_t *n)
+{
+    bool is_ta = false;
+    napi_is_typedarray(env, v, &is_ta);
+    if (!is_ta) return -1;
+    napi_typedarray_type tt;
+    size_t off;
+    napi_value ab;
+    if (napi_get_typedarray_info(env, v, &tt, n, data, &ab, &off) != napi_ok) return -1;
+    return tt == want ? 0 : -1;
+}
+
+static int is_nullish(napi_env env, napi_value v)
+{
+    napi_valuetype t;
+    napi_typeof(env, v, &t);
+    return t == napi_null || t == napi_undefined;
+}
+
+static int get_i32(napi_env env, napi_value v, int32_t *out)
+{
+    return napi_get_value_int32(env, v, out) == napi_ok ? 0 : -1;
+}
+
+#define ARGS(N)                                                               \
+    size_t argc = N;                                                          \
+    napi_value argv[N];                                                       \
+    CHECK_NAPI(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));    \
+    if (argc < N) {                                                           \
+        napi_throw_type_error(env, NULL, "qq_napi: expected " #N " arguments"); \
+        return NULL;                                                          \
+    }
+
+static napi_value js_init(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    int32_t dev;
+    if (get_i32(env, argv[0], &dev)) {
+        napi_throw_type_error(env, NULL, "init(device): device must be an integer");
+        return NULL;
+    }
+    qq_ctx *ctx = NULL;
+    int rc = qq_init(dev, &ctx);
+    if (rc) return throw_qq(env, "qq_init", rc, NULL);
+    handle *h = (handle *)calloc(1, sizeof(handle));
+    if (!h) {
+        qq_destroy(ctx);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->kind = H_CTX;
+    h->ptr = ctx;
+    return new_handle(env, h);
+}
+
+static napi_value js_last_error(napi_env env, napi_callback_info info)
+{
+    size_t argc = 1;
+    napi_value argv[1], out;
+    CHECK_NAPI(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+    qq_ctx *ctx = NULL;
+    if (argc >= 1 && !is_nullish(env, argv[0])) {
+        handle *h = get_handle(env, argv[0], H_CTX);
+        if (!h) return NULL;
+        ctx = (qq_ctx *)h->ptr;
+    }
+    CHECK_NAPI(env, napi_create_string_utf8(env, qq_last_error(ctx), NAPI_AUTO_LENGTH, &out));
+    return out;
+}
+
+/* child handle that keeps its context's JS handle alive */
+static handle *child_of(napi_env env, napi_value ctxv, handle *ch, int kind)
+{
+    handle *h = (handle *)calloc(1, sizeof(handle));
+    if (!h) return NULL;
+    h->kind = kind;
+    h->ctx = ch;
+    if (napi_create_reference(env, ctxv, 1, &h->ctx_ref) != napi_ok) {
+        free(h);
+        return NULL;
+    }
+    return h;
+}
+
+static napi_value js_upload_q80(napi_env env, napi_callback_info info)
+{
+    ARGS(6);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    uint8_t *bytes;
+    size_t len;
+    int32_t off, in_dim, out_dim, n_mats;
+    if (get_bytes(env, argv[1], &bytes, &len) || get_i32(env, argv[2], &off) ||
+        get_i32(env, argv[3], &in_dim) || get_i32(env, argv[4], &out_dim) || get_i32(env, argv[5], &n_mats) ||
+        off < 0 || (size_t)off > len) {
+        napi_throw_type_error(env, NULL, "uploadQ80(ctx, bytes, byteOffset, inDim, outDim, nMats)");
+        return NULL;
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    qq_tensor *t = NULL;
+    int rc = qq_q8_0_upload(ctx, bytes + off, len - off, in_dim, out_dim, n_mats, &t);
+    if (rc) return throw_qq(env, "qq_q8_0_upload", rc, ctx);
+    handle *h = child_of(env, argv[0], ch, H_TENSOR);
+    if (!h) {
+        qq_tensor_release(ctx, t);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->ptr = t;
+    h->in_dim = in_dim;
+    h->out_dim = out_dim;
+    h->n_mats = n_mats;
+    return new_handle(env, h);
+}
+
+static napi_value js_matvec(napi_env env, napi_callback_info info)
+{
+    ARGS(5);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *th = get_handle(env, argv[1], H_TENSOR);
+    if (!th) return NULL;
+    int32_t mat, rows;
+    float *x;
+    size_t nx;
+    if (get_i32(env, argv[2], &mat) || get_typed(env, argv[3], napi_float32_array, (void **)&x, &nx) ||
+        get_i32(env, argv[4], &rows) || rows < 0) {
+        napi_throw_type_error(env, NULL, "matvec(ctx, tensor, mat, x: Float32Array, rows)");
+        return NULL;
+    }
+    if (nx < (size_t)rows * th->in_dim) {
+        napi_throw_range_error(env, NULL, "matvec: input shorter than rows * inDim");
+        return NULL;
+    }
+    napi_value ab, out;
+    void *ydata;
+    const size_t ny = (size_t)rows * th->out_dim;
+    CHECK_NAPI(env, napi_create_arraybuffer(env, ny * 4, &ydata, &ab));
+    CHECK_NAPI(env, napi_create_typedarray(env, napi_float32_array, ny, ab, 0, &out));
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_q8_0_matvec(ctx, (qq_tensor *)th->ptr, mat, x, (float *)ydata, rows);
+    if (rc) return throw_qq(env, "qq_q8_0_matvec", rc, ctx);
+    return out;
+}
+
+static napi_value js_moe_create(napi_env env, napi_callback_info info)
+{
+    ARGS(12);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    uint8_t *rbytes;
+    size_t rlen;
+    int32_t roff, rtype, H, F, E, K;
+    if (get_bytes(env, argv[1], &rbytes, &rlen) || get_i32(env, argv[2], &roff) ||
+        get_i32(env, argv[3], &rtype) || get_i32(env, argv[8], &H) || get_i32(env, argv[9], &F) ||
+        get_i32(env, argv[10], &E) || get_i32(env, argv[11], &K) || roff < 0 || (size_t)roff > rlen) {
+        napi_throw_type_error(env, NULL,
+                              "moeCreate(ctx, routerBytes, routerOffset, routerType, bias, gate, up, down, H, F, E, K)");
+        return NULL;
+    }
+    const size_t need = rtype == QQ_TYPE_F32 ? (size_t)E * H * 4 : (size_t)E * ((H + 31) / 32) * 34;
+    if (rlen - roff < need) {
+        napi_throw_range_error(env, NULL, "moeCreate: router tensor is shorter than [H, E]");
+        return NULL;
+    }
+    float *bias = NULL;
+    if (!is_nullish(env, argv[4])) {
+        size_t nb;
+        if (get_typed(env, argv[4], napi_float32_array, (void **)&bias, &nb) || nb < (size_t)E) {
+            napi_throw_type_error(env, NULL, "moeCreate: bias must be a Float32Array of E values or null");
+            return NULL;
+        }
+    }
+    handle *g = get_handle(env, argv[5], H_TENSOR);
+    if (!g) return NULL;
+    handle *u = get_handle(env, argv[6], H_TENSOR);
+    if (!u) return NULL;
+    handle *d = get_handle(env, argv[7], H_TENSOR);
+    if (!d) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    qq_moe *m = NULL;
+    int rc = qq_moe_create(ctx, rbytes + roff, rtype, bias, (qq_tensor *)g->ptr, (qq_tensor *)u->ptr,
+                           (qq_tensor *)d->ptr, H, F, E, K, &m);
+    if (rc) return throw_qq(env, "qq_moe_create", rc, ctx);
+    handle *h = child_of(env, argv[0], ch, H_MOE);
+    if (!h) {
+        qq_moe_release(ctx, m);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->ptr = m;
+    h->H = H;
+    h->E = E;
+    h->K = K;
+    for (int i = 0; i < 3; i++) napi_create_reference(env, argv[5 + i], 1, &h->keep[i]);
+    return new_handle(env, h);
+}
+
+static napi_value js_moe_forward(napi_env env, napi_callback_info info)
+{
+    ARGS(7);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *mh = get_handle(env, argv[1], H_MOE);
+    if (!mh) return NULL;
+    float *x, *hid;
+    size_t nx, nh;
+    int32_t T;
+    bool want_probs = false;
+    if (get_typed(env, argv[2], napi_float32_array, (void **)&x, &nx) ||
+        get_typed(env, argv[3], napi_float32_array, (void **)&hid, &nh) || get_i32(env, argv[4], &T) || T < 0 ||
+        napi_get_value_bool(env, argv[6], &want_probs) != napi_ok) {
+        napi_throw_type_error(env, NULL,
+                              "moeForward(ctx, moe, x: Float32Array, hidden: Float32Array, T, mask, wantProbs)");
+        return NULL;
+    }
+    if (nx < (size_t)T * mh->H || nh < (size_t)T * mh->H) {
+        napi_throw_range_error(env, NULL, "moeForward: x / hidden shorter than T * H");
+        return NULL;
+    }
+    uint8_t *mask = NULL;
+    if (!is_nullish(env, argv[5])) {
+        size_t nm;
+        if (get_typed(env, argv[5], napi_uint8_array, (void **)&mask, &nm) || nm < (size_t)mh->E) {
+            napi_throw_type_error(env, NULL, "moeForward: mask must be a Uint8Array of E entries or null");
+            return NULL;
+        }
+    }
+    napi_value res, v_idx, v_w, v_p, ab;
+    void *didx, *dw, *dp = NULL;
+    CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)T * mh->K * 4, &didx, &ab));
+    CHECK_NAPI(env, napi_create_typedarray(env, napi_int32_array, (size_t)T * mh->K, ab, 0, &v_idx));
+    CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)T * mh->K * 8, &dw, &ab));
+    CHECK_NAPI(env, napi_create_typedarray(env, napi_float64_array, (size_t)T * mh->K, ab, 0, &v_w));
+    if (want_probs) {
+        CHECK_NAPI(env, napi_create_arraybuffer(env, (size_t)T * mh->E * 4, &dp, &ab));
+        CHECK_NAPI(env, napi_create_typedarray(env, napi_float32_array, (size_t)T * mh->E, ab, 0, &v_p));
+    } else {
+        CHECK_NAPI(env, napi_get_null(env, &v_p));
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_moe_forward(ctx, (qq_moe *)mh->ptr, x, hid, T, mask, (int32_t *)didx, (double *)dw, (float *)dp);
+    if (rc) return throw_qq(env, "qq_moe_forward", rc, ctx);
+    CHECK_NAPI(env, napi_create_object(env, &res));
+    CHECK_NAPI(env, napi_set_named_property(env, res, "idx", v_idx));
+    CHECK_NAPI(env, napi_set_named_property(env, res, "w", v_w));
+    CHECK_NAPI(env, napi_set_named_property(env, res, "probs", v_p));
+    return res;
+}
+
+static napi_value js_release(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    void *data = NULL;
+    napi_valuetype t;
+    if (napi_typeof(env, argv[0], &t) != napi_ok || t != napi_external ||
+        napi_get_value_external(env, argv[0], &data) != napi_ok || !data) {
+        napi_throw_type_error(env, NULL, "release(handle)");
+        return NULL;
+    }
+    release_handle(env, (handle *)data);
+    return NULL;
+}
+
+static napi_value module_init(napi_env env, napi_value exports)
+{
+    const napi_property_descriptor props[] = {
+        {"init", NULL, js_init, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lastError", NULL, js_last_error, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"uploadQ80", NULL, js_upload_q80, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvec", NULL, js_matvec, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"moeCreate", NULL, js_moe_create, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"moeForward", NULL, js_moe_forward, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"release", NULL, js_release, NULL, NULL, NULL, napi_enumerable, NULL},
+    };
+    if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;
+    return exports;
+}
+
+NAPI_MODULE(NODE_GYP_MODULE_NAME, module_init)
