@@ -138,6 +138,25 @@ def cpu_baseline(seconds):
                       "1 thread of %d host cores" % (n, el, ncores)}
 
 
+def copy_calibration(steps):
+    """A plain copy of known size: FETCH_SIZE and WRITE_SIZE of one dispatch
+    should each read 1 GiB; the ratio calibrates the traffic counters."""
+    import torch
+    n = 1 << 30
+    a = torch.ones(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty_like(a)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        b.copy_(a)
+    ev1.record()
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / steps
+    print(json.dumps({"copy_bytes": n, "ms": round(ms, 4), "read_plus_write_gbps": round(2 * n / (ms * 1e6), 1)}))
+    return 0
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -147,7 +166,12 @@ def main():
     ap.add_argument("--layers", type=int, default=16, help="distinct layer instances rotated over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only time a 1 GiB device-to-device copy (reference kernel for the "
+                         "rocprof FETCH_SIZE / WRITE_SIZE scale factors)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration(args.steps)
 
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus %d refused)"

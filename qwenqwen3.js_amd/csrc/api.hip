@@ -73,19 +73,18 @@ static int check_device_error(qq_ctx *ctx)
     return QQ_OK;
 }
 
-void prof_begin(qq_ctx *ctx, int id)
-{
-    if (!ctx->prof_on || ctx->prof_n >= ctx->prof_cap) return;
-    const int i = ctx->prof_n;
-    ctx->prof_id[i] = id;
-    (void)hipEventRecord(ctx->prof_ev[2 * i], ctx->stream);
-}
+void prof_begin(qq_ctx *ctx, int id) { ctx->prof_kind = id; }
 
-void prof_end(qq_ctx *ctx)
+void prof_end(qq_ctx *ctx) { ctx->prof_kind = -1; }
+
+void prof_slot(qq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop)
 {
-    if (!ctx->prof_on || ctx->prof_n >= ctx->prof_cap) return;
-    (void)hipEventRecord(ctx->prof_ev[2 * ctx->prof_n + 1], ctx->stream);
-    ctx->prof_n++;
+    *start = *stop = nullptr;
+    if (!ctx->prof_on || ctx->prof_kind < 0 || ctx->prof_n >= ctx->prof_cap) return;
+    const int i = ctx->prof_n++;
+    ctx->prof_id[i] = ctx->prof_kind;
+    *start = ctx->prof_ev[2 * i];
+    *stop = ctx->prof_ev[2 * i + 1];
 }
 
 static void prof_free(qq_ctx *ctx)
@@ -173,6 +172,7 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "hipStreamCreate");
     }
     ctx->own_stream = 1;
+    ctx->prof_kind = -1;
     if ((e = hipEventCreate(&ctx->ev0)) != hipSuccess || (e = hipEventCreate(&ctx->ev1)) != hipSuccess) {
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;

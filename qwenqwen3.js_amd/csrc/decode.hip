@@ -388,9 +388,9 @@ size_t decode_work_bytes(const qq_moe *m)
 }
 
 template <int NBW>
-static void launch_experts(const DecodeArgs &a, dim3 grid, hipStream_t st)
+static void launch_experts(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
 {
-    hipLaunchKernelGGL(moe_decode_experts_kernel<NBW>, grid, dim3(DEC_THREADS), 0, st, a);
+    QQ_LAUNCH(ctx, moe_decode_experts_kernel<NBW>, grid, dim3(DEC_THREADS), 0, a);
 }
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
@@ -434,17 +434,17 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
     const dim3 grid(m->E + m->K * a.NS);
     prof_begin(ctx, K_DECODE_EXPERTS);
-    if (nbw <= 1) launch_experts<1>(a, grid, ctx->stream);
-    else if (nbw <= 2) launch_experts<2>(a, grid, ctx->stream);
-    else if (nbw <= 4) launch_experts<4>(a, grid, ctx->stream);
-    else launch_experts<8>(a, grid, ctx->stream);
+    if (nbw <= 1) launch_experts<1>(ctx, a, grid);
+    else if (nbw <= 2) launch_experts<2>(ctx, a, grid);
+    else if (nbw <= 4) launch_experts<4>(ctx, a, grid);
+    else launch_experts<8>(ctx, a, grid);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
 
     const int nsp = (a.NS + 7) / 8;
     const dim3 cgrid((m->H + 31) / 32);
 #define QQ_CB(N)                                                                                 \
-    hipLaunchKernelGGL(moe_decode_combine_kernel<N>, cgrid, dim3(256), 0, ctx->stream, a.partial, \
+    QQ_LAUNCH(ctx, moe_decode_combine_kernel<N>, cgrid, dim3(256), 0, a.partial, \
                        m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden)
     prof_begin(ctx, K_DECODE_COMBINE);
     if (nsp <= 1) QQ_CB(1);

@@ -345,7 +345,7 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
     int nt = 256;
     while (nt > 32 && (size_t)nt * m->E * 4 > 32768) nt >>= 1;
     prof_begin(ctx, K_DISPATCH);
-    hipLaunchKernelGGL(moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4, ctx->stream,
+    QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4,
                        idx, (int)P, m->E, mask, counts, offsets, perm, inv);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
@@ -373,11 +373,11 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         const dim3 grid(m->E, a.nbF);
         prof_begin(ctx, K_GROUPED_GATEUP);
         switch (nbw_bucket(a.nbH)) {
-        case 1: hipLaunchKernelGGL(moe_grouped_gateup_kernel<1>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 2: hipLaunchKernelGGL(moe_grouped_gateup_kernel<2>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 4: hipLaunchKernelGGL(moe_grouped_gateup_kernel<4>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 8: hipLaunchKernelGGL(moe_grouped_gateup_kernel<8>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        default: hipLaunchKernelGGL(moe_grouped_gateup_kernel<16>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
+        case 1: QQ_LAUNCH(ctx, moe_grouped_gateup_kernel<1>, grid, dim3(GR_THREADS), 0, a); break;
+        case 2: QQ_LAUNCH(ctx, moe_grouped_gateup_kernel<2>, grid, dim3(GR_THREADS), 0, a); break;
+        case 4: QQ_LAUNCH(ctx, moe_grouped_gateup_kernel<4>, grid, dim3(GR_THREADS), 0, a); break;
+        case 8: QQ_LAUNCH(ctx, moe_grouped_gateup_kernel<8>, grid, dim3(GR_THREADS), 0, a); break;
+        default: QQ_LAUNCH(ctx, moe_grouped_gateup_kernel<16>, grid, dim3(GR_THREADS), 0, a); break;
         }
         prof_end(ctx);
         QQ_HIP(ctx, hipGetLastError());
@@ -386,17 +386,17 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         const dim3 grid(m->E, (m->H + QK - 1) / QK);
         prof_begin(ctx, K_GROUPED_DOWN);
         switch (nbw_bucket(a.nbF)) {
-        case 1: hipLaunchKernelGGL(moe_grouped_down_kernel<1>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 2: hipLaunchKernelGGL(moe_grouped_down_kernel<2>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 4: hipLaunchKernelGGL(moe_grouped_down_kernel<4>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        case 8: hipLaunchKernelGGL(moe_grouped_down_kernel<8>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
-        default: hipLaunchKernelGGL(moe_grouped_down_kernel<16>, grid, dim3(GR_THREADS), 0, ctx->stream, a); break;
+        case 1: QQ_LAUNCH(ctx, moe_grouped_down_kernel<1>, grid, dim3(GR_THREADS), 0, a); break;
+        case 2: QQ_LAUNCH(ctx, moe_grouped_down_kernel<2>, grid, dim3(GR_THREADS), 0, a); break;
+        case 4: QQ_LAUNCH(ctx, moe_grouped_down_kernel<4>, grid, dim3(GR_THREADS), 0, a); break;
+        case 8: QQ_LAUNCH(ctx, moe_grouped_down_kernel<8>, grid, dim3(GR_THREADS), 0, a); break;
+        default: QQ_LAUNCH(ctx, moe_grouped_down_kernel<16>, grid, dim3(GR_THREADS), 0, a); break;
         }
         prof_end(ctx);
         QQ_HIP(ctx, hipGetLastError());
     }
     prof_begin(ctx, K_COMBINE);
-    hipLaunchKernelGGL(moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0, ctx->stream,
+    QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0,
                        y, m->H, m->K, inv, w, hidden);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());

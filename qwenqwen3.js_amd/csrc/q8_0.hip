@@ -43,7 +43,7 @@ int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t)
     const size_t nblocks = (size_t)t->n_mats * t->out_dim * t->nb;
     const unsigned grid = (unsigned)((nblocks + 255) / 256);
     prof_begin(ctx, K_REPACK);
-    hipLaunchKernelGGL(repack_q8_0_kernel, dim3(grid), dim3(256), 0, ctx->stream, gguf_dev,
+    QQ_LAUNCH(ctx, repack_q8_0_kernel, dim3(grid), dim3(256), 0, gguf_dev,
                        t->qs, t->d, nblocks, t->out_dim, t->nb);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
@@ -143,15 +143,13 @@ int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x,
     const unsigned gx = (unsigned)((t->out_dim + 31) / 32);
     prof_begin(ctx, K_MATVEC);
     if (rows >= 4)
-        hipLaunchKernelGGL((q8_0_matvec_kernel<4>), dim3(gx, (rows + 3) / 4), dim3(256), 0,
-                           ctx->stream, t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y,
+        QQ_LAUNCH(ctx, (q8_0_matvec_kernel<4>), dim3(gx, (rows + 3) / 4), dim3(256), 0, t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y,
                            ldy, rows);
     else if (rows >= 2)
-        hipLaunchKernelGGL((q8_0_matvec_kernel<2>), dim3(gx, (rows + 1) / 2), dim3(256), 0,
-                           ctx->stream, t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y,
+        QQ_LAUNCH(ctx, (q8_0_matvec_kernel<2>), dim3(gx, (rows + 1) / 2), dim3(256), 0, t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y,
                            ldy, rows);
     else
-        hipLaunchKernelGGL((q8_0_matvec_kernel<1>), dim3(gx, rows), dim3(256), 0, ctx->stream,
+        QQ_LAUNCH(ctx, (q8_0_matvec_kernel<1>), dim3(gx, rows), dim3(256), 0,
                            t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y, ldy, rows);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());

@@ -3,6 +3,7 @@
 
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
+#include <hip/hip_ext.h>
 #include <cstddef>
 #include <cstdint>
 #include <cstdio>
@@ -80,6 +81,7 @@ struct qq_ctx {
     uint32_t epoch;
     // per-kernel event pairs (qq_profile_*): pool of 2*prof_cap events
     int prof_on;
+    int prof_kind;             // kernel id of the launches being issued, -1 none
     int prof_n, prof_cap;
     hipEvent_t *prof_ev;
     int *prof_id;
@@ -102,9 +104,22 @@ enum KernelId {
     K_COUNT
 };
 
-// Bracket one launch with an event pair when profiling is on.
+// Launches between prof_begin(ctx, id) and prof_end(ctx) are reported under
+// kernel id `id`.  When profiling is on, each QQ_LAUNCH there takes the next
+// event pair of the pool and hands it to hipExtLaunchKernelGGL, which stamps
+// the start and end of the dispatch packet itself (no event packets between
+// kernels, so the timing matches a kernel trace).
 void prof_begin(qq_ctx *ctx, int id);
 void prof_end(qq_ctx *ctx);
+void prof_slot(qq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop);
+
+#define QQ_LAUNCH(ctx, kernel, grid, block, shm, ...)                                  \
+    do {                                                                               \
+        hipEvent_t qq_e0_ = nullptr, qq_e1_ = nullptr;                                 \
+        ::qq::prof_slot(ctx, &qq_e0_, &qq_e1_);                                        \
+        hipExtLaunchKernelGGL(kernel, grid, block, shm, (ctx)->stream, qq_e0_, qq_e1_, 0, \
+                              __VA_ARGS__);                                            \
+    } while (0)
 
 int set_error(qq_ctx *ctx, const char *fmt, ...);
 int check_hip(qq_ctx *ctx, hipError_t e, const char *what);

@@ -117,11 +117,10 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, floa
     do {                                                                                          \
         dim3 g((T + TT - 1) / TT, (m->E + EB - 1) / EB);                                          \
         if (q8)                                                                                   \
-            hipLaunchKernelGGL((router_logits_kernel<TT, EB, true>), g, dim3(256), 0, ctx->stream, \
+            QQ_LAUNCH(ctx, (router_logits_kernel<TT, EB, true>), g, dim3(256), 0, \
                                x, T, W, logits);                                                  \
         else                                                                                      \
-            hipLaunchKernelGGL((router_logits_kernel<TT, EB, false>), g, dim3(256), 0,           \
-                               ctx->stream, x, T, W, logits);                                     \
+            QQ_LAUNCH(ctx, (router_logits_kernel<TT, EB, false>), g, dim3(256), 0, x, T, W, logits);                                     \
     } while (0)
     prof_begin(ctx, K_ROUTER_LOGITS);
     if (T <= 2)
@@ -134,7 +133,7 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, floa
 #undef QQ_RL
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_ROUTER_TOPK);
-    hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, ctx->stream, logits,
+    QQ_LAUNCH(ctx, router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, logits,
                        T, m->E, m->K, m->bias, idx, w, probs);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
