@@ -124,9 +124,9 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
 int qq_timer_start(qq_ctx *ctx);
 int qq_timer_stop(qq_ctx *ctx, float *ms);
 
-/* Per-kernel timing: while enabled, every kernel launch on the context is
- * bracketed by a HIP event pair on the launch stream (up to max_launches
- * launches; 0 disables).  qq_profile_read waits for the stream and returns,
+/* Per-kernel timing: while enabled, every kernel launch on the context
+ * carries its own start/stop event pair, stamped by the dispatch itself
+ * (hipExtLaunchKernelGGL), up to max_launches launches; 0 disables.  qq_profile_read waits for the stream and returns,
  * for each kernel id < n, the summed milliseconds and the launch count, then
  * clears the record.  qq_profile_name(id) names the kernel. */
 int qq_profile_enable(qq_ctx *ctx, int max_launches);
