@@ -116,6 +116,16 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
                        int T, const uint8_t *mask, int32_t *idx_dev, double *w_dev,
                        float *probs_dev);
 
+/* Token batches (T > 1) of at least `tokens` rows per chunk run their expert
+ * products as fp16 MFMA grouped GEMMs (fp16 activations and dequantised
+ * weights, fp32 accumulation: ~1e-3 relative L2 on the layer output);
+ * smaller batches, and every batch when `tokens` is 0, keep the fp32 path
+ * (~1e-7).  Routing (top-K indices, weights, probs) is exact on both paths.
+ * Default QQ_MFMA_MIN_TOKENS_DEFAULT.  No reference counterpart: the
+ * reference's prefill is T sequential fp32 calls (src/lfm2-engine.js:550-555). */
+#define QQ_MFMA_MIN_TOKENS_DEFAULT 512
+int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens);
+
 /* ---- measurement ------------------------------------------------------ */
 
 /* Record a HIP event pair around work enqueued between qq_timer_start and

@@ -55,6 +55,7 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes)
 static const char *const kKernelNames[K_COUNT] = {
     "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
     "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
+    "cast_f16",         "mfma_gateup",    "mfma_down",
 };
 
 // Read and clear the device error word; non-zero means a bounded device-side
@@ -173,6 +174,7 @@ int qq_init(int device, qq_ctx **out)
     }
     ctx->own_stream = 1;
     ctx->prof_kind = -1;
+    ctx->mfma_min_tokens = QQ_MFMA_MIN_TOKENS_DEFAULT;
     if ((e = hipEventCreate(&ctx->ev0)) != hipSuccess || (e = hipEventCreate(&ctx->ev1)) != hipSuccess) {
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -419,19 +421,33 @@ int qq_moe_release(qq_ctx *ctx, qq_moe *m)
 // Token batches: logits | idx | w | grouped work, per chunk of tokens.
 constexpr int T_CHUNK = 4096;
 
-static size_t forward_scratch(const qq_moe *m, int T)
+// Path of one chunk of tn tokens: the fp16 MFMA GEMMs for chunks of at least
+// ctx->mfma_min_tokens rows, the fp32 grouped kernels otherwise.
+static bool use_mfma(const qq_ctx *ctx, const qq_moe *m, int tn, const float *x)
+{
+    return ctx->mfma_min_tokens > 0 && tn >= ctx->mfma_min_tokens && mfma_supported(m) &&
+           ((uintptr_t)x & 15) == 0;
+}
+
+static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
 {
     if (decode_supported(m, T)) return align256(decode_work_bytes(m));
-    const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
-    return align256(Tc * m->E * 4) + align256(Tc * m->K * 4) + align256(Tc * m->K * 8) +
-           align256(grouped_work_bytes(m, (int)Tc));
+    const int Tc = T < T_CHUNK ? T : T_CHUNK;
+    size_t work = grouped_work_bytes(m, Tc);
+    if (ctx->mfma_min_tokens > 0 && mfma_supported(m)) {
+        // any chunk of at least mfma_min_tokens rows may take the MFMA path
+        const size_t mw = mfma_work_bytes(m, Tc);
+        if (Tc >= ctx->mfma_min_tokens && mw > work) work = mw;
+    }
+    return align256((size_t)Tc * m->E * 4) + align256((size_t)Tc * m->K * 4) +
+           align256((size_t)Tc * m->K * 8) + align256(work);
 }
 
 // x, hidden (and the optional outputs) are device pointers; scratch starts at `base`.
 static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                         const MaskBits &mask, int32_t *idx, double *w, float *probs, size_t base)
 {
-    int rc = ensure_scratch(ctx, base + forward_scratch(m, T));
+    int rc = ensure_scratch(ctx, base + forward_scratch(ctx, m, T));
     if (rc) return rc;
     char *s = static_cast<char *>(ctx->scratch) + base;
     if (decode_supported(m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs, s);
@@ -448,7 +464,11 @@ static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hid
         const float *cx = x + (size_t)t0 * m->H;
         float *ch = hidden + (size_t)t0 * m->H;
         if ((rc = launch_router_topk(ctx, m, cx, tn, logits, ci, cw, cp))) return rc;
-        if ((rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work))) return rc;
+        if (use_mfma(ctx, m, tn, cx))
+            rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work);
+        else
+            rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work);
+        if (rc) return rc;
     }
     return QQ_OK;
 }
@@ -486,7 +506,7 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     const size_t xb = (size_t)T * m->H * 4;
     const size_t ib = (size_t)T * m->K * 4, wb = (size_t)T * m->K * 8, pb = (size_t)T * m->E * 4;
     const size_t io = 2 * align256(xb) + align256(ib) + align256(wb) + align256(pb);
-    if ((rc = ensure_scratch(ctx, io + forward_scratch(m, T)))) return rc;
+    if ((rc = ensure_scratch(ctx, io + forward_scratch(ctx, m, T)))) return rc;
     char *s = static_cast<char *>(ctx->scratch);
     float *dx = reinterpret_cast<float *>(s);
     float *dh = reinterpret_cast<float *>(s + align256(xb));
@@ -502,6 +522,14 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     if (probs) QQ_HIP(ctx, hipMemcpyAsync(probs, dp, pb, hipMemcpyDeviceToHost, ctx->stream));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return check_device_error(ctx);
+}
+
+int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (tokens < 0) return set_error(ctx, "set_mfma_min_tokens: %d < 0", tokens);
+    ctx->mfma_min_tokens = tokens;
+    return QQ_OK;
 }
 
 // ---- measurement ------------------------------------------------------------

@@ -34,7 +34,8 @@ struct GrMT {
 // ---------------------------------------------------------------------------
 __global__ void moe_dispatch_kernel(const int32_t *__restrict__ idx, int P, int E, MaskBits mask,
                                     int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
-                                    int32_t *__restrict__ perm, int32_t *__restrict__ inv)
+                                    int32_t *__restrict__ perm, int32_t *__restrict__ inv,
+                                    DispatchTiles tiles)
 {
     extern __shared__ int cnt[];
     __shared__ int offs[MAX_E + 1];
@@ -58,16 +59,23 @@ __global__ void moe_dispatch_kernel(const int32_t *__restrict__ idx, int P, int 
     }
     __syncthreads();
     if (tid == 0) {
-        int o = 0;
+        int o = 0, nt = 0;
         for (int e = 0; e < E; e++) {
             const int c = offs[e];
             offs[e] = o;
             counts[e] = c;
             offsets[e] = o;
             o += c;
+            // row tiles of at most tiles.bm slots, expert by expert
+            if (tiles.bm > 0)
+                for (int m0 = 0; m0 < c && nt < tiles.cap; m0 += tiles.bm, nt++) {
+                    tiles.e[nt] = e;
+                    tiles.m0[nt] = m0;
+                }
         }
         offs[E] = o;
         offsets[E] = o;
+        if (tiles.bm > 0) *tiles.n = nt;
     }
     __syncthreads();
     for (int p = p0; p < p1; p++) {
@@ -315,6 +323,31 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restric
     hidden[(size_t)t * H + j] = hidden[(size_t)t * H + j] + acc;
 }
 
+int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, const MaskBits &mask,
+                    int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
+                    const DispatchTiles &tiles)
+{
+    int nt = 256;
+    while (nt > 32 && (size_t)nt * m->E * 4 > 32768) nt >>= 1;
+    prof_begin(ctx, K_DISPATCH);
+    QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4, idx, P, m->E,
+              mask, counts, offsets, perm, inv, tiles);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const float *y, const int32_t *inv,
+                   const double *w, float *hidden)
+{
+    prof_begin(ctx, K_COMBINE);
+    QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0, y, m->H, m->K,
+              inv, w, hidden);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
 static int nbw_bucket(int nb)
 {
     const int n = (nb + GR_WAVES - 1) / GR_WAVES;
@@ -342,13 +375,8 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
     float *g = reinterpret_cast<float *>(p);           p += al(P * m->F * 4);
     float *y = reinterpret_cast<float *>(p);
 
-    int nt = 256;
-    while (nt > 32 && (size_t)nt * m->E * 4 > 32768) nt >>= 1;
-    prof_begin(ctx, K_DISPATCH);
-    QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4,
-                       idx, (int)P, m->E, mask, counts, offsets, perm, inv);
-    prof_end(ctx);
-    QQ_HIP(ctx, hipGetLastError());
+    int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, DispatchTiles{});
+    if (rc) return rc;
 
     GroupArgs a;
     a.x = x;
@@ -395,12 +423,7 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         prof_end(ctx);
         QQ_HIP(ctx, hipGetLastError());
     }
-    prof_begin(ctx, K_COMBINE);
-    QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0,
-                       y, m->H, m->K, inv, w, hidden);
-    prof_end(ctx);
-    QQ_HIP(ctx, hipGetLastError());
-    return QQ_OK;
+    return launch_combine(ctx, m, T, y, inv, w, hidden);
 }
 
 }  // namespace qq

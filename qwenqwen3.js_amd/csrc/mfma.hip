@@ -1,0 +1,371 @@
+// mfma.hip -- prefill chunks on the matrix cores: grouped fp16 MFMA GEMMs.
+//
+// For a chunk of prompt tokens the (token, rank) pairs routed to one expert
+// form a dense [n_e x H] x [H x F] contraction (the reference runs them as
+// n_e separate matvecs, src/lfm2-engine.js:471-478 per token).  After the
+// dispatch (grouped.hip) every expert's slots are cut into row tiles of
+// MF_BM slots, and per (row tile, column tile):
+//   gate/up  A = fp16 activations of the tile's tokens (gathered by perm),
+//            B = 64 gate + 64 up columns dequantised from Q8_0 into LDS as
+//            fp16 w = fp16(q * d); v_mfma_f32_16x16x32_f16 with fp32
+//            accumulators; epilogue silu(g) * u -> fp16 act[slot][F]
+//   down     A = act rows of the tile, B = 128 down columns dequantised
+//            likewise -> y[slot][H] fp32
+// followed by the gather combine of the fp32 path (rank order, fp32 steps).
+// One Q8_0 block (32 values of the reduction dimension) is one MFMA K step;
+// the next block's global loads are in flight while the current block's
+// MFMAs run, and LDS is double buffered with one barrier per step.
+//
+// Accuracy: fp16 activations and weights (relative rounding 2^-11 each),
+// fp32 accumulation: ~1e-3 relative L2 on the layer output, inside the 1e-2
+// bound of the MFMA path.  SwiGLU products and weights must stay inside the
+// fp16 range (|v| < 65504); beyond it they become inf and show in the output.
+#include "qq_device.h"
+
+namespace qq {
+
+typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+constexpr int MF_BM = 128;       // slots per row tile
+constexpr int MF_BN = 128;       // weight columns per workgroup
+constexpr int MF_LD = 40;        // LDS row stride in halves (80 B: 16 rows of a
+                                 // fragment read hit 16 distinct 16-byte bank groups)
+constexpr int MF_THREADS = 256;  // 4 waves, 2 x 2 over the 128 x 128 tile
+
+struct MfmaArgs {
+    const _Float16 *xh;      // [T][H] activations in fp16
+    _Float16 *act;           // [slots][F] SwiGLU products (down input)
+    float *y;                // [slots][H] expert outputs
+    const int32_t *perm, *counts, *offsets;
+    const int32_t *tile_e, *tile_m0, *n_tiles;
+    const int8_t *gq, *uq, *dq;
+    const uint16_t *gd, *ud, *dd;   // fp16 scale bits
+    int H, F, K, nbH, nbF;
+};
+
+// x fp32 -> fp16 (round to nearest even), 4 values per thread.
+__global__ __launch_bounds__(256) void cast_f16_kernel(const float4 *__restrict__ x,
+                                                       uint2 *__restrict__ y, size_t n4)
+{
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) return;
+    const float4 v = x[i];
+    const h2_t a = {(_Float16)v.x, (_Float16)v.y};
+    const h2_t b = {(_Float16)v.z, (_Float16)v.w};
+    y[i] = make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+// 16 int8 weights of one column (half a Q8_0 block) and the block's fp16
+// scale -> 16 fp16 values w = fp16(q * d), in k order.  Each byte is made
+// offset binary (u = q + 128) and paired with the exponent byte 0x64, so the
+// half 0x64uu is exactly 1024 + u; subtracting 1152 gives q exactly, and the
+// multiply by d is the one rounding.
+__device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4 &lo, uint4 &hi)
+{
+    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u,
+                           q.w ^ 0x80808080u};
+    const h2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const h2_t dd = {d, d};
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        // bytes {b0, 0x64, b1, 0x64} and {b2, 0x64, b3, 0x64}
+        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u);
+        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u);
+        const h2_t a = (__builtin_bit_cast(h2_t, p0) + off) * dd;
+        const h2_t b = (__builtin_bit_cast(h2_t, p1) + off) * dd;
+        o[2 * i] = __builtin_bit_cast(uint32_t, a);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, b);
+    }
+    lo = make_uint4(o[0], o[1], o[2], o[3]);
+    hi = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
+__device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
+
+// Fragment of a 16 x 32 operand from LDS: lane l holds row (l % 16),
+// k = 8 * (l / 16) .. + 7 (the v_mfma_f32_16x16x32_f16 operand layout).
+__device__ __forceinline__ h8_t frag(const _Float16 (*s)[MF_LD], int row0, int lane)
+{
+    return *reinterpret_cast<const h8_t *>(&s[row0 + (lane & 15)][8 * (lane >> 4)]);
+}
+
+// ---------------------------------------------------------------------------
+// gate/up: tile = MF_BM slots x 64 features (64 gate + 64 up columns).
+// Wave (wm, wn): slots wm*64 .. +64, features wn*32 .. +32 -> 4 x (2 gate +
+// 2 up) fragments of 16 x 16.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
+{
+    __shared__ __align__(16) _Float16 As[2][MF_BM][MF_LD];
+    __shared__ __align__(16) _Float16 Bs[2][MF_BN][MF_LD];
+    __shared__ int rowtok[MF_BM];
+
+    const int nft = (a.F + 63) / 64;
+    const int tile = blockIdx.x / nft, ft = blockIdx.x - tile * nft;
+    if (tile >= *a.n_tiles) return;
+    const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
+    const int n = min(MF_BM, a.counts[e] - m0);
+    const int slot0 = a.offsets[e] + m0;
+    const int f0 = ft * 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    if (tid < MF_BM) rowtok[tid] = a.perm[slot0 + min(tid, n - 1)] / a.K;
+    __syncthreads();
+
+    // staging: thread -> row / column tid/2, 16-value half tid&1
+    const int sr = tid >> 1, sh = tid & 1;
+    const _Float16 *xrow = a.xh + (size_t)rowtok[sr] * a.H + sh * 16;
+    const int f = f0 + (sr & 63);
+    const int fc = min(f, a.F - 1);
+    const bool f_ok = f < a.F;
+    const int8_t *wq = sr < 64 ? a.gq : a.uq;
+    const uint16_t *wd = sr < 64 ? a.gd : a.ud;
+
+    uint4 xa, xb, wv;
+    uint16_t ws;
+    auto load = [&](int kb) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(xrow + kb * QK);
+        xa = xp[0];
+        xb = xp[1];
+        const size_t o = bm_index(e, a.nbH, kb, a.F, fc);
+        wv = *reinterpret_cast<const uint4 *>(wq + o * QK + sh * 16);
+        ws = wd[o];
+    };
+    auto store = [&](int buf) {
+        uint4 *ap = reinterpret_cast<uint4 *>(&As[buf][sr][sh * 16]);
+        ap[0] = xa;
+        ap[1] = xb;
+        uint4 lo, hi;
+        dequant16(wv, f_ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
+        uint4 *bp = reinterpret_cast<uint4 *>(&Bs[buf][sr][sh * 16]);
+        bp[0] = lo;
+        bp[1] = hi;
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const bool active = wm * 64 < n;   // wave-uniform: rows beyond the group are skipped
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < a.nbH; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < a.nbH) load(kb + 1);
+        if (active) {
+            h8_t af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) af[i] = frag(As[buf], wm * 64 + i * 16, lane);
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                bf[j] = frag(Bs[buf], (j >> 1) * 64 + wn * 32 + (j & 1) * 16, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kb + 1 < a.nbH) store(buf ^ 1);
+        __syncthreads();
+    }
+    if (!active) return;
+
+    // lane holds rows 4*(lane/16) + r, column lane % 16 of each fragment
+    const int cl = lane & 15, rq = 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int ff = f0 + wn * 32 + j * 16 + cl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = wm * 64 + i * 16 + rq + r;
+                if (row < n && ff < a.F) {
+                    const float g = acc[i][j][r], u = acc[i][j + 2][r];
+                    const float v = g / (1.0f + __expf(-g)) * u;
+                    a.act[(size_t)(slot0 + row) * a.F + ff] = (_Float16)v;
+                }
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+// down: tile = MF_BM slots x 128 output columns; wave (wm, wn): slots
+// wm*64 .. +64, columns wn*64 .. +64 -> 4 x 4 fragments.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(MF_THREADS) void moe_mfma_down_kernel(MfmaArgs a)
+{
+    __shared__ __align__(16) _Float16 As[2][MF_BM][MF_LD];
+    __shared__ __align__(16) _Float16 Bs[2][MF_BN][MF_LD];
+
+    const int nht = (a.H + MF_BN - 1) / MF_BN;
+    const int tile = blockIdx.x / nht, ht = blockIdx.x - tile * nht;
+    if (tile >= *a.n_tiles) return;
+    const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
+    const int n = min(MF_BM, a.counts[e] - m0);
+    const int slot0 = a.offsets[e] + m0;
+    const int h0 = ht * MF_BN;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;
+
+    const int sr = tid >> 1, sh = tid & 1;
+    const _Float16 *arow = a.act + (size_t)(slot0 + min(sr, n - 1)) * a.F + sh * 16;
+    const int h = h0 + sr;
+    const int hc = min(h, a.H - 1);
+    const bool h_ok = h < a.H;
+
+    uint4 xa, xb, wv;
+    uint16_t ws;
+    auto load = [&](int kb) {
+        const uint4 *xp = reinterpret_cast<const uint4 *>(arow + kb * QK);
+        xa = xp[0];
+        xb = xp[1];
+        const size_t o = bm_index(e, a.nbF, kb, a.H, hc);
+        wv = *reinterpret_cast<const uint4 *>(a.dq + o * QK + sh * 16);
+        ws = a.dd[o];
+    };
+    auto store = [&](int buf) {
+        uint4 *ap = reinterpret_cast<uint4 *>(&As[buf][sr][sh * 16]);
+        ap[0] = xa;
+        ap[1] = xb;
+        uint4 lo, hi;
+        dequant16(wv, h_ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
+        uint4 *bp = reinterpret_cast<uint4 *>(&Bs[buf][sr][sh * 16]);
+        bp[0] = lo;
+        bp[1] = hi;
+    };
+
+    f4_t acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+    const bool active = wm * 64 < n;
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int kb = 0; kb < a.nbF; kb++) {
+        const int buf = kb & 1;
+        if (kb + 1 < a.nbF) load(kb + 1);
+        if (active) {
+            h8_t af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) af[i] = frag(As[buf], wm * 64 + i * 16, lane);
+#pragma unroll
+            for (int j = 0; j < 4; j++) bf[j] = frag(Bs[buf], wn * 64 + j * 16, lane);
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kb + 1 < a.nbF) store(buf ^ 1);
+        __syncthreads();
+    }
+    if (!active) return;
+
+    const int cl = lane & 15, rq = 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int hh = h0 + wn * 64 + j * 16 + cl;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int row = wm * 64 + i * 16 + rq + r;
+                if (row < n && hh < a.H) a.y[(size_t)(slot0 + row) * a.H + hh] = acc[i][j][r];
+            }
+        }
+}
+
+// ---------------------------------------------------------------------------
+
+bool mfma_supported(const qq_moe *m) { return m->H % QK == 0 && m->F % QK == 0; }
+
+static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+static int tile_cap(const qq_moe *m, int T) { return T * m->K / MF_BM + m->E; }
+
+size_t mfma_work_bytes(const qq_moe *m, int T)
+{
+    const size_t P = (size_t)T * m->K;
+    const size_t cap = (size_t)tile_cap(m, T);
+    return al256((size_t)m->E * 4) + al256((size_t)(m->E + 1) * 4) + 2 * al256(P * 4) +
+           2 * al256(cap * 4) + 256 + al256((size_t)T * m->H * 2) + al256(P * m->F * 2) +
+           al256(P * m->H * 4);
+}
+
+int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                    const MaskBits &mask, const int32_t *idx, const double *w, char *work)
+{
+    const size_t P = (size_t)T * m->K;
+    const int cap = tile_cap(m, T);
+    char *p = work;
+    int32_t *counts = reinterpret_cast<int32_t *>(p);  p += al256((size_t)m->E * 4);
+    int32_t *offsets = reinterpret_cast<int32_t *>(p); p += al256((size_t)(m->E + 1) * 4);
+    int32_t *perm = reinterpret_cast<int32_t *>(p);    p += al256(P * 4);
+    int32_t *inv = reinterpret_cast<int32_t *>(p);     p += al256(P * 4);
+    DispatchTiles tiles;
+    tiles.bm = MF_BM;
+    tiles.cap = cap;
+    tiles.e = reinterpret_cast<int32_t *>(p);          p += al256((size_t)cap * 4);
+    tiles.m0 = reinterpret_cast<int32_t *>(p);         p += al256((size_t)cap * 4);
+    tiles.n = reinterpret_cast<int32_t *>(p);          p += 256;
+    _Float16 *xh = reinterpret_cast<_Float16 *>(p);    p += al256((size_t)T * m->H * 2);
+    _Float16 *act = reinterpret_cast<_Float16 *>(p);   p += al256(P * m->F * 2);
+    float *y = reinterpret_cast<float *>(p);
+
+    int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, tiles);
+    if (rc) return rc;
+
+    const size_t n4 = (size_t)T * m->H / 4;
+    prof_begin(ctx, K_CAST_F16);
+    QQ_LAUNCH(ctx, cast_f16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+              reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(xh), n4);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+
+    MfmaArgs a;
+    a.xh = xh;
+    a.act = act;
+    a.y = y;
+    a.perm = perm;
+    a.counts = counts;
+    a.offsets = offsets;
+    a.tile_e = tiles.e;
+    a.tile_m0 = tiles.m0;
+    a.n_tiles = tiles.n;
+    a.gq = m->gate->qs;
+    a.uq = m->up->qs;
+    a.dq = m->down->qs;
+    a.gd = reinterpret_cast<const uint16_t *>(m->gate->d);
+    a.ud = reinterpret_cast<const uint16_t *>(m->up->d);
+    a.dd = reinterpret_cast<const uint16_t *>(m->down->d);
+    a.H = m->H;
+    a.F = m->F;
+    a.K = m->K;
+    a.nbH = m->H / QK;
+    a.nbF = m->F / QK;
+
+    prof_begin(ctx, K_MFMA_GATEUP);
+    QQ_LAUNCH(ctx, moe_mfma_gateup_kernel, dim3((unsigned)cap * ((m->F + 63) / 64)),
+              dim3(MF_THREADS), 0, a);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    prof_begin(ctx, K_MFMA_DOWN);
+    QQ_LAUNCH(ctx, moe_mfma_down_kernel, dim3((unsigned)cap * ((m->H + MF_BN - 1) / MF_BN)),
+              dim3(MF_THREADS), 0, a);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return launch_combine(ctx, m, T, y, inv, w, hidden);
+}
+
+}  // namespace qq

@@ -79,6 +79,8 @@ struct qq_ctx {
     uint64_t *sync_slots;
     uint32_t *sync_err;
     uint32_t epoch;
+    // token batches of at least this many rows take the fp16 MFMA path (0: never)
+    int mfma_min_tokens;
     // per-kernel event pairs (qq_profile_*): pool of 2*prof_cap events
     int prof_on;
     int prof_kind;             // kernel id of the launches being issued, -1 none
@@ -101,6 +103,9 @@ enum KernelId {
     K_GROUPED_GATEUP,
     K_GROUPED_DOWN,
     K_COMBINE,
+    K_CAST_F16,
+    K_MFMA_GATEUP,
+    K_MFMA_DOWN,
     K_COUNT
 };
 
@@ -144,6 +149,26 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
                       char *work);
 size_t grouped_work_bytes(const qq_moe *m, int T);
+// Optional row-tile table written by the dispatch kernel: tile i covers slots
+// [m0[i], m0[i] + bm) of expert e[i] (clipped to the expert's count); *n = tiles.
+struct DispatchTiles {
+    int bm = 0;            // 0: no table
+    int cap = 0;           // capacity of e[] / m0[]
+    int32_t *e = nullptr;
+    int32_t *m0 = nullptr;
+    int32_t *n = nullptr;
+};
+int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, const MaskBits &mask,
+                    int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
+                    const DispatchTiles &tiles);
+int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const float *y, const int32_t *inv,
+                   const double *w, float *hidden);
+// fp16 MFMA grouped GEMMs for prefill chunks (mfma.hip); needs H and F
+// multiples of 32 and 16-byte aligned activations.
+bool mfma_supported(const qq_moe *m);
+size_t mfma_work_bytes(const qq_moe *m, int T);
+int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                    const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                        const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 

@@ -23,7 +23,7 @@ EXPORTS = (
     "qq_q8_0_upload", "qq_q8_0_upload_dev", "qq_tensor_release",
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
-    "qq_timer_start", "qq_timer_stop",
+    "qq_set_mfma_min_tokens", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
 )
 
@@ -59,6 +59,7 @@ def load():
         "qq_moe_release": (I, [P, P]),
         "qq_moe_forward": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_dev": (I, [P, P, P, P, I, P, P, P, P]),
+        "qq_set_mfma_min_tokens": (I, [P, I]),
         "qq_timer_start": (I, [P]),
         "qq_timer_stop": (I, [P, ctypes.POINTER(ctypes.c_float)]),
         "qq_profile_enable": (I, [P, I]),
@@ -110,6 +111,10 @@ class Context:
 
     def synchronize(self):
         self.check(self.L.qq_synchronize(self.h), "qq_synchronize")
+
+    def set_mfma_min_tokens(self, tokens):
+        """Token batches of >= tokens rows use the fp16 MFMA path (0: never)."""
+        self.check(self.L.qq_set_mfma_min_tokens(self.h, int(tokens)), "qq_set_mfma_min_tokens")
 
     def timer_start(self):
         self.check(self.L.qq_timer_start(self.h), "qq_timer_start")

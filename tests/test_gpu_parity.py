@@ -1,9 +1,11 @@
 """GPU parity: the HIP path through the C ABI against the CPU oracle.
 
-Tolerances (fp32 GEMV path): top-K indices bit-exact; sigmoid probabilities
-and normalised weights bit-exact; the MoE contribution within 1e-4 relative
-L2 of the oracle's.
+Tolerances: top-K indices, sigmoid probabilities and normalised weights
+bit-exact on every path; the MoE contribution within 1e-4 relative L2 of the
+oracle's on the fp32 paths and within 1e-2 on the fp16 MFMA path (prefill
+chunks of at least qq_set_mfma_min_tokens rows).
 """
+import contextlib
 import sys
 
 import numpy as np
@@ -16,6 +18,18 @@ from _util import full_layer, gpu_context, moe_delta, rel_l2, upload_layer
 pytestmark = pytest.mark.gpu
 
 TOL_GEMV = 1e-4
+TOL_MFMA = 1e-2
+
+
+@contextlib.contextmanager
+def mfma_min_tokens(n):
+    """Route token batches of >= n rows to the MFMA path for the block's duration."""
+    ctx = gpu_context()
+    ctx.set_mfma_min_tokens(n)
+    try:
+        yield
+    finally:
+        ctx.set_mfma_min_tokens(512)
 
 
 def _say(*a):
@@ -192,15 +206,50 @@ def test_moe_decode_batch64_full():
     assert len(np.unique(idx)) >= 28
 
 
-def test_moe_prefill_2048_skewed():
-    """2048-token chunk with Zipf-skewed routing: all top-K bit-exact, sampled rows checked."""
+@pytest.mark.parametrize("path", ["mfma", "fp32"])
+def test_moe_prefill_2048_skewed(path):
+    """2048-token chunk with Zipf-skewed routing: all top-K bit-exact, sampled rows checked
+    (MFMA path at 1e-2, fp32 grouped path at 1e-4)."""
+    _say("prefill 2048", path)
     L = full_layer(2, bias="zipf")
     x, hid = synth.activations(303, 2048, 2048)
     rows = np.random.default_rng(0).choice(2048, 24, replace=False)
-    _, idx, w, probs = _check_moe(L, x, hid, rows=rows)
+    with mfma_min_tokens(512 if path == "mfma" else 0):
+        _, idx, w, probs = _check_moe(L, x, hid, rows=rows,
+                                      tol=TOL_MFMA if path == "mfma" else TOL_GEMV)
     r_idx, r_w, r_probs = oracle.moe_route(L, x)
     np.testing.assert_array_equal(idx, r_idx)
     np.testing.assert_array_equal(w, r_w)
     np.testing.assert_array_equal(probs, r_probs)
     counts = np.bincount(idx.ravel(), minlength=32)
     assert counts.max() >= 300 and counts.min() < 10, counts
+
+
+@pytest.mark.parametrize("case", [
+    dict(H=64, F=64, E=8, K=2, T=40),
+    dict(H=256, F=96, E=4, K=2, T=300),      # several row tiles per expert, ragged column tile
+    dict(H=128, F=160, E=16, K=4, T=33),     # many groups smaller than one fragment
+    dict(H=2048, F=1792, E=64, K=8, T=64),
+    dict(H=4096, F=96, E=16, K=2, T=20),
+])
+def test_moe_mfma_small(case):
+    """The MFMA GEMMs on small shapes (threshold lowered to 2 rows), every row checked."""
+    _say("moe mfma", case)
+    T = case.pop("T")
+    L = synth.moe_layer(51, **case)
+    x, hid = synth.activations(52, T, case["H"])
+    with mfma_min_tokens(2):
+        _check_moe(L, x, hid, tol=TOL_MFMA)
+
+
+def test_moe_mfma_mask_and_unsupported_shape():
+    """Mask on the MFMA path; a hidden size that is not a multiple of 32 stays on the
+    fp32 path (1e-4) even when the threshold asks for MFMA."""
+    L = synth.moe_layer(61, H=128, F=96, E=8, K=3)
+    x, hid = synth.activations(62, 24, 128)
+    r_idx, _, _ = oracle.moe_route(L, x)
+    with mfma_min_tokens(2):
+        _check_moe(L, x, hid, mask={int(r_idx[0, 0]), int(r_idx[3, 2])}, tol=TOL_MFMA)
+        L2 = synth.moe_layer(63, H=100, F=64, E=8, K=2)
+        x2, hid2 = synth.activations(64, 24, 100)
+        _check_moe(L2, x2, hid2, tol=TOL_GEMV)
