@@ -55,7 +55,7 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes)
 static const char *const kKernelNames[K_COUNT] = {
     "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
     "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
-    "cast_f16",         "mfma_gateup",    "mfma_down",
+    "cast_f16",         "mfma_gateup",    "mfma_down",      "stream_gateup", "stream_down",
 };
 
 // Read and clear the device error word; non-zero means a bounded device-side
@@ -422,11 +422,16 @@ int qq_moe_release(qq_ctx *ctx, qq_moe *m)
 constexpr int T_CHUNK = 4096;
 
 // Path of one chunk of tn tokens: the fp16 MFMA GEMMs for chunks of at least
-// ctx->mfma_min_tokens rows, the fp32 grouped kernels otherwise.
-static bool use_mfma(const qq_ctx *ctx, const qq_moe *m, int tn, const float *x)
+// ctx->mfma_min_tokens rows; below that the split-fp16 streaming kernels
+// (fp32 accuracy); the fp32 vector-unit grouped kernels for shapes neither
+// takes (H or F not a multiple of 32, unaligned activations).
+enum Path { PATH_MFMA, PATH_STREAM, PATH_GROUPED };
+
+static Path chunk_path(const qq_ctx *ctx, const qq_moe *m, int tn, const float *x)
 {
-    return ctx->mfma_min_tokens > 0 && tn >= ctx->mfma_min_tokens && mfma_supported(m) &&
-           ((uintptr_t)x & 15) == 0;
+    if (!mfma_supported(m) || ((uintptr_t)x & 15) != 0) return PATH_GROUPED;
+    if (ctx->mfma_min_tokens > 0 && tn >= ctx->mfma_min_tokens) return PATH_MFMA;
+    return PATH_STREAM;
 }
 
 static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
@@ -434,12 +439,13 @@ static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
     if (decode_supported(m, T)) return align256(decode_work_bytes(m));
     const int Tc = T < T_CHUNK ? T : T_CHUNK;
     size_t work = grouped_work_bytes(m, Tc);
-    if (ctx->mfma_min_tokens > 0 && mfma_supported(m)) {
-        // any chunk of at least mfma_min_tokens rows may take the MFMA path
-        const size_t mw = mfma_work_bytes(m, Tc);
-        if (Tc >= ctx->mfma_min_tokens && mw > work) work = mw;
+    if (mfma_supported(m)) {
+        // the first chunk is the largest; a last, smaller chunk may take another path
+        work = std::max(work, stream_work_bytes(m, Tc));
+        if (ctx->mfma_min_tokens > 0 && Tc >= ctx->mfma_min_tokens)
+            work = std::max(work, mfma_work_bytes(m, Tc));
     }
-    return align256((size_t)Tc * m->E * 4) + align256((size_t)Tc * m->K * 4) +
+    return align256(router_work_bytes(m, Tc)) + align256((size_t)Tc * m->K * 4) +
            align256((size_t)Tc * m->K * 8) + align256(work);
 }
 
@@ -452,8 +458,8 @@ static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hid
     char *s = static_cast<char *>(ctx->scratch) + base;
     if (decode_supported(m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs, s);
     const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
-    float *logits = reinterpret_cast<float *>(s);
-    int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(Tc * m->E * 4));
+    double *part = reinterpret_cast<double *>(s);
+    int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(router_work_bytes(m, (int)Tc)));
     double *sw = reinterpret_cast<double *>(reinterpret_cast<char *>(sidx) + align256(Tc * m->K * 4));
     char *work = reinterpret_cast<char *>(sw) + align256(Tc * m->K * 8);
     for (int t0 = 0; t0 < T; t0 += T_CHUNK) {
@@ -463,11 +469,12 @@ static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hid
         float *cp = probs ? probs + (size_t)t0 * m->E : nullptr;
         const float *cx = x + (size_t)t0 * m->H;
         float *ch = hidden + (size_t)t0 * m->H;
-        if ((rc = launch_router_topk(ctx, m, cx, tn, logits, ci, cw, cp))) return rc;
-        if (use_mfma(ctx, m, tn, cx))
-            rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work);
-        else
-            rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work);
+        if ((rc = launch_router_topk(ctx, m, cx, tn, part, ci, cw, cp))) return rc;
+        switch (chunk_path(ctx, m, tn, cx)) {
+        case PATH_MFMA: rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
+        case PATH_STREAM: rc = launch_moe_stream(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
+        default: rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
+        }
         if (rc) return rc;
     }
     return QQ_OK;

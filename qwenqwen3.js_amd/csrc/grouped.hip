@@ -28,60 +28,96 @@ struct GrMT {
 };
 
 // ---------------------------------------------------------------------------
-// Dispatch: one workgroup of NT threads, thread t owns pairs [t*C, t*C + C).
-// LDS: cnt[NT][E] per-thread expert counts, turned into per-thread offsets by
-// a column scan.
+// Dispatch: one workgroup of NT threads (NT a multiple of 64), thread t owns
+// pairs [t*C, t*C + C).  LDS cnt[E][NT]: per-thread expert counts, turned
+// into per-thread exclusive offsets by one wave-level scan per expert.
+// Slots of an expert are therefore in pair order (token order).
 // ---------------------------------------------------------------------------
+// Exclusive scan over the 64 lanes; *total = sum of all lanes.
+__device__ __forceinline__ int wave_excl_scan(int v, int *total)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int u = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += u;
+    }
+    *total = __shfl(incl, WAVE - 1, WAVE);
+    return incl - v;
+}
+
 __global__ void moe_dispatch_kernel(const int32_t *__restrict__ idx, int P, int E, MaskBits mask,
                                     int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
                                     int32_t *__restrict__ perm, int32_t *__restrict__ inv,
                                     DispatchTiles tiles)
 {
-    extern __shared__ int cnt[];
+    extern __shared__ int cnt[];          // [E][NT]
     __shared__ int offs[MAX_E + 1];
     const int NT = blockDim.x, tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1), wave = tid / WAVE, NW = NT / WAVE;
     const int C = (P + NT - 1) / NT;
     const int p0 = min(P, tid * C), p1 = min(P, p0 + C);
-    for (int e = 0; e < E; e++) cnt[tid * E + e] = 0;
+    for (int e = 0; e < E; e++) cnt[e * NT + tid] = 0;
     for (int p = p0; p < p1; p++) {
         const int e = idx[p];
-        if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) cnt[tid * E + e]++;
+        if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) cnt[e * NT + tid]++;
     }
     __syncthreads();
-    for (int e = tid; e < E; e += NT) {
-        int base = 0;
-        for (int t = 0; t < NT; t++) {
-            const int c = cnt[t * E + e];
-            cnt[t * E + e] = base;
-            base += c;
+    // per expert: lane l scans threads [l*R, l*R + R) serially, then the wave
+    // scans the 64 lane sums
+    const int R = NT / WAVE;
+    for (int e = wave; e < E; e += NW) {
+        int *c = cnt + e * NT + lane * R;
+        int sum = 0;
+        for (int r = 0; r < R; r++) sum += c[r];
+        int total;
+        int base = wave_excl_scan(sum, &total);
+        for (int r = 0; r < R; r++) {
+            const int v = c[r];
+            c[r] = base;
+            base += v;
         }
-        offs[e] = base;
+        if (lane == 0) offs[e] = total;
     }
     __syncthreads();
-    if (tid == 0) {
-        int o = 0, nt = 0;
+    if (wave == 0) {
+        // exclusive scan of the expert totals, 64 experts at a time
+        int run = 0;
+        for (int e0 = 0; e0 < E; e0 += WAVE) {
+            const int e = e0 + lane;
+            const int c = e < E ? offs[e] : 0;
+            int tot;
+            const int o = run + wave_excl_scan(c, &tot);
+            if (e < E) {
+                offs[e] = o;
+                counts[e] = c;
+                offsets[e] = o;
+            }
+            run += tot;
+        }
+        if (lane == 0) {
+            offs[E] = run;
+            offsets[E] = run;
+        }
+    }
+    __syncthreads();
+    if (tid == 0 && tiles.bm > 0) {
+        // row tiles of at most tiles.bm slots, expert by expert
+        int nt = 0;
         for (int e = 0; e < E; e++) {
-            const int c = offs[e];
-            offs[e] = o;
-            counts[e] = c;
-            offsets[e] = o;
-            o += c;
-            // row tiles of at most tiles.bm slots, expert by expert
-            if (tiles.bm > 0)
-                for (int m0 = 0; m0 < c && nt < tiles.cap; m0 += tiles.bm, nt++) {
-                    tiles.e[nt] = e;
-                    tiles.m0[nt] = m0;
-                }
+            const int c = offs[e + 1] - offs[e];
+            for (int m0 = 0; m0 < c && nt < tiles.cap; m0 += tiles.bm, nt++) {
+                tiles.e[nt] = e;
+                tiles.m0[nt] = m0;
+            }
         }
-        offs[E] = o;
-        offsets[E] = o;
-        if (tiles.bm > 0) *tiles.n = nt;
+        *tiles.n = nt;
     }
-    __syncthreads();
     for (int p = p0; p < p1; p++) {
         const int e = idx[p];
         if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) {
-            const int pos = offs[e] + cnt[tid * E + e]++;
+            const int pos = offs[e] + cnt[e * NT + tid]++;
             perm[pos] = p;
             inv[p] = pos;
         } else {
@@ -327,8 +363,9 @@ int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, con
                     int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                     const DispatchTiles &tiles)
 {
-    int nt = 256;
-    while (nt > 32 && (size_t)nt * m->E * 4 > 32768) nt >>= 1;
+    // threads: a multiple of 64, at most 1024, cnt[E][NT] within 64 KiB of LDS
+    int nt = 1024;
+    while (nt > WAVE && (size_t)nt * m->E * 4 > 65536) nt >>= 1;
     prof_begin(ctx, K_DISPATCH);
     QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4, idx, P, m->E,
               mask, counts, offsets, perm, inv, tiles);

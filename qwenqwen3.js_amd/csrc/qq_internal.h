@@ -106,6 +106,8 @@ enum KernelId {
     K_CAST_F16,
     K_MFMA_GATEUP,
     K_MFMA_DOWN,
+    K_STREAM_GATEUP,
+    K_STREAM_DOWN,
     K_COUNT
 };
 
@@ -141,7 +143,11 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes);
 int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t);
 int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, int ldx,
                        float *y, int ldy, int rows);
-int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, float *logits,
+// Router of a token batch: binary64 partial logits (router_work_bytes of
+// scratch at `part`), then top-K.
+constexpr int ROUTER_MAX_SPLIT = 8;
+size_t router_work_bytes(const qq_moe *m, int T);
+int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
                        int32_t *idx, double *w, float *probs);
 bool decode_supported(const qq_moe *m, int T);
 size_t decode_work_bytes(const qq_moe *m);
@@ -169,6 +175,11 @@ bool mfma_supported(const qq_moe *m);
 size_t mfma_work_bytes(const qq_moe *m, int T);
 int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                     const MaskBits &mask, const int32_t *idx, const double *w, char *work);
+// Split-fp16 MFMA kernels with weights streamed into registers, for decode
+// batches at fp32 accuracy (stream.hip); same shape needs as the MFMA path.
+size_t stream_work_bytes(const qq_moe *m, int T);
+int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                      const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                        const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 

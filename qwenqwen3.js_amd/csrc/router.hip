@@ -1,13 +1,24 @@
 // router.hip -- LFM2-MoE router for token batches: binary64 logits, then
 // sigmoid / expert-bias top-K / renormalisation (src/lfm2-engine.js:417-447).
+//
+// logits[t][e] = fp32(sum_k x[t][k] * W[e][k]).  Every product of a binary32
+// activation with a binary32 (or exactly dequantised Q8_0) weight is exact in
+// binary64, so computing the sum in binary64 in any fixed order gives the
+// reference's fp32 logit except when the two binary64 sums straddle an fp32
+// rounding boundary (probability ~2^-29 per logit).
+//
+// The sum is a small [T x H] x [H x E] product on the binary64 matrix cores
+// (v_mfma_f64_16x16x4f64): a workgroup takes 16 tokens x 32 experts x one
+// slice of H; the slices' partial sums are stored in binary64 and added in
+// slice order by the top-K kernel.
 #include "qq_device.h"
 
 namespace qq {
 
-// Router weight of expert e at input index k (F32: column e of [H, E]; Q8_0:
-// block-major panel, exactly dequantised).  Products with a binary32
-// activation are exact in binary64, so only the summation order differs from
-// the reference's sequential loop.
+typedef double d4_t __attribute__((ext_vector_type(4)));
+
+// Router weight of expert e (F32: column e of [H, E] = E rows of H floats;
+// Q8_0: block-major panel, exactly dequantised).
 struct RouterW {
     const float *f32;
     const int8_t *qs;
@@ -21,12 +32,87 @@ struct RouterW {
         }
         return (double)f32[(size_t)e * H + k];
     }
+    // weights k .. k+3 of expert e (k % 4 == 0, k + 3 < H), zero when e >= E
+    __device__ __forceinline__ void at4(int e, int k, bool q8, double (&w)[4]) const
+    {
+        const int ec = min(e, E - 1);
+        const double z = e < E ? 1.0 : 0.0;
+        if (q8) {
+            const size_t o = bm_index(0, nb, k >> 5, E, ec);
+            const int q = *reinterpret_cast<const int *>(qs + o * QK + (k & 31));
+            const double sc = (double)__half2float(d[o]) * z;
+#pragma unroll
+            for (int j = 0; j < 4; j++) w[j] = (double)(int8_t)(q >> (8 * j)) * sc;
+        } else {
+            const float4 v = *reinterpret_cast<const float4 *>(f32 + (size_t)ec * H + k);
+            w[0] = (double)v.x * z;
+            w[1] = (double)v.y * z;
+            w[2] = (double)v.z * z;
+            w[3] = (double)v.w * z;
+        }
+    }
 };
 
-// Grid (ceil(T/TT), ceil(E/EB)); 256 threads split k; fixed-order reduction.
+// ---------------------------------------------------------------------------
+// Matrix-core logits.  Grid (ceil(T/16), KS, ceil(E/32)), 4 waves.  Lane l of
+// a wave loads 4 consecutive k of token row l%16 and of expert rows l%16 and
+// 16 + l%16 at k = k0 + 4*(l/16); the j-th of them feeds the j-th of four
+// MFMAs, so the four instructions cover k0 .. k0+15 exactly once.  Waves take
+// 16-wide k steps round robin inside the workgroup's slice; the four waves'
+// accumulators are added in wave order.  part[ks][t][e] (binary64).
+// f64 accumulator layout: lane l, element r -> row 4r + l/16, column l%16.
+// ---------------------------------------------------------------------------
+template <bool Q8>
+__global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int T,
+                                                          RouterW W, int kchunk,
+                                                          double *__restrict__ part)
+{
+    __shared__ double red[4][16][33];
+    const int t0 = blockIdx.x * 16, ks = blockIdx.y, e0 = blockIdx.z * 32;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const int t = t0 + r16;
+    const double tz = t < T ? 1.0 : 0.0;
+    const float *xr = x + (size_t)min(t, T - 1) * W.H;
+    const int ka = ks * kchunk, kb = min(W.H, ka + kchunk);
+
+    d4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 2
+    for (int k = ka + 16 * wave; k < kb; k += 64) {
+        const int kk = k + 4 * kq;
+        const float4 xv = *reinterpret_cast<const float4 *>(xr + kk);
+        double wa[4], wb[4];
+        W.at4(e0 + r16, kk, Q8, wa);
+        W.at4(e0 + 16 + r16, kk, Q8, wb);
+        const double xd[4] = {(double)xv.x * tz, (double)xv.y * tz, (double)xv.z * tz,
+                              (double)xv.w * tz};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wa[j], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wb[j], acc1, 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        red[wave][4 * r + kq][r16] = acc0[r];
+        red[wave][4 * r + kq][16 + r16] = acc1[r];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 16 * 32; i += 256) {
+        const int tt = i >> 5, ee = i & 31;
+        const double s = ((red[0][tt][ee] + red[1][tt][ee]) + red[2][tt][ee]) + red[3][tt][ee];
+        if (t0 + tt < T && e0 + ee < W.E) part[((size_t)ks * T + t0 + tt) * W.E + e0 + ee] = s;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Vector-unit logits for shapes the matrix-core kernel does not take (H not a
+// multiple of 16).  Grid (ceil(T/TT), ceil(E/EB)); 256 threads split k; fixed-
+// order reduction.  Writes part[0][t][e].
+// ---------------------------------------------------------------------------
 template <int TT, int EB, bool Q8>
 __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restrict__ x, int T,
-                                                            RouterW W, float *__restrict__ logits)
+                                                            RouterW W, double *__restrict__ part)
 {
     __shared__ double red[4][TT * EB];
     const int t0 = blockIdx.x * TT;
@@ -64,13 +150,14 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
         const int a = threadIdx.x / EB, b = threadIdx.x % EB;
         const int i = threadIdx.x;
         const double s = ((red[0][i] + red[1][i]) + red[2][i]) + red[3][i];
-        if (t0 + a < T && e0 + b < E) logits[(size_t)(t0 + a) * E + e0 + b] = (float)s;
+        if (t0 + a < T && e0 + b < E) part[(size_t)(t0 + a) * E + e0 + b] = s;
     }
 }
 
-// One wavefront per token.
+// One wavefront per token: logit = fp32(sum of the KS partial sums in order),
+// then sigmoid, bias, stable top-K and renormalisation.
 __global__ __launch_bounds__(256) void router_topk_kernel(
-    const float *__restrict__ logits, int T, int E, int K, const float *__restrict__ bias,
+    const double *__restrict__ part, int KS, int T, int E, int K, const float *__restrict__ bias,
     int32_t *__restrict__ idx, double *__restrict__ w, float *__restrict__ probs)
 {
     constexpr int EPL = MAX_E / WAVE;
@@ -81,7 +168,12 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = lane + WAVE * i;
-        lg[i] = (e < E) ? logits[(size_t)t * E + e] : 0.0f;
+        double s = 0.0;
+        if (e < E) {
+            s = part[(size_t)t * E + e];
+            for (int ks = 1; ks < KS; ks++) s += part[((size_t)ks * T + t) * E + e];
+        }
+        lg[i] = (float)s;
     }
     WaveRoute<EPL> R;
     wave_route<EPL>(lg, E, K, bias, R);
@@ -101,7 +193,23 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
 }
 
-int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, float *logits,
+// Number of H slices for T tokens: enough workgroups to spread over the chip,
+// at most ROUTER_MAX_SPLIT, and slices of at least 64 k.
+static int router_split(const qq_moe *m, int T)
+{
+    if (m->H % 16 != 0) return 1;
+    const int tiles = ((T + 15) / 16) * ((m->E + 31) / 32);
+    int ks = 1;
+    while (ks < ROUTER_MAX_SPLIT && tiles * ks < 512 && m->H / (2 * ks) >= 64) ks *= 2;
+    return ks;
+}
+
+size_t router_work_bytes(const qq_moe *m, int T)
+{
+    return (size_t)router_split(m, T) * T * m->E * sizeof(double);
+}
+
+int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
                        int32_t *idx, double *w, float *probs)
 {
     if (T <= 0) return QQ_OK;
@@ -113,28 +221,28 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, floa
     W.H = m->H;
     W.E = m->E;
     W.nb = (m->H + QK - 1) / QK;
-#define QQ_RL(TT, EB)                                                                             \
-    do {                                                                                          \
-        dim3 g((T + TT - 1) / TT, (m->E + EB - 1) / EB);                                          \
-        if (q8)                                                                                   \
-            QQ_LAUNCH(ctx, (router_logits_kernel<TT, EB, true>), g, dim3(256), 0, \
-                               x, T, W, logits);                                                  \
-        else                                                                                      \
-            QQ_LAUNCH(ctx, (router_logits_kernel<TT, EB, false>), g, dim3(256), 0, x, T, W, logits);                                     \
-    } while (0)
+    const int KS = ((uintptr_t)x & 15) == 0 ? router_split(m, T) : 1;
+
     prof_begin(ctx, K_ROUTER_LOGITS);
-    if (T <= 2)
-        QQ_RL(1, 1);
-    else if (T <= 32)
-        QQ_RL(1, 8);
-    else
-        QQ_RL(4, 8);
+    if (m->H % 16 == 0 && ((uintptr_t)x & 15) == 0) {
+        const int kchunk = ((m->H + KS * 64 - 1) / (KS * 64)) * 64;
+        const dim3 g((T + 15) / 16, KS, (m->E + 31) / 32);
+        if (q8)
+            QQ_LAUNCH(ctx, router_mfma_kernel<true>, g, dim3(256), 0, x, T, W, kchunk, part);
+        else
+            QQ_LAUNCH(ctx, router_mfma_kernel<false>, g, dim3(256), 0, x, T, W, kchunk, part);
+    } else {
+        const dim3 g((T + 3) / 4, (m->E + 7) / 8);
+        if (q8)
+            QQ_LAUNCH(ctx, (router_logits_kernel<4, 8, true>), g, dim3(256), 0, x, T, W, part);
+        else
+            QQ_LAUNCH(ctx, (router_logits_kernel<4, 8, false>), g, dim3(256), 0, x, T, W, part);
+    }
     prof_end(ctx);
-#undef QQ_RL
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_ROUTER_TOPK);
-    QQ_LAUNCH(ctx, router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, logits,
-                       T, m->E, m->K, m->bias, idx, w, probs);
+    QQ_LAUNCH(ctx, router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, part, KS, T, m->E, m->K,
+              m->bias, idx, w, probs);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

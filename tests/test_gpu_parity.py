@@ -133,6 +133,8 @@ def _check_moe(L, x, hid, mask=None, tol=TOL_GEMV, rows=None):
     dict(H=2048, F=64, E=32, K=4, T=3),
     dict(H=64, F=1792, E=32, K=4, T=2),
     dict(H=100, F=50, E=5, K=5, T=3),        # K == E, ragged dims
+    dict(H=128, F=96, E=4, K=2, T=100),      # 32-slot tiles, several per expert
+    dict(H=256, F=320, E=8, K=3, T=200),
 ])
 def test_moe_small(case):
     _say("moe small", case)
