@@ -3,19 +3,18 @@
 //
 // With ~8 rows per expert (64 tokens, 32 experts, top-4) every weight is used
 // by very few rows, so the layer is bound by streaming the experts' Q8_0
-// weights from HBM once.  Weights go straight from HBM into registers (no
-// LDS): a workgroup owns one expert, one tile of 16*MF slots and a group of
-// 128 weight columns; its 4 waves split the reduction dimension block by
-// block and their partial sums are added in wave order through LDS.
+// weights from HBM once.  A workgroup owns one expert, one tile of 16*MF
+// slots and a group of 128 weight columns; its 4 waves split the reduction
+// dimension block by block (each streaming its blocks through a private LDS
+// ring, below) and their partial sums are added in wave order through LDS.
 //
-// Accuracy (the fp32 path's 1e-4 relative L2): every operand is split into
-// two fp16 halves, a = a_hi + a_lo, w = w_hi + w_lo, and each 16x16x32 tile
-// takes three MFMAs, a_hi*w_hi + a_hi*w_lo + a_lo*w_hi, with fp32
-// accumulation.  w = q * d needs 19 significant bits; w_hi = fp16(q*d) and
-// w_lo = fp16(q*d - w_hi) (one fused multiply-add) hold it exactly unless
-// w_lo falls below the fp16 normal range.  The dropped a_lo*w_lo term and the
-// fp16 rounding of the low halves are ~2^-22 relative, so the products are
-// accurate to ~1e-7 like the fp32 kernels.
+// Accuracy (the fp32 path's 1e-4 relative L2): activations are split into
+// two fp16 halves, a = a_hi + a_lo (22 significant bits); the int8 weights
+// are exact in fp16.  Per 32-value block two MFMAs give the block's partial
+// sum a_hi*q + a_lo*q with exact products and fp32 accumulation, and the
+// block's fp16 scale is applied to that fp32 partial (one FMA per output),
+// as the reference applies d per block.  Error ~1e-7 relative, like the fp32
+// kernels.
 //   gate/up  A = x rows of the tile's tokens (gathered by perm), B = 64 gate +
 //            64 up columns; epilogue silu(g) * u -> act[slot][F] (fp32)
 //   down     A = act rows, B = 128 down columns -> y[slot][H] (fp32)
@@ -42,147 +41,244 @@ struct StreamArgs {
     int H, F, K, nbH, nbF;
 };
 
-// 8 consecutive fp32 values -> high and low fp16 halves (v - hi is exact in
-// fp32; its fp16 rounding is the split's only loss).
+// 8 consecutive fp32 values -> high and low fp16 halves.  hi is rounded
+// toward zero (v_cvt_pkrtz_f16_f32); v - hi is exact in fp32 and its fp16
+// rounding is the split's only loss.
 __device__ __forceinline__ void split8(const float4 a, const float4 b, h8_t &hi, h8_t &lo)
 {
     const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    uint32_t hw[4], lw[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const _Float16 h = (_Float16)v[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(v[i] - (float)h);
+    for (int i = 0; i < 4; i++) {
+        const h2_t h = __builtin_bit_cast(h2_t, __builtin_amdgcn_cvt_pkrtz(v[2 * i], v[2 * i + 1]));
+        hw[i] = __builtin_bit_cast(uint32_t, h);
+        lw[i] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(v[2 * i] - (float)h[0],
+                                                                          v[2 * i + 1] - (float)h[1]));
     }
+    hi = __builtin_bit_cast(h8_t, make_uint4(hw[0], hw[1], hw[2], hw[3]));
+    lo = __builtin_bit_cast(h8_t, make_uint4(lw[0], lw[1], lw[2], lw[3]));
 }
 
-// 8 int8 weights (one lane's share of a 16x32 fragment) and their fp16 scale
-// -> w_hi = fp16(q*d), w_lo = fp16(q*d - w_hi).  Bytes are made offset binary
-// and paired with the exponent byte 0x64 (half 0x64uu = 1024 + u), so
-// subtracting 1152 gives q exactly in fp16.
-__device__ __forceinline__ void dequant8_split(const uint2 q, const _Float16 d, h8_t &hi, h8_t &lo)
+// 8 int8 weights (one lane's share of a 16x32 fragment) -> 8 fp16 holding
+// the same integers exactly.  Bytes are made offset binary and paired with
+// the exponent byte 0x64 (half 0x64uu = 1024 + u); subtracting 1152 gives q.
+__device__ __forceinline__ h8_t int8_to_f16x8(const uint2 q)
 {
     const uint32_t w[2] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u};
     const h2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    const h2_t dd = {d, d};
+    uint32_t o[4];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u);
         const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u);
-        const h2_t q0 = __builtin_bit_cast(h2_t, p0) + off;
-        const h2_t q1 = __builtin_bit_cast(h2_t, p1) + off;
-        const h2_t h0 = q0 * dd, h1 = q1 * dd;
-        const h2_t l0 = __builtin_elementwise_fma(q0, dd, -h0);
-        const h2_t l1 = __builtin_elementwise_fma(q1, dd, -h1);
-        hi[4 * i] = h0[0];
-        hi[4 * i + 1] = h0[1];
-        hi[4 * i + 2] = h1[0];
-        hi[4 * i + 3] = h1[1];
-        lo[4 * i] = l0[0];
-        lo[4 * i + 1] = l0[1];
-        lo[4 * i + 2] = l1[0];
-        lo[4 * i + 3] = l1[1];
+        o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p0) + off);
+        o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p1) + off);
     }
+    return __builtin_bit_cast(h8_t, make_uint4(o[0], o[1], o[2], o[3]));
 }
 
-// One reduction block (32 values) of a wave's operands.
+// ---------------------------------------------------------------------------
+// Operand stream.  Each wave keeps a ring of ST_D stages in LDS; a stage holds
+// one 32-value block of the reduction for the workgroup: the 16*MF activation
+// rows (128 B each) and the 128 weight columns (two halves of 64 columns,
+// 32 int8 each) with their 128 fp16 scales.  Stages are filled by
+// global_load_lds copies straight from memory (no registers held while in
+// flight), issued from inline assembly so that the compiler's wait-counter
+// pass leaves them alone; a stage is only ever read by the wave that filled
+// it, so the wave's own vector-memory counter is the only synchronisation:
+//   S0 S1 | S2 [wait S0] use 0 | S3 [wait S1] use 1 | ...
+// When block i is used exactly two stages (2 * ST_NDMA copies) were issued
+// after S_i, so "vmcnt <= 2 * ST_NDMA" means S_i has landed.  No other vector
+// memory instruction is issued inside the loop.
+// Activation rows are stored with their 16-byte chunks permuted, chunk c of
+// row r at position c ^ ((r >> 1) & 7), so that the 16 rows of a fragment
+// read fall in 16 different bank groups.
+// ---------------------------------------------------------------------------
+constexpr int ST_D = 3;                          // stages per wave
+constexpr int ST_HALF = 64 * QK;                 // 64 columns x 32 int8
+
 template <int MF>
-struct StBlk {
-    float4 a[MF][2];         // A: row lane%16 (+16 m), k = 8*(lane/16) .. +7
-    uint2 q[ST_NF];          // B: column lane%16 of fragment j, same k
-    uint16_t s[ST_NF];       // B scales
+struct StLayout {
+    static constexpr int A = 0;                          // 16*MF rows x 128 B
+    static constexpr int B = 16 * MF * 128;              // two halves of ST_HALF
+    static constexpr int S = B + 2 * ST_HALF;            // 2 x 64 fp16 scales
+    static constexpr int STAGE = S + 256;
+    static constexpr int NDMA = 2 * MF + 4 + 1;          // copies per stage
 };
 
-// Where fragment j's 16 columns come from: matrix pointer and column index.
-struct ColSrc {
-    const int8_t *q;
-    const uint16_t *d;
-    int col;                 // clamped into range
-    bool ok;
-};
-
-template <int MF>
-__device__ __forceinline__ void st_load(StBlk<MF> &b, const float *const (&arow)[MF], int kb, int e,
-                                        int nb, int rows, const ColSrc (&src)[ST_NF], int lane)
+__device__ __forceinline__ uint32_t lds_u32(const void *p)
 {
-    const int ko = kb * QK + 8 * (lane >> 4);
-#pragma unroll
-    for (int m = 0; m < MF; m++) {
-        b.a[m][0] = *reinterpret_cast<const float4 *>(arow[m] + ko);
-        b.a[m][1] = *reinterpret_cast<const float4 *>(arow[m] + ko + 4);
-    }
-#pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const size_t o = bm_index(e, nb, kb, rows, src[j].col);
-        b.q[j] = *reinterpret_cast<const uint2 *>(src[j].q + o * QK + 8 * (lane >> 4));
-        b.s[j] = src[j].d[o];
-    }
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// global_load_lds: each lane copies `size` bytes from its own address to
+// LDS (M0 + lane * size); M0 is set right before (one wait state after an
+// SALU write to M0).
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
+}
+
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
 }
 
 template <int MF>
-__device__ __forceinline__ void st_compute(const StBlk<MF> &b, const ColSrc (&src)[ST_NF],
+struct StSrc {
+    const char *abase;          // activation rows (bytes)
+    uint32_t aoff[MF * 2];      // copy instruction i: lane's 16 bytes of row 8i + lane/8
+    const int8_t *qb[2];        // weights of column halves 0 / 1 at the expert's block 0
+    const uint16_t *db[2];      // their scales
+    uint32_t qoff[4];           // weight copy instruction i: lane's 16 bytes (half i/2)
+    uint32_t doff;              // scale copy: lane's 2 scales (half lane/32), in halves
+    uint32_t qstep, dstep;      // one block: rows * 32 bytes, rows halves
+    bool ok[ST_NF];             // fragment j's column in range (else its scale is zero)
+};
+
+// Copy block kb into the stage at LDS address `st` (ST_NDMA instructions).
+template <int MF>
+__device__ __forceinline__ void st_stage(const StSrc<MF> &s, uint32_t st, int kb)
+{
+    using L = StLayout<MF>;
+    const int lane = threadIdx.x & (WAVE - 1);
+    const char *ab = s.abase + (size_t)kb * QK * 4;
+#pragma unroll
+    for (int i = 0; i < 2 * MF; i++) dma16(ab + s.aoff[i], st + L::A + i * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        dma16(s.qb[i >> 1] + (size_t)kb * s.qstep + s.qoff[i], st + L::B + i * 1024);
+    dma4(s.db[lane >> 5] + (size_t)kb * s.dstep + s.doff, st + L::S);
+}
+
+// Fragment j: column 16*(j%4) + lane%16 of half j/4, k = 8*(lane/16) .. +7.
+// The block's int8 weights enter the MFMA exactly (as fp16 integers); the
+// block's scale is applied to the block's fp32 partial sum:
+//   acc += d * (a_hi * q + a_lo * q).
+// A lane's four outputs of a fragment share one column, hence one scale.
+template <int MF>
+__device__ __forceinline__ void st_compute(const char *st, const StSrc<MF> &s,
                                            f4_t (&acc)[MF][ST_NF])
 {
+    using L = StLayout<MF>;
+    const int lane = threadIdx.x & (WAVE - 1);
     h8_t ah[MF], al[MF];
 #pragma unroll
-    for (int m = 0; m < MF; m++) split8(b.a[m][0], b.a[m][1], ah[m], al[m]);
+    for (int m = 0; m < MF; m++) {
+        const int r = 16 * m + (lane & 15);
+        const int sw = (r >> 1) & 7, c = 2 * (lane >> 4);
+        const float4 a0 = *reinterpret_cast<const float4 *>(st + L::A + r * 128 + 16 * (c ^ sw));
+        const float4 a1 = *reinterpret_cast<const float4 *>(st + L::A + r * 128 + 16 * ((c + 1) ^ sw));
+        split8(a0, a1, ah[m], al[m]);
+    }
 #pragma unroll
     for (int j = 0; j < ST_NF; j++) {
-        h8_t wh, wl;
-        const _Float16 d = src[j].ok ? __builtin_bit_cast(_Float16, b.s[j]) : (_Float16)0.0f;
-        dequant8_split(b.q[j], d, wh, wl);
+        const int c = 16 * (j & 3) + (lane & 15);
+        const uint2 q = *reinterpret_cast<const uint2 *>(st + L::B + (j >> 2) * ST_HALF + c * QK +
+                                                         8 * (lane >> 4));
+        const uint16_t sb = *reinterpret_cast<const uint16_t *>(st + L::S + (j >> 2) * 128 + 2 * c);
+        const float d = s.ok[j] ? (float)__builtin_bit_cast(_Float16, sb) : 0.0f;
+        const h8_t qh = int8_to_f16x8(q);
 #pragma unroll
         for (int m = 0; m < MF; m++) {
-            acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], wh, acc[m][j], 0, 0, 0);
-            acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], wl, acc[m][j], 0, 0, 0);
-            acc[m][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[m], wh, acc[m][j], 0, 0, 0);
+            f4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], qh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
+            p = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[m], qh, p, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[m][j][r] = fmaf(p[r], d, acc[m][j][r]);
         }
     }
 }
 
-// Wave w reduces blocks w, w+4, w+8, ... of nb; two blocks are in flight
-// while one is multiplied.  Loads are branch-free (clamped block index).
+// Wave w reduces blocks w, w+4, w+8, ... of nb in its ring `ring` (ST_D
+// stages).  Copies past the wave's last block reload that block (clamped,
+// never read) so that every step issues the same instructions.  On return
+// every copy of this wave has landed.
 template <int MF>
-__device__ __forceinline__ void st_mainloop(const float *const (&arow)[MF], int e, int nb, int rows,
-                                            const ColSrc (&src)[ST_NF], int wave, int lane,
+__device__ __forceinline__ void st_mainloop(const StSrc<MF> &s, char *ring, int nb, int wave,
                                             f4_t (&acc)[MF][ST_NF])
 {
-    const int last = nb - 1;
-    StBlk<MF> b0, b1;
-    st_load<MF>(b0, arow, min(wave, last), e, nb, rows, src, lane);
-    st_load<MF>(b1, arow, min(wave + 4, last), e, nb, rows, src, lane);
-    for (int kb = wave; kb < nb; kb += 8) {
-        StBlk<MF> n0, n1;
-        st_load<MF>(n0, arow, min(kb + 8, last), e, nb, rows, src, lane);
-        st_compute<MF>(b0, src, acc);
-        st_load<MF>(n1, arow, min(kb + 12, last), e, nb, rows, src, lane);
-        if (kb + 4 < nb) st_compute<MF>(b1, src, acc);
-        b0 = n0;
-        b1 = n1;
+    using L = StLayout<MF>;
+    const int nblk = (nb - wave + 3) / 4;
+    if (nblk > 0) {
+        const int lastb = wave + 4 * (nblk - 1);
+        const uint32_t r0 = __builtin_amdgcn_readfirstlane(lds_u32(ring));
+        st_stage<MF>(s, r0, min(wave, lastb));
+        st_stage<MF>(s, r0 + L::STAGE, min(wave + 4, lastb));
+        for (int i = 0; i < nblk; i++) {
+            st_stage<MF>(s, r0 + ((i + 2) % ST_D) * L::STAGE, min(wave + 4 * (i + 2), lastb));
+            wait_vm<2 * L::NDMA>();
+            st_compute<MF>(ring + (i % ST_D) * L::STAGE, s, acc);
+        }
     }
+    wait_vm<0>();
 }
 
-// Partial sums of the 4 waves -> red[wave][row][col] (fp32).
+// Copy offsets: activation row r of the tile has byte offset rowoff(r);
+// weight halves start at columns c0[0], c0[1] of a matrix with `rows`
+// columns per block (clamped into range).
+template <int MF, typename RowOff>
+__device__ __forceinline__ void st_offsets(StSrc<MF> &s, RowOff rowoff, const int (&c0)[2],
+                                           int rows, int lane)
+{
+#pragma unroll
+    for (int i = 0; i < 2 * MF; i++) {
+        const int r = 8 * i + (lane >> 3);
+        const int chunk = (lane & 7) ^ ((r >> 1) & 7);   // lands at position lane & 7
+        s.aoff[i] = rowoff(r) + 16 * chunk;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int c = min(c0[i >> 1] + 32 * (i & 1) + (lane >> 1), rows - 1);
+        s.qoff[i] = (uint32_t)c * QK + 16 * (lane & 1);
+    }
+    s.doff = (uint32_t)min(c0[lane >> 5] + 2 * (lane & 31), rows - 2);
+#pragma unroll
+    for (int j = 0; j < ST_NF; j++) s.ok[j] = c0[j >> 2] + 16 * (j & 3) + (lane & 15) < rows;
+}
+
+// Cross-wave sums of fragment row block m: each wave writes its fragments of
+// half 0 to red0 and of half 1 to red1 ([wave][16 rows][64 + 1 columns]).
 template <int MF>
-__device__ __forceinline__ void st_spill(float (*red)[16 * MF][16 * ST_NF + 1],
-                                         const f4_t (&acc)[MF][ST_NF], int wave, int lane)
+__device__ __forceinline__ void st_spill(float (*red0)[16][65], float (*red1)[16][65],
+                                         const f4_t (&acc)[MF][ST_NF], int m, int wave, int lane)
 {
     const int cl = lane & 15, rq = 4 * (lane >> 4);
 #pragma unroll
-    for (int m = 0; m < MF; m++)
+    for (int j = 0; j < ST_NF; j++)
 #pragma unroll
-        for (int j = 0; j < ST_NF; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) red[wave][16 * m + rq + r][16 * j + cl] = acc[m][j][r];
+        for (int r = 0; r < 4; r++)
+            (j < 4 ? red0 : red1)[wave][rq + r][16 * (j & 3) + cl] = acc[m][j][r];
 }
 
+__device__ __forceinline__ float wave_order_sum(const float (*red)[16][65], int row, int c)
+{
+    return ((red[0][row][c] + red[1][row][c]) + red[2][row][c]) + red[3][row][c];
+}
+
+template <int MF>
+constexpr int st_lds_bytes()
+{
+    return 4 * ST_D * StLayout<MF>::STAGE;
+}
+static_assert(2 * 4 * 16 * 65 * 4 <= st_lds_bytes<1>(), "reduction tiles must fit the rings");
+
 // ---------------------------------------------------------------------------
-// gate/up: columns 0..63 of the workgroup are gate features f0 .. f0+63,
-// 64..127 the same up features.
+// gate/up: column half 0 = gate features f0 .. f0+63, half 1 = the same up
+// features.
 // ---------------------------------------------------------------------------
 template <int MF>
-__global__ __launch_bounds__(ST_THREADS) void moe_stream_gateup_kernel(StreamArgs a)
+__global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(StreamArgs a)
 {
-    __shared__ float red[4][16 * MF][16 * ST_NF + 1];
+    __shared__ __align__(16) char lds[st_lds_bytes<MF>()];
     const int ncg = (a.F + 63) / 64;
     const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
     if (tile >= *a.n_tiles) return;
@@ -192,51 +288,54 @@ __global__ __launch_bounds__(ST_THREADS) void moe_stream_gateup_kernel(StreamArg
     const int f0 = cg * 64;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
 
-    const float *arow[MF];
-#pragma unroll
-    for (int m = 0; m < MF; m++) {
-        const int r = min(16 * m + (lane & 15), n - 1);
-        arow[m] = a.x + (size_t)(a.perm[slot0 + r] / a.K) * a.H;
-    }
-    ColSrc src[ST_NF];
-#pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const int f = f0 + 16 * (j & 3) + (lane & 15);
-        src[j].q = j < 4 ? a.gq : a.uq;
-        src[j].d = j < 4 ? a.gd : a.ud;
-        src[j].col = min(f, a.F - 1);
-        src[j].ok = f < a.F;
-    }
+    StSrc<MF> src;
+    src.abase = reinterpret_cast<const char *>(a.x);
+    const size_t eb = (size_t)e * a.nbH * a.F;     // expert's first block-row
+    src.qb[0] = a.gq + eb * QK;
+    src.qb[1] = a.uq + eb * QK;
+    src.db[0] = a.gd + eb;
+    src.db[1] = a.ud + eb;
+    src.qstep = (uint32_t)a.F * QK;
+    src.dstep = (uint32_t)a.F;
+    const int c0[2] = {f0, f0};
+    st_offsets<MF>(src, [&](int r) {
+        return (uint32_t)(a.perm[slot0 + min(r, n - 1)] / a.K) * a.H * 4;
+    }, c0, a.F, lane);
+
     f4_t acc[MF][ST_NF];
 #pragma unroll
     for (int m = 0; m < MF; m++)
 #pragma unroll
         for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(arow, e, a.nbH, a.F, src, wave, lane, acc);
-    st_spill<MF>(red, acc, wave, lane);
-    __syncthreads();
-    for (int i = threadIdx.x; i < 16 * MF * 64; i += ST_THREADS) {
-        const int row = i >> 6, c = i & 63;
-        const int f = f0 + c;
-        if (row < n && f < a.F) {
-            const float g = ((red[0][row][c] + red[1][row][c]) + red[2][row][c]) + red[3][row][c];
-            const float u = ((red[0][row][64 + c] + red[1][row][64 + c]) + red[2][row][64 + c]) +
-                            red[3][row][64 + c];
-            const double g64 = (double)g;
-            const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
-            a.act[(size_t)(slot0 + row) * a.F + f] = sg * u;
+    st_mainloop<MF>(src, lds + wave * ST_D * StLayout<MF>::STAGE, a.nbH, wave, acc);
+    float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
+    float (*red1)[16][65] = red0 + 4;
+#pragma unroll
+    for (int m = 0; m < MF; m++) {
+        __syncthreads();
+        st_spill<MF>(red0, red1, acc, m, wave, lane);
+        __syncthreads();
+        for (int i = threadIdx.x; i < 16 * 64; i += ST_THREADS) {
+            const int row = i >> 6, c = i & 63;
+            const int f = f0 + c;
+            if (16 * m + row < n && f < a.F) {
+                const float g = wave_order_sum(red0, row, c), u = wave_order_sum(red1, row, c);
+                const double g64 = (double)g;
+                const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
+                a.act[(size_t)(slot0 + 16 * m + row) * a.F + f] = sg * u;
+            }
         }
     }
 }
 
 // ---------------------------------------------------------------------------
-// down: 128 output columns h0 .. h0+127.
+// down: 128 output columns h0 .. h0+127 (halves h0 and h0 + 64).
 // ---------------------------------------------------------------------------
 template <int MF>
-__global__ __launch_bounds__(ST_THREADS) void moe_stream_down_kernel(StreamArgs a)
+__global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamArgs a)
 {
-    __shared__ float red[4][16 * MF][16 * ST_NF + 1];
+    __shared__ __align__(16) char lds[st_lds_bytes<MF>()];
     const int ncg = (a.H + 127) / 128;
     const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
     if (tile >= *a.n_tiles) return;
@@ -246,34 +345,38 @@ __global__ __launch_bounds__(ST_THREADS) void moe_stream_down_kernel(StreamArgs 
     const int h0 = cg * 128;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
 
-    const float *arow[MF];
-#pragma unroll
-    for (int m = 0; m < MF; m++)
-        arow[m] = a.act + (size_t)(slot0 + min(16 * m + (lane & 15), n - 1)) * a.F;
-    ColSrc src[ST_NF];
-#pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const int h = h0 + 16 * j + (lane & 15);
-        src[j].q = a.dq;
-        src[j].d = a.dd;
-        src[j].col = min(h, a.H - 1);
-        src[j].ok = h < a.H;
-    }
+    StSrc<MF> src;
+    src.abase = reinterpret_cast<const char *>(a.act);
+    const size_t eb = (size_t)e * a.nbF * a.H;
+    src.qb[0] = src.qb[1] = a.dq + eb * QK;
+    src.db[0] = src.db[1] = a.dd + eb;
+    src.qstep = (uint32_t)a.H * QK;
+    src.dstep = (uint32_t)a.H;
+    const int c0[2] = {h0, h0 + 64};
+    st_offsets<MF>(src, [&](int r) { return (uint32_t)(slot0 + min(r, n - 1)) * a.F * 4; }, c0,
+                   a.H, lane);
+
     f4_t acc[MF][ST_NF];
 #pragma unroll
     for (int m = 0; m < MF; m++)
 #pragma unroll
         for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(arow, e, a.nbF, a.H, src, wave, lane, acc);
-    st_spill<MF>(red, acc, wave, lane);
-    __syncthreads();
-    for (int i = threadIdx.x; i < 16 * MF * 128; i += ST_THREADS) {
-        const int row = i >> 7, c = i & 127;
-        const int h = h0 + c;
-        if (row < n && h < a.H)
-            a.y[(size_t)(slot0 + row) * a.H + h] =
-                ((red[0][row][c] + red[1][row][c]) + red[2][row][c]) + red[3][row][c];
+    st_mainloop<MF>(src, lds + wave * ST_D * StLayout<MF>::STAGE, a.nbF, wave, acc);
+    float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
+    float (*red1)[16][65] = red0 + 4;
+#pragma unroll
+    for (int m = 0; m < MF; m++) {
+        __syncthreads();
+        st_spill<MF>(red0, red1, acc, m, wave, lane);
+        __syncthreads();
+        for (int i = threadIdx.x; i < 16 * 128; i += ST_THREADS) {
+            const int row = i >> 7, c = i & 127;
+            const int h = h0 + c;
+            if (16 * m + row < n && h < a.H)
+                a.y[(size_t)(slot0 + 16 * m + row) * a.H + h] =
+                    wave_order_sum(c < 64 ? red0 : red1, row, c & 63);
+        }
     }
 }
 
