@@ -168,15 +168,18 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         // rank: experts ordered before this one by (score desc, index asc);
-        // the rank-k expert is the k-th element of a stable descending sort
+        // the rank-k expert is the k-th element of a stable descending sort.
+        // Branch-free over all 64 slots of sh_score (slots >= E hold -inf and
+        // never rank before a real expert).
         int rank = 0;
-        for (int i0 = 0; i0 < a.E; i0 += 4) {
+#pragma unroll
+        for (int i0 = 0; i0 < WAVE; i0 += 4) {
             const float4 q = *reinterpret_cast<const float4 *>(&sh_score[i0]);
             const float qq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int i = i0 + u;
-                rank += (i < a.E && (qq[u] > sc || (qq[u] == sc && i < lane))) ? 1 : 0;
+                rank += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < lane));
             }
         }
         if (lane >= a.E) rank = INT_MAX;

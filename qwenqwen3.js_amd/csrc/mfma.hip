@@ -30,8 +30,6 @@ typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr int MF_BM = 128;       // slots per row tile
 constexpr int MF_BN = 128;       // weight columns per workgroup
-constexpr int MF_LD = 40;        // LDS row stride in halves (80 B: 16 rows of a
-                                 // fragment read hit 16 distinct 16-byte bank groups)
 constexpr int MF_THREADS = 256;  // 4 waves, 2 x 2 over the 128 x 128 tile
 
 struct MfmaArgs {
@@ -85,11 +83,89 @@ __device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4
 
 __device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
-// Fragment of a 16 x 32 operand from LDS: lane l holds row (l % 16),
-// k = 8 * (l / 16) .. + 7 (the v_mfma_f32_16x16x32_f16 operand layout).
-__device__ __forceinline__ h8_t frag(const _Float16 (*s)[MF_LD], int row0, int lane)
+// LDS tile of one operand and stage: 128 rows x 32 halves (64 B, four 16-byte
+// chunks).  Chunk c of row r sits at r*64 + 16*(c ^ ((r >> 2) & 3)): the 16
+// rows of a fragment read (same chunk) land in 16 different 16-byte bank
+// groups, and so do the staging writes.
+constexpr int MF_TILE = MF_BM * 64;
+
+__device__ __forceinline__ int tile_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+
+// Per-thread staging sources: 32 bytes (16 halves) of one A row and 16 int8 of
+// one B column per Q8_0 block, advanced by a fixed stride per block.
+struct MfSrc {
+    const char *a;           // A row, this thread's half of block 0
+    const int8_t *q;         // B column, this thread's half of block 0
+    const uint16_t *d;       // the column's scale at block 0
+    size_t qstep, dstep;     // one block of the B matrix (rows * 32 bytes, rows halves)
+    bool ok;                 // B column in range (else zero scale)
+};
+
+// Shared main loop of the two GEMMs.  Stage = A tile + B tile (fp16); two
+// stages double buffered; the next block's global loads are in flight while
+// this block's MFMAs run.  Wave fragments: A rows aoff[i] (i < 4), B columns
+// boff[j] (j < 4) of the tile (row bases of 16-row fragments).
+__device__ __forceinline__ void mf_mainloop(const MfSrc &src, int nb, char *lds, int sr, int sh,
+                                            const int (&arow)[4], const int (&bcol)[4],
+                                            f4_t (&acc)[4][4])
 {
-    return *reinterpret_cast<const h8_t *>(&s[row0 + (lane & 15)][8 * (lane >> 4)]);
+    const int lane = threadIdx.x & (WAVE - 1);
+    // staging offsets: this thread writes chunks 2sh, 2sh+1 of row sr
+    const int w0 = tile_off(sr, 2 * sh), w1 = tile_off(sr, 2 * sh + 1);
+    // fragment offsets: row base + lane%16, chunk lane/16
+    int ao[4], bo[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) ao[i] = tile_off(arow[i] + (lane & 15), lane >> 4);
+#pragma unroll
+    for (int j = 0; j < 4; j++) bo[j] = MF_TILE + tile_off(bcol[j] + (lane & 15), lane >> 4);
+
+    const char *ap = src.a;
+    const int8_t *qp = src.q;
+    const uint16_t *dp = src.d;
+    uint4 xa, xb, wv;
+    uint16_t ws;
+    auto load = [&]() {
+        xa = *reinterpret_cast<const uint4 *>(ap);
+        xb = *reinterpret_cast<const uint4 *>(ap + 16);
+        wv = *reinterpret_cast<const uint4 *>(qp);
+        ws = *dp;
+        ap += QK * 2;
+        qp += src.qstep;
+        dp += src.dstep;
+    };
+    auto store = [&](char *st) {
+        *reinterpret_cast<uint4 *>(st + w0) = xa;
+        *reinterpret_cast<uint4 *>(st + w1) = xb;
+        uint4 lo, hi;
+        dequant16(wv, src.ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
+        *reinterpret_cast<uint4 *>(st + MF_TILE + w0) = lo;
+        *reinterpret_cast<uint4 *>(st + MF_TILE + w1) = hi;
+    };
+    auto compute = [&](const char *st) {
+        h8_t af[4], bf[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const h8_t *>(st + ao[i]);
+#pragma unroll
+        for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const h8_t *>(st + bo[j]);
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    load();
+    store(lds);
+    __syncthreads();
+    for (int kb = 0; kb < nb; kb++) {
+        char *cur = lds + (kb & 1) * 2 * MF_TILE;
+        char *nxt = lds + ((kb + 1) & 1) * 2 * MF_TILE;
+        const bool more = kb + 1 < nb;
+        if (more) load();
+        compute(cur);
+        if (more) store(nxt);
+        __syncthreads();
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -99,8 +175,7 @@ __device__ __forceinline__ h8_t frag(const _Float16 (*s)[MF_LD], int row0, int l
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
 {
-    __shared__ __align__(16) _Float16 As[2][MF_BM][MF_LD];
-    __shared__ __align__(16) _Float16 Bs[2][MF_BN][MF_LD];
+    __shared__ __align__(16) char lds[4 * MF_TILE];
     __shared__ int rowtok[MF_BM];
 
     const int nft = (a.F + 63) / 64;
@@ -118,64 +193,25 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
 
     // staging: thread -> row / column tid/2, 16-value half tid&1
     const int sr = tid >> 1, sh = tid & 1;
-    const _Float16 *xrow = a.xh + (size_t)rowtok[sr] * a.H + sh * 16;
     const int f = f0 + (sr & 63);
     const int fc = min(f, a.F - 1);
-    const bool f_ok = f < a.F;
-    const int8_t *wq = sr < 64 ? a.gq : a.uq;
-    const uint16_t *wd = sr < 64 ? a.gd : a.ud;
+    MfSrc src;
+    src.a = reinterpret_cast<const char *>(a.xh + (size_t)rowtok[sr] * a.H) + sh * 32;
+    const size_t o = bm_index(e, a.nbH, 0, a.F, fc);
+    src.q = (sr < 64 ? a.gq : a.uq) + o * QK + sh * 16;
+    src.d = (sr < 64 ? a.gd : a.ud) + o;
+    src.qstep = (size_t)a.F * QK;
+    src.dstep = (size_t)a.F;
+    src.ok = f < a.F;
 
-    uint4 xa, xb, wv;
-    uint16_t ws;
-    auto load = [&](int kb) {
-        const uint4 *xp = reinterpret_cast<const uint4 *>(xrow + kb * QK);
-        xa = xp[0];
-        xb = xp[1];
-        const size_t o = bm_index(e, a.nbH, kb, a.F, fc);
-        wv = *reinterpret_cast<const uint4 *>(wq + o * QK + sh * 16);
-        ws = wd[o];
-    };
-    auto store = [&](int buf) {
-        uint4 *ap = reinterpret_cast<uint4 *>(&As[buf][sr][sh * 16]);
-        ap[0] = xa;
-        ap[1] = xb;
-        uint4 lo, hi;
-        dequant16(wv, f_ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
-        uint4 *bp = reinterpret_cast<uint4 *>(&Bs[buf][sr][sh * 16]);
-        bp[0] = lo;
-        bp[1] = hi;
-    };
-
+    const int arow[4] = {wm * 64, wm * 64 + 16, wm * 64 + 32, wm * 64 + 48};
+    const int bcol[4] = {wn * 32, wn * 32 + 16, 64 + wn * 32, 64 + wn * 32 + 16};
     f4_t acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const bool active = wm * 64 < n;   // wave-uniform: rows beyond the group are skipped
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kb = 0; kb < a.nbH; kb++) {
-        const int buf = kb & 1;
-        if (kb + 1 < a.nbH) load(kb + 1);
-        if (active) {
-            h8_t af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = frag(As[buf], wm * 64 + i * 16, lane);
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                bf[j] = frag(Bs[buf], (j >> 1) * 64 + wn * 32 + (j & 1) * 16, lane);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kb + 1 < a.nbH) store(buf ^ 1);
-        __syncthreads();
-    }
-    if (!active) return;
+    mf_mainloop(src, a.nbH, lds, sr, sh, arow, bcol, acc);
 
     // lane holds rows 4*(lane/16) + r, column lane % 16 of each fragment
     const int cl = lane & 15, rq = 4 * (lane >> 4);
@@ -202,8 +238,7 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(MF_THREADS) void moe_mfma_down_kernel(MfmaArgs a)
 {
-    __shared__ __align__(16) _Float16 As[2][MF_BM][MF_LD];
-    __shared__ __align__(16) _Float16 Bs[2][MF_BN][MF_LD];
+    __shared__ __align__(16) char lds[4 * MF_TILE];
 
     const int nht = (a.H + MF_BN - 1) / MF_BN;
     const int tile = blockIdx.x / nht, ht = blockIdx.x - tile * nht;
@@ -216,61 +251,25 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_down_kernel(MfmaArgs a)
     const int wm = wave & 1, wn = wave >> 1;
 
     const int sr = tid >> 1, sh = tid & 1;
-    const _Float16 *arow = a.act + (size_t)(slot0 + min(sr, n - 1)) * a.F + sh * 16;
     const int h = h0 + sr;
     const int hc = min(h, a.H - 1);
-    const bool h_ok = h < a.H;
+    MfSrc src;
+    src.a = reinterpret_cast<const char *>(a.act + (size_t)(slot0 + min(sr, n - 1)) * a.F) + sh * 32;
+    const size_t o = bm_index(e, a.nbF, 0, a.H, hc);
+    src.q = a.dq + o * QK + sh * 16;
+    src.d = a.dd + o;
+    src.qstep = (size_t)a.H * QK;
+    src.dstep = (size_t)a.H;
+    src.ok = h < a.H;
 
-    uint4 xa, xb, wv;
-    uint16_t ws;
-    auto load = [&](int kb) {
-        const uint4 *xp = reinterpret_cast<const uint4 *>(arow + kb * QK);
-        xa = xp[0];
-        xb = xp[1];
-        const size_t o = bm_index(e, a.nbF, kb, a.H, hc);
-        wv = *reinterpret_cast<const uint4 *>(a.dq + o * QK + sh * 16);
-        ws = a.dd[o];
-    };
-    auto store = [&](int buf) {
-        uint4 *ap = reinterpret_cast<uint4 *>(&As[buf][sr][sh * 16]);
-        ap[0] = xa;
-        ap[1] = xb;
-        uint4 lo, hi;
-        dequant16(wv, h_ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
-        uint4 *bp = reinterpret_cast<uint4 *>(&Bs[buf][sr][sh * 16]);
-        bp[0] = lo;
-        bp[1] = hi;
-    };
-
+    const int arow[4] = {wm * 64, wm * 64 + 16, wm * 64 + 32, wm * 64 + 48};
+    const int bcol[4] = {wn * 64, wn * 64 + 16, wn * 64 + 32, wn * 64 + 48};
     f4_t acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-    const bool active = wm * 64 < n;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kb = 0; kb < a.nbF; kb++) {
-        const int buf = kb & 1;
-        if (kb + 1 < a.nbF) load(kb + 1);
-        if (active) {
-            h8_t af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = frag(As[buf], wm * 64 + i * 16, lane);
-#pragma unroll
-            for (int j = 0; j < 4; j++) bf[j] = frag(Bs[buf], wn * 64 + j * 16, lane);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kb + 1 < a.nbF) store(buf ^ 1);
-        __syncthreads();
-    }
-    if (!active) return;
+    mf_mainloop(src, a.nbF, lds, sr, sh, arow, bcol, acc);
 
     const int cl = lane & 15, rq = 4 * (lane >> 4);
 #pragma unroll
