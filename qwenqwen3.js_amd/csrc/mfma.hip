@@ -83,13 +83,19 @@ __device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4
 
 __device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
-// LDS tile of one operand and stage: 128 rows x 32 halves (64 B, four 16-byte
-// chunks).  Chunk c of row r sits at r*64 + 16*(c ^ ((r >> 2) & 3)): the 16
-// rows of a fragment read (same chunk) land in 16 different 16-byte bank
-// groups, and so do the staging writes.
-constexpr int MF_TILE = MF_BM * 64;
-
-__device__ __forceinline__ int tile_off(int r, int c) { return r * 64 + 16 * (c ^ ((r >> 2) & 3)); }
+// LDS tile of one operand and stage: 128 rows x KB Q8_0 blocks (32*KB halves,
+// 4*KB chunks of 16 bytes).  Chunk c of row r sits at r*64*KB + 16*(c ^ s(r))
+// with s(r) = (r >> 2) & 3 for KB = 1 and (r >> 1) & 7 for KB = 2: the 16
+// rows of a fragment read (same chunk) fall in 16 different 16-byte bank
+// groups of a 256-byte bank row, and so do the staging writes.
+template <int KB>
+struct MfTile {
+    static constexpr int BYTES = MF_BM * 64 * KB;
+    static __device__ __forceinline__ int off(int r, int c)
+    {
+        return r * 64 * KB + 16 * (c ^ (KB == 1 ? ((r >> 2) & 3) : ((r >> 1) & 7)));
+    }
+};
 
 // Per-thread staging sources: 32 bytes (16 halves) of one A row and 16 int8 of
 // one B column per Q8_0 block, advanced by a fixed stride per block.
@@ -101,66 +107,87 @@ struct MfSrc {
     bool ok;                 // B column in range (else zero scale)
 };
 
-// Shared main loop of the two GEMMs.  Stage = A tile + B tile (fp16); two
-// stages double buffered; the next block's global loads are in flight while
-// this block's MFMAs run.  Wave fragments: A rows aoff[i] (i < 4), B columns
-// boff[j] (j < 4) of the tile (row bases of 16-row fragments).
+// Shared main loop of the two GEMMs over nb blocks (nb % KB == 0).  Stage = A
+// tile + B tile (fp16) of KB blocks; two stages double buffered; the next
+// stage's global loads are in flight while this stage's MFMAs run; one
+// barrier per stage.  Wave fragments: A rows arow[i], B columns bcol[j] (row
+// bases of 16-row fragments within the tile).
+template <int KB>
 __device__ __forceinline__ void mf_mainloop(const MfSrc &src, int nb, char *lds, int sr, int sh,
                                             const int (&arow)[4], const int (&bcol)[4],
                                             f4_t (&acc)[4][4])
 {
+    using T = MfTile<KB>;
     const int lane = threadIdx.x & (WAVE - 1);
-    // staging offsets: this thread writes chunks 2sh, 2sh+1 of row sr
-    const int w0 = tile_off(sr, 2 * sh), w1 = tile_off(sr, 2 * sh + 1);
-    // fragment offsets: row base + lane%16, chunk lane/16
-    int ao[4], bo[4];
+    // staging offsets: block b of this thread's row sr, chunks 4b + 2sh, +1
+    int w0[KB], w1[KB];
 #pragma unroll
-    for (int i = 0; i < 4; i++) ao[i] = tile_off(arow[i] + (lane & 15), lane >> 4);
+    for (int b = 0; b < KB; b++) {
+        w0[b] = T::off(sr, 4 * b + 2 * sh);
+        w1[b] = T::off(sr, 4 * b + 2 * sh + 1);
+    }
+    // fragment offsets: row base + lane%16, chunk 4b + lane/16
+    int ao[KB][4], bo[KB][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) bo[j] = MF_TILE + tile_off(bcol[j] + (lane & 15), lane >> 4);
+    for (int b = 0; b < KB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            ao[b][i] = T::off(arow[i] + (lane & 15), 4 * b + (lane >> 4));
+            bo[b][i] = T::BYTES + T::off(bcol[i] + (lane & 15), 4 * b + (lane >> 4));
+        }
 
     const char *ap = src.a;
     const int8_t *qp = src.q;
     const uint16_t *dp = src.d;
-    uint4 xa, xb, wv;
-    uint16_t ws;
+    uint4 xa[KB], xb[KB], wv[KB];
+    uint16_t ws[KB];
     auto load = [&]() {
-        xa = *reinterpret_cast<const uint4 *>(ap);
-        xb = *reinterpret_cast<const uint4 *>(ap + 16);
-        wv = *reinterpret_cast<const uint4 *>(qp);
-        ws = *dp;
-        ap += QK * 2;
-        qp += src.qstep;
-        dp += src.dstep;
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            xa[b] = *reinterpret_cast<const uint4 *>(ap + b * QK * 2);
+            xb[b] = *reinterpret_cast<const uint4 *>(ap + b * QK * 2 + 16);
+            wv[b] = *reinterpret_cast<const uint4 *>(qp + b * src.qstep);
+            ws[b] = dp[b * src.dstep];
+        }
+        ap += KB * QK * 2;
+        qp += KB * src.qstep;
+        dp += KB * src.dstep;
     };
     auto store = [&](char *st) {
-        *reinterpret_cast<uint4 *>(st + w0) = xa;
-        *reinterpret_cast<uint4 *>(st + w1) = xb;
-        uint4 lo, hi;
-        dequant16(wv, src.ok ? half_bits(ws) : (_Float16)0.0f, lo, hi);
-        *reinterpret_cast<uint4 *>(st + MF_TILE + w0) = lo;
-        *reinterpret_cast<uint4 *>(st + MF_TILE + w1) = hi;
+#pragma unroll
+        for (int b = 0; b < KB; b++) {
+            *reinterpret_cast<uint4 *>(st + w0[b]) = xa[b];
+            *reinterpret_cast<uint4 *>(st + w1[b]) = xb[b];
+            uint4 lo, hi;
+            dequant16(wv[b], src.ok ? half_bits(ws[b]) : (_Float16)0.0f, lo, hi);
+            *reinterpret_cast<uint4 *>(st + T::BYTES + w0[b]) = lo;
+            *reinterpret_cast<uint4 *>(st + T::BYTES + w1[b]) = hi;
+        }
     };
     auto compute = [&](const char *st) {
-        h8_t af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const h8_t *>(st + ao[i]);
+        for (int b = 0; b < KB; b++) {
+            h8_t af[4], bf[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const h8_t *>(st + bo[j]);
+            for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const h8_t *>(st + ao[b][i]);
 #pragma unroll
-        for (int i = 0; i < 4; i++)
+            for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const h8_t *>(st + bo[b][j]);
 #pragma unroll
-            for (int j = 0; j < 4; j++)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
     };
 
+    const int nst = nb / KB;
     load();
     store(lds);
     __syncthreads();
-    for (int kb = 0; kb < nb; kb++) {
-        char *cur = lds + (kb & 1) * 2 * MF_TILE;
-        char *nxt = lds + ((kb + 1) & 1) * 2 * MF_TILE;
-        const bool more = kb + 1 < nb;
+    for (int k = 0; k < nst; k++) {
+        char *cur = lds + (k & 1) * 2 * T::BYTES;
+        char *nxt = lds + ((k + 1) & 1) * 2 * T::BYTES;
+        const bool more = k + 1 < nst;
         if (more) load();
         compute(cur);
         if (more) store(nxt);
@@ -173,9 +200,10 @@ __device__ __forceinline__ void mf_mainloop(const MfSrc &src, int nb, char *lds,
 // Wave (wm, wn): slots wm*64 .. +64, features wn*32 .. +32 -> 4 x (2 gate +
 // 2 up) fragments of 16 x 16.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
+template <int KB>
+__global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_gateup_kernel(MfmaArgs a)
 {
-    __shared__ __align__(16) char lds[4 * MF_TILE];
+    __shared__ __align__(16) char lds[4 * MfTile<KB>::BYTES];
     __shared__ int rowtok[MF_BM];
 
     const int nft = (a.F + 63) / 64;
@@ -211,7 +239,7 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    mf_mainloop(src, a.nbH, lds, sr, sh, arow, bcol, acc);
+    mf_mainloop<KB>(src, a.nbH, lds, sr, sh, arow, bcol, acc);
 
     // lane holds rows 4*(lane/16) + r, column lane % 16 of each fragment
     const int cl = lane & 15, rq = 4 * (lane >> 4);
@@ -236,9 +264,10 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_gateup_kernel(MfmaArgs a)
 // down: tile = MF_BM slots x 128 output columns; wave (wm, wn): slots
 // wm*64 .. +64, columns wn*64 .. +64 -> 4 x 4 fragments.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(MF_THREADS) void moe_mfma_down_kernel(MfmaArgs a)
+template <int KB>
+__global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_down_kernel(MfmaArgs a)
 {
-    __shared__ __align__(16) char lds[4 * MF_TILE];
+    __shared__ __align__(16) char lds[4 * MfTile<KB>::BYTES];
 
     const int nht = (a.H + MF_BN - 1) / MF_BN;
     const int tile = blockIdx.x / nht, ht = blockIdx.x - tile * nht;
@@ -269,7 +298,7 @@ __global__ __launch_bounds__(MF_THREADS) void moe_mfma_down_kernel(MfmaArgs a)
     for (int i = 0; i < 4; i++)
 #pragma unroll
         for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    mf_mainloop(src, a.nbF, lds, sr, sh, arow, bcol, acc);
+    mf_mainloop<KB>(src, a.nbF, lds, sr, sh, arow, bcol, acc);
 
     const int cl = lane & 15, rq = 4 * (lane >> 4);
 #pragma unroll
@@ -354,14 +383,15 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     a.nbH = m->H / QK;
     a.nbF = m->F / QK;
 
+    // one Q8_0 block per pipeline stage: two per stage halve the barriers but
+    // double the LDS per workgroup, and the lost occupancy costs more
+    const dim3 g1((unsigned)cap * ((m->F + 63) / 64)), g2((unsigned)cap * ((m->H + MF_BN - 1) / MF_BN));
     prof_begin(ctx, K_MFMA_GATEUP);
-    QQ_LAUNCH(ctx, moe_mfma_gateup_kernel, dim3((unsigned)cap * ((m->F + 63) / 64)),
-              dim3(MF_THREADS), 0, a);
+    QQ_LAUNCH(ctx, moe_mfma_gateup_kernel<1>, g1, dim3(MF_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_MFMA_DOWN);
-    QQ_LAUNCH(ctx, moe_mfma_down_kernel, dim3((unsigned)cap * ((m->H + MF_BN - 1) / MF_BN)),
-              dim3(MF_THREADS), 0, a);
+    QQ_LAUNCH(ctx, moe_mfma_down_kernel<1>, g2, dim3(MF_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return launch_combine(ctx, m, T, y, inv, w, hidden);
