@@ -84,16 +84,17 @@ __device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4
 __device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
 // LDS tile of one operand and stage: 128 rows x KB Q8_0 blocks (32*KB halves,
-// 4*KB chunks of 16 bytes).  Chunk c of row r sits at r*64*KB + 16*(c ^ s(r))
-// with s(r) = (r >> 2) & 3 for KB = 1 and (r >> 1) & 7 for KB = 2: the 16
-// rows of a fragment read (same chunk) fall in 16 different 16-byte bank
-// groups of a 256-byte bank row, and so do the staging writes.
+// 4*KB chunks of 16 bytes).  Chunk c of row r sits at r*64*KB + 16*(c ^ s(r)).
+// For KB = 1, s(r) = ((r >> 1) ^ (r >> 2)) & 3: any 8 consecutive rows of a
+// fragment read (same chunk) fall in 8 different 16-byte groups of a 128-byte
+// bank row and any 16 in 16 different groups of a 256-byte one; so do the
+// staging writes.  For KB = 2, s(r) = (r >> 1) & 7.
 template <int KB>
 struct MfTile {
     static constexpr int BYTES = MF_BM * 64 * KB;
     static __device__ __forceinline__ int off(int r, int c)
     {
-        return r * 64 * KB + 16 * (c ^ (KB == 1 ? ((r >> 2) & 3) : ((r >> 1) & 7)));
+        return r * 64 * KB + 16 * (c ^ (KB == 1 ? (((r >> 1) ^ (r >> 2)) & 3) : ((r >> 1) & 7)));
     }
 };
 
