@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the LFM2-MoE Q8_0 MoE layer on one MI355X.
+"""Benchmark of the LFM2-MoE Q8_0 MoE feed-forward path on one MI355X.
 
 Metric: MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0.
 
@@ -10,10 +10,16 @@ Q8_0 experts), rotating over `--layers` independently seeded layer instances
 (16 x 374 MB = 6 GB resident) so that consecutive steps never find their
 expert weights in L2 or the 256 MB Infinity Cache.
 
+Other workloads (--workload): decode_b64 (64-token decode batch), prefill_2048
+(2048-token chunk, Zipf-skewed routing), stack22_decode / stack22_prefill (22
+independently seeded layers, rmsnorm + MoE per layer, 1 token resp. a
+4096-token chunk per step), matvec (one Q8_0 matvec 1024 -> 3072, rotating
+over 80 weights).
+
 Inputs are generated on the device before the timed region.  Times come from
 HIP events on the stream the kernels run on; the per-kernel roofline figure
-comes from a second pass over the same steps with every launch bracketed by
-its own event pair (qq_profile_*).
+comes from a second pass over the same steps in which every launch carries
+its own start/stop events (hipExtLaunchKernelGGL, qq_profile_*).
 
 Prints one JSON line.
 """
@@ -31,15 +37,22 @@ sys.path.insert(0, os.path.join(ROOT, "qwenqwen3.js_amd"))
 
 METRIC = "MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0"
 HBM_PEAK_GBPS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
 H, F, E, K = 2048, 1792, 32, 4
 QBLK = 34
+STACK_LAYERS = 22
+MV_IN, MV_OUT = 1024, 3072
 
 WORKLOADS = {
-    # name: (T tokens per step, bias kind, description)
-    "decode_b1": (1, "uniform", "moe_layer_decode_batch1"),
-    "decode_b64": (64, "uniform", "moe_layer_decode_batch64"),
-    "prefill_2048": (2048, "zipf", "moe_layer_prefill_2048_zipf"),
+    # name: (kind, T tokens per step, bias kind, config name)
+    "decode_b1": ("layer", 1, "uniform", "moe_layer_decode_batch1"),
+    "decode_b64": ("layer", 64, "uniform", "moe_layer_decode_batch64"),
+    "prefill_2048": ("layer", 2048, "zipf", "moe_layer_prefill_2048_zipf"),
+    "stack22_decode": ("stack", 1, "uniform", "moe_stack22_decode_batch1"),
+    "stack22_prefill": ("stack", 4096, "uniform", "moe_stack22_prefill_4096"),
+    "matvec": ("matvec", 1, None, "q8_0_matvec_1024x3072"),
 }
+MFMA_KERNELS = ("mfma_gateup", "mfma_down")
 
 
 def expert_bytes():
@@ -48,7 +61,7 @@ def expert_bytes():
     return gate, down
 
 
-def kernel_bytes(name, T, n_experts, n_pairs):
+def kernel_bytes(name, T, n_experts):
     """Algorithmic HBM bytes of one launch of `name`: every weight, router and
     activation byte the math needs, once; intermediate buffers the kernels
     exchange (partial sums, grouped rows) are not counted."""
@@ -60,26 +73,24 @@ def kernel_bytes(name, T, n_experts, n_pairs):
         return 2 * T * H * 4
     if name == "router_logits":
         return E * H * 4 + T * H * 4
-    if name == "grouped_gateup":
+    if name in ("grouped_gateup", "stream_gateup", "mfma_gateup"):
         return n_experts * 2 * gate + T * H * 4
-    if name == "grouped_down":
+    if name in ("grouped_down", "stream_down", "mfma_down"):
         return n_experts * down
-    if name == "combine":
+    if name in ("combine", "rmsnorm"):
         return 2 * T * H * 4
+    if name == "q8_0_matvec":
+        return MV_OUT * (MV_IN // 32) * QBLK + MV_IN * 4 + MV_OUT * 4
     return None
-
-
-MFMA_KERNELS = ("mfma_gateup", "mfma_down")
-MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
 
 
 def kernel_flops(name, n_pairs):
     """Algorithmic FLOPs of one launch of an expert-product kernel over n_pairs
     (token, expert) rows: 2 per multiply-add of the real rows only (padding
     rows of a tile are not counted)."""
-    if name in ("mfma_gateup", "grouped_gateup"):
+    if name in ("mfma_gateup", "grouped_gateup", "stream_gateup"):
         return 2.0 * n_pairs * H * 2 * F
-    if name in ("mfma_down", "grouped_down"):
+    if name in ("mfma_down", "grouped_down", "stream_down"):
         return 2.0 * n_pairs * F * H
     return None
 
@@ -117,25 +128,55 @@ def make_layer(torch, ctx, seed, bias_kind):
     return ctx.moe_create(router, qq_hip.TYPE_F32, bias, *tensors, H, F, E, K)
 
 
-def cpu_baseline(seconds):
-    """The reference's CPU path restated for Node 12 (oracle/moe_ref.js: same loop
-    order and float64 arithmetic as src/tensor.js / src/lfm2-engine.js, checked bit
-    for bit against the C oracle by the tests), timed on one host thread:
-    tokens/sec through one MoE layer on a bounded sample of single-token calls.
-    Without node, the C oracle is timed instead."""
+def make_matvec_weight(torch, ctx, seed):
+    """One GGUF Q8_0 [1024, 3072] weight made on the device, repacked by the library."""
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    nblk = MV_OUT * (MV_IN // 32)
+    blocks = torch.empty((nblk, QBLK), dtype=torch.uint8, device="cuda")
+    blocks[:, 2:] = torch.randint(-127, 128, (nblk, 32), generator=g, device="cuda",
+                                  dtype=torch.int8).view(torch.uint8)
+    d = (torch.randn(nblk, generator=g, device="cuda").abs() * 0.002).to(torch.float16)
+    blocks[:, :2] = d.view(torch.uint8).view(nblk, 2)
+    torch.cuda.synchronize()
+    return ctx.upload_q8_0_dev(blocks.data_ptr(), blocks.numel(), MV_IN, MV_OUT, 1)
+
+
+def _node_bench(mode, seconds):
     import shutil
     node = shutil.which("node")
+    if not node:
+        return None
+    p = subprocess.run([node, os.path.join(ROOT, "oracle", "moe_ref.js"), mode, str(seconds)],
+                       capture_output=True, text=True, timeout=seconds * 4 + 120, check=True)
+    return json.loads(p.stdout.strip().splitlines()[-1])
+
+
+def cpu_baseline(seconds, kind):
+    """The reference's CPU path restated for Node 12 (oracle/moe_ref.js: same loop
+    order and float64 arithmetic as src/tensor.js / src/lfm2-engine.js, checked bit
+    for bit against the C oracle by the tests), timed on one host thread on a
+    bounded sample.  Without node, the C oracle is timed instead."""
     ncores = os.cpu_count() or 0
-    if node:
-        p = subprocess.run([node, os.path.join(ROOT, "oracle", "moe_ref.js"), "bench", str(seconds)],
-                           capture_output=True, text=True, timeout=seconds * 4 + 120, check=True)
-        r = json.loads(p.stdout.strip().splitlines()[-1])
+    if kind == "matvec":
+        r = _node_bench("bench-matvec", seconds)
+        if r:
+            return {"value": round(r["matvecs_per_s"], 3), "unit": "matvecs/s", "cores": 1,
+                    "kind": "port",
+                    "sample": "%d matmulQ80xF32 calls (1024 -> 3072 Q8_0) in %.1f s: the "
+                              "reference's JS CPU path restated for Node %s, 1 thread of %d host "
+                              "cores" % (r["matvecs"], r["seconds"], r["node"], ncores)}
+    per = STACK_LAYERS if kind == "stack" else 1
+    r = _node_bench("bench", seconds)
+    if r:
         return {
-            "value": round(r["tokens_per_s"], 3), "unit": "tokens/s", "cores": 1, "kind": "port",
-            "sample": "%d single-token MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts) in "
-                      "%.1f s: the reference's JS CPU path restated for Node %s, 1 thread of %d "
-                      "host cores; tokens are independent, so tokens/s is the rate at any batch"
-                      % (r["tokens"], r["seconds"], r["node"], ncores),
+            "value": round(r["tokens_per_s"] / per, 4), "unit": "tokens/s", "cores": 1,
+            "kind": "port",
+            "sample": "%d single-token MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts) "
+                      "in %.1f s: the reference's JS CPU path restated for Node %s, 1 thread of %d "
+                      "host cores; tokens are independent, so tokens/s is the rate at any batch%s"
+                      % (r["tokens"], r["seconds"], r["node"], ncores,
+                         "; divided by %d layers for the stack" % per if per > 1 else ""),
         }
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
@@ -148,7 +189,7 @@ def cpu_baseline(seconds):
         oracle.moe_ffn(L, x[n % 64:n % 64 + 1], hid[n % 64:n % 64 + 1])
         n += 1
     el = time.perf_counter() - t0
-    return {"value": round(n / el, 3), "unit": "tokens/s", "cores": 1, "kind": "port",
+    return {"value": round(n / el / per, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": "%d single-token MoE-layer calls in %.1f s on the C oracle (node absent), "
                       "1 thread of %d host cores" % (n, el, ncores)}
 
@@ -170,6 +211,64 @@ def copy_calibration(steps):
     ms = ev0.elapsed_time(ev1) / steps
     print(json.dumps({"copy_bytes": n, "ms": round(ms, 4), "read_plus_write_gbps": round(2 * n / (ms * 1e6), 1)}))
     return 0
+
+
+def timed(torch, ctx, stream, step, steps, warmup, launches_per_step):
+    """Warm up, time `steps` steps between two events on the library stream,
+    then run the same steps again with per-launch events.  Returns
+    (total_ms, {kernel: (ms_sum, count)})."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for i in range(steps):
+        step(i)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ctx.synchronize()          # raises if a device-side wait expired
+    total_ms = ev0.elapsed_time(ev1)
+    ctx.profile_enable(steps * launches_per_step)
+    for i in range(steps):
+        step(i)
+    prof = ctx.profile_read()
+    ctx.profile_enable(0)
+    ctx.synchronize()
+    return total_ms, prof
+
+
+def kernel_table(prof, T, n_exp, n_pairs):
+    kernels = {}
+    for name, (ms, cnt) in prof.items():
+        b = kernel_bytes(name, T, n_exp)
+        avg_us = 1000.0 * ms / cnt
+        kernels[name] = {"avg_us": round(avg_us, 3), "launches": cnt,
+                         "bytes": None if b is None else int(b),
+                         "gbps": None if b is None else round(b / (avg_us * 1e3), 1)}
+        fl = kernel_flops(name, n_pairs)
+        if fl is not None:
+            kernels[name]["tflops"] = round(fl / (avg_us * 1e6), 1)
+    return kernels
+
+
+def roofline_of(prof, kernels, workload):
+    """Roofline entry of the kernel with the largest total time."""
+    dom = max(prof, key=lambda n: prof[n][0])
+    k = kernels[dom]
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_%s.json" % workload)
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get(dom)
+    if dom in MFMA_KERNELS:
+        return dom, {"kernel": dom, "bound": "mfma", "achieved": k["tflops"],
+                     "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(k["tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": traffic}
+    return dom, {"kernel": dom, "bound": "hbm", "achieved": k["gbps"], "peak": HBM_PEAK_GBPS,
+                 "unit": "GB/s",
+                 "frac": None if k["gbps"] is None else round(k["gbps"] / HBM_PEAK_GBPS, 4),
+                 "traffic": traffic}
 
 
 def main():
@@ -196,91 +295,90 @@ def main():
     import torch
     import qq_hip
 
-    T, bias_kind, wname = WORKLOADS[args.workload]
+    kind, T, bias_kind, wname = WORKLOADS[args.workload]
     torch.cuda.init()
     ctx = qq_hip.Context(0)
     # the library launches on this stream; every event below is recorded on it
     stream = torch.cuda.Stream()
     torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
-
-    n_layers = args.layers if T == 1 else min(args.layers, 4)
-    layers = [make_layer(torch, ctx, 1000 + i, bias_kind) for i in range(n_layers)]
-    S = 64 if T == 1 else 2
     gx = torch.Generator(device="cuda")
     gx.manual_seed(99)
-    X = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
-    HID = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
-    idx = torch.empty((S, T, K), dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
+    extra = {}
 
-    def step(i):
-        s = i % S
-        layers[i % n_layers].forward_dev(X[s].data_ptr(), HID[s].data_ptr(), T,
-                                         idx_ptr=idx[s].data_ptr())
+    if kind == "matvec":
+        n_w = 80                      # 80 x 3.36 MB > the 256 MB Infinity Cache
+        keep = [make_matvec_weight(torch, ctx, 500 + i) for i in range(n_w)]
+        X = torch.randn((64, MV_IN), generator=gx, device="cuda", dtype=torch.float32)
+        Y = torch.empty((64, MV_OUT), device="cuda", dtype=torch.float32)
+        torch.cuda.synchronize()
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
+        def step(i):
+            keep[i % n_w].matvec_dev(X[i % 64].data_ptr(), Y[i % 64].data_ptr(), 1)
 
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    ev1.record(stream)
-    torch.cuda.synchronize()
-    ctx.synchronize()          # raises if a device-side wait expired
-    total_ms = ev0.elapsed_time(ev1)
-    ms_per_step = total_ms / args.steps
-
-    # distinct experts per step (weights each step must read at least once)
-    used = idx.cpu().numpy()
-    n_exp = float(np.mean([len(np.unique(used[s])) for s in range(min(S, args.steps))]))
-    n_pairs = T * K
-
-    # per-kernel pass: same steps, every launch bracketed by its own events
-    ctx.profile_enable(args.steps * 8)
-    for i in range(args.steps):
-        step(i)
-    prof = ctx.profile_read()
-    ctx.profile_enable(0)
-    ctx.synchronize()
-    kernels = {}
-    for name, (ms, cnt) in prof.items():
-        b = kernel_bytes(name, T, n_exp, n_pairs)
-        avg_us = 1000.0 * ms / cnt
-        fl = kernel_flops(name, n_pairs)
-        kernels[name] = {"avg_us": round(avg_us, 3), "launches": cnt,
-                         "bytes": None if b is None else int(b),
-                         "gbps": None if b is None else round(b / (avg_us * 1e3), 1)}
-        if fl is not None:
-            kernels[name]["tflops"] = round(fl / (avg_us * 1e6), 1)
-    dom = max(prof, key=lambda n: prof[n][0])
-    dom_k = kernels[dom]
-
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_%s.json" % args.workload)
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get(dom)
-
-    if dom in MFMA_KERNELS:
-        roofline = {"kernel": dom, "bound": "mfma", "achieved": dom_k["tflops"],
-                    "peak": MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(dom_k["tflops"] / MFMA_PEAK_TFLOPS, 4), "traffic": traffic}
+        total_ms, prof = timed(torch, ctx, stream, step, args.steps, args.warmup, 2)
+        ms_per_step = total_ms / args.steps
+        kernels = kernel_table(prof, 1, 0, 0)
+        dom, roofline = roofline_of(prof, kernels, args.workload)
+        value, unit = args.steps / (total_ms / 1000.0), "matvecs/s"
+        config = {"workload": wname, "in_dim": MV_IN, "out_dim": MV_OUT, "weights": "Q8_0",
+                  "weight_instances": n_w}
+        dtype = "f32"
+        extra["hbm_gbps"] = round(kernel_bytes("q8_0_matvec", 1, 0) / (ms_per_step * 1e6), 1)
     else:
-        roofline = {"kernel": dom, "bound": "hbm", "achieved": dom_k["gbps"],
-                    "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                    "frac": None if dom_k["gbps"] is None else round(dom_k["gbps"] / HBM_PEAK_GBPS, 4),
-                    "traffic": traffic}
-    layer_flops = 6.0 * n_pairs * H * F
-    lb = layer_bytes(T, n_exp)
-    tokens_per_s = T * args.steps / (total_ms / 1000.0)
+        stack = kind == "stack"
+        n_layers = STACK_LAYERS if stack else (args.layers if T == 1 else min(args.layers, 4))
+        keep = [make_layer(torch, ctx, 1000 + i, bias_kind) for i in range(n_layers)]
+        S = 64 if T == 1 else 2
+        X = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
+        HID = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
+        XN = torch.empty((T, H), device="cuda", dtype=torch.float32)
+        idx = torch.empty((S, n_layers if stack else 1, T, K), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+
+        if stack:
+            def step(i):
+                # one token (or chunk) through every layer: x = rmsnorm(hidden), hidden += MoE(x)
+                s = i % S
+                for li, layer in enumerate(keep):
+                    ctx.rmsnorm_dev(HID[s].data_ptr(), None, XN.data_ptr(), T, H, 1e-5)
+                    layer.forward_dev(XN.data_ptr(), HID[s].data_ptr(), T,
+                                      idx_ptr=idx[s, li].data_ptr())
+        else:
+            def step(i):
+                s = i % S
+                keep[i % n_layers].forward_dev(X[s].data_ptr(), HID[s].data_ptr(), T,
+                                               idx_ptr=idx[s, 0].data_ptr())
+
+        calls = n_layers if stack else 1
+        total_ms, prof = timed(torch, ctx, stream, step, args.steps, args.warmup, 10 * calls)
+        ms_per_step = total_ms / args.steps
+        # distinct experts per layer call (weights each call must read at least once)
+        used = idx.cpu().numpy()
+        ns = min(S, args.steps)
+        n_exp = float(np.mean([len(np.unique(used[s, l])) for s in range(ns)
+                               for l in range(used.shape[1])]))
+        n_pairs = T * K
+        kernels = kernel_table(prof, T, n_exp, n_pairs)
+        dom, roofline = roofline_of(prof, kernels, args.workload)
+        value, unit = T * args.steps / (total_ms / 1000.0), "tokens/s"
+        config = {"workload": wname, "H": H, "F": F, "E": E, "K": K, "T": T,
+                  "weights": "Q8_0", "activations": "f32", "router": "f32 (f64 accumulate)",
+                  "layer_instances": n_layers, "distinct_experts_per_layer_call": round(n_exp, 2)}
+        if stack:
+            config["per_layer"] = "rmsnorm(hidden) -> MoE -> hidden +="
+        dtype = "f16" if dom in MFMA_KERNELS else "f32"
+        lb = layer_bytes(T, n_exp) * calls
+        extra["hbm_gbps_layer"] = round(lb / (ms_per_step * 1e6), 1)
+        extra["hbm_frac_layer"] = round(lb / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4)
+        extra["tflops_layer"] = round(6.0 * n_pairs * H * F * calls / (ms_per_step * 1e9), 2)
+        if stack and T == 1:
+            extra["us_per_token"] = round(ms_per_step * 1000.0, 2)
+
     result = {
         "metric": METRIC,
-        "value": round(tokens_per_s, 1),
-        "unit": "tokens/s",
+        "value": round(value, 1),
+        "unit": unit,
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
@@ -288,25 +386,21 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16" if dom in MFMA_KERNELS else "f32",
+        "dtype": dtype,
         "data": "synthetic",
-        "config": {"workload": wname, "H": H, "F": F, "E": E, "K": K, "T": T,
-                   "weights": "Q8_0", "activations": "f32", "router": "f32 (f64 accumulate)",
-                   "layer_instances": n_layers, "distinct_experts_per_step": round(n_exp, 2)},
-        "hbm_gbps_layer": round(lb / (ms_per_step * 1e6), 1),
-        "hbm_frac_layer": round(lb / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
-        "tflops_layer": round(layer_flops / (ms_per_step * 1e9), 2),
-        "roofline": roofline,
-        "kernels": kernels,
+        "config": config,
     }
-    for l in layers:
-        for t in l._keep:
+    result.update(extra)
+    result["roofline"] = roofline
+    result["kernels"] = kernels
+    for obj in keep:
+        for t in getattr(obj, "_keep", ()):
             t.release()
-        l.release()
+        obj.release()
     ctx.close()
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, kind)
     print(json.dumps(result), flush=True)
     return 0
 

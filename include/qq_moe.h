@@ -126,6 +126,14 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
 #define QQ_MFMA_MIN_TOKENS_DEFAULT 512
 int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens);
 
+/* rmsnorm (src/tensor.js:103-114) of T rows of H floats, the ffn_norm step
+ * that produces the MoE input (src/lfm2-engine.js:251-252):
+ *   out[i] = w[i] * x[i] / sqrt(sum_j x[j]^2 / H + eps)   (binary64 math)
+ * weight_dev: H floats (_readWeightF32 of ffn_norm.weight) or NULL for 1.
+ * Device pointers; enqueued, not waited for; out may equal x. */
+int qq_rmsnorm_dev(qq_ctx *ctx, const float *x_dev, const float *weight_dev, float *out_dev, int T,
+                   int H, double eps);
+
 /* ---- measurement ------------------------------------------------------ */
 
 /* Record a HIP event pair around work enqueued between qq_timer_start and

@@ -20,6 +20,7 @@
 //                                      outputs are raw little-endian files)
 //   node moe_ref.js bench <seconds>    time single-token MoE-layer calls on a
 //                                      seeded LFM2-8B-A1B-shaped layer; prints JSON
+//   node moe_ref.js bench-matvec <s>   time matmulQ80xF32 on a 1024 -> 3072 weight
 
 const fs = require('fs');
 
@@ -282,6 +283,28 @@ function bench(seconds) {
                                           threads: 1, node: process.version }) + '\n');
 }
 
+// matmulQ80xF32 on a 1024 -> 3072 Q8_0 weight (the Qwen3-0.6B FFN up-proj
+// shape), one thread: matvecs per second.
+function benchMatvec(seconds) {
+    const IN = 1024, OUT = 3072;
+    const next = rng(777);
+    const meta = { buffer: q8Tensor(next, IN, OUT, 1), offset: 0, shape: [IN, OUT], type: 8 };
+    const x = new Float32Array(IN);
+    for (let i = 0; i < IN; i++) x[i] = ((next() & 0xffff) / 65536 - 0.5) * 3.4;
+    matmulQ80xF32(meta, x);   // warm-up (JIT)
+    let n = 0;
+    const t0 = process.hrtime.bigint();
+    let el = 0;
+    while (el < seconds) {
+        x[n & 1023] += 1e-3;
+        matmulQ80xF32(meta, x);
+        n++;
+        el = Number(process.hrtime.bigint() - t0) / 1e9;
+    }
+    process.stdout.write(JSON.stringify({ matvecs: n, seconds: el, matvecs_per_s: n / el,
+                                          threads: 1, node: process.version }) + '\n');
+}
+
 module.exports = { halfToNumber, matmulQ80xF32, matmulF32xF32, matmulGeneric, readWeightF32,
                    siluInPlace, mulInPlace, addVec, expertSlice, moEFFN };
 
@@ -289,8 +312,9 @@ if (require.main === module) {
     const cmd = process.argv[2];
     if (cmd === 'run') runJob(process.argv[3]);
     else if (cmd === 'bench') bench(Number(process.argv[3] || 10));
+    else if (cmd === 'bench-matvec') benchMatvec(Number(process.argv[3] || 10));
     else {
-        process.stderr.write('usage: node moe_ref.js run <job.json> | bench <seconds>\n');
+        process.stderr.write('usage: node moe_ref.js run <job.json> | bench <seconds> | bench-matvec <seconds>\n');
         process.exit(2);
     }
 }

@@ -56,6 +56,7 @@ static const char *const kKernelNames[K_COUNT] = {
     "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
     "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
     "cast_f16",         "mfma_gateup",    "mfma_down",      "stream_gateup", "stream_down",
+    "rmsnorm",
 };
 
 // Read and clear the device error word; non-zero means a bounded device-side
@@ -537,6 +538,17 @@ int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens)
     if (tokens < 0) return set_error(ctx, "set_mfma_min_tokens: %d < 0", tokens);
     ctx->mfma_min_tokens = tokens;
     return QQ_OK;
+}
+
+int qq_rmsnorm_dev(qq_ctx *ctx, const float *x_dev, const float *weight_dev, float *out_dev, int T,
+                   int H, double eps)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (T < 0 || H <= 0) return set_error(ctx, "rmsnorm: bad shape T=%d H=%d", T, H);
+    if (T == 0) return QQ_OK;
+    if (!x_dev || !out_dev) return set_error(ctx, "rmsnorm: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    return launch_rmsnorm(ctx, x_dev, weight_dev, out_dev, T, H, eps);
 }
 
 // ---- measurement ------------------------------------------------------------

@@ -108,6 +108,7 @@ enum KernelId {
     K_MFMA_DOWN,
     K_STREAM_GATEUP,
     K_STREAM_DOWN,
+    K_RMSNORM,
     K_COUNT
 };
 
@@ -180,6 +181,8 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
 size_t stream_work_bytes(const qq_moe *m, int T);
 int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                       const MaskBits &mask, const int32_t *idx, const double *w, char *work);
+int launch_rmsnorm(qq_ctx *ctx, const float *x, const float *w, float *out, int T, int H,
+                   double eps);
 int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                        const MaskBits &mask, const int32_t *idx, const double *w, char *work);
 

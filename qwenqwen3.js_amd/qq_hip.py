@@ -4,6 +4,10 @@ The product's host language is JavaScript (js/, napi/); this module is the
 second binding of the same C ABI, used by the parity tests and bench.py.
 It never computes anything itself: when libqqmoe.so is missing or the device
 cannot be opened it raises, there is no CPU fallback.
+
+torch bundles a HIP runtime under the same soname (libamdhip64.so.7) as the
+one libqqmoe.so links; the first one loaded serves the whole process.  A
+process that also uses torch imports torch before this module.
 """
 import ctypes
 import os
@@ -23,7 +27,7 @@ EXPORTS = (
     "qq_q8_0_upload", "qq_q8_0_upload_dev", "qq_tensor_release",
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
-    "qq_set_mfma_min_tokens", "qq_timer_start", "qq_timer_stop",
+    "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
 )
 
@@ -60,6 +64,7 @@ def load():
         "qq_moe_forward": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_dev": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
+        "qq_rmsnorm_dev": (I, [P, P, P, P, I, I, ctypes.c_double]),
         "qq_timer_start": (I, [P]),
         "qq_timer_stop": (I, [P, ctypes.POINTER(ctypes.c_float)]),
         "qq_profile_enable": (I, [P, I]),
@@ -111,6 +116,11 @@ class Context:
 
     def synchronize(self):
         self.check(self.L.qq_synchronize(self.h), "qq_synchronize")
+
+    def rmsnorm_dev(self, x_ptr, weight_ptr, out_ptr, T, H, eps=1e-5):
+        """out = rmsnorm(x) * weight (weight_ptr None: unit weight), device pointers."""
+        self.check(self.L.qq_rmsnorm_dev(self.h, x_ptr, weight_ptr, out_ptr, int(T), int(H),
+                                         float(eps)), "qq_rmsnorm_dev")
 
     def set_mfma_min_tokens(self, tokens):
         """Token batches of >= tokens rows use the fp16 MFMA path (0: never)."""
