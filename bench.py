@@ -17,9 +17,12 @@ independently seeded layers, rmsnorm + MoE per layer, 1 token resp. a
 over 80 weights).
 
 Inputs are generated on the device before the timed region.  Times come from
-HIP events on the stream the kernels run on; the per-kernel roofline figure
-comes from a second pass over the same steps in which every launch carries
-its own start/stop events (hipExtLaunchKernelGGL, qq_profile_*).
+HIP events on the stream the kernels run on.  `value` times the steps
+launched call by call; `graph_ms_per_step` times the same steps replayed from
+HIP graphs recorded through the library (one graph per distinct step,
+qq_capture_begin/end).  The per-kernel roofline figure comes from a third
+pass over the same steps in which every launch carries its own start/stop
+events (hipExtLaunchKernelGGL, qq_profile_*).
 
 Prints one JSON line.
 """
@@ -213,29 +216,45 @@ def copy_calibration(steps):
     return 0
 
 
-def timed(torch, ctx, stream, step, steps, warmup, launches_per_step):
-    """Warm up, time `steps` steps between two events on the library stream,
-    then run the same steps again with per-launch events.  Returns
-    (total_ms, {kernel: (ms_sum, count)})."""
+def _time_steps(torch, ctx, stream, run, steps, warmup):
     for i in range(warmup):
-        step(i)
+        run(i)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     for i in range(steps):
-        step(i)
+        run(i)
     ev1.record(stream)
     torch.cuda.synchronize()
     ctx.synchronize()          # raises if a device-side wait expired
-    total_ms = ev0.elapsed_time(ev1)
+    return ev0.elapsed_time(ev1)
+
+
+def timed(torch, ctx, stream, step, period, steps, warmup, launches_per_step):
+    """step(i) enqueues step i and depends only on i % period.
+
+    Times `steps` steps between two events on the library stream twice: with
+    every step's calls launched one by one, and with step i replayed from a
+    HIP graph recorded once per residue i % period (qq_capture_begin/end).
+    Then runs the steps once more, launched one by one with per-launch
+    events.  Returns (eager_ms, graph_ms, {kernel: (ms_sum, count)})."""
+    eager_ms = _time_steps(torch, ctx, stream, step, steps, warmup)
+    graphs = []
+    for r in range(period):
+        ctx.capture_begin()
+        step(r)
+        graphs.append(ctx.capture_end())
+    graph_ms = _time_steps(torch, ctx, stream, lambda i: graphs[i % period].launch(), steps, warmup)
+    for g in graphs:
+        g.release()
     ctx.profile_enable(steps * launches_per_step)
     for i in range(steps):
         step(i)
     prof = ctx.profile_read()
     ctx.profile_enable(0)
     ctx.synchronize()
-    return total_ms, prof
+    return eager_ms, graph_ms, prof
 
 
 def kernel_table(prof, T, n_exp, n_pairs):
@@ -309,14 +328,16 @@ def main():
     if kind == "matvec":
         n_w = 80                      # 80 x 3.36 MB > the 256 MB Infinity Cache
         keep = [make_matvec_weight(torch, ctx, 500 + i) for i in range(n_w)]
-        X = torch.randn((64, MV_IN), generator=gx, device="cuda", dtype=torch.float32)
-        Y = torch.empty((64, MV_OUT), device="cuda", dtype=torch.float32)
+        X = torch.randn((16, MV_IN), generator=gx, device="cuda", dtype=torch.float32)
+        Y = torch.empty((16, MV_OUT), device="cuda", dtype=torch.float32)
         torch.cuda.synchronize()
+        period = n_w
 
         def step(i):
-            keep[i % n_w].matvec_dev(X[i % 64].data_ptr(), Y[i % 64].data_ptr(), 1)
+            keep[i % n_w].matvec_dev(X[i % 16].data_ptr(), Y[i % 16].data_ptr(), 1)
 
-        total_ms, prof = timed(torch, ctx, stream, step, args.steps, args.warmup, 2)
+        total_ms, graph_ms, prof = timed(torch, ctx, stream, step, period, args.steps,
+                                         args.warmup, 2)
         ms_per_step = total_ms / args.steps
         kernels = kernel_table(prof, 1, 0, 0)
         dom, roofline = roofline_of(prof, kernels, args.workload)
@@ -351,7 +372,9 @@ def main():
                                                idx_ptr=idx[s, 0].data_ptr())
 
         calls = n_layers if stack else 1
-        total_ms, prof = timed(torch, ctx, stream, step, args.steps, args.warmup, 10 * calls)
+        period = S if stack else int(np.lcm(S, n_layers))
+        total_ms, graph_ms, prof = timed(torch, ctx, stream, step, period, args.steps,
+                                         args.warmup, 10 * calls)
         ms_per_step = total_ms / args.steps
         # distinct experts per layer call (weights each call must read at least once)
         used = idx.cpu().numpy()
@@ -391,6 +414,8 @@ def main():
         "config": config,
     }
     result.update(extra)
+    # the same steps replayed from HIP graphs
+    result["graph_ms_per_step"] = round(graph_ms / args.steps, 5)
     result["roofline"] = roofline
     result["kernels"] = kernels
     for obj in keep:

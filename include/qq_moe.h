@@ -42,6 +42,7 @@ extern "C" {
 typedef struct qq_ctx qq_ctx;
 typedef struct qq_tensor qq_tensor;
 typedef struct qq_moe qq_moe;
+typedef struct qq_graph qq_graph;
 
 /* ---- context --------------------------------------------------------- */
 
@@ -151,6 +152,24 @@ int qq_profile_enable(qq_ctx *ctx, int max_launches);
 int qq_profile_read(qq_ctx *ctx, float *ms_sum, int *count, int n);
 const char *qq_profile_name(int id);
 int qq_profile_kernel_count(void);
+
+/* ---- graphs ------------------------------------------------------------ */
+
+/* Record the device-pointer calls (qq_moe_forward_dev, qq_q8_0_matvec_dev,
+ * qq_rmsnorm_dev) made between qq_capture_begin and qq_capture_end on the
+ * context's stream into a HIP graph, and replay it with qq_graph_launch
+ * (enqueued, not waited for).  A replay runs the same kernels on the same
+ * pointers; every decode call draws a fresh router epoch on the device, so
+ * replays are independent.  While a capture is open, entry points that copy
+ * host memory, synchronise, allocate or profile fail with QQ_E_ARG, and a
+ * call whose scratch exceeds what the context already holds fails: run each
+ * call once before capturing it.  No reference counterpart: the reference
+ * records WebGPU command encoders per token (src/webgpu.js:1954-2034); this
+ * is the serving-loop form of the same idea. */
+int qq_capture_begin(qq_ctx *ctx);
+int qq_capture_end(qq_ctx *ctx, qq_graph **out);
+int qq_graph_launch(qq_ctx *ctx, const qq_graph *g);
+int qq_graph_release(qq_ctx *ctx, qq_graph *g);
 
 #ifdef __cplusplus
 }

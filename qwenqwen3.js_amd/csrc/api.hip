@@ -28,6 +28,9 @@ int check_hip(qq_ctx *ctx, hipError_t e, const char *what)
 int ensure_scratch(qq_ctx *ctx, size_t bytes)
 {
     if (bytes <= ctx->scratch_bytes) return QQ_OK;
+    if (ctx->capturing)
+        return set_error(ctx, "call needs %zu scratch bytes, the context holds %zu: run it once "
+                              "before capturing", bytes, ctx->scratch_bytes);
     // in-flight kernels may still use the old arena
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (ctx->scratch) (void)hipFree(ctx->scratch);
@@ -49,6 +52,15 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes)
     const size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
     QQ_HIP(ctx, hipHostMalloc(&ctx->pinned, sz, hipHostMallocDefault));
     ctx->pinned_bytes = sz;
+    return QQ_OK;
+}
+
+// Entry points that copy to or from the host, synchronise or allocate cannot
+// be recorded into a graph.
+static int no_capture(qq_ctx *ctx, const char *what)
+{
+    if (ctx && ctx->capturing)
+        return set_error(ctx, "%s cannot run while a graph capture is open", what);
     return QQ_OK;
 }
 
@@ -182,7 +194,9 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "hipEventCreate");
     }
     void *sync = nullptr;
-    const size_t sync_bytes = 2 * MAX_E * sizeof(uint64_t) + 256;
+    const size_t sync_bytes =
+        ((size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS) *
+            sizeof(uint64_t) + 256;
     if ((e = hipMalloc(&sync, sync_bytes)) != hipSuccess || (e = hipMemset(sync, 0, sync_bytes)) != hipSuccess) {
         if (sync) (void)hipFree(sync);
         (void)hipEventDestroy(ctx->ev0);
@@ -192,8 +206,10 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "sync area");
     }
     ctx->sync_slots = static_cast<uint64_t *>(sync);
-    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_slots + 2 * MAX_E);
-    ctx->epoch = 0;
+    ctx->sync_local = ctx->sync_slots + SYNC_REPLICAS * SYNC_REPLICA_WORDS;
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_local + SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS);
+    ctx->sync_epoch = ctx->sync_err + 16;
+    ctx->capturing = 0;
     *out = ctx;
     return QQ_OK;
 }
@@ -202,6 +218,11 @@ void qq_destroy(qq_ctx *ctx)
 {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
+    if (ctx->capturing) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(ctx->stream, &g);
+        if (g) (void)hipGraphDestroy(g);
+    }
     (void)hipStreamSynchronize(ctx->stream);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
@@ -218,6 +239,7 @@ const char *qq_last_error(const qq_ctx *ctx) { return ctx ? ctx->err : g_init_er
 int qq_set_stream(qq_ctx *ctx, void *hip_stream)
 {
     if (!ctx) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_set_stream")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->stream);
@@ -234,6 +256,7 @@ int qq_set_stream(qq_ctx *ctx, void *hip_stream)
 int qq_synchronize(qq_ctx *ctx)
 {
     if (!ctx) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_synchronize")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return check_device_error(ctx);
@@ -245,6 +268,7 @@ static int upload_common(qq_ctx *ctx, const void *src, bool src_on_device, size_
                          int in_dim, int out_dim, int n_mats, qq_tensor **out)
 {
     if (!ctx || !out || !src) return set_error(ctx, "qq_q8_0_upload: NULL argument");
+    if (int rc = no_capture(ctx, "qq_q8_0_upload")) return rc;
     *out = nullptr;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     qq_tensor *t = nullptr;
@@ -299,6 +323,7 @@ int qq_q8_0_upload_dev(qq_ctx *ctx, const void *gguf_bytes_dev, size_t nbytes, i
 int qq_tensor_release(qq_ctx *ctx, qq_tensor *t)
 {
     if (!t) return QQ_OK;
+    if (int rc = no_capture(ctx, "qq_tensor_release")) return rc;
     if (ctx) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
@@ -335,6 +360,7 @@ int qq_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, flo
     if (rc) return rc;
     if (rows == 0) return QQ_OK;
     if (!x || !y) return set_error(ctx, "matvec: NULL buffer");
+    if ((rc = no_capture(ctx, "qq_q8_0_matvec"))) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     const size_t xb = (size_t)rows * t->in_dim * 4, yb = (size_t)rows * t->out_dim * 4;
     if ((rc = ensure_scratch(ctx, align256(xb) + yb))) return rc;
@@ -407,6 +433,7 @@ int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const 
 int qq_moe_release(qq_ctx *ctx, qq_moe *m)
 {
     if (!m) return QQ_OK;
+    if (int rc = no_capture(ctx, "qq_moe_release")) return rc;
     if (ctx) {
         (void)hipSetDevice(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
@@ -507,6 +534,7 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     int rc = forward_check(ctx, m, T);
     if (rc || T == 0) return rc;
     if (!x || !hidden) return set_error(ctx, "moe_forward: NULL buffer");
+    if ((rc = no_capture(ctx, "qq_moe_forward"))) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     MaskBits mb;
     if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
@@ -563,6 +591,7 @@ int qq_timer_start(qq_ctx *ctx)
 int qq_timer_stop(qq_ctx *ctx, float *ms)
 {
     if (!ctx || !ms) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_timer_stop")) return rc;
     QQ_HIP(ctx, hipEventRecord(ctx->ev1, ctx->stream));
     QQ_HIP(ctx, hipEventSynchronize(ctx->ev1));
     QQ_HIP(ctx, hipEventElapsedTime(ms, ctx->ev0, ctx->ev1));
@@ -572,6 +601,7 @@ int qq_timer_stop(qq_ctx *ctx, float *ms)
 int qq_profile_enable(qq_ctx *ctx, int max_launches)
 {
     if (!ctx) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_profile_enable")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     ctx->prof_on = 0;
@@ -601,6 +631,7 @@ int qq_profile_enable(qq_ctx *ctx, int max_launches)
 int qq_profile_read(qq_ctx *ctx, float *ms_sum, int *count, int n)
 {
     if (!ctx || !ms_sum || !count) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_profile_read")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     for (int i = 0; i < n; i++) {
@@ -626,5 +657,75 @@ const char *qq_profile_name(int id)
 }
 
 int qq_profile_kernel_count(void) { return K_COUNT; }
+
+// ---- graphs -------------------------------------------------------------------
+
+struct qq_graph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+
+int qq_capture_begin(qq_ctx *ctx)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (ctx->capturing) return set_error(ctx, "qq_capture_begin: a capture is already open");
+    if (ctx->prof_on) return set_error(ctx, "qq_capture_begin: per-launch profiling is on");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    ctx->capturing = 1;
+    return QQ_OK;
+}
+
+int qq_capture_end(qq_ctx *ctx, qq_graph **out)
+{
+    if (!ctx || !out) return QQ_E_ARG;
+    *out = nullptr;
+    if (!ctx->capturing) return set_error(ctx, "qq_capture_end: no capture is open");
+    ctx->capturing = 0;
+    hipGraph_t g = nullptr;
+    hipError_t e = hipStreamEndCapture(ctx->stream, &g);
+    if (e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return check_hip(ctx, e, "hipStreamEndCapture (a call inside the capture failed?)");
+    }
+    qq_graph *qg = new (std::nothrow) qq_graph();
+    if (!qg) {
+        (void)hipGraphDestroy(g);
+        return set_error(ctx, "host allocation failed");
+    }
+    qg->graph = g;
+    e = hipGraphInstantiate(&qg->exec, g, nullptr, nullptr, 0);
+    if (e != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        delete qg;
+        return check_hip(ctx, e, "hipGraphInstantiate");
+    }
+    *out = qg;
+    return QQ_OK;
+}
+
+int qq_graph_launch(qq_ctx *ctx, const qq_graph *g)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!g) return set_error(ctx, "qq_graph_launch: NULL graph");
+    if (int rc = no_capture(ctx, "qq_graph_launch")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipGraphLaunch(g->exec, ctx->stream));
+    return QQ_OK;
+}
+
+int qq_graph_release(qq_ctx *ctx, qq_graph *g)
+{
+    if (!g) return QQ_OK;
+    if (int rc = no_capture(ctx, "qq_graph_release")) return rc;
+    if (ctx) {
+        (void)hipSetDevice(ctx->device);
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    (void)hipGraphExecDestroy(g->exec);
+    (void)hipGraphDestroy(g->graph);
+    delete g;
+    return QQ_OK;
+}
 
 }  // extern "C"

@@ -2,25 +2,34 @@
 //
 // Reference: Lfm2Engine._moEFFN, src/lfm2-engine.js:413-487, for one token.
 //
-// Launch 1 (moe_decode_experts): E router workgroups + K*NS expert-unit
-// workgroups (NS = ceil(F/32)).
-//   * router workgroup e: binary64 dot of x with router column e, fp32 logit,
-//     p_e = fp32 sigmoid (binary64 math) and selection score s_e = fp32(p_e +
-//     bias_e), published as two 64-bit words slot_s[e] = (epoch << 32) | s_e
-//     and slot_p[e] = (epoch << 32) | p_e with relaxed device-scope stores.
-//     Value and epoch travel together, so no fence (and no cache write-back or
-//     invalidate) is needed on either side, and every expert has its own
-//     words, so nothing is contended.
-//   * expert-unit workgroup (k, s): stages x in LDS (and, in waves 1-7, its
-//     3-level int8 decomposition), waits in wave 0 (bounded) until all E score
-//     slots carry this call's epoch, ranks the experts itself (rank of e =
-//     number of experts ordered before it by (score desc, index asc): the
-//     order of a stable descending sort; identical in every workgroup), then
-//     streams one F-slice of the rank-k expert: gate and up rows f in
-//     [32s, 32s+32) (2 x 32 rows x H), SwiGLU, and the matching down block
-//     column s (H rows x 32), writing the partial down product
+// Launch 1 (moe_decode_experts): 8 * ceil(E/8) router workgroups + K*NS
+// expert-unit workgroups (NS = ceil(F/32)).
+//   * router workgroup i (group g = i / 8): binary64 dots of x with router
+//     columns 8g .. 8g+7 (one per wave), fp32 logits, p_e = fp32 sigmoid (binary64 math) and
+//     selection scores s_e = fp32(p_e + bias_e), published as 64-bit words
+//     slot_s[e] = (epoch << 32) | s_e and slot_p[e] = (epoch << 32) | p_e.
+//     Workgroups are dealt to the 8 XCDs round robin, so the 8 copies of a
+//     group land on the 8 XCDs: each writes the table of its own XCD, which
+//     stays in that XCD's L2, and copy 0 also writes SYNC_REPLICAS
+//     device-coherent copies of the table.
+//   * expert-unit workgroup (k, s): stages x in LDS (and its 3-level int8
+//     decomposition), waits in wave 0 (bounded) until all E score
+//     slots carry this call's epoch -- polling its XCD's table through L2
+//     first, and the device-coherent copy u % SYNC_REPLICAS if that has not
+//     filled within DEC_LOCAL_TICKS (so progress never depends on where the
+//     dispatcher placed the router workgroups) -- ranks the experts itself
+//     (rank of e = number of experts ordered before it by (score desc, index
+//     asc): the order of a stable descending sort; identical in every
+//     workgroup), then streams one F-slice of the rank-k expert: gate and up
+//     rows f in [32s, 32s+32) (2 x 32 rows x H), SwiGLU, and the matching down
+//     block column s (H rows x 32), writing the partial down product
 //     partial[k][s][0..H).  Every weight load is issued before any
 //     arithmetic; dot products use v_dot4_i32_i8.
+//   Value and epoch travel together in one word, so no fence (and no cache
+//   write-back or invalidate) is needed on either side, and every expert has
+//   its own words, so nothing is contended.  The epoch is a device word that
+//   the combine launch of each call advances, so replaying a recorded graph
+//   of decode calls draws a fresh epoch every time.
 //   Workgroup (0, 0) also writes the routing outputs.
 // Launch 2 (moe_decode_combine): y_k = sum_s partial[k][s] in a fixed order,
 //   acc = fp32(acc + w_k * y_k) in rank order, hidden += acc.
@@ -36,6 +45,19 @@ namespace qq {
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * WAVE;
 constexpr uint64_t DEC_WAIT_TICKS = 5000000;   // 50 ms at the 100 MHz wall clock
+constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the XCD's own table, then the copies
+constexpr int RT_EPW = 8;                      // experts per router workgroup (one per wave)
+constexpr int RT_COPIES = 8;                   // router workgroups per expert group
+static_assert(RT_EPW == DEC_WAVES && RT_EPW * 8 == WAVE, "router lane layout");
+
+// XCD (accelerator complex die) this wave runs on.
+__device__ __forceinline__ uint32_t xcc_id()
+{
+    uint32_t x;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
+    return x;
+}
+
 
 struct DecodeArgs {
     const float *x;
@@ -45,6 +67,8 @@ struct DecodeArgs {
     const int8_t *rq;
     const __half *rd;
     int router_q8;
+    int router_vec4;      // F32 router, H % 4 == 0, x 16-byte aligned
+    int n_router;         // router workgroups: RT_COPIES * ceil(E / RT_EPW)
     const float *bias;
     const int8_t *gq;
     const __half *gd;
@@ -53,9 +77,13 @@ struct DecodeArgs {
     const int8_t *dq;
     const __half *dd;
     MaskBits mask;
-    uint32_t epoch;
-    uint64_t *slot_s;     // [E] (epoch << 32 | selection score bits), persist across calls
-    uint64_t *slot_p;     // [E] (epoch << 32 | sigmoid probability bits)
+    const uint32_t *epoch_word;   // this call's epoch is *epoch_word + 1
+    // Slot tables, persistent across calls, each [0, 64) epoch << 32 | selection
+    // score bits, [64, 128) epoch << 32 | probability bits:
+    //   slots: SYNC_REPLICAS device-coherent copies, SYNC_REPLICA_WORDS apart;
+    //   local: one table per XCD (SYNC_LOCAL_WORDS apart), kept in that XCD's L2
+    uint64_t *slots;
+    uint64_t *local;
     float *partial;       // [K][NS][H]
     int32_t *route_idx;   // [K]
     double *route_w;      // [K]
@@ -65,17 +93,27 @@ struct DecodeArgs {
     uint32_t *err;
 };
 
-// Bounded wait until lanes < E of `slots` carry `epoch`; returns the word.
-__device__ __forceinline__ uint64_t wait_slots(const uint64_t *slots, int E, uint32_t epoch, int lane,
-                                               int &ok)
+// Bounded wait until lanes < E of a slot table carry `epoch`; returns the
+// word.  Polls the XCD's own table (`loc`) while `use_loc` and for
+// DEC_LOCAL_TICKS, then the device-coherent copy `glob`; use_loc tells on
+// return which table answered.  Both are device-scope loads: for a line
+// written from the same XCD one is answered by that XCD's L2 in about
+// 0.2 us, against about 1-2 us for a line written from another XCD.
+__device__ __forceinline__ uint64_t wait_slots(const uint64_t *loc, const uint64_t *glob, int E,
+                                               uint32_t epoch, int lane, int &ok, bool &use_loc)
 {
     const uint64_t t0 = wall_clock64();
     uint64_t v;
     while (true) {
-        v = (lane < E) ? __hip_atomic_load(&slots[lane], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                       : ((uint64_t)epoch << 32);
+        if (lane < E)
+            v = __hip_atomic_load(use_loc ? &loc[lane] : &glob[lane], __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
+        else
+            v = (uint64_t)epoch << 32;
         if (__all((uint32_t)(v >> 32) == epoch)) break;
-        if (wall_clock64() - t0 > DEC_WAIT_TICKS) {
+        const uint64_t dt = wall_clock64() - t0;
+        if (dt > DEC_LOCAL_TICKS) use_loc = false;
+        if (dt > DEC_WAIT_TICKS) {
             ok = 0;
             break;
         }
@@ -99,135 +137,184 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     __shared__ float redg[DEC_WAVES][QK];
     __shared__ float redu[DEC_WAVES][QK];
     __shared__ double rsum[DEC_WAVES];
-    __shared__ int sh_e, sh_ok;
+    __shared__ int sh_ok;
+    __shared__ int rank_part[DEC_WAVES][WAVE];
     __shared__ int sh_rank_e[MAX_K];
     __shared__ float sh_rank_p[MAX_K];
     __shared__ __align__(16) float sh_score[WAVE];
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = threadIdx.x / WAVE;
+    // advanced by the previous call's combine kernel, so identical in every workgroup
+    const uint32_t epoch = a.epoch_word[0] + 1u;
 
-    if ((int)blockIdx.x < a.E) {
-        // ---- router workgroup: logit, sigmoid, score of expert e ----
-        const int e = blockIdx.x;
-        double acc = 0.0;
-        if (!a.router_q8 && (a.H & 3) == 0) {
-            const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-            const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32 + (size_t)e * a.H);
-            for (int k4 = threadIdx.x; k4 < a.H / 4; k4 += DEC_THREADS) {
-                const float4 xv = x4[k4], wv = w4[k4];
-                acc = fma((double)xv.x, (double)wv.x, acc);
-                acc = fma((double)xv.y, (double)wv.y, acc);
-                acc = fma((double)xv.z, (double)wv.z, acc);
-                acc = fma((double)xv.w, (double)wv.w, acc);
-            }
-        } else {
-            for (int k = threadIdx.x; k < a.H; k += DEC_THREADS) {
-                double wv;
-                if (a.router_q8) {
-                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e);
-                    wv = (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]);
-                } else {
-                    wv = (double)a.rf32[(size_t)e * a.H + k];
-                }
-                acc = fma((double)a.x[k], wv, acc);
-            }
-        }
-        acc = wave_sum(acc);
-        if (lane == 0) rsum[wave] = acc;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            double s = rsum[0];
+    const bool router = (int)blockIdx.x < a.n_router;
+    // router workgroup i: experts e0 .. e0+7 of group i / RT_COPIES, wave w takes e0 + w
+    const int e0 = (blockIdx.x / RT_COPIES) * RT_EPW;
+    const int H4 = a.H >> 2;
+    float4 rw[NBW];
+    if (router && a.router_vec4) {
+        // issued before x is staged; columns past H meet the zero padding of xl
+        const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32) + (size_t)min(e0 + wave, a.E - 1) * H4;
 #pragma unroll
-            for (int w = 1; w < DEC_WAVES; w++) s = s + rsum[w];
-            // lfm2-engine.js:420-431
-            const float logit = (float)s;
-            const float p = (float)(1.0 / (1.0 + exp(-(double)logit)));
-            const float sc = p + a.bias[e];
-            const uint64_t ep = (uint64_t)a.epoch << 32;
-            __hip_atomic_store(&a.slot_p[e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(&a.slot_s[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        return;
+        for (int i = 0; i < NBW; i++) rw[i] = w4[min(lane + WAVE * i, H4 - 1)];
     }
-
-    const int unit = blockIdx.x - a.E;
-    const int kslot = unit / a.NS;
-    const int s = unit - kslot * a.NS;
 
     // ---- x -> LDS ----
     for (int i = threadIdx.x; i < XN; i += DEC_THREADS) xl[i] = (i < a.H) ? a.x[i] : 0.0f;
     __syncthreads();
 
-    // ---- routing (lfm2-engine.js:433-447) in wave 0; waves 1-7 decompose x ----
-    if (wave == 0) {
-        int ok = 1;
-        const uint64_t v = wait_slots(a.slot_s, a.E, a.epoch, lane, ok);
-        const float sc = (lane < a.E) ? __uint_as_float((uint32_t)v) : -INFINITY;
-        sh_score[lane] = sc;
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        // rank: experts ordered before this one by (score desc, index asc);
-        // the rank-k expert is the k-th element of a stable descending sort.
-        // Branch-free over all 64 slots of sh_score (slots >= E hold -inf and
-        // never rank before a real expert).
-        int rank = 0;
+    if (router) {
+        // ---- router workgroup: logits, sigmoid, scores (lfm2-engine.js:418-431) ----
+        // Workgroup i runs on XCD i % 8 (the dispatcher deals workgroups to the
+        // XCDs round robin), so each XCD gets a full set of router workgroups
+        // and its table fills from its own L2.  Nothing depends on that for
+        // correctness: copy 0 of each group also fills the device-coherent
+        // tables, which waiters fall back to.
+        const int ew = min(e0 + wave, a.E - 1);
+        double acc = 0.0;
+        if (a.router_vec4) {
+            // four independent chains (one per float4 component), then joined
+            const float4 *x4 = reinterpret_cast<const float4 *>(xl);
+            double ax = 0.0, ay = 0.0, az = 0.0, aw = 0.0;
 #pragma unroll
-        for (int i0 = 0; i0 < WAVE; i0 += 4) {
-            const float4 q = *reinterpret_cast<const float4 *>(&sh_score[i0]);
-            const float qq[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const int i = i0 + u;
-                rank += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < lane));
+            for (int i = 0; i < NBW; i++) {
+                const float4 xv = x4[lane + WAVE * i];
+                ax = fma((double)xv.x, (double)rw[i].x, ax);
+                ay = fma((double)xv.y, (double)rw[i].y, ay);
+                az = fma((double)xv.z, (double)rw[i].z, az);
+                aw = fma((double)xv.w, (double)rw[i].w, aw);
+            }
+            acc = (ax + ay) + (az + aw);
+        } else {
+            for (int k = lane; k < a.H; k += WAVE) {
+                double wv;
+                if (a.router_q8) {
+                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, ew);
+                    wv = (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]);
+                } else {
+                    wv = (double)a.rf32[(size_t)ew * a.H + k];
+                }
+                acc = fma((double)xl[k], wv, acc);
             }
         }
-        if (lane >= a.E) rank = INT_MAX;
-        const uint64_t hit = __ballot(rank == kslot);
-        if (lane == 0) {
-            sh_e = hit ? (int)__builtin_ctzll(hit) : 0;
-            sh_ok = ok && hit != 0;
-            if (!ok) atomicOr(a.err, 1u);
-        }
-        if (unit == 0 && ok) {
-            // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457)
-            int okp = 1;
-            const uint64_t pv = wait_slots(a.slot_p, a.E, a.epoch, lane, okp);
-            if (!okp && lane == 0) atomicOr(a.err, 2u);
-            const float p = __uint_as_float((uint32_t)pv);
-            if (a.out_probs && lane < a.E) a.out_probs[lane] = p;
-            if (rank < a.K) {
-                sh_rank_e[rank] = lane;
-                sh_rank_p[rank] = p;
-            }
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-            if (lane == 0) {
-                double sumW = 1e-6;
-                for (int k = 0; k < a.K; k++) sumW = sumW + (double)sh_rank_p[k];
-                const double inv = 1.0 / sumW;
-                for (int k = 0; k < a.K; k++) {
-                    const double wk = (double)sh_rank_p[k] * inv;
-                    a.route_idx[k] = sh_rank_e[k];
-                    a.route_w[k] = wk;
-                    if (a.out_idx) a.out_idx[k] = sh_rank_e[k];
-                    if (a.out_w) a.out_w[k] = wk;
+        acc = wave_sum_dpp(acc);
+        if (lane == 0) rsum[wave] = acc;
+        __syncthreads();
+        if (wave == 0) {
+            // lane = 8 j + r: expert e0 + j; copies r and r + 8 of the device table
+            const int j = lane >> 3, r = lane & 7;
+            const int e = e0 + j;
+            if (e < a.E) {
+                // lfm2-engine.js:420-431
+                const float logit = (float)rsum[j];
+                const float p = (float)(1.0 / (1.0 + exp(-(double)logit)));
+                const float sc = p + a.bias[e];
+                const uint64_t ep = (uint64_t)epoch << 32;
+                if (r == 0) {
+                    uint64_t *tab = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
+                    __hip_atomic_store(&tab[WAVE + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    __hip_atomic_store(&tab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                }
+                if (blockIdx.x % RT_COPIES == 0) {
+#pragma unroll
+                    for (int c = r; c < SYNC_REPLICAS; c += 8) {
+                        uint64_t *tab = a.slots + (size_t)c * SYNC_REPLICA_WORDS;
+                        __hip_atomic_store(&tab[WAVE + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        __hip_atomic_store(&tab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
                 }
             }
         }
-    } else {
-        for (int c = threadIdx.x - WAVE; c < NHB; c += DEC_THREADS - WAVE) {
-            Lev3 L;
-            decompose16(&xl[16 * c], L);
-            xq1[c] = L.l1;
-            xq2[c] = L.l2;
-            xq3[c] = L.l3;
-            xsig[c] = L.sig;
+        return;
+    }
+
+    const int unit = blockIdx.x - a.n_router;
+    const uint64_t *tab = a.slots + (size_t)(unit % SYNC_REPLICAS) * SYNC_REPLICA_WORDS;
+    const uint64_t *loc = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
+    const int kslot = unit / a.NS;
+    const int s = unit - kslot * a.NS;
+
+    // ---- x -> three int8 levels, four lanes per 16-value chunk ----
+    // (whole waves take part: 4 * NHB is a multiple of 64)
+    for (int t = threadIdx.x; t < 4 * NHB; t += DEC_THREADS) {
+        const float4 v = reinterpret_cast<const float4 *>(xl)[t];   // x[4t .. 4t+3]
+        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        m = fmaxf(m, __shfl_xor(m, 1, WAVE));
+        m = fmaxf(m, __shfl_xor(m, 2, WAVE));
+        const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
+        uint32_t p1, p2, p3;
+        decompose4(v, inv, p1, p2, p3);
+        reinterpret_cast<uint32_t *>(xq1)[t] = p1;
+        reinterpret_cast<uint32_t *>(xq2)[t] = p2;
+        reinterpret_cast<uint32_t *>(xq3)[t] = p3;
+        if ((t & 3) == 0) xsig[t >> 2] = m * (1.0f / 127.0f);
+    }
+
+    // ---- routing (lfm2-engine.js:433-447) ----
+    bool use_loc = true;
+    if (wave == 0) {
+        int ok = 1;
+        const uint64_t v = wait_slots(loc, tab, a.E, epoch, lane, ok, use_loc);
+        sh_score[lane] = (lane < a.E) ? __uint_as_float((uint32_t)v) : -INFINITY;
+        if (lane == 0) {
+            sh_ok = ok;
+            if (!ok) atomicOr(a.err, 1u);
         }
     }
     __syncthreads();
     if (!sh_ok) return;
-    const int e = sh_e;
+    // rank of expert `lane`: experts ordered before it by (score desc, index
+    // asc), so the rank-k expert is the k-th element of a stable descending
+    // sort.  Wave w counts over slots 8w .. 8w+7 (slots >= E hold -inf and
+    // never rank before a real expert); every wave then sums the counts.
+    {
+        const float sc = sh_score[lane];
+        const float4 q0 = reinterpret_cast<const float4 *>(sh_score)[2 * wave];
+        const float4 q1 = reinterpret_cast<const float4 *>(sh_score)[2 * wave + 1];
+        const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+        int part = 0;
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = 8 * wave + u;
+            part += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < lane));
+        }
+        rank_part[wave][lane] = part;
+    }
+    __syncthreads();
+    int rank = 0;
+#pragma unroll
+    for (int w = 0; w < DEC_WAVES; w++) rank += rank_part[w][lane];
+    if (lane >= a.E) rank = INT_MAX;
+    const uint64_t hit = __ballot(rank == kslot);   // the same in every wave
+    if (!hit) return;
+    const int e = (int)__builtin_ctzll(hit);
+    if (unit == 0 && wave == 0) {
+        // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457)
+        int okp = 1;
+        const uint64_t pv = wait_slots(loc + WAVE, tab + WAVE, a.E, epoch, lane, okp, use_loc);
+        if (!okp && lane == 0) atomicOr(a.err, 2u);
+        const float p = __uint_as_float((uint32_t)pv);
+        if (a.out_probs && lane < a.E) a.out_probs[lane] = p;
+        if (rank < a.K) {
+            sh_rank_e[rank] = lane;
+            sh_rank_p[rank] = p;
+        }
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (lane == 0) {
+            double sumW = 1e-6;
+            for (int k = 0; k < a.K; k++) sumW = sumW + (double)sh_rank_p[k];
+            const double inv = 1.0 / sumW;
+            for (int k = 0; k < a.K; k++) {
+                const double wk = (double)sh_rank_p[k] * inv;
+                a.route_idx[k] = sh_rank_e[k];
+                a.route_w[k] = wk;
+                if (a.out_idx) a.out_idx[k] = sh_rank_e[k];
+                if (a.out_w) a.out_w[k] = wk;
+            }
+        }
+    }
     if (mask_has(a.mask, e)) return;   // the combine skips masked ranks
 
     const int h = lane & 1;
@@ -336,8 +423,11 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
 template <int NSP>
 __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
     const float *__restrict__ partial, int H, int NS, int K, const int32_t *__restrict__ route_idx,
-    const double *__restrict__ route_w, MaskBits mask, float *__restrict__ hidden)
+    const double *__restrict__ route_w, MaskBits mask, float *__restrict__ hidden,
+    uint32_t *__restrict__ epoch_word)
 {
+    // the experts kernel of this call has finished: the next call takes a new epoch
+    if (blockIdx.x == 0 && threadIdx.x == 0) epoch_word[0] = epoch_word[0] + 1u;
     __shared__ float red[MAX_K][8][32];
     const int jl = threadIdx.x & 31;
     const int q = threadIdx.x >> 5;
@@ -421,10 +511,11 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.dq = m->down->qs;
     a.dd = m->down->d;
     a.mask = mask;
-    if (++ctx->epoch == 0) ctx->epoch = 1;
-    a.epoch = ctx->epoch;
-    a.slot_s = ctx->sync_slots;
-    a.slot_p = ctx->sync_slots + MAX_E;
+    a.slots = ctx->sync_slots;
+    a.local = ctx->sync_local;
+    a.router_vec4 = !a.router_q8 && (m->H & 3) == 0;
+    a.n_router = RT_COPIES * ((m->E + RT_EPW - 1) / RT_EPW);
+    a.epoch_word = ctx->sync_epoch;
     a.err = ctx->sync_err;
     const size_t part_b = ((size_t)m->K * a.NS * m->H * 4 + 255) & ~(size_t)255;
     a.partial = reinterpret_cast<float *>(work);
@@ -435,7 +526,7 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.out_probs = out_probs;
 
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
-    const dim3 grid(m->E + m->K * a.NS);
+    const dim3 grid(a.n_router + m->K * a.NS);
     prof_begin(ctx, K_DECODE_EXPERTS);
     if (nbw <= 1) launch_experts<1>(ctx, a, grid);
     else if (nbw <= 2) launch_experts<2>(ctx, a, grid);
@@ -448,7 +539,7 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     const dim3 cgrid((m->H + 31) / 32);
 #define QQ_CB(N)                                                                                 \
     QQ_LAUNCH(ctx, moe_decode_combine_kernel<N>, cgrid, dim3(256), 0, a.partial, \
-                       m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden)
+                       m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden, ctx->sync_epoch)
     prof_begin(ctx, K_DECODE_COMBINE);
     if (nsp <= 1) QQ_CB(1);
     else if (nsp <= 2) QQ_CB(2);

@@ -22,6 +22,38 @@ __device__ __forceinline__ double wave_sum(double v)
     return v;
 }
 
+// v from the lane picked by the DPP control CTRL (a permutation within each
+// row of 16 lanes), both halves moved by the data-parallel-primitive path
+// rather than through LDS.
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v)
+{
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const int lo = __builtin_amdgcn_mov_dpp((int)(uint32_t)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_mov_dpp((int)(uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __longlong_as_double((long long)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo));
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int l)
+{
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// Sum over the 64 lanes of a wavefront (all lanes active), the same value in
+// every lane: quads by quad permutations, rows of 16 by row rotations, then
+// the four row sums in row order.
+__device__ __forceinline__ double wave_sum_dpp(double v)
+{
+    v += dpp_f64<0xB1>(v);    // quad_perm [1,0,3,2]
+    v += dpp_f64<0x4E>(v);    // quad_perm [2,3,0,1]
+    v += dpp_f64<0x124>(v);   // row_ror:4
+    v += dpp_f64<0x128>(v);   // row_ror:8
+    return ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
+}
+
 // 16 int8 weights (one int4 = 4 dwords) against 16 fp32 activations.
 // Each dword is flipped to offset binary (q + 128) so that every byte
 // converts with a single v_cvt_f32_ubyteN; the constant 128 * sum(x) is
@@ -112,16 +144,15 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
            ((uint32_t)(d & 0xff) << 24);
 }
 
-__device__ __forceinline__ void decompose16(const float *v, Lev3 &o)
+// Three levels of four values, packed as they are formed (few live registers).
+__device__ __forceinline__ void decompose4(const float4 v, float inv, uint32_t &p1, uint32_t &p2,
+                                           uint32_t &p3)
 {
-    float m = 0.0f;
+    const float vv[4] = {v.x, v.y, v.z, v.w};
+    int q1[4], q2[4], q3[4];
 #pragma unroll
-    for (int i = 0; i < 16; i++) m = fmaxf(m, fabsf(v[i]));
-    int q1[16], q2[16], q3[16];
-    const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const float t = v[i] * inv;
+    for (int i = 0; i < 4; i++) {
+        const float t = vv[i] * inv;
         const float a1 = fminf(fmaxf(rintf(t), -127.0f), 127.0f);
         const float t2 = (t - a1) * 254.0f;
         const float a2 = fminf(fmaxf(rintf(t2), -127.0f), 127.0f);
@@ -131,13 +162,29 @@ __device__ __forceinline__ void decompose16(const float *v, Lev3 &o)
         q2[i] = (int)a2;
         q3[i] = (int)a3;
     }
+    p1 = pack4_i8(q1[0], q1[1], q1[2], q1[3]);
+    p2 = pack4_i8(q2[0], q2[1], q2[2], q2[3]);
+    p3 = pack4_i8(q3[0], q3[1], q3[2], q3[3]);
+}
+
+// v: 16 values, 16-byte aligned.
+__device__ __forceinline__ void decompose16(const float *v, Lev3 &o)
+{
+    const float4 *v4 = reinterpret_cast<const float4 *>(v);
+    float m = 0.0f;
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const float4 q = v4[g];
+        m = fmaxf(m, fmaxf(fmaxf(fabsf(q.x), fabsf(q.y)), fmaxf(fabsf(q.z), fabsf(q.w))));
+    }
+    const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
     o.sig = m * (1.0f / 127.0f);
-    o.l1 = make_int4((int)pack4_i8(q1[0], q1[1], q1[2], q1[3]), (int)pack4_i8(q1[4], q1[5], q1[6], q1[7]),
-                     (int)pack4_i8(q1[8], q1[9], q1[10], q1[11]), (int)pack4_i8(q1[12], q1[13], q1[14], q1[15]));
-    o.l2 = make_int4((int)pack4_i8(q2[0], q2[1], q2[2], q2[3]), (int)pack4_i8(q2[4], q2[5], q2[6], q2[7]),
-                     (int)pack4_i8(q2[8], q2[9], q2[10], q2[11]), (int)pack4_i8(q2[12], q2[13], q2[14], q2[15]));
-    o.l3 = make_int4((int)pack4_i8(q3[0], q3[1], q3[2], q3[3]), (int)pack4_i8(q3[4], q3[5], q3[6], q3[7]),
-                     (int)pack4_i8(q3[8], q3[9], q3[10], q3[11]), (int)pack4_i8(q3[12], q3[13], q3[14], q3[15]));
+    uint32_t a[4], b[4], c[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) decompose4(v4[g], inv, a[g], b[g], c[g]);
+    o.l1 = make_int4((int)a[0], (int)a[1], (int)a[2], (int)a[3]);
+    o.l2 = make_int4((int)b[0], (int)b[1], (int)b[2], (int)b[3]);
+    o.l3 = make_int4((int)c[0], (int)c[1], (int)c[2], (int)c[3]);
 }
 
 __device__ __forceinline__ int sdot16(const int4 q, const int4 a)

@@ -19,6 +19,13 @@ constexpr int QBLK = 34;      // bytes per GGUF Q8_0 block {fp16 d, int8 qs[32]}
 constexpr int WAVE = 64;      // CDNA wavefront width
 constexpr int MAX_E = 256;    // experts supported by the router and the mask bitset
 constexpr int MAX_K = 16;     // experts used per token
+// Decode router exchange: copies of the per-expert slot table, each
+// 4352 B apart so that the copies start in different DRAM channels.
+constexpr int SYNC_REPLICAS = 16;
+constexpr int SYNC_REPLICA_WORDS = 544;
+// ... and one table per XCD (XCC_ID < 16), 1 KiB apart.
+constexpr int SYNC_LOCAL_TABLES = 16;
+constexpr int SYNC_LOCAL_WORDS = 128;
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
 struct MaskBits {
@@ -74,11 +81,17 @@ struct qq_ctx {
     // timing events of the bench entry points
     hipEvent_t ev0, ev1;
     // device words shared by the kernels of this context: the decode router's
-    // per-expert (epoch, score) and (epoch, probability) slots (2*MAX_E) and
-    // the error word
+    // SYNC_REPLICAS device-coherent tables and SYNC_LOCAL_TABLES per-XCD
+    // tables of per-expert (epoch, score) and (epoch, probability) slots,
+    // then the error word and the decode epoch (advanced
+    // on the device by every decode combine, so a replayed graph of decode
+    // launches sees a fresh epoch each time)
     uint64_t *sync_slots;
+    uint64_t *sync_local;
     uint32_t *sync_err;
-    uint32_t epoch;
+    uint32_t *sync_epoch;
+    // a graph capture on `stream` is open (qq_capture_begin)
+    int capturing;
     // token batches of at least this many rows take the fp16 MFMA path (0: never)
     int mfma_min_tokens;
     // per-kernel event pairs (qq_profile_*): pool of 2*prof_cap events

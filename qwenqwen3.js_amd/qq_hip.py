@@ -29,6 +29,7 @@ EXPORTS = (
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
     "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
+    "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
 )
 
 _lib = None
@@ -71,6 +72,10 @@ def load():
         "qq_profile_read": (I, [P, P, P, I]),
         "qq_profile_name": (ctypes.c_char_p, [I]),
         "qq_profile_kernel_count": (I, []),
+        "qq_capture_begin": (I, [P]),
+        "qq_capture_end": (I, [P, PP]),
+        "qq_graph_launch": (I, [P, P]),
+        "qq_graph_release": (I, [P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -82,6 +87,22 @@ def load():
 
 def _ptr(a):
     return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Graph:
+    """A recorded sequence of device-pointer calls (qq_capture_end)."""
+
+    def __init__(self, ctx, h):
+        self.ctx = ctx
+        self.h = h
+
+    def launch(self):
+        self.ctx.check(self.ctx.L.qq_graph_launch(self.ctx.h, self.h), "qq_graph_launch")
+
+    def release(self):
+        if self.h:
+            self.ctx.check(self.ctx.L.qq_graph_release(self.ctx.h, self.h), "qq_graph_release")
+            self.h = None
 
 
 class Context:
@@ -116,6 +137,16 @@ class Context:
 
     def synchronize(self):
         self.check(self.L.qq_synchronize(self.h), "qq_synchronize")
+
+    def capture_begin(self):
+        """Start recording the device-pointer calls on this context into a graph."""
+        self.check(self.L.qq_capture_begin(self.h), "qq_capture_begin")
+
+    def capture_end(self):
+        """Close the recording; returns a Graph to replay."""
+        g = ctypes.c_void_p()
+        self.check(self.L.qq_capture_end(self.h, ctypes.byref(g)), "qq_capture_end")
+        return Graph(self, g)
 
     def rmsnorm_dev(self, x_ptr, weight_ptr, out_ptr, T, H, eps=1e-5):
         """out = rmsnorm(x) * weight (weight_ptr None: unit weight), device pointers."""
