@@ -353,18 +353,16 @@ def main():
         S = 64 if T == 1 else 2
         X = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
         HID = torch.randn((S, T, H), generator=gx, device="cuda", dtype=torch.float32)
-        XN = torch.empty((T, H), device="cuda", dtype=torch.float32)
         idx = torch.empty((S, n_layers if stack else 1, T, K), dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
 
         if stack:
             def step(i):
-                # one token (or chunk) through every layer: x = rmsnorm(hidden), hidden += MoE(x)
+                # one token (or chunk) through every layer: hidden += MoE(rmsnorm(hidden))
                 s = i % S
                 for li, layer in enumerate(keep):
-                    ctx.rmsnorm_dev(HID[s].data_ptr(), None, XN.data_ptr(), T, H, 1e-5)
-                    layer.forward_dev(XN.data_ptr(), HID[s].data_ptr(), T,
-                                      idx_ptr=idx[s, li].data_ptr())
+                    layer.forward_norm_dev(HID[s].data_ptr(), T, eps=1e-5,
+                                           idx_ptr=idx[s, li].data_ptr())
         else:
             def step(i):
                 s = i % S

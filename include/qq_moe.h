@@ -117,6 +117,19 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
                        int T, const uint8_t *mask, int32_t *idx_dev, double *w_dev,
                        float *probs_dev);
 
+/* The FFN sub-block of an MoE layer (src/lfm2-engine.js:250-257): the
+ * ffn_norm RMSNorm of the residual row (src/tensor.js:103-114), then the MoE
+ * block on it:
+ *   x = rmsnorm(hidden) * norm_w     (norm_w_dev NULL: unit weight)
+ *   hidden += MoE(x)
+ * for T rows, with the same routing outputs as qq_moe_forward_dev.  A
+ * single row is normalised inside the decode kernel (no separate launch);
+ * the result equals qq_rmsnorm_dev followed by qq_moe_forward_dev bit for
+ * bit.  Device pointers; enqueued, not waited for. */
+int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev,
+                            const float *norm_w_dev, double eps, int T, const uint8_t *mask,
+                            int32_t *idx_dev, double *w_dev, float *probs_dev);
+
 /* Token batches (T > 1) of at least `tokens` rows per chunk run their expert
  * products as fp16 MFMA grouped GEMMs (fp16 activations and dequantised
  * weights, fp32 accumulation: ~1e-3 relative L2 on the layer output);

@@ -528,6 +528,32 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
     return forward_impl(ctx, m, x_dev, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, 0);
 }
 
+int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev, const float *norm_w_dev,
+                            double eps, int T, const uint8_t *mask, int32_t *idx_dev,
+                            double *w_dev, float *probs_dev)
+{
+    int rc = forward_check(ctx, m, T);
+    if (rc || T == 0) return rc;
+    if (!hidden_dev) return set_error(ctx, "moe_forward_norm: NULL buffer");
+    if (!(eps >= 0.0)) return set_error(ctx, "moe_forward_norm: eps %g", eps);
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
+    const NormArgs norm{norm_w_dev, eps};
+    if (decode_supported(m, T)) {
+        // every workgroup of the decode kernel normalises the row itself
+        if ((rc = ensure_scratch(ctx, forward_scratch(ctx, m, T)))) return rc;
+        return launch_moe_decode(ctx, m, hidden_dev, hidden_dev, mb, idx_dev, w_dev, probs_dev,
+                                 static_cast<char *>(ctx->scratch), &norm);
+    }
+    // x = rmsnorm(hidden) at the start of the scratch, then the forward
+    const size_t xb = align256((size_t)T * m->H * 4);
+    if ((rc = ensure_scratch(ctx, xb + forward_scratch(ctx, m, T)))) return rc;
+    float *x = static_cast<float *>(ctx->scratch);
+    if ((rc = launch_rmsnorm(ctx, hidden_dev, norm_w_dev, x, T, m->H, eps))) return rc;
+    return forward_impl(ctx, m, x, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, xb);
+}
+
 int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
                    const uint8_t *mask, int32_t *idx, double *w, float *probs)
 {

@@ -60,7 +60,10 @@ __device__ __forceinline__ uint32_t xcc_id()
 
 
 struct DecodeArgs {
-    const float *x;
+    const float *x;       // the MoE input, or the residual row when norm
+    int norm;             // x = rmsnorm(x) * norm_w is formed in every workgroup
+    const float *norm_w;  // NULL: unit weight
+    double eps;
     int H, F, E, K;
     int nbH, nbF, NS;
     const float *rf32;
@@ -160,8 +163,36 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
         for (int i = 0; i < NBW; i++) rw[i] = w4[min(lane + WAVE * i, H4 - 1)];
     }
 
-    // ---- x -> LDS ----
-    for (int i = threadIdx.x; i < XN; i += DEC_THREADS) xl[i] = (i < a.H) ? a.x[i] : 0.0f;
+    // ---- x -> LDS (ffn_norm first when asked: lfm2-engine.js:251-252) ----
+    {
+        static_assert(DEC_THREADS == NORM_THREADS, "the decode kernel normalises like rmsnorm_kernel");
+        constexpr int XPT = (XN + DEC_THREADS - 1) / DEC_THREADS;
+        float xv[XPT];
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int k = threadIdx.x + DEC_THREADS * i;
+            xv[i] = (k < a.H) ? a.x[k] : 0.0f;
+        }
+        if (a.norm) {
+            float wv[XPT];
+#pragma unroll
+            for (int i = 0; i < XPT; i++) {
+                const int k = threadIdx.x + DEC_THREADS * i;
+                wv[i] = (a.norm_w && k < a.H) ? a.norm_w[k] : 1.0f;
+            }
+            double ss = 0.0;   // padding adds exact zeros
+#pragma unroll
+            for (int i = 0; i < XPT; i++) ss = fma((double)xv[i], (double)xv[i], ss);
+            const double inv = rms_inv(block_sum_f64<DEC_WAVES>(ss, rsum), a.H, a.eps);
+#pragma unroll
+            for (int i = 0; i < XPT; i++) xv[i] = (float)((double)wv[i] * (double)xv[i] * inv);
+        }
+#pragma unroll
+        for (int i = 0; i < XPT; i++) {
+            const int k = threadIdx.x + DEC_THREADS * i;
+            if (k < XN) xl[k] = xv[i];
+        }
+    }
     __syncthreads();
 
     if (router) {
@@ -488,10 +519,13 @@ static void launch_experts(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      char *work)
+                      char *work, const NormArgs *norm)
 {
     DecodeArgs a;
     a.x = x;
+    a.norm = norm != nullptr;
+    a.norm_w = norm ? norm->w : nullptr;
+    a.eps = norm ? norm->eps : 0.0;
     a.H = m->H;
     a.F = m->F;
     a.E = m->E;

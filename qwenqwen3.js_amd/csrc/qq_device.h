@@ -54,6 +54,30 @@ __device__ __forceinline__ double wave_sum_dpp(double v)
     return ((readlane_f64(v, 0) + readlane_f64(v, 16)) + readlane_f64(v, 32)) + readlane_f64(v, 48);
 }
 
+// Sum over a block of NW wavefronts: waves by wave_sum_dpp, then the NW wave
+// sums in wave order (red: NW doubles of LDS).  Contains a __syncthreads.
+template <int NW>
+__device__ __forceinline__ double block_sum_f64(double v, double *red)
+{
+    v = wave_sum_dpp(v);
+    if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    double s = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) s = s + red[w];
+    return s;
+}
+
+// RMSNorm of one row (src/tensor.js:103-114) by a block of NORM_THREADS:
+// thread t sums x[k]^2 for k = t, t + NORM_THREADS, ... in order (exact
+// squares, binary64), block_sum_f64 joins the threads; every kernel that
+// normalises a row goes through this, so they agree bit for bit.
+constexpr int NORM_THREADS = 512;
+__device__ __forceinline__ double rms_inv(double sumsq, int H, double eps)
+{
+    return 1.0 / sqrt(sumsq / (double)H + eps);
+}
+
 // 16 int8 weights (one int4 = 4 dwords) against 16 fp32 activations.
 // Each dword is flipped to offset binary (q + 128) so that every byte
 // converts with a single v_cvt_f32_ubyteN; the constant 128 * sum(x) is

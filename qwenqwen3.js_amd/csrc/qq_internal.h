@@ -165,9 +165,15 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
                        int32_t *idx, double *w, float *probs);
 bool decode_supported(const qq_moe *m, int T);
 size_t decode_work_bytes(const qq_moe *m);
+// ffn_norm folded into a forward: x = rmsnorm(x) * w (w NULL: unit weight).
+struct NormArgs {
+    const float *w;
+    double eps;
+};
+
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      char *work);
+                      char *work, const NormArgs *norm = nullptr);
 size_t grouped_work_bytes(const qq_moe *m, int T);
 // Optional row-tile table written by the dispatch kernel: tile i covers slots
 // [m0[i], m0[i] + bm) of expert e[i] (clipped to the expert's count); *n = tiles.

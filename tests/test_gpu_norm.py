@@ -38,3 +38,66 @@ def test_rmsnorm_matches_oracle(T, H):
     assert (ulp == 0).mean() > 0.99
     refw = (ref.astype(np.float64) * w.astype(np.float64))
     assert np.max(np.abs(gw - refw) / np.maximum(np.abs(refw), 1e-30)) < 3e-7
+
+
+@pytest.mark.parametrize("T,mfma,weighted", [(1, 0, False), (1, 0, True), (64, 0, True),
+                                             (96, 64, False)])
+def test_fused_norm_moe_matches_two_calls(T, mfma, weighted):
+    """qq_moe_forward_norm_dev == qq_rmsnorm_dev then qq_moe_forward_dev, bit for bit
+    (a single row is normalised inside the decode kernel)."""
+    import torch
+    import synth
+    from _util import upload_layer
+    print("fused norm+moe", T, mfma, weighted, flush=True)
+    ctx = gpu_context()
+    ctx.set_mfma_min_tokens(mfma)
+    L = synth.moe_layer(41, H=512, F=256, E=16, K=4)
+    m = upload_layer(ctx, L)
+    try:
+        rng = np.random.default_rng(T + 7)
+        h0 = (rng.standard_normal((T, 512)) * 2).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, 512).astype(np.float32) if weighted else None
+        dh0 = torch.from_numpy(h0).cuda()
+        dw = torch.from_numpy(w).cuda() if weighted else None
+        wp = dw.data_ptr() if weighted else None
+        idx_a = torch.empty((T, 4), dtype=torch.int32, device="cuda")
+        idx_b = torch.empty_like(idx_a)
+        ha, hb = dh0.clone(), dh0.clone()
+        xn = torch.empty_like(dh0)
+        torch.cuda.synchronize()
+        m.forward_norm_dev(ha.data_ptr(), T, norm_w_ptr=wp, eps=1e-5, idx_ptr=idx_a.data_ptr())
+        ctx.rmsnorm_dev(hb.data_ptr(), wp, xn.data_ptr(), T, 512, 1e-5)
+        m.forward_dev(xn.data_ptr(), hb.data_ptr(), T, idx_ptr=idx_b.data_ptr())
+        ctx.synchronize()
+        assert np.array_equal(idx_a.cpu().numpy(), idx_b.cpu().numpy())
+        assert np.array_equal(ha.cpu().numpy(), hb.cpu().numpy())
+    finally:
+        ctx.set_mfma_min_tokens(512)
+        m.release()
+
+
+def test_fused_norm_moe_decode_against_oracle():
+    """One token through ffn_norm (unit weight) + the MoE block at the LFM2-8B-A1B shape."""
+    import torch
+    import synth
+    from _util import full_layer, upload_layer, rel_l2, moe_delta
+    print("fused norm+moe oracle", flush=True)
+    ctx = gpu_context()
+    L = full_layer(7)
+    m = upload_layer(ctx, L)
+    try:
+        _, h0 = synth.activations(17, 1, 2048)
+        x = oracle.rmsnorm_unit(h0[0], 1e-5)[None, :]
+        ref_h, ref_idx, ref_w, _ = oracle.moe_ffn(L, x, h0)
+        dh = torch.from_numpy(h0).cuda()
+        idx = torch.empty((1, 4), dtype=torch.int32, device="cuda")
+        wts = torch.empty((1, 4), dtype=torch.float64, device="cuda")
+        torch.cuda.synchronize()
+        m.forward_norm_dev(dh.data_ptr(), 1, eps=1e-5, idx_ptr=idx.data_ptr(), w_ptr=wts.data_ptr())
+        ctx.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), ref_idx)
+        assert np.array_equal(wts.cpu().numpy(), ref_w)
+        got = dh.cpu().numpy()
+        assert rel_l2(moe_delta(got, h0), moe_delta(ref_h, h0)) < 1e-4
+    finally:
+        m.release()
