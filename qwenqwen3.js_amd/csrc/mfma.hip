@@ -254,7 +254,8 @@ __global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_gateup_kernel(MfmaArgs
                 const int row = wm * 64 + i * 16 + rq + r;
                 if (row < n && ff < a.F) {
                     const float g = acc[i][j][r], u = acc[i][j + 2][r];
-                    const float v = g / (1.0f + __expf(-g)) * u;
+                    // hardware exp and reciprocal (~1 ulp each), far inside the fp16 rounding
+                    const float v = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     a.act[(size_t)(slot0 + row) * a.F + ff] = (_Float16)v;
                 }
             }

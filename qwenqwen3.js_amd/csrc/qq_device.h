@@ -78,6 +78,34 @@ __device__ __forceinline__ double rms_inv(double sumsq, int H, double eps)
     return 1.0 / sqrt(sumsq / (double)H + eps);
 }
 
+// LDS byte address of a __shared__ object.
+__device__ __forceinline__ uint32_t lds_u32(const void *p)
+{
+    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
+}
+
+// global_load_lds: each lane copies `size` bytes from its own address to
+// LDS (M0 + lane * size); M0 is set right before (one wait state after an
+// SALU write to M0).
+__device__ __forceinline__ void dma16(const void *g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
+}
+
+__device__ __forceinline__ void dma4(const void *g, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
+                 :: "v"(g), "s"(lds) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vm()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
+}
+
 // 16 int8 weights (one int4 = 4 dwords) against 16 fp32 activations.
 // Each dword is flipped to offset binary (q + 128) so that every byte
 // converts with a single v_cvt_f32_ubyteN; the constant 128 * sum(x) is

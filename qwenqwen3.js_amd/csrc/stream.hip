@@ -106,33 +106,6 @@ struct StLayout {
     static constexpr int NDMA = 2 * MF + 4 + 1;          // copies per stage
 };
 
-__device__ __forceinline__ uint32_t lds_u32(const void *p)
-{
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char *)p;
-}
-
-// global_load_lds: each lane copies `size` bytes from its own address to
-// LDS (M0 + lane * size); M0 is set right before (one wait state after an
-// SALU write to M0).
-__device__ __forceinline__ void dma16(const void *g, uint32_t lds)
-{
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(g), "s"(lds) : "memory");
-}
-
-__device__ __forceinline__ void dma4(const void *g, uint32_t lds)
-{
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-                 :: "v"(g), "s"(lds) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vm()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(N) : "memory");
-}
-
 template <int MF>
 struct StSrc {
     const char *abase;          // activation rows (bytes)
