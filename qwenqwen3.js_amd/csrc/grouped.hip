@@ -6,8 +6,8 @@
 // (token, rank) pairs are grouped by expert so that each expert's weights are
 // read once per batch:
 //   dispatch   counts[e], offsets[e] (exclusive scan), perm[slot] = pair and
-//              inv[pair] = slot; slots of one expert are in token order
-//              (stable); pairs whose expert is masked get inv = -1.
+//              inv[pair] = slot (order within an expert unspecified); pairs
+//              whose expert is masked get inv = -1.
 //   gate/up    grid (E, ceil(F/32)): the workgroup keeps its 32 gate and up
 //              rows in registers and runs every slot of its expert against
 //              them, MT tokens at a time from LDS -> g[slot][F].
@@ -28,10 +28,12 @@ struct GrMT {
 };
 
 // ---------------------------------------------------------------------------
-// Dispatch: one workgroup of NT threads (NT a multiple of 64), thread t owns
-// pairs [t*C, t*C + C).  LDS cnt[E][NT]: per-thread expert counts, turned
-// into per-thread exclusive offsets by one wave-level scan per expert.
-// Slots of an expert are therefore in pair order (token order).
+// Dispatch: one workgroup of NT threads; pair p is handled by thread p % NT.
+// Pass 1 counts pairs per expert with LDS atomics, one wave scans the counts
+// into offsets (and cuts the row tiles), pass 2 hands out slots with LDS
+// atomics.  The order of slots within an expert is therefore unspecified;
+// nothing depends on it: every slot row is computed on its own and the
+// combine reads slots through inv, so results are the same bit for bit.
 // ---------------------------------------------------------------------------
 // Exclusive scan over the 64 lanes; *total = sum of all lanes.
 __device__ __forceinline__ int wave_excl_scan(int v, int *total)
@@ -47,46 +49,44 @@ __device__ __forceinline__ int wave_excl_scan(int v, int *total)
     return incl - v;
 }
 
-__global__ void moe_dispatch_kernel(const int32_t *__restrict__ idx, int P, int E, MaskBits mask,
-                                    int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
-                                    int32_t *__restrict__ perm, int32_t *__restrict__ inv,
-                                    DispatchTiles tiles)
+constexpr int DISP_THREADS = 1024;
+constexpr int DISP_ROUND = 16;   // pair loads in flight per thread
+
+__global__ __launch_bounds__(DISP_THREADS) void moe_dispatch_kernel(
+    const int32_t *__restrict__ idx, int P, int E, MaskBits mask, int32_t *__restrict__ counts,
+    int32_t *__restrict__ offsets, int32_t *__restrict__ perm, int32_t *__restrict__ inv,
+    DispatchTiles tiles)
 {
-    extern __shared__ int cnt[];          // [E][NT]
-    __shared__ int offs[MAX_E + 1];
-    const int NT = blockDim.x, tid = threadIdx.x;
-    const int lane = tid & (WAVE - 1), wave = tid / WAVE, NW = NT / WAVE;
-    const int C = (P + NT - 1) / NT;
-    const int p0 = min(P, tid * C), p1 = min(P, p0 + C);
-    for (int e = 0; e < E; e++) cnt[e * NT + tid] = 0;
-    for (int p = p0; p < p1; p++) {
-        const int e = idx[p];
-        if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) cnt[e * NT + tid]++;
+    __shared__ int cnt[MAX_E], cur[MAX_E], offs[MAX_E + 1];
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    for (int e = tid; e < E; e += DISP_THREADS) {
+        cnt[e] = 0;
+        cur[e] = 0;
     }
     __syncthreads();
-    // per expert: lane l scans threads [l*R, l*R + R) serially, then the wave
-    // scans the 64 lane sums
-    const int R = NT / WAVE;
-    for (int e = wave; e < E; e += NW) {
-        int *c = cnt + e * NT + lane * R;
-        int sum = 0;
-        for (int r = 0; r < R; r++) sum += c[r];
-        int total;
-        int base = wave_excl_scan(sum, &total);
-        for (int r = 0; r < R; r++) {
-            const int v = c[r];
-            c[r] = base;
-            base += v;
+    constexpr int STEP = DISP_THREADS * DISP_ROUND;
+    for (int b0 = 0; b0 < P; b0 += STEP) {
+        int ev[DISP_ROUND];
+#pragma unroll
+        for (int i = 0; i < DISP_ROUND; i++) {
+            const int p = b0 + tid + DISP_THREADS * i;
+            ev[i] = p < P ? idx[p] : -1;
         }
-        if (lane == 0) offs[e] = total;
+#pragma unroll
+        for (int i = 0; i < DISP_ROUND; i++) {
+            const int e = ev[i];
+            if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
     if (wave == 0) {
-        // exclusive scan of the expert totals, 64 experts at a time
-        int run = 0;
+        // exclusive scan of the expert counts, 64 experts at a time, then
+        // row tiles of at most tiles.bm slots: lane e writes its expert's
+        // tiles at the exclusive scan of the tile counts
+        int run = 0, trun = 0;
         for (int e0 = 0; e0 < E; e0 += WAVE) {
             const int e = e0 + lane;
-            const int c = e < E ? offs[e] : 0;
+            const int c = e < E ? cnt[e] : 0;
             int tot;
             const int o = run + wave_excl_scan(c, &tot);
             if (e < E) {
@@ -95,33 +95,43 @@ __global__ void moe_dispatch_kernel(const int32_t *__restrict__ idx, int P, int 
                 offsets[e] = o;
             }
             run += tot;
+            if (tiles.bm > 0) {
+                const int nte = (c + tiles.bm - 1) / tiles.bm;
+                int ttot;
+                int t = trun + wave_excl_scan(nte, &ttot);
+                for (int m0 = 0; m0 < c && t < tiles.cap; m0 += tiles.bm, t++) {
+                    tiles.e[t] = e;
+                    tiles.m0[t] = m0;
+                }
+                trun += ttot;
+            }
         }
         if (lane == 0) {
             offs[E] = run;
             offsets[E] = run;
+            if (tiles.bm > 0) *tiles.n = min(trun, tiles.cap);
         }
     }
     __syncthreads();
-    if (tid == 0 && tiles.bm > 0) {
-        // row tiles of at most tiles.bm slots, expert by expert
-        int nt = 0;
-        for (int e = 0; e < E; e++) {
-            const int c = offs[e + 1] - offs[e];
-            for (int m0 = 0; m0 < c && nt < tiles.cap; m0 += tiles.bm, nt++) {
-                tiles.e[nt] = e;
-                tiles.m0[nt] = m0;
-            }
+    for (int b0 = 0; b0 < P; b0 += STEP) {
+        int ev[DISP_ROUND];
+#pragma unroll
+        for (int i = 0; i < DISP_ROUND; i++) {
+            const int p = b0 + tid + DISP_THREADS * i;
+            ev[i] = p < P ? idx[p] : -1;
         }
-        *tiles.n = nt;
-    }
-    for (int p = p0; p < p1; p++) {
-        const int e = idx[p];
-        if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) {
-            const int pos = offs[e] + cnt[e * NT + tid]++;
-            perm[pos] = p;
-            inv[p] = pos;
-        } else {
-            inv[p] = -1;
+#pragma unroll
+        for (int i = 0; i < DISP_ROUND; i++) {
+            const int p = b0 + tid + DISP_THREADS * i;
+            if (p >= P) break;
+            const int e = ev[i];
+            if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) {
+                const int pos = offs[e] + atomicAdd(&cur[e], 1);
+                perm[pos] = p;
+                inv[p] = pos;
+            } else {
+                inv[p] = -1;
+            }
         }
     }
 }
@@ -363,23 +373,70 @@ int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, con
                     int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                     const DispatchTiles &tiles)
 {
-    // threads: a multiple of 64, at most 1024, cnt[E][NT] within 64 KiB of LDS
-    int nt = 1024;
-    while (nt > WAVE && (size_t)nt * m->E * 4 > 65536) nt >>= 1;
     prof_begin(ctx, K_DISPATCH);
-    QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(nt), (size_t)nt * m->E * 4, idx, P, m->E,
-              mask, counts, offsets, perm, inv, tiles);
+    QQ_LAUNCH(ctx, moe_dispatch_kernel, dim3(1), dim3(DISP_THREADS), 0, idx, P, m->E, mask, counts,
+              offsets, perm, inv, tiles);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
 }
 
-int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const float *y, const int32_t *inv,
-                   const double *w, float *hidden)
+// The same per element, four consecutive columns per thread (H % 4 == 0,
+// 16-byte aligned rows); y rows in fp32 or, from the fp16 MFMA path, fp16.
+template <typename YT>
+__global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict__ y, int H, int K,
+                                                           const int32_t *__restrict__ inv,
+                                                           const double *__restrict__ w,
+                                                           float *__restrict__ hidden)
+{
+    const int t = blockIdx.y;
+    const int j = 4 * (blockIdx.x * 256 + threadIdx.x);
+    if (j >= H) return;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k = 0; k < K; k++) {
+        const int p = t * K + k;
+        const int s = inv[p];
+        if (s < 0) continue;
+        const double wk = w[p];
+        float v[4];
+        if constexpr (sizeof(YT) == 4) {
+            const float4 q = *reinterpret_cast<const float4 *>(y + (size_t)s * H + j);
+            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+        } else {
+            const uint2 q = *reinterpret_cast<const uint2 *>(y + (size_t)s * H + j);
+            const _Float16 *h = reinterpret_cast<const _Float16 *>(&q);
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] = (float)h[i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = (float)((double)acc[i] + wk * (double)v[i]);
+    }
+    float4 *hp = reinterpret_cast<float4 *>(hidden + (size_t)t * H + j);
+    float4 hv = *hp;
+    hv.x = hv.x + acc[0];
+    hv.y = hv.y + acc[1];
+    hv.z = hv.z + acc[2];
+    hv.w = hv.w + acc[3];
+    *hp = hv;
+}
+
+int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const void *y, bool y_f16,
+                   const int32_t *inv, const double *w, float *hidden)
 {
     prof_begin(ctx, K_COMBINE);
-    QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0, y, m->H, m->K,
-              inv, w, hidden);
+    const bool vec = m->H % 4 == 0 && ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)y & 15) == 0;
+    const dim3 g4((m->H / 4 + 255) / 256, T);
+    if (y_f16) {
+        if (!vec) return set_error(ctx, "combine: fp16 rows need H %% 4 == 0 and aligned buffers");
+        QQ_LAUNCH(ctx, moe_combine4_kernel<_Float16>, g4, dim3(256), 0,
+                  static_cast<const _Float16 *>(y), m->H, m->K, inv, w, hidden);
+    } else if (vec) {
+        QQ_LAUNCH(ctx, moe_combine4_kernel<float>, g4, dim3(256), 0, static_cast<const float *>(y),
+                  m->H, m->K, inv, w, hidden);
+    } else {
+        QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0,
+                  static_cast<const float *>(y), m->H, m->K, inv, w, hidden);
+    }
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
@@ -460,7 +517,7 @@ int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         prof_end(ctx);
         QQ_HIP(ctx, hipGetLastError());
     }
-    return launch_combine(ctx, m, T, y, inv, w, hidden);
+    return launch_combine(ctx, m, T, y, false, inv, w, hidden);
 }
 
 }  // namespace qq

@@ -10,16 +10,17 @@
 //            fp16 w = fp16(q * d); v_mfma_f32_16x16x32_f16 with fp32
 //            accumulators; epilogue silu(g) * u -> fp16 act[slot][F]
 //   down     A = act rows of the tile, B = 128 down columns dequantised
-//            likewise -> y[slot][H] fp32
+//            likewise -> y[slot][H] fp16
 // followed by the gather combine of the fp32 path (rank order, fp32 steps).
 // One Q8_0 block (32 values of the reduction dimension) is one MFMA K step;
 // the next block's global loads are in flight while the current block's
 // MFMAs run, and LDS is double buffered with one barrier per step.
 //
-// Accuracy: fp16 activations and weights (relative rounding 2^-11 each),
-// fp32 accumulation: ~1e-3 relative L2 on the layer output, inside the 1e-2
-// bound of the MFMA path.  SwiGLU products and weights must stay inside the
-// fp16 range (|v| < 65504); beyond it they become inf and show in the output.
+// Accuracy: fp16 activations, weights and expert outputs (relative rounding
+// 2^-11 each), fp32 accumulation: ~1e-3 relative L2 on the layer output,
+// inside the 1e-2 bound of the MFMA path.  SwiGLU products, weights and
+// expert outputs must stay inside the fp16 range (|v| < 65504); beyond it
+// they become inf and show in the output.
 #include "qq_device.h"
 
 namespace qq {
@@ -35,7 +36,7 @@ constexpr int MF_THREADS = 256;  // 4 waves, 2 x 2 over the 128 x 128 tile
 struct MfmaArgs {
     const _Float16 *xh;      // [T][H] activations in fp16
     _Float16 *act;           // [slots][F] SwiGLU products (down input)
-    float *y;                // [slots][H] expert outputs
+    _Float16 *y;             // [slots][H] expert outputs (fp16)
     const int32_t *perm, *counts, *offsets;
     const int32_t *tile_e, *tile_m0, *n_tiles;
     const int8_t *gq, *uq, *dq;
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_down_kernel(MfmaArgs a
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int row = wm * 64 + i * 16 + rq + r;
-                if (row < n && hh < a.H) a.y[(size_t)(slot0 + row) * a.H + hh] = acc[i][j][r];
+                if (row < n && hh < a.H) a.y[(size_t)(slot0 + row) * a.H + hh] = (_Float16)acc[i][j][r];
             }
         }
 }
@@ -330,7 +331,7 @@ size_t mfma_work_bytes(const qq_moe *m, int T)
     const size_t cap = (size_t)tile_cap(m, T);
     return al256((size_t)m->E * 4) + al256((size_t)(m->E + 1) * 4) + 2 * al256(P * 4) +
            2 * al256(cap * 4) + 256 + al256((size_t)T * m->H * 2) + al256(P * m->F * 2) +
-           al256(P * m->H * 4);
+           al256(P * m->H * 2);
 }
 
 int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
@@ -351,7 +352,7 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     tiles.n = reinterpret_cast<int32_t *>(p);          p += 256;
     _Float16 *xh = reinterpret_cast<_Float16 *>(p);    p += al256((size_t)T * m->H * 2);
     _Float16 *act = reinterpret_cast<_Float16 *>(p);   p += al256(P * m->F * 2);
-    float *y = reinterpret_cast<float *>(p);
+    _Float16 *y = reinterpret_cast<_Float16 *>(p);
 
     int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, tiles);
     if (rc) return rc;
@@ -396,7 +397,7 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     QQ_LAUNCH(ctx, moe_mfma_down_kernel<1>, g2, dim3(MF_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
-    return launch_combine(ctx, m, T, y, inv, w, hidden);
+    return launch_combine(ctx, m, T, y, true, inv, w, hidden);
 }
 
 }  // namespace qq

@@ -32,9 +32,16 @@ struct MaskBits {
     uint32_t w[MAX_E / 32];
 };
 
+// The word is picked by a chain of selects over the (uniform, kernel-argument)
+// words rather than by a dynamic index, which on the device would turn every
+// lookup into a memory load of the argument block.
 __host__ __device__ inline bool mask_has(const MaskBits &m, int e)
 {
-    return (m.w[e >> 5] >> (e & 31)) & 1u;
+    const int i = e >> 5;
+    uint32_t w = 0;
+#pragma unroll
+    for (int k = 0; k < MAX_E / 32; k++) w = (i == k) ? m.w[k] : w;
+    return (w >> (e & 31)) & 1u;
 }
 
 }  // namespace qq
@@ -187,8 +194,10 @@ struct DispatchTiles {
 int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, const MaskBits &mask,
                     int32_t *counts, int32_t *offsets, int32_t *perm, int32_t *inv,
                     const DispatchTiles &tiles);
-int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const float *y, const int32_t *inv,
-                   const double *w, float *hidden);
+// hidden[t] += sum_k w[t,k] * y[inv[t,k]] (ranks in order, fp32 steps); y rows
+// fp32, or fp16 when y_f16 (the MFMA path's outputs).
+int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const void *y, bool y_f16,
+                   const int32_t *inv, const double *w, float *hidden);
 // fp16 MFMA grouped GEMMs for prefill chunks (mfma.hip); needs H and F
 // multiples of 32 and 16-byte aligned activations.
 bool mfma_supported(const qq_moe *m);

@@ -431,7 +431,7 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
         QQ_LAUNCH(ctx, moe_stream_down_kernel<2>, dim3(g2), dim3(ST_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
-    return launch_combine(ctx, m, T, y, inv, w, hidden);
+    return launch_combine(ctx, m, T, y, false, inv, w, hidden);
 }
 
 }  // namespace qq
