@@ -96,6 +96,19 @@ int qq_q8_0_matvec_dev(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x_
 int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const float *bias,
                   const qq_tensor *gate, const qq_tensor *up, const qq_tensor *down,
                   int H, int F, int E, int K, qq_moe **out);
+
+/* Router gating of the layer (default QQ_GATING_SIGMOID_BIAS):
+ *   QQ_GATING_SIGMOID_BIAS  LFM2-MoE (src/lfm2-engine.js:417-447): sigmoid
+ *                           probabilities, selection by probability + bias,
+ *                           weights p_k / (1e-6 + sum p).
+ *   QQ_GATING_SOFTMAX       Qwen3-MoE (src/qwen3-engine.js:304-325):
+ *                           softmaxInPlace (src/tensor.js:150-164) over the
+ *                           router logits, selection by probability, weights
+ *                           p_k / sum p (0 when the sum is 0); bias unused.
+ * probs outputs carry the sigmoid resp. softmax probabilities. */
+#define QQ_GATING_SIGMOID_BIAS 0
+#define QQ_GATING_SOFTMAX      1
+int qq_moe_set_gating(qq_ctx *ctx, qq_moe *m, int gating);
 int qq_moe_release(qq_ctx *ctx, qq_moe *m);
 
 /* Lfm2Engine._moEFFN (src/lfm2-engine.js:413-487) over T tokens, each row

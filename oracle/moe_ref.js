@@ -12,7 +12,9 @@
 //   _readWeightF32  src/tensor.js:80-100
 //   siluInPlace / mulInPlace / addVec   src/tensor.js:167-185
 //   _expertSlice    src/lfm2-engine.js:489-505
-//   _moEFFN         src/lfm2-engine.js:413-487
+//   _moEFFN         src/lfm2-engine.js:413-487 (sigmoid + expert bias gating)
+//   softmaxInPlace  src/tensor.js:150-164
+//   Qwen3 _moEFFN   src/qwen3-engine.js:304-363 (softmax gating, no bias)
 // Node 12 has no DataView.getFloat16, so binary16 is decoded in closed form.
 //
 // CLI:
@@ -165,6 +167,54 @@ function moEFFN(eng, layerIdx, layer) {
     addVec(eng.bufHidden, eng.bufMoEOut);
 }
 
+function softmaxInPlace(arr, start, end) {
+    let maxVal = arr[start];
+    for (let i = start + 1; i < end; i++) if (arr[i] > maxVal) maxVal = arr[i];
+    let sumExp = 0;
+    for (let i = start; i < end; i++) {
+        arr[i] = Math.exp(arr[i] - maxVal);
+        sumExp += arr[i];
+    }
+    const invSum = 1.0 / sumExp;
+    for (let i = start; i < end; i++) arr[i] *= invSum;
+}
+
+// The Qwen3-MoE block: softmax over the router logits, top-K by probability,
+// weights renormalised from 0 (no 1e-6, no bias).  Top-K comes from the layer
+// (src/qwen3-engine.js:73, 310), not the engine.
+function moEFFNSoftmax(eng, layerIdx, layer) {
+    const K = layer.nExpertsUsed;
+    const probs = matmulGeneric(layer.routerWeight, eng.bufNormed);
+    softmaxInPlace(probs, 0, probs.length);
+    const order = Array.from(probs).map(function (v, i) { return [v, i]; });
+    order.sort(function (a, b) { return b[0] - a[0]; });
+    const chosen = [], chosenP = [];
+    for (let k = 0; k < K; k++) {
+        chosen.push(order[k][1]);
+        chosenP.push(order[k][0]);
+    }
+    let sum = 0;
+    for (let k = 0; k < K; k++) sum += chosenP[k];
+    const inv = sum > 0 ? 1 / sum : 0;
+    if (eng.onRouterUpdate) {
+        eng.onRouterUpdate({ layer: layerIdx, probs: Array.from(probs), selected: chosen,
+                             weights: chosenP.map(function (p) { return p * inv; }) });
+    }
+    eng.bufMoEOut.fill(0);
+    for (let k = 0; k < K; k++) {
+        const e = chosen[k];
+        if (eng.expertMask && eng.expertMask.has(e)) continue;
+        const wk = chosenP[k] * inv;
+        const g = matmulGeneric(expertSlice(layer.ffnGateExps, e), eng.bufNormed);
+        siluInPlace(g);
+        const u = matmulGeneric(expertSlice(layer.ffnUpExps, e), eng.bufNormed);
+        mulInPlace(g, u);
+        const y = matmulGeneric(expertSlice(layer.ffnDownExps, e), g);
+        for (let i = 0; i < y.length; i++) eng.bufMoEOut[i] += wk * y[i];
+    }
+    addVec(eng.bufHidden, eng.bufMoEOut);
+}
+
 // ---------------------------------------------------------------- CLI helpers
 
 function readRaw(path) {
@@ -196,6 +246,7 @@ function runJob(jobPath) {
         ffnGateExps: tensor(job.gate, [H, F, E], 8),
         ffnUpExps: tensor(job.up, [H, F, E], 8),
         ffnDownExps: tensor(job.down, [F, H, E], 8),
+        nExpertsUsed: K,
     };
     const X = new Float32Array(readRaw(job.x));
     const hid = new Float32Array(readRaw(job.hidden));
@@ -210,7 +261,8 @@ function runJob(jobPath) {
             for (let k = 0; k < K; k++) { idx[t * K + k] = info.selected[k]; w[t * K + k] = info.weights[k]; }
             for (let e = 0; e < E; e++) probs[t * E + e] = info.probs[e];
         };
-        moEFFN(eng, job.layer || 0, layer);
+        if (job.gating === 'softmax') moEFFNSoftmax(eng, job.layer || 0, layer);
+        else moEFFN(eng, job.layer || 0, layer);
         hid.set(eng.bufHidden, t * H);
     }
     writeRaw(job.out_hidden, hid);
@@ -306,7 +358,8 @@ function benchMatvec(seconds) {
 }
 
 module.exports = { halfToNumber, matmulQ80xF32, matmulF32xF32, matmulGeneric, readWeightF32,
-                   siluInPlace, mulInPlace, addVec, expertSlice, moEFFN };
+                   siluInPlace, mulInPlace, addVec, expertSlice, moEFFN, softmaxInPlace,
+                   moEFFNSoftmax };
 
 if (require.main === module) {
     const cmd = process.argv[2];

@@ -59,6 +59,10 @@ def lib():
     return _lib
 
 
+GATING_SIGMOID_BIAS = 0   # LFM2: sigmoid, expert bias for selection, 1e-6 in the sum
+GATING_SOFTMAX = 1        # Qwen3-MoE: softmax, no bias, sum from 0
+
+
 class MoeLayer(ctypes.Structure):
     _fields_ = [
         ("H", ctypes.c_int), ("F", ctypes.c_int), ("E", ctypes.c_int), ("K", ctypes.c_int),
@@ -69,6 +73,7 @@ class MoeLayer(ctypes.Structure):
         ("gate", ctypes.c_void_p), ("gate_off", ctypes.c_size_t),
         ("up", ctypes.c_void_p), ("up_off", ctypes.c_size_t),
         ("down", ctypes.c_void_p), ("down_off", ctypes.c_size_t),
+        ("gating", ctypes.c_int),
     ]
 
 
@@ -138,7 +143,8 @@ def _layer_struct(layer, keep):
                     bias=ptr(layer["bias"]) if has_bias else None, bias_off=0,
                     gate=ptr(layer["gate"]), gate_off=0,
                     up=ptr(layer["up"]), up_off=0,
-                    down=ptr(layer["down"]), down_off=0)
+                    down=ptr(layer["down"]), down_off=0,
+                    gating=GATING_SOFTMAX if layer.get("gating") == "softmax" else GATING_SIGMOID_BIAS)
 
 
 def moe_route(layer, x):

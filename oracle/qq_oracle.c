@@ -200,6 +200,55 @@ static size_t expert_offset(int in_dim, int hid_dim, int e)
     return (size_t)e * hid_dim * bytes_per_col;
 }
 
+/* src/tensor.js:150-164 softmaxInPlace over a Float32Array: the max in fp32,
+ * exp of the (exact) binary64 difference stored to fp32, a sequential binary64
+ * sum of the stored values, then each value times 1/sum stored to fp32. */
+static void softmax_f32(float *a, int n)
+{
+    float maxv = a[0];
+    for (int i = 1; i < n; i++)
+        if (a[i] > maxv) maxv = a[i];
+    double sum = 0.0;
+    for (int i = 0; i < n; i++) {
+        a[i] = (float)exp((double)a[i] - (double)maxv);
+        sum = sum + (double)a[i];
+    }
+    const double inv = 1.0 / sum;
+    for (int i = 0; i < n; i++) a[i] = (float)((double)a[i] * inv);
+}
+
+/* src/qwen3-engine.js:305-330 for one token, logits already formed: softmax,
+ * stable descending sort by probability, weights renormalised from 0. */
+static int route_token_softmax(const qo_moe_layer *L, int32_t *idx_out, double *w_out,
+                               float *probs_out, float *logits, int *order, float *rw,
+                               double *inv_out)
+{
+    const int E = L->E, K = L->K;
+    softmax_f32(logits, E);
+    for (int e = 0; e < E; e++) rw[e] = logits[e];
+    for (int e = 0; e < E; e++) order[e] = e;
+    for (int i = 1; i < E; i++) {      /* stable insertion sort, as above */
+        int v = order[i];
+        int j = i - 1;
+        while (j >= 0 && rw[order[j]] < rw[v]) {
+            order[j + 1] = order[j];
+            j--;
+        }
+        order[j + 1] = v;
+    }
+    double sumW = 0.0;
+    for (int k = 0; k < K; k++) sumW = sumW + (double)rw[order[k]];
+    const double invSum = sumW > 0 ? 1.0 / sumW : 0.0;
+    for (int k = 0; k < K; k++) {
+        if (idx_out) idx_out[k] = order[k];
+        if (w_out) w_out[k] = (double)rw[order[k]] * invSum;
+    }
+    if (probs_out)
+        for (int e = 0; e < E; e++) probs_out[e] = rw[e];
+    *inv_out = invSum;
+    return 0;
+}
+
 /* src/lfm2-engine.js:417-457 for one token: fills rw (probabilities),
  * order (rank order) and invSum; writes the telemetry outputs. */
 static int route_token(const qo_moe_layer *L, const float *x, int32_t *idx_out,
@@ -211,6 +260,7 @@ static int route_token(const qo_moe_layer *L, const float *x, int32_t *idx_out,
     /* 1. router logits (lfm2-engine.js:418) */
     if (qo_matmul_generic(L->router_type, L->router, L->router_off, H, E, x, logits))
         return -1;
+    if (L->gating == QO_GATING_SOFTMAX) return route_token_softmax(L, idx_out, w_out, probs_out, logits, order, rw, inv_out);
     /* 2. sigmoid (lfm2-engine.js:420-424) */
     for (int e = 0; e < E; e++)
         rw[e] = (float)(1.0 / (1.0 + exp(-(double)logits[e])));

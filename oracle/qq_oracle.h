@@ -71,7 +71,14 @@ typedef struct {
     const uint8_t *gate;    size_t gate_off;
     const uint8_t *up;      size_t up_off;
     const uint8_t *down;    size_t down_off;
+    int gating;         /* QO_GATING_SIGMOID_BIAS (LFM2) or QO_GATING_SOFTMAX (Qwen3) */
 } qo_moe_layer;
+
+/* Router gating functions: LFM2's sigmoid with expert-bias selection and
+ * 1e-6-seeded renormalisation (src/lfm2-engine.js:417-447), Qwen3-MoE's
+ * softmax with renormalisation from 0 (src/qwen3-engine.js:304-325). */
+#define QO_GATING_SIGMOID_BIAS 0
+#define QO_GATING_SOFTMAX      1
 
 /* Lfm2Engine._moEFFN (src/lfm2-engine.js:413-487) applied to T independent
  * tokens in order (the reference's prefill is T sequential single-token

@@ -64,9 +64,10 @@ def zipf_bias(rng, E, s=ZIPF_S, alpha=ZIPF_ALPHA):
 
 
 def moe_layer(seed, H=2048, F=1792, E=32, K=4, bias="uniform", router_type=TYPE_F32,
-              router_std=0.02):
+              router_std=0.02, gating="sigmoid"):
     """One LFM2-MoE MoE layer's tensors, as Lfm2Engine binds them
-    (src/lfm2-engine.js:129-137).
+    (src/lfm2-engine.js:129-137), or with gating="softmax" a Qwen3-MoE layer
+    (src/qwen3-engine.js:48-73: no bias tensor; pass bias=None).
 
     bias: "uniform" -> U(-0.01, 0.01) F32; "zipf" -> Zipf(1.1) skew; None -> absent.
     router_type: TYPE_F32 (float32 [H, E]) or TYPE_Q8_0.
@@ -93,6 +94,7 @@ def moe_layer(seed, H=2048, F=1792, E=32, K=4, bias="uniform", router_type=TYPE_
         "gate": q8_0_tensor(rng, H, F, E),
         "up": q8_0_tensor(rng, H, F, E),
         "down": q8_0_tensor(rng, F, H, E),
+        "gating": gating,
     }
 
 

@@ -405,6 +405,7 @@ int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const 
     m->up = up;
     m->down = down;
     m->has_bias = bias != nullptr;
+    m->gating = QQ_GATING_SIGMOID_BIAS;
     int rc = QQ_OK;
     hipError_t e = hipMalloc(&m->bias, (size_t)E * 4);
     if (e == hipSuccess) {
@@ -427,6 +428,16 @@ int qq_moe_create(qq_ctx *ctx, const void *router_bytes, int router_type, const 
         return rc;
     }
     *out = m;
+    return QQ_OK;
+}
+
+int qq_moe_set_gating(qq_ctx *ctx, qq_moe *m, int gating)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!m) return set_error(ctx, "moe_set_gating: NULL layer");
+    if (gating != QQ_GATING_SIGMOID_BIAS && gating != QQ_GATING_SOFTMAX)
+        return set_error(ctx, "moe_set_gating: unknown gating %d", gating);
+    m->gating = gating;
     return QQ_OK;
 }
 

@@ -70,7 +70,7 @@ struct DecodeArgs {
     const int8_t *rq;
     const __half *rd;
     int router_q8;
-    int router_vec4;      // F32 router, H % 4 == 0, x 16-byte aligned
+    int router_vec4;      // F32 router, H % 4 == 0
     int n_router;         // router workgroups: RT_COPIES * ceil(E / RT_EPW)
     const float *bias;
     const int8_t *gq;
@@ -502,7 +502,10 @@ __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
 
 bool decode_supported(const qq_moe *m, int T)
 {
-    return T == 1 && m->E <= WAVE && m->H <= 8 * DEC_WAVES * QK;
+    // the decode kernel implements LFM2's sigmoid + bias gating; softmax
+    // layers take the batched path at T = 1 too
+    return T == 1 && m->gating == QQ_GATING_SIGMOID_BIAS && m->E <= WAVE && m->K <= m->E &&
+           m->H <= 8 * DEC_WAVES * QK;
 }
 
 size_t decode_work_bytes(const qq_moe *m)

@@ -284,24 +284,64 @@ __device__ __forceinline__ bool rank_before(float av, int ai, float bv, int bi)
     return (av > bv) || (av == bv && ai < bi);
 }
 
+// Softmax gating (Qwen3-MoE, src/qwen3-engine.js:305-321 with softmaxInPlace,
+// src/tensor.js:150-164): probabilities p_e = fp32(fp32(exp(l_e - max)) * (1/S))
+// with S the binary64 sum of the fp32 exponentials in expert order (one lane
+// adds them in that order, as the reference does), selection by p_e itself,
+// and the weights renormalised from 0 (1/sum, or 0 when the sum is 0).
+template <int EPL>
+__device__ __forceinline__ void softmax_probs(const float (&logit)[EPL], int E, float (&prob)[EPL])
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+        if (lane + WAVE * i < E) mx = fmaxf(mx, logit[i]);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, WAVE));
+    float ex[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++)
+        ex[i] = (lane + WAVE * i < E) ? (float)exp((double)logit[i] - (double)mx) : 0.0f;
+    double sum = 0.0;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int n = min(WAVE, E - WAVE * i);
+        const int bits = __float_as_int(ex[i]);
+        for (int l = 0; l < n; l++)
+            sum = sum + (double)__int_as_float(__builtin_amdgcn_readlane(bits, l));
+    }
+    const double inv = 1.0 / sum;
+#pragma unroll
+    for (int i = 0; i < EPL; i++) prob[i] = (float)((double)ex[i] * inv);
+}
+
+// softmax: Qwen3 gating (bias unused); otherwise LFM2's sigmoid + bias.
 template <int EPL>
 __device__ __forceinline__ void wave_route(const float (&logit)[EPL], int E, int K,
-                                           const float *__restrict__ bias, WaveRoute<EPL> &out)
+                                           const float *__restrict__ bias, bool softmax,
+                                           WaveRoute<EPL> &out)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     float s[EPL];
+    if (softmax) {
+        softmax_probs<EPL>(logit, E, out.prob);
 #pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int e = lane + WAVE * i;
-        out.prob[i] = 0.0f;
-        s[i] = 0.0f;
-        if (e < E) {
-            out.prob[i] = (float)(1.0 / (1.0 + exp(-(double)logit[i])));
-            s[i] = out.prob[i] + bias[e];
+        for (int i = 0; i < EPL; i++) s[i] = out.prob[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int e = lane + WAVE * i;
+            out.prob[i] = 0.0f;
+            s[i] = 0.0f;
+            if (e < E) {
+                out.prob[i] = (float)(1.0 / (1.0 + exp(-(double)logit[i])));
+                s[i] = out.prob[i] + bias[e];
+            }
         }
     }
     uint32_t taken = 0;
-    double sumW = 1e-6;
+    double sumW = softmax ? 0.0 : 1e-6;
 #pragma unroll
     for (int k = 0; k < MAX_K; k++) {   // fully unrolled: idx/p stay in registers
         out.idx[k] = INT_MAX;
@@ -334,7 +374,7 @@ __device__ __forceinline__ void wave_route(const float (&logit)[EPL], int E, int
         out.p[k] = bp;
         sumW = sumW + (double)bp;
     }
-    out.inv = 1.0 / sumW;
+    out.inv = softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
 }
 
 }  // namespace qq

@@ -70,6 +70,7 @@ struct qq_moe {
     qq_tensor *router_q8;      // owned copy when the router is Q8_0
     float *bias;               // [E] selection bias (zeros when absent)
     int has_bias;
+    int gating;                // QQ_GATING_SIGMOID_BIAS or QQ_GATING_SOFTMAX
     const qq_tensor *gate, *up, *down;   // borrowed; the caller keeps them alive
 };
 

@@ -155,10 +155,11 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 }
 
 // One wavefront per token: logit = fp32(sum of the KS partial sums in order),
-// then sigmoid, bias, stable top-K and renormalisation.
+// then the layer's gating (sigmoid + bias, or softmax), stable top-K and
+// renormalisation.
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const double *__restrict__ part, int KS, int T, int E, int K, const float *__restrict__ bias,
-    int32_t *__restrict__ idx, double *__restrict__ w, float *__restrict__ probs)
+    int softmax, int32_t *__restrict__ idx, double *__restrict__ w, float *__restrict__ probs)
 {
     constexpr int EPL = MAX_E / WAVE;
     const int lane = threadIdx.x & (WAVE - 1);
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         lg[i] = (float)s;
     }
     WaveRoute<EPL> R;
-    wave_route<EPL>(lg, E, K, bias, R);
+    wave_route<EPL>(lg, E, K, bias, softmax != 0, R);
     if (probs) {
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
@@ -242,7 +243,7 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_ROUTER_TOPK);
     QQ_LAUNCH(ctx, router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, part, KS, T, m->E, m->K,
-              m->bias, idx, w, probs);
+              m->bias, m->gating == QQ_GATING_SOFTMAX ? 1 : 0, idx, w, probs);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

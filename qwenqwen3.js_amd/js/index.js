@@ -6,7 +6,8 @@
 //   matmulQ80xF32(meta, input)      src/tensor.js:26-53
 //   matmulGeneric(meta, input)      src/tensor.js:485-496 (type 8; other types are
 //                                   delegated to the matmulGeneric being replaced)
-//   Lfm2Engine.prototype._moEFFN    src/lfm2-engine.js:413-487
+//   Lfm2Engine.prototype._moEFFN    src/lfm2-engine.js:413-487 (sigmoid + bias gating)
+//   Qwen3Engine.prototype._moEFFN   src/qwen3-engine.js:304-363 (softmax gating)
 // plus a batched entry point with no reference counterpart:
 //   device.moeForward(layer, X, hidden, T, {mask, wantProbs})
 //
@@ -47,6 +48,9 @@ function readWeightF32(meta, n) {
     }
     throw new Error('Unsupported weight type for norm: ' + meta.type);
 }
+
+const GATING_SIGMOID_BIAS = 0;   // LFM2-MoE
+const GATING_SOFTMAX = 1;        // Qwen3-MoE
 
 function asFloat32(a) {
     return (a instanceof Float32Array) ? a : Float32Array.from(a);
@@ -90,9 +94,15 @@ class MoEDevice {
         throw new Error('Unsupported tensor type for matmul: ' + meta.type);
     }
 
-    // One device MoE handle per layer object (src/lfm2-engine.js:129-137).
-    layerHandle(layer, E, K) {
-        if (layer._qqMoe) return layer._qqMoe;
+    // One device MoE handle per layer object (src/lfm2-engine.js:129-137,
+    // src/qwen3-engine.js:49-73).
+    layerHandle(layer, E, K, gating) {
+        const gt_ = gating === undefined ? GATING_SIGMOID_BIAS : gating;
+        if (layer._qqMoe) {
+            if (layer._qqMoe.K !== K || layer._qqMoe.gating !== gt_)
+                throw new Error('MoE layer was bound with K=' + layer._qqMoe.K + ', gating=' + layer._qqMoe.gating);
+            return layer._qqMoe;
+        }
         const g = layer.ffnGateExps, u = layer.ffnUpExps, d = layer.ffnDownExps;
         const H = g.shape[0], F = g.shape[1];
         if (g.type !== 8 || u.type !== 8 || d.type !== 8)
@@ -103,9 +113,10 @@ class MoEDevice {
         const ut = this.tensorFor(u, H, F, E);
         const dt = this.tensorFor(d, F, H, E);
         const r = layer.routerWeight;
-        const bias = layer.expProbsBias ? readWeightF32(layer.expProbsBias, E) : null;
+        const bias = (gt_ === GATING_SIGMOID_BIAS && layer.expProbsBias) ? readWeightF32(layer.expProbsBias, E) : null;
         const moe = this.native.moeCreate(this.ctx, r.buffer, r.offset, r.type, bias, gt, ut, dt, H, F, E, K);
-        const handle = { moe: moe, H: H, F: F, E: E, K: K };
+        if (gt_ !== GATING_SIGMOID_BIAS) this.native.moeSetGating(this.ctx, moe, gt_);
+        const handle = { moe: moe, H: H, F: F, E: E, K: K, gating: gt_ };
         Object.defineProperty(layer, '_qqMoe', { value: handle, enumerable: false, configurable: true });
         return handle;
     }
@@ -116,7 +127,7 @@ class MoEDevice {
         const o = opts || {};
         const K = o.K !== undefined ? o.K : 4;
         const E = layer.ffnGateExps.shape[2];
-        const h = this.layerHandle(layer, E, K);
+        const h = this.layerHandle(layer, E, K, o.gating);
         let mask = null;
         if (o.mask && o.mask.size) {
             mask = new Uint8Array(h.E);
@@ -143,6 +154,23 @@ class MoEDevice {
         }
     }
 
+    // Qwen3Engine._moEFFN (src/qwen3-engine.js:304-363): softmax gating, top-K
+    // from the layer (layer.nExpertsUsed), same telemetry payload.
+    moEFFNQwen3(eng, layerIdx, layer) {
+        const want = !!eng.onRouterUpdate;
+        const r = this.moeForward(layer, eng.bufNormed, eng.bufHidden, 1,
+                                  { K: layer.nExpertsUsed, gating: GATING_SOFTMAX, mask: eng.expertMask,
+                                    wantProbs: want });
+        if (want) {
+            eng.onRouterUpdate({
+                layer: layerIdx,
+                probs: Array.from(r.probs),
+                selected: Array.from(r.idx),
+                weights: Array.from(r.w),
+            });
+        }
+    }
+
     release() {
         if (this.ctx) {
             this.native.release(this.ctx);
@@ -153,7 +181,8 @@ class MoEDevice {
 
 // Rebind the reference's globals (or any object holding them) to the device:
 // matmulQ80xF32, matmulGeneric (type 8 here, other types to the previous
-// function) and Lfm2Engine.prototype._moEFFN.  Throws when the device is
+// function), Lfm2Engine.prototype._moEFFN and Qwen3Engine.prototype._moEFFN
+// (each when the scope defines the class).  Throws when the device is
 // unavailable; nothing is rebound in that case.
 function install(scope, opts) {
     const o = opts || {};
@@ -166,8 +195,14 @@ function install(scope, opts) {
             return dev.moEFFN(this, layerIdx, layer);
         };
     }
+    if (scope.Qwen3Engine && scope.Qwen3Engine.prototype) {
+        scope.Qwen3Engine.prototype._moEFFN = function (layerIdx, layer) {
+            return dev.moEFFNQwen3(this, layerIdx, layer);
+        };
+    }
     return dev;
 }
 
 module.exports = { MoEDevice: MoEDevice, install: install, readWeightF32: readWeightF32,
-                   halfToNumber: halfToNumber, ADDON_PATH: ADDON_PATH };
+                   halfToNumber: halfToNumber, ADDON_PATH: ADDON_PATH,
+                   GATING_SIGMOID_BIAS: GATING_SIGMOID_BIAS, GATING_SOFTMAX: GATING_SOFTMAX };

@@ -348,6 +348,25 @@ static napi_value js_moe_create(napi_env env, napi_callback_info info)
     return new_handle(env, h);
 }
 
+// qq_moe_set_gating: 0 = LFM2 sigmoid + bias (default), 1 = Qwen3 softmax.
+static napi_value js_moe_set_gating(napi_env env, napi_callback_info info)
+{
+    ARGS(3);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *mh = get_handle(env, argv[1], H_MOE);
+    if (!mh) return NULL;
+    int32_t gating;
+    if (get_i32(env, argv[2], &gating)) {
+        napi_throw_type_error(env, NULL, "moeSetGating(ctx, moe, gating)");
+        return NULL;
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_moe_set_gating(ctx, (qq_moe *)mh->ptr, gating);
+    if (rc) return throw_qq(env, "qq_moe_set_gating", rc, ctx);
+    return NULL;
+}
+
 static napi_value js_moe_forward(napi_env env, napi_callback_info info)
 {
     ARGS(7);
@@ -422,6 +441,7 @@ static napi_value module_init(napi_env env, napi_value exports)
         {"uploadQ80", NULL, js_upload_q80, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvec", NULL, js_matvec, NULL, NULL, NULL, napi_enumerable, NULL},
         {"moeCreate", NULL, js_moe_create, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"moeSetGating", NULL, js_moe_set_gating, NULL, NULL, NULL, napi_enumerable, NULL},
         {"moeForward", NULL, js_moe_forward, NULL, NULL, NULL, napi_enumerable, NULL},
         {"release", NULL, js_release, NULL, NULL, NULL, napi_enumerable, NULL},
     };

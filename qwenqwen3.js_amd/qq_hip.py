@@ -20,6 +20,8 @@ LIB_PATH = os.path.join(_HERE, "libqqmoe.so")
 QQ_OK = 0
 TYPE_F32 = 0
 TYPE_Q8_0 = 8
+GATING_SIGMOID_BIAS = 0   # LFM2-MoE
+GATING_SOFTMAX = 1        # Qwen3-MoE
 
 # Every symbol include/qq_moe.h declares (tests/test_abi.py keeps them in sync).
 EXPORTS = (
@@ -27,7 +29,7 @@ EXPORTS = (
     "qq_q8_0_upload", "qq_q8_0_upload_dev", "qq_tensor_release",
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
-    "qq_moe_forward_norm_dev",
+    "qq_moe_forward_norm_dev", "qq_moe_set_gating",
     "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
@@ -66,6 +68,7 @@ def load():
         "qq_moe_forward": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_dev": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_norm_dev": (I, [P, P, P, P, ctypes.c_double, I, P, P, P, P]),
+        "qq_moe_set_gating": (I, [P, P, I]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
         "qq_rmsnorm_dev": (I, [P, P, P, P, I, I, ctypes.c_double]),
         "qq_timer_start": (I, [P]),
@@ -231,6 +234,11 @@ class MoeLayer:
         self.ctx, self.h = ctx, h
         self.H, self.F, self.E, self.K = H, F, E, K
         self._keep = keep
+
+    def set_gating(self, gating):
+        """GATING_SIGMOID_BIAS (LFM2-MoE, default) or GATING_SOFTMAX (Qwen3-MoE)."""
+        self.ctx.check(self.ctx.L.qq_moe_set_gating(self.ctx.h, self.h, int(gating)), "qq_moe_set_gating")
+        return self
 
     def forward(self, x, hidden, mask=None, want_probs=True):
         """_moEFFN over T tokens on host arrays.  Returns (hidden_out, idx, w, probs)."""

@@ -38,4 +38,8 @@ def upload_layer(ctx, L):
     gate = ctx.upload_q8_0(L["gate"], H, F, E)
     up = ctx.upload_q8_0(L["up"], H, F, E)
     down = ctx.upload_q8_0(L["down"], F, H, E)
-    return ctx.moe_create(L["router"], L["router_type"], L.get("bias"), gate, up, down, H, F, E, K)
+    m = ctx.moe_create(L["router"], L["router_type"], L.get("bias"), gate, up, down, H, F, E, K)
+    if L.get("gating") == "softmax":
+        import qq_hip
+        m.set_gating(qq_hip.GATING_SOFTMAX)
+    return m

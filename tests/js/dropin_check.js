@@ -2,7 +2,9 @@
 // GPU check of the JavaScript drop-in (qwenqwen3.js_amd/js) against the Node
 // restatement of the reference (oracle/moe_ref.js), in one process, on the
 // same seeded tensors.  Prints one JSON line; exits 1 on any failure.
-//   node dropin_check.js <H> <F> <E> <K> <tokens>
+//   node dropin_check.js <H> <F> <E> <K> <tokens> [sigmoid|softmax]
+// "softmax" checks Qwen3Engine._moEFFN (no bias tensor, K from the layer)
+// instead of Lfm2Engine._moEFFN.
 const path = require('path');
 const ref = require(path.join(__dirname, '..', '..', 'oracle', 'moe_ref.js'));
 const qq = require(path.join(__dirname, '..', '..', 'qwenqwen3.js_amd', 'js'));
@@ -10,6 +12,7 @@ const qq = require(path.join(__dirname, '..', '..', 'qwenqwen3.js_amd', 'js'));
 const H = Number(process.argv[2] || 256), F = Number(process.argv[3] || 96);
 const E = Number(process.argv[4] || 16), K = Number(process.argv[5] || 4);
 const NT = Number(process.argv[6] || 6);
+const SOFTMAX = process.argv[7] === 'softmax';
 
 let s = 0x9e3779b9;
 function next() { s ^= s << 13; s >>>= 0; s ^= s >>> 17; s ^= s << 5; s >>>= 0; return s; }
@@ -37,28 +40,30 @@ function relL2(a, b) {
 }
 
 const router = new Float32Array(E * H);
-for (let i = 0; i < router.length; i++) router[i] = gauss() * 0.02;
+for (let i = 0; i < router.length; i++) router[i] = gauss() * (SOFTMAX ? 0.05 : 0.02);
 const bias = new Float32Array(E);
 for (let e = 0; e < E; e++) bias[e] = (gauss()) * 0.005;
 const layer = {
     routerWeight: { buffer: router.buffer, offset: 0, shape: [H, E], type: 0 },
-    expProbsBias: { buffer: bias.buffer, offset: 0, shape: [E], type: 0 },
+    expProbsBias: SOFTMAX ? null : { buffer: bias.buffer, offset: 0, shape: [E], type: 0 },
     ffnGateExps: { buffer: q8(H, F, E), offset: 0, shape: [H, F, E], type: 8 },
     ffnUpExps: { buffer: q8(H, F, E), offset: 0, shape: [H, F, E], type: 8 },
     ffnDownExps: { buffer: q8(F, H, E), offset: 0, shape: [F, H, E], type: 8 },
+    nExpertsUsed: K,
 };
 
 class FakeEngine {
     constructor() {
-        this.nExperts = E; this.nExpertsUsed = K;
+        this.nExperts = E; this.nExpertsUsed = SOFTMAX ? 0 : K;   // Qwen3 reads K from the layer
         this.bufNormed = new Float32Array(H); this.bufHidden = new Float32Array(H);
         this.bufMoEOut = new Float32Array(H); this.expertMask = null; this.onRouterUpdate = null;
     }
-    _moEFFN(l, layer) { return ref.moEFFN(this, l, layer); }
+    _moEFFN(l, layer) { return SOFTMAX ? ref.moEFFNSoftmax(this, l, layer) : ref.moEFFN(this, l, layer); }
 }
 class DevEngine extends FakeEngine {}
 
-const scope = { matmulGeneric: ref.matmulGeneric, Lfm2Engine: DevEngine };
+const scope = { matmulGeneric: ref.matmulGeneric };
+scope[SOFTMAX ? 'Qwen3Engine' : 'Lfm2Engine'] = DevEngine;
 const dev = qq.install(scope, { device: 0 });
 const result = { ok: true, tokens: NT, H: H, F: F, E: E, K: K, max_rel_l2: 0, checks: [] };
 function check(name, cond, extra) {
@@ -94,7 +99,9 @@ for (let t = 0; t < NT; t++) {
 const T = 5, X = new Float32Array(T * H), hid = new Float32Array(T * H);
 for (let i = 0; i < X.length; i++) { X[i] = gauss(); hid[i] = gauss(); }
 const hidDev = Float32Array.from(hid);
-const rbat = dev.moeForward(layer, X, hidDev, T, { K: K, wantProbs: true });
+const rbat = dev.moeForward(layer, X, hidDev, T,
+                            { K: K, gating: SOFTMAX ? qq.GATING_SOFTMAX : qq.GATING_SIGMOID_BIAS,
+                              wantProbs: true });
 const c = new FakeEngine();
 let rc = null;
 c.onRouterUpdate = function (r) { rc = r; };

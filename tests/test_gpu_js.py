@@ -15,7 +15,9 @@ CHECK = os.path.join(ROOT, "tests", "js", "dropin_check.js")
 pytestmark = [pytest.mark.gpu, pytest.mark.skipif(NODE is None, reason="node is not installed")]
 
 
-@pytest.mark.parametrize("shape", [(256, 96, 16, 4, 6), (2048, 1792, 32, 4, 3), (100, 50, 5, 5, 4)])
+@pytest.mark.parametrize("shape", [(256, 96, 16, 4, 6), (2048, 1792, 32, 4, 3), (100, 50, 5, 5, 4),
+                                   (256, 96, 16, 4, 6, "softmax"),       # Qwen3Engine._moEFFN
+                                   (2048, 768, 128, 8, 2, "softmax")])   # Qwen3-30B-A3B layer shape
 def test_js_dropin(shape):
     print("js drop-in", shape, flush=True)
     p = subprocess.run([NODE, CHECK] + [str(v) for v in shape], capture_output=True, text=True, timeout=240)

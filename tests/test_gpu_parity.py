@@ -255,3 +255,47 @@ def test_moe_mfma_mask_and_unsupported_shape():
         L2 = synth.moe_layer(63, H=100, F=64, E=8, K=2)
         x2, hid2 = synth.activations(64, 24, 100)
         _check_moe(L2, x2, hid2, tol=TOL_GEMV)
+
+
+# ---------------------------------------------------------------- Qwen3-MoE softmax gating
+
+@pytest.mark.parametrize("case", [
+    dict(H=64, F=64, E=8, K=2, T=1),
+    dict(H=100, F=50, E=5, K=5, T=1),        # K == E
+    dict(H=96, F=160, E=6, K=3, T=4),
+    dict(H=2048, F=768, E=128, K=8, T=1),    # Qwen3-30B-A3B decode (E = 128: two experts a lane)
+    dict(H=2048, F=768, E=128, K=8, T=9),
+    dict(H=256, F=320, E=8, K=3, T=200),
+])
+def test_moe_softmax_gating(case):
+    """Qwen3Engine._moEFFN (qwen3-engine.js:304-363): softmax probabilities, selection by
+    probability, weights p / sum p; top-K, probabilities and weights bit-exact."""
+    _say("moe softmax", case)
+    T = case.pop("T")
+    L = synth.moe_layer(71, bias=None, gating="softmax", router_std=0.05, **case)
+    x, hid = synth.activations(72, T, case["H"])
+    _check_moe(L, x, hid)
+
+
+def test_moe_softmax_q8_router_mask_and_mfma():
+    """Q8_0 router, expert mask, and the MFMA path under softmax gating."""
+    L = synth.moe_layer(73, H=256, F=96, E=16, K=4, bias=None, gating="softmax",
+                        router_type=synth.TYPE_Q8_0)
+    x, hid = synth.activations(74, 40, 256)
+    r_idx, _, _ = oracle.moe_route(L, x)
+    _check_moe(L, x, hid, mask={int(r_idx[0, 0])})
+    with mfma_min_tokens(2):
+        _check_moe(L, x, hid, tol=TOL_MFMA)
+
+
+def test_moe_softmax_set_gating_rejects_unknown():
+    ctx = gpu_context()
+    L = synth.moe_layer(75, H=64, F=64, E=8, K=2, bias=None)
+    m = upload_layer(ctx, L)
+    try:
+        with pytest.raises(RuntimeError, match="gating"):
+            m.set_gating(7)
+    finally:
+        for t in m._keep:
+            t.release()
+        m.release()

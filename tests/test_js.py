@@ -41,6 +41,7 @@ def run_js_moe(tmp_path, L, x, hid, mask=None):
         "down": _save(d, "down.bin", L["down"]),
         "x": _save(d, "x.bin", x), "hidden": _save(d, "hidden.bin", hid),
         "mask": sorted(mask) if mask else None,
+        "gating": L.get("gating", "sigmoid"),
         "out_hidden": os.path.join(d, "o_hidden.bin"), "out_idx": os.path.join(d, "o_idx.bin"),
         "out_w": os.path.join(d, "o_w.bin"), "out_probs": os.path.join(d, "o_probs.bin"),
     }
@@ -61,6 +62,10 @@ def run_js_moe(tmp_path, L, x, hid, mask=None):
     dict(seed=3, H=128, F=64, E=16, K=4, T=5, router_type=synth.TYPE_Q8_0),
     dict(seed=4, H=100, F=50, E=5, K=5, T=3),
     dict(seed=5, H=2048, F=1792, E=32, K=4, T=2),
+    dict(seed=7, H=128, F=96, E=64, K=8, T=5, bias=None, gating="softmax", router_std=0.2),
+    dict(seed=8, H=2048, F=768, E=128, K=8, T=2, bias=None, gating="softmax"),
+    dict(seed=9, H=96, F=64, E=16, K=4, T=4, bias=None, gating="softmax",
+         router_type=synth.TYPE_Q8_0),
 ])
 def test_js_restatement_matches_c_oracle(tmp_path, case):
     case = dict(case)
@@ -102,7 +107,8 @@ def test_js_matvec_matches_c_oracle(tmp_path):
         np.testing.assert_array_equal(y, oracle.matmul_generic(typ, w, in_dim, out_dim, x))
 
 
-ADDON_EXPORTS = ["init", "lastError", "uploadQ80", "matvec", "moeCreate", "moeForward", "release"]
+ADDON_EXPORTS = ["init", "lastError", "uploadQ80", "matvec", "moeCreate", "moeSetGating", "moeForward",
+                 "release"]
 
 
 def test_addon_exports():

@@ -228,6 +228,79 @@ def test_route_q8_router_and_no_bias():
     np.testing.assert_array_equal(idx, np.argsort(-p.astype(np.float64), axis=1, kind="stable")[:, :4])
 
 
+# ------------------------------------------------------- softmax gating (Qwen3)
+
+def _onehot_logit_layer(logits, K):
+    """A softmax-gated layer whose router logits for x = e_0 are exactly
+    `logits` (one product per logit: x_0 * W[e][0] = 1 * logit)."""
+    E = len(logits)
+    L = _small_layer(20, H=32, F=32, E=E, K=K, bias=None, gating="softmax")
+    router = np.zeros((E, 32), np.float32)
+    router[:, 0] = logits
+    L["router"] = router.view(np.uint8).ravel()
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 1.0
+    return L, x
+
+
+def test_softmax_route_closed_forms():
+    # equal logits: every probability 1/E exactly, the first K experts (ties go
+    # to the lower index), every weight 1/K exactly (E, K powers of two)
+    L, x = _onehot_logit_layer(np.full(16, 0.75, np.float32), 4)
+    idx, w, probs = oracle.moe_route(L, x)
+    assert (probs == np.float32(1 / 16)).all()
+    assert (idx[0] == [0, 1, 2, 3]).all()
+    assert (w[0] == 0.25).all()
+    # one dominant logit: probability 1, weight 1 (the others underflow)
+    lg = np.zeros(8, np.float32)
+    lg[5] = 200.0
+    L, x = _onehot_logit_layer(lg, 1)
+    idx, w, probs = oracle.moe_route(L, x)
+    assert idx[0, 0] == 5 and w[0, 0] == 1.0 and probs[0, 5] == 1.0
+    # a tie at the K boundary goes to the lower index
+    L, x = _onehot_logit_layer(np.array([0, 3, 1, 3, 2, 0], np.float32), 2)
+    idx, _, _ = oracle.moe_route(L, x)
+    assert (idx[0] == [1, 3]).all()
+
+
+def test_softmax_route_against_float64_softmax():
+    L = _small_layer(21, H=256, E=64, K=8, bias=None, gating="softmax", router_std=0.2)
+    x, _ = synth.activations(22, 100, 256)
+    idx, w, probs = oracle.moe_route(L, x)
+    W = L["router"].view(np.float32).reshape(64, 256).astype(np.float64)
+    logits = (x.astype(np.float64) @ W.T).astype(np.float32).astype(np.float64)
+    ref = np.exp(logits - logits.max(axis=1, keepdims=True))
+    ref /= ref.sum(axis=1, keepdims=True)
+    np.testing.assert_allclose(probs, ref, rtol=2e-7, atol=1e-30)
+    np.testing.assert_array_equal(
+        idx, np.argsort(-probs.astype(np.float64), axis=1, kind="stable")[:, :8])
+    for t in range(len(x)):
+        assert probs[t, idx[t]].min() >= np.delete(probs[t], idx[t]).max()
+    # renormalised from 0: the weights sum to 1 (to rounding)
+    np.testing.assert_allclose(w.sum(axis=1), 1.0, rtol=1e-12)
+    S = np.take_along_axis(probs.astype(np.float64), idx, axis=1)
+    np.testing.assert_allclose(w, S / S.sum(axis=1, keepdims=True), rtol=1e-15)
+
+
+def test_softmax_layer_invariants():
+    # identical experts: the block adds sum_k w_k * expert(x) = expert(x) (sum w = 1)
+    L = _small_layer(23, H=64, F=64, E=16, K=4, bias=None, gating="softmax", router_std=0.2)
+    for name in ("gate", "up", "down"):
+        per = L[name].size // 16
+        L[name] = np.tile(L[name][:per], 16)
+    x, hid = synth.activations(24, 6, 64)
+    out, idx, w, _ = oracle.moe_ffn(L, x, hid)
+    L1 = dict(L, E=1, K=1, router=np.zeros(64, np.float32).view(np.uint8))
+    for name in ("gate", "up", "down"):
+        L1[name] = L[name][:L[name].size // 16]
+    one, _, _, _ = oracle.moe_ffn(L1, x, hid)
+    np.testing.assert_allclose(out - hid, one - hid, rtol=1e-5, atol=1e-7)
+    # masking every selected expert leaves hidden unchanged
+    for t in range(len(x)):
+        o, _, _, _ = oracle.moe_ffn(L, x[t:t + 1], hid[t:t + 1], mask=set(idx[t].tolist()))
+        np.testing.assert_array_equal(o, hid[t:t + 1])
+
+
 # ------------------------------------------------------------------ whole block
 
 def test_moe_dense_rederivation():
