@@ -112,3 +112,90 @@ def matvec_case(seed, in_dim=1024, out_dim=3072):
     w = q8_0_tensor(rng, in_dim, out_dim)
     x = rng.standard_normal(in_dim).astype(np.float32)
     return w, x
+
+
+# ---------------------------------------------------------------- GGUF files
+
+# GGUF v3 as published with ggml (docs/gguf.md): little-endian header
+# {"GGUF", u32 version, u64 n_tensors, u64 n_kv}; KV = {string key, u32 type,
+# value}; string = {u64 len, bytes}; array = {u32 elem type, u64 n, elems};
+# tensor info = {string name, u32 n_dims, u64 ne[n_dims], u32 type,
+# u64 offset from the data section}; the data section starts at the next
+# multiple of general.alignment (32 when the key is absent) and each tensor's
+# data is aligned the same way.
+GGUF_KV_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?",
+               10: "<Q", 11: "<q", 12: "<d"}
+GGUF_STRING, GGUF_ARRAY = 8, 9
+
+
+def _gguf_str(s):
+    import struct
+    b = s.encode("utf-8") if isinstance(s, str) else bytes(s)
+    return struct.pack("<Q", len(b)) + b
+
+
+def _gguf_value(typ, v):
+    import struct
+    if typ == GGUF_STRING:
+        return _gguf_str(v)
+    if typ == GGUF_ARRAY:
+        et, items = v
+        return struct.pack("<IQ", et, len(items)) + b"".join(_gguf_value(et, x) for x in items)
+    return struct.pack(GGUF_KV_FMT[typ], v)
+
+
+def gguf_file(kvs, tensors, version=3, alignment=None):
+    """Bytes of a GGUF file.
+
+    kvs: [(key, type, value)], array values as (elem_type, [items]);
+    tensors: [(name, shape, type, data bytes)];
+    alignment: when given, written as general.alignment (u32) ahead of kvs.
+    Returns (bytes, {name: absolute data offset})."""
+    import struct
+    al = 32 if alignment is None else alignment
+    kv_list = ([("general.alignment", 4, alignment)] if alignment is not None else []) + list(kvs)
+    head = b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(kv_list))
+    head += b"".join(_gguf_str(k) + struct.pack("<I", t) + _gguf_value(t, v) for k, t, v in kv_list)
+    raw = [np.ascontiguousarray(t[3]).view(np.uint8).tobytes() for t in tensors]
+    rel, pos = [], 0
+    for data in raw:
+        pos = -(-pos // al) * al
+        rel.append(pos)
+        pos += len(data)
+    for (name, shape, typ, _), r in zip(tensors, rel):
+        head += _gguf_str(name) + struct.pack("<I", len(shape))
+        head += b"".join(struct.pack("<Q", d) for d in shape) + struct.pack("<IQ", typ, r)
+    start = -(-len(head) // al) * al
+    out = bytearray(head) + bytearray(start - len(head))
+    for data, r in zip(raw, rel):
+        out += bytearray(start + r - len(out))
+        out += data
+    return bytes(out), {t[0]: start + r for t, r in zip(tensors, rel)}
+
+
+def moe_gguf(layers, arch="lfm2moe", K=None, alignment=None, extra_kvs=()):
+    """A GGUF file holding MoE blocks 0..n-1 built from oracle-format layer
+    dicts (moe_layer), with the tensor names the engines bind
+    (src/lfm2-engine.js:131-136, src/qwen3-engine.js:49-69) and the arch keys
+    they read.  Returns (bytes, {name: offset})."""
+    L0 = layers[0]
+    kvs = [("general.architecture", GGUF_STRING, arch),
+           (arch + ".block_count", 4, len(layers)),
+           (arch + ".embedding_length", 4, L0["H"]),
+           (arch + ".expert_count", 4, L0["E"]),
+           (arch + ".expert_feed_forward_length", 4, L0["F"])]
+    if K is not None:
+        kvs.append((arch + ".expert_used_count", 4, K))
+    kvs += list(extra_kvs)
+    tensors = []
+    for b, L in enumerate(layers):
+        H, F, E = L["H"], L["F"], L["E"]
+        p = "blk.%d." % b
+        tensors.append((p + "ffn_norm.weight", [H], TYPE_F32, np.ones(H, np.float32)))
+        tensors.append((p + "ffn_gate_inp.weight", [H, E], L["router_type"], L["router"]))
+        if L.get("bias") is not None:
+            tensors.append((p + "exp_probs_b.bias", [E], TYPE_F32, L["bias"]))
+        tensors.append((p + "ffn_gate_exps.weight", [H, F, E], TYPE_Q8_0, L["gate"]))
+        tensors.append((p + "ffn_up_exps.weight", [H, F, E], TYPE_Q8_0, L["up"]))
+        tensors.append((p + "ffn_down_exps.weight", [F, H, E], TYPE_Q8_0, L["down"]))
+    return gguf_file(kvs, tensors, alignment=alignment)

@@ -452,6 +452,7 @@ int qq_moe_release(qq_ctx *ctx, qq_moe *m)
     if (m->bias) (void)hipFree(m->bias);
     if (m->router_f32) (void)hipFree(m->router_f32);
     if (m->router_q8) qq_tensor_release(ctx, m->router_q8);
+    for (qq_tensor *t : m->owned) qq_tensor_release(ctx, t);
     delete m;
     return QQ_OK;
 }

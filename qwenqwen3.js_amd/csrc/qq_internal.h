@@ -71,7 +71,8 @@ struct qq_moe {
     float *bias;               // [E] selection bias (zeros when absent)
     int has_bias;
     int gating;                // QQ_GATING_SIGMOID_BIAS or QQ_GATING_SOFTMAX
-    const qq_tensor *gate, *up, *down;   // borrowed; the caller keeps them alive
+    const qq_tensor *gate, *up, *down;   // borrowed; the caller keeps them alive ...
+    qq_tensor *owned[3];                 // ... unless the layer owns them (GGUF loader)
 };
 
 struct qq_ctx {

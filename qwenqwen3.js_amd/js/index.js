@@ -8,8 +8,11 @@
 //                                   delegated to the matmulGeneric being replaced)
 //   Lfm2Engine.prototype._moEFFN    src/lfm2-engine.js:413-487 (sigmoid + bias gating)
 //   Qwen3Engine.prototype._moEFFN   src/qwen3-engine.js:304-363 (softmax gating)
-// plus a batched entry point with no reference counterpart:
-//   device.moeForward(layer, X, hidden, T, {mask, wantProbs})
+// plus entry points with no reference counterpart:
+//   device.moeForward(layer, X, hidden, T, {mask, wantProbs})   T tokens at once
+//   device.attachGGUF(path)   MoE blocks come from the file (memory-mapped,
+//                             repacked straight to the device) instead of from
+//                             the engine's ArrayBuffers
 //
 // There is no CPU fallback: when the addon or the device is missing, the
 // constructor and install() throw.  Written for Node 12 (no `?.`, no `??`).
@@ -62,6 +65,19 @@ class MoEDevice {
         this.ctx = this.native.init(device === undefined ? 0 : (device | 0));
         this._tensors = new WeakMap();   // ArrayBuffer -> Map(key -> device tensor)
         this.fallbackMatmul = null;
+        this._gguf = null;
+    }
+
+    // Bind MoE blocks from a GGUF file: the layer of block l is read from the
+    // file's blk.l.* tensors by the native reader (include/qq_gguf.h), which
+    // maps the file instead of holding it in one ArrayBuffer (the reference
+    // slices the File per tensor for the same reason, src/gguf.js:350-374).
+    // Returns the file's tensor table [{name, shape, type, offset, nbytes}].
+    attachGGUF(path) {
+        const g = this.native.ggufOpen(String(path));
+        if (this._gguf) this.native.release(this._gguf);
+        this._gguf = g;
+        return this.native.ggufTensors(g);
     }
 
     // Device copy of a GGUF Q8_0 tensor, uploaded (and repacked) once per
@@ -96,12 +112,20 @@ class MoEDevice {
 
     // One device MoE handle per layer object (src/lfm2-engine.js:129-137,
     // src/qwen3-engine.js:49-73).
-    layerHandle(layer, E, K, gating) {
+    layerHandle(layer, E, K, gating, block) {
         const gt_ = gating === undefined ? GATING_SIGMOID_BIAS : gating;
         if (layer._qqMoe) {
             if (layer._qqMoe.K !== K || layer._qqMoe.gating !== gt_)
                 throw new Error('MoE layer was bound with K=' + layer._qqMoe.K + ', gating=' + layer._qqMoe.gating);
             return layer._qqMoe;
+        }
+        if (this._gguf && block !== undefined && block !== null) {
+            const p = this.native.ggufMoeParams(this._gguf, block, K, gt_);
+            if (p.E !== E) throw new Error('GGUF block ' + block + ' has ' + p.E + ' experts, the layer ' + E);
+            const moe = this.native.ggufMoeLayer(this.ctx, this._gguf, block, K, gt_);
+            const handle = { moe: moe, H: p.H, F: p.F, E: p.E, K: p.K, gating: gt_ };
+            Object.defineProperty(layer, '_qqMoe', { value: handle, enumerable: false, configurable: true });
+            return handle;
         }
         const g = layer.ffnGateExps, u = layer.ffnUpExps, d = layer.ffnDownExps;
         const H = g.shape[0], F = g.shape[1];
@@ -127,7 +151,7 @@ class MoEDevice {
         const o = opts || {};
         const K = o.K !== undefined ? o.K : 4;
         const E = layer.ffnGateExps.shape[2];
-        const h = this.layerHandle(layer, E, K, o.gating);
+        const h = this.layerHandle(layer, E, K, o.gating, o.block);
         let mask = null;
         if (o.mask && o.mask.size) {
             mask = new Uint8Array(h.E);
@@ -143,7 +167,7 @@ class MoEDevice {
     moEFFN(eng, layerIdx, layer) {
         const want = !!eng.onRouterUpdate;
         const r = this.moeForward(layer, eng.bufNormed, eng.bufHidden, 1,
-                                  { K: eng.nExpertsUsed, mask: eng.expertMask, wantProbs: want });
+                                  { K: eng.nExpertsUsed, mask: eng.expertMask, wantProbs: want, block: layerIdx });
         if (want) {
             eng.onRouterUpdate({
                 layer: layerIdx,
@@ -160,7 +184,7 @@ class MoEDevice {
         const want = !!eng.onRouterUpdate;
         const r = this.moeForward(layer, eng.bufNormed, eng.bufHidden, 1,
                                   { K: layer.nExpertsUsed, gating: GATING_SOFTMAX, mask: eng.expertMask,
-                                    wantProbs: want });
+                                    wantProbs: want, block: layerIdx });
         if (want) {
             eng.onRouterUpdate({
                 layer: layerIdx,
@@ -172,6 +196,10 @@ class MoEDevice {
     }
 
     release() {
+        if (this._gguf) {
+            this.native.release(this._gguf);
+            this._gguf = null;
+        }
         if (this.ctx) {
             this.native.release(this.ctx);
             this.ctx = null;

@@ -19,7 +19,12 @@
  *              mask: Uint8Array|null, wantProbs) -> {idx, w, probs}
  *       hidden is updated in place; idx Int32Array(T*K), w Float64Array(T*K),
  *       probs Float32Array(T*E) or null
- *   release(handle)    frees a tensor / moe / ctx now instead of at GC
+ *   moeSetGating(ctx, moe, gating)       0 = LFM2 sigmoid + bias, 1 = Qwen3 softmax
+ *   ggufOpen(path) -> gguf               memory-mapped GGUF reader (include/qq_gguf.h)
+ *   ggufTensors(gguf) -> [{name, shape, type, offset, nbytes}]
+ *   ggufMoeParams(gguf, block, K, gating) -> {H, F, E, K, gating, routerType, hasBias}
+ *   ggufMoeLayer(ctx, gguf, block, K, gating) -> moe (owns its expert tensors)
+ *   release(handle)    frees a tensor / moe / ctx / gguf now instead of at GC
  */
 #include <node_api.h>
 #include <stdint.h>
@@ -27,13 +32,14 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "../../include/qq_gguf.h"
 #include "../../include/qq_moe.h"
 
-enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3 };
+enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3, H_GGUF = 4 };
 
 typedef struct handle {
     int kind;
-    void *ptr;           /* qq_ctx*, qq_tensor* or qq_moe* (NULL once released) */
+    void *ptr;           /* qq_ctx*, qq_tensor*, qq_moe* or qq_gguf* (NULL once released) */
     struct handle *ctx;  /* owning context handle (tensor, moe) */
     napi_ref ctx_ref;    /* keeps the context alive while this handle lives */
     napi_ref keep[3];    /* moe: keeps gate/up/down tensors alive */
@@ -65,6 +71,7 @@ static void release_handle(napi_env env, handle *h)
     case H_TENSOR: qq_tensor_release(ctx, (qq_tensor *)h->ptr); break;
     case H_MOE: qq_moe_release(ctx, (qq_moe *)h->ptr); break;
     case H_CTX: qq_destroy((qq_ctx *)h->ptr); break;
+    case H_GGUF: qq_gguf_close((qq_gguf *)h->ptr); break;
     }
     h->ptr = NULL;
     for (int i = 0; i < 3; i++)
@@ -419,6 +426,137 @@ static napi_value js_moe_forward(napi_env env, napi_callback_info info)
     return res;
 }
 
+static napi_value throw_gguf(napi_env env, const char *what, int rc)
+{
+    char msg[640];
+    snprintf(msg, sizeof msg, "%s failed (%d): %s", what, rc, qq_gguf_last_error());
+    napi_throw_error(env, NULL, msg);
+    return NULL;
+}
+
+static napi_value js_gguf_open(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    char path[4096];
+    size_t n = 0;
+    if (napi_get_value_string_utf8(env, argv[0], path, sizeof path, &n) != napi_ok || n + 1 >= sizeof path) {
+        napi_throw_type_error(env, NULL, "ggufOpen(path: string)");
+        return NULL;
+    }
+    qq_gguf *g = NULL;
+    int rc = qq_gguf_open(path, &g);
+    if (rc) return throw_gguf(env, "qq_gguf_open", rc);
+    handle *h = (handle *)calloc(1, sizeof(handle));
+    if (!h) {
+        qq_gguf_close(g);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->kind = H_GGUF;
+    h->ptr = g;
+    return new_handle(env, h);
+}
+
+static napi_value set_num(napi_env env, napi_value obj, const char *key, double v)
+{
+    napi_value x;
+    if (napi_create_double(env, v, &x) != napi_ok || napi_set_named_property(env, obj, key, x) != napi_ok)
+        return NULL;
+    return obj;
+}
+
+static napi_value js_gguf_tensors(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    handle *gh = get_handle(env, argv[0], H_GGUF);
+    if (!gh) return NULL;
+    const qq_gguf *g = (const qq_gguf *)gh->ptr;
+    qq_gguf_header_info hd;
+    int rc = qq_gguf_header(g, &hd);
+    if (rc) return throw_gguf(env, "qq_gguf_header", rc);
+    napi_value arr;
+    CHECK_NAPI(env, napi_create_array_with_length(env, (size_t)hd.tensor_count, &arr));
+    for (uint64_t i = 0; i < hd.tensor_count; i++) {
+        qq_gguf_tensor t;
+        rc = qq_gguf_tensor_info(g, i, &t);
+        if (rc) return throw_gguf(env, "qq_gguf_tensor_info", rc);
+        napi_value o, name, shape;
+        CHECK_NAPI(env, napi_create_object(env, &o));
+        CHECK_NAPI(env, napi_create_string_utf8(env, t.name, NAPI_AUTO_LENGTH, &name));
+        CHECK_NAPI(env, napi_set_named_property(env, o, "name", name));
+        CHECK_NAPI(env, napi_create_array_with_length(env, (size_t)t.n_dims, &shape));
+        for (int d = 0; d < t.n_dims && d < 4; d++) {
+            napi_value x;
+            CHECK_NAPI(env, napi_create_double(env, (double)t.shape[d], &x));
+            CHECK_NAPI(env, napi_set_element(env, shape, (uint32_t)d, x));
+        }
+        CHECK_NAPI(env, napi_set_named_property(env, o, "shape", shape));
+        if (!set_num(env, o, "type", t.type) || !set_num(env, o, "offset", (double)t.offset) ||
+            !set_num(env, o, "nbytes", (double)t.nbytes)) {
+            napi_throw_error(env, NULL, "qq_napi: N-API call failed");
+            return NULL;
+        }
+        CHECK_NAPI(env, napi_set_element(env, arr, (uint32_t)i, o));
+    }
+    return arr;
+}
+
+static napi_value js_gguf_moe_params(napi_env env, napi_callback_info info)
+{
+    ARGS(4);
+    handle *gh = get_handle(env, argv[0], H_GGUF);
+    if (!gh) return NULL;
+    int32_t block, K, gating;
+    if (get_i32(env, argv[1], &block) || get_i32(env, argv[2], &K) || get_i32(env, argv[3], &gating)) {
+        napi_throw_type_error(env, NULL, "ggufMoeParams(gguf, block, K, gating)");
+        return NULL;
+    }
+    qq_gguf_moe_info p;
+    int rc = qq_gguf_moe_params((const qq_gguf *)gh->ptr, block, K, gating, &p);
+    if (rc) return throw_gguf(env, "qq_gguf_moe_params", rc);
+    napi_value o;
+    CHECK_NAPI(env, napi_create_object(env, &o));
+    if (!set_num(env, o, "H", p.H) || !set_num(env, o, "F", p.F) || !set_num(env, o, "E", p.E) ||
+        !set_num(env, o, "K", p.K) || !set_num(env, o, "gating", p.gating) ||
+        !set_num(env, o, "routerType", p.router_type) || !set_num(env, o, "hasBias", p.has_bias)) {
+        napi_throw_error(env, NULL, "qq_napi: N-API call failed");
+        return NULL;
+    }
+    return o;
+}
+
+static napi_value js_gguf_moe_layer(napi_env env, napi_callback_info info)
+{
+    ARGS(5);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *gh = get_handle(env, argv[1], H_GGUF);
+    if (!gh) return NULL;
+    int32_t block, K, gating;
+    if (get_i32(env, argv[2], &block) || get_i32(env, argv[3], &K) || get_i32(env, argv[4], &gating)) {
+        napi_throw_type_error(env, NULL, "ggufMoeLayer(ctx, gguf, block, K, gating)");
+        return NULL;
+    }
+    qq_gguf_moe_info p;
+    int rc = qq_gguf_moe_params((const qq_gguf *)gh->ptr, block, K, gating, &p);
+    if (rc) return throw_gguf(env, "qq_gguf_moe_params", rc);
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    qq_moe *m = NULL;
+    rc = qq_gguf_moe_layer(ctx, (const qq_gguf *)gh->ptr, block, K, gating, &m);
+    if (rc) return throw_qq(env, "qq_gguf_moe_layer", rc, ctx);
+    handle *h = child_of(env, argv[0], ch, H_MOE);
+    if (!h) {
+        qq_moe_release(ctx, m);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->ptr = m;
+    h->H = p.H;
+    h->E = p.E;
+    h->K = p.K;
+    return new_handle(env, h);
+}
+
 static napi_value js_release(napi_env env, napi_callback_info info)
 {
     ARGS(1);
@@ -443,6 +581,10 @@ static napi_value module_init(napi_env env, napi_value exports)
         {"moeCreate", NULL, js_moe_create, NULL, NULL, NULL, napi_enumerable, NULL},
         {"moeSetGating", NULL, js_moe_set_gating, NULL, NULL, NULL, napi_enumerable, NULL},
         {"moeForward", NULL, js_moe_forward, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"ggufOpen", NULL, js_gguf_open, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"ggufTensors", NULL, js_gguf_tensors, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"ggufMoeParams", NULL, js_gguf_moe_params, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"ggufMoeLayer", NULL, js_gguf_moe_layer, NULL, NULL, NULL, napi_enumerable, NULL},
         {"release", NULL, js_release, NULL, NULL, NULL, napi_enumerable, NULL},
     };
     if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;

@@ -34,6 +34,28 @@ EXPORTS = (
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
 )
+# ... and include/qq_gguf.h
+GGUF_EXPORTS = (
+    "qq_gguf_open", "qq_gguf_open_memory", "qq_gguf_close", "qq_gguf_last_error", "qq_gguf_header",
+    "qq_gguf_find_tensor", "qq_gguf_tensor_info", "qq_gguf_find_key", "qq_gguf_kv_info",
+    "qq_gguf_kv_number", "qq_gguf_kv_string", "qq_gguf_kv_array", "qq_gguf_kv_array_number",
+    "qq_gguf_moe_params", "qq_gguf_moe_layer",
+)
+
+
+class GgufHeader(ctypes.Structure):
+    _fields_ = [("version", ctypes.c_uint32), ("tensor_count", ctypes.c_uint64),
+                ("kv_count", ctypes.c_uint64), ("file_size", ctypes.c_uint64),
+                ("alignment", ctypes.c_uint64), ("data_offset", ctypes.c_uint64)]
+
+
+class GgufTensor(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("n_dims", ctypes.c_int), ("shape", ctypes.c_uint64 * 4),
+                ("type", ctypes.c_uint32), ("offset", ctypes.c_uint64), ("nbytes", ctypes.c_uint64)]
+
+
+class GgufMoeInfo(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in ("H", "F", "E", "K", "gating", "router_type", "has_bias")]
 
 _lib = None
 
@@ -81,6 +103,25 @@ def load():
         "qq_capture_end": (I, [P, PP]),
         "qq_graph_launch": (I, [P, P]),
         "qq_graph_release": (I, [P, P]),
+        "qq_gguf_open": (I, [ctypes.c_char_p, PP]),
+        "qq_gguf_open_memory": (I, [P, S, PP]),
+        "qq_gguf_close": (None, [P]),
+        "qq_gguf_last_error": (ctypes.c_char_p, []),
+        "qq_gguf_header": (I, [P, ctypes.POINTER(GgufHeader)]),
+        "qq_gguf_find_tensor": (ctypes.c_int64, [P, ctypes.c_char_p]),
+        "qq_gguf_tensor_info": (I, [P, ctypes.c_uint64, ctypes.POINTER(GgufTensor)]),
+        "qq_gguf_find_key": (ctypes.c_int64, [P, ctypes.c_char_p]),
+        "qq_gguf_kv_info": (I, [P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_char_p),
+                                ctypes.POINTER(ctypes.c_uint32)]),
+        "qq_gguf_kv_number": (I, [P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_double)]),
+        "qq_gguf_kv_string": (I, [P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_void_p),
+                                  ctypes.POINTER(ctypes.c_uint64)]),
+        "qq_gguf_kv_array": (I, [P, ctypes.c_uint64, ctypes.POINTER(ctypes.c_uint32),
+                                 ctypes.POINTER(ctypes.c_uint64)]),
+        "qq_gguf_kv_array_number": (I, [P, ctypes.c_uint64, ctypes.c_uint64,
+                                        ctypes.POINTER(ctypes.c_double)]),
+        "qq_gguf_moe_params": (I, [P, I, I, I, ctypes.POINTER(GgufMoeInfo)]),
+        "qq_gguf_moe_layer": (I, [P, P, I, I, I, PP]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -203,6 +244,98 @@ class Context:
         self.check(self.L.qq_moe_create(self.h, _ptr(r), router_type, _ptr(b), gate.h, up.h, down.h,
                                         H, F, E, K, ctypes.byref(h)), "qq_moe_create")
         return MoeLayer(self, h, H, F, E, K, (gate, up, down))
+
+
+class Gguf:
+    """Native GGUF reader (include/qq_gguf.h) over a file (memory-mapped) or
+    over caller bytes; needs no device."""
+
+    def __init__(self, path=None, data=None):
+        self.L = load()
+        h = ctypes.c_void_p()
+        if path is not None:
+            rc = self.L.qq_gguf_open(os.fsencode(path), ctypes.byref(h))
+            self._data = None
+        else:
+            self._data = (ctypes.c_uint8 * len(data)).from_buffer_copy(data) if len(data) else None
+            rc = self.L.qq_gguf_open_memory(self._data, len(data), ctypes.byref(h))
+        if rc != QQ_OK:
+            raise QQError("qq_gguf_open failed (%d): %s" % (rc, self.L.qq_gguf_last_error().decode()))
+        self.h = h
+
+    def check(self, rc, what):
+        if rc != QQ_OK:
+            raise QQError("%s failed (%d): %s" % (what, rc, self.L.qq_gguf_last_error().decode()))
+
+    def close(self):
+        if self.h:
+            self.L.qq_gguf_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def header(self):
+        hd = GgufHeader()
+        self.check(self.L.qq_gguf_header(self.h, ctypes.byref(hd)), "qq_gguf_header")
+        return {f: getattr(hd, f) for f, _ in GgufHeader._fields_}
+
+    def tensors(self):
+        out = []
+        for i in range(self.header()["tensor_count"]):
+            t = GgufTensor()
+            self.check(self.L.qq_gguf_tensor_info(self.h, i, ctypes.byref(t)), "qq_gguf_tensor_info")
+            out.append(dict(name=t.name.decode("utf-8", "replace"), shape=list(t.shape[:t.n_dims]),
+                            type=t.type, offset=t.offset, nbytes=t.nbytes))
+        return out
+
+    def find_tensor(self, name):
+        return self.L.qq_gguf_find_tensor(self.h, name.encode())
+
+    def find_key(self, key):
+        return self.L.qq_gguf_find_key(self.h, key.encode())
+
+    def kv(self, i):
+        """(key, type, value): numbers as float, strings as str, arrays as
+        (elem_type, n, numeric items or None)."""
+        k, t = ctypes.c_char_p(), ctypes.c_uint32()
+        self.check(self.L.qq_gguf_kv_info(self.h, i, ctypes.byref(k), ctypes.byref(t)), "qq_gguf_kv_info")
+        typ = t.value
+        if typ == 8:
+            p, n = ctypes.c_void_p(), ctypes.c_uint64()
+            self.check(self.L.qq_gguf_kv_string(self.h, i, ctypes.byref(p), ctypes.byref(n)), "kv_string")
+            val = ctypes.string_at(p, n.value).decode("utf-8", "replace") if n.value else ""
+        elif typ == 9:
+            et, n = ctypes.c_uint32(), ctypes.c_uint64()
+            self.check(self.L.qq_gguf_kv_array(self.h, i, ctypes.byref(et), ctypes.byref(n)), "kv_array")
+            items = None
+            if et.value not in (8, 9):
+                items = []
+                for j in range(n.value):
+                    v = ctypes.c_double()
+                    self.check(self.L.qq_gguf_kv_array_number(self.h, i, j, ctypes.byref(v)), "kv_array_number")
+                    items.append(v.value)
+            val = (et.value, n.value, items)
+        else:
+            v = ctypes.c_double()
+            self.check(self.L.qq_gguf_kv_number(self.h, i, ctypes.byref(v)), "qq_gguf_kv_number")
+            val = v.value
+        return k.value.decode("utf-8", "replace"), typ, val
+
+    def moe_params(self, block, K=0, gating=-1):
+        info = GgufMoeInfo()
+        self.check(self.L.qq_gguf_moe_params(self.h, block, K, gating, ctypes.byref(info)), "qq_gguf_moe_params")
+        return {f: getattr(info, f) for f, _ in GgufMoeInfo._fields_}
+
+    def moe_layer(self, ctx, block, K=0, gating=-1):
+        """Upload block `block` to ctx's device (qq_gguf_moe_layer); the layer owns its tensors."""
+        p = self.moe_params(block, K, gating)
+        h = ctypes.c_void_p()
+        ctx.check(self.L.qq_gguf_moe_layer(ctx.h, self.h, block, K, gating, ctypes.byref(h)), "qq_gguf_moe_layer")
+        return MoeLayer(ctx, h, p["H"], p["F"], p["E"], p["K"], ())
 
 
 class Tensor:

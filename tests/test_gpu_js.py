@@ -26,3 +26,23 @@ def test_js_dropin(shape):
     bad = [c for c in res["checks"] if not c["ok"]]
     assert res["ok"] and not bad, (bad, p.stderr[-2000:])
     assert res["max_rel_l2"] < 1e-4
+
+
+@pytest.mark.parametrize("arch", ["lfm2moe", "qwen3moe"])
+def test_js_attach_gguf(tmp_path, arch):
+    """MoEDevice.attachGGUF: _moEFFN with the layers bound from a GGUF file."""
+    import synth
+    print("js gguf", arch, flush=True)
+    kw = dict(bias=None, gating="softmax", router_std=0.05) if arch == "qwen3moe" else {}
+    layers = [synth.moe_layer(60 + b, H=256, F=96, E=16, K=4, **kw) for b in range(2)]
+    data, _ = synth.moe_gguf(layers, arch=arch, K=4)
+    path = tmp_path / "m.gguf"
+    path.write_bytes(data)
+    p = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "gguf_check.js"), str(path),
+                        "softmax" if arch == "qwen3moe" else "sigmoid", "3"],
+                       capture_output=True, text=True, timeout=240)
+    assert p.stdout.strip(), p.stderr
+    res = json.loads(p.stdout.strip().splitlines()[-1])
+    bad = [c for c in res["checks"] if not c["ok"]]
+    assert res["ok"] and not bad, (bad, p.stderr[-2000:])
+    assert res["max_rel_l2"] < 1e-4

@@ -108,7 +108,7 @@ def test_js_matvec_matches_c_oracle(tmp_path):
 
 
 ADDON_EXPORTS = ["init", "lastError", "uploadQ80", "matvec", "moeCreate", "moeSetGating", "moeForward",
-                 "release"]
+                 "ggufOpen", "ggufTensors", "ggufMoeParams", "ggufMoeLayer", "release"]
 
 
 def test_addon_exports():
@@ -128,3 +128,27 @@ def test_install_fails_loudly_without_device():
     out = p.stdout.strip()
     assert out.startswith("threw: qq_init failed"), out
     assert out.endswith("| cpu")   # nothing was rebound
+
+
+def test_addon_gguf_reader_matches_oracle(tmp_path):
+    """ggufOpen / ggufTensors / ggufMoeParams need no device: the addon's view of
+    a synthetic two-block file equals the oracle's GGUFReader restatement."""
+    import gguf_ref
+    L = synth.moe_layer(13, H=64, F=32, E=8, K=2)
+    data, _ = synth.moe_gguf([L, L], K=3, alignment=64)
+    path = tmp_path / "m.gguf"
+    path.write_bytes(data)
+    code = ("const a=require(%r); const g=a.ggufOpen(%r);"
+            "console.log(JSON.stringify({t:a.ggufTensors(g), p:a.ggufMoeParams(g,1,0,-1)}));"
+            "a.release(g); let e=''; try { a.ggufOpen(%r); } catch (x) { e=String(x); }"
+            "console.log(JSON.stringify(e));") % (
+        os.path.join(ROOT, "qwenqwen3.js_amd", "qq_napi.node"), str(path), str(path) + ".missing")
+    p = subprocess.run([NODE, "-e", code], capture_output=True, text=True, timeout=60, check=True)
+    lines = p.stdout.strip().splitlines()
+    got = json.loads(lines[0])
+    r = gguf_ref.Reader(data)
+    assert got["t"] == [dict(name=t["name"], shape=t["shape"], type=t["type"], offset=t["offset"],
+                             nbytes=t["nbytes"]) for t in r.tensors]
+    H, F, E, K, gating, rtype, has_bias = gguf_ref.moe_params(r, 1)
+    assert got["p"] == dict(H=H, F=F, E=E, K=K, gating=gating, routerType=rtype, hasBias=has_bias)
+    assert K == 3 and "cannot open" in json.loads(lines[1])
