@@ -4,17 +4,14 @@
 // form a dense [n_e x H] x [H x F] contraction (the reference runs them as
 // n_e separate matvecs, src/lfm2-engine.js:471-478 per token).  After the
 // dispatch (grouped.hip) every expert's slots are cut into row tiles of
-// MF_BM slots, and per (row tile, column tile):
+// MG_BM slots, and per (row tile, column tile):
 //   gate/up  A = fp16 activations of the tile's tokens (gathered by perm),
-//            B = 64 gate + 64 up columns dequantised from Q8_0 into LDS as
-//            fp16 w = fp16(q * d); v_mfma_f32_16x16x32_f16 with fp32
-//            accumulators; epilogue silu(g) * u -> fp16 act[slot][F]
-//   down     A = act rows of the tile, B = 128 down columns dequantised
-//            likewise -> y[slot][H] fp16
+//            B = gate and up columns dequantised from Q8_0 to fp16
+//            w = fp16(q * d); fp32 accumulators; epilogue silu(g) * u ->
+//            fp16 act[slot][F]
+//   down     A = act rows of the tile, B = down columns likewise ->
+//            y[slot][H] fp16
 // followed by the gather combine of the fp32 path (rank order, fp32 steps).
-// One Q8_0 block (32 values of the reduction dimension) is one MFMA K step;
-// the next block's global loads are in flight while the current block's
-// MFMAs run, and LDS is double buffered with one barrier per step.
 //
 // Accuracy: fp16 activations, weights and expert outputs (relative rounding
 // 2^-11 each), fp32 accumulation: ~1e-3 relative L2 on the layer output,
@@ -28,10 +25,6 @@ namespace qq {
 typedef _Float16 h8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
-
-constexpr int MF_BM = 128;       // slots per row tile
-constexpr int MF_BN = 128;       // weight columns per workgroup
-constexpr int MF_THREADS = 256;  // 4 waves, 2 x 2 over the 128 x 128 tile
 
 struct MfmaArgs {
     const _Float16 *xh;      // [T][H] activations in fp16
@@ -84,237 +77,314 @@ __device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4
 
 __device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit_cast(_Float16, b); }
 
-// LDS tile of one operand and stage: 128 rows x KB Q8_0 blocks (32*KB halves,
-// 4*KB chunks of 16 bytes).  Chunk c of row r sits at r*64*KB + 16*(c ^ s(r)).
-// For KB = 1, s(r) = ((r >> 1) ^ (r >> 2)) & 3: any 8 consecutive rows of a
-// fragment read (same chunk) fall in 8 different 16-byte groups of a 128-byte
-// bank row and any 16 in 16 different groups of a 256-byte one; so do the
-// staging writes.  For KB = 2, s(r) = (r >> 1) & 7.
-template <int KB>
-struct MfTile {
-    static constexpr int BYTES = MF_BM * 64 * KB;
-    static __device__ __forceinline__ int off(int r, int c)
-    {
-        return r * 64 * KB + 16 * (c ^ (KB == 1 ? (((r >> 1) ^ (r >> 2)) & 3) : ((r >> 1) & 7)));
-    }
+// ---------------------------------------------------------------------------
+// Grouped GEMM on v_mfma_f32_32x32x16_f16.
+//
+// Workgroup = one row tile (MG_BM slots of one expert) x a column tile; its
+// 4 waves split the columns, and every wave computes all MG_BM rows of its
+// columns for two 32-column B matrices (gate/up: the same 32 features of the
+// gate and of the up tensor; down: two adjacent 32-column groups).  Wave tile
+// 128 x 64, accumulators 4 row fragments x 2 x 16 floats.
+//
+// Per Q8_0 block (32 values of the reduction dimension) and stage:
+//   A  the tile's 128 rows x 32 halves (8 KB), copied by the 4 waves with
+//      global_load_lds_dwordx4 in an XOR-swizzled row order, shared by all;
+//   B  each wave's raw int8 columns (2 x 32 columns x 32 B), copied as is;
+//      each wave reads back only its own columns and dequantises them in
+//      registers to fp16 w = fp16(q * d);
+//   d  the fp16 scales of the tile's columns (waves 0 and 1, 256 B each).
+// The copies run MG_AHEAD blocks ahead through a ring of MG_STAGES stages;
+// one barrier per block.  The reduction index is permuted identically in A
+// and B: lane half h = lane / 32 carries k = 16h + 8s + j in MFMA step s,
+// so a lane's B operand is the 16 contiguous bytes 16h .. 16h+15 of its
+// column's block and its A operand is chunk 2h + s of its row.
+// ---------------------------------------------------------------------------
+typedef float f16v_t __attribute__((ext_vector_type(16)));
+
+constexpr int MG_BM = 128;
+constexpr int MG_THREADS = 256;
+#ifndef MG_STAGES_CFG
+#define MG_STAGES_CFG 4
+#define MG_AHEAD_CFG 2
+#define MG_OCC_CFG 2
+#endif
+constexpr int MG_STAGES = MG_STAGES_CFG;
+constexpr int MG_AHEAD = MG_AHEAD_CFG;       // blocks copied ahead of the one being read
+constexpr int MG_A = MG_BM * 64;             // A: 128 rows x 64 B
+constexpr int MG_B = 4 * 2 * 1024;           // B: 4 waves x 2 matrices x 32 columns x 32 B
+constexpr int MG_S = 2 * 256;                // scales: 2 x 128 columns x 2 B
+constexpr int MG_STAGE = MG_A + MG_B + MG_S;
+// The copy of block h + MG_AHEAD is issued after the barrier of block h.  A
+// wave may then still be reading stage h (B operands of block h) and stage
+// h - 1 (A fragments of block h - 1), and the stage rewritten held block
+// h + MG_AHEAD - MG_STAGES, whose last read precedes barrier h when
+// MG_AHEAD <= MG_STAGES - 2.
+static_assert(MG_STAGES >= MG_AHEAD + 2 && MG_AHEAD >= 1, "ring stage written while still read");
+
+// A slot of (row r, 16-byte chunk c): rows of 4 chunks, chunk order XORed
+// with s(r) = ((r >> 1) ^ (r >> 2)) & 3, so that the 16 rows a 16-lane group
+// of a fragment read touches 16 different 16-byte bank groups.
+__device__ __forceinline__ int mg_aslot(int r, int c) { return 4 * r + (c ^ (((r >> 1) ^ (r >> 2)) & 3)); }
+
+// B slot of (column f in 0..31, half h): lanes 0-15, 16-31, 32-47, 48-63 of a
+// fragment read land in 16 consecutive slots each.
+__device__ __forceinline__ int mg_bslot(int f, int h) { return (f & 15) + 16 * h + 32 * (f >> 4); }
+
+// Copy sources of block 0: wave-uniform bases plus 32-bit per-lane offsets.
+struct MgSrc {
+    const char *abase, *bbase0, *bbase1, *sbase;
+    uint32_t a0, a1;           // this lane's A chunks for its two copies
+    uint32_t b0, b1;           // this lane's 16 B of the two B matrices
+    uint32_t sc;               // waves 0, 1: this lane's 4 bytes of scales
+    size_t bstep, sstep;       // one block of B (columns * 32 B) and of the scales (columns * 2 B)
 };
 
-// Per-thread staging sources: 32 bytes (16 halves) of one A row and 16 int8 of
-// one B column per Q8_0 block, advanced by a fixed stride per block.
-struct MfSrc {
-    const char *a;           // A row, this thread's half of block 0
-    const int8_t *q;         // B column, this thread's half of block 0
-    const uint16_t *d;       // the column's scale at block 0
-    size_t qstep, dstep;     // one block of the B matrix (rows * 32 bytes, rows halves)
-    bool ok;                 // B column in range (else zero scale)
-};
-
-// Shared main loop of the two GEMMs over nb blocks (nb % KB == 0).  Stage = A
-// tile + B tile (fp16) of KB blocks; two stages double buffered; the next
-// stage's global loads are in flight while this stage's MFMAs run; one
-// barrier per stage.  Wave fragments: A rows arow[i], B columns bcol[j] (row
-// bases of 16-row fragments within the tile).
-template <int KB>
-__device__ __forceinline__ void mf_mainloop(const MfSrc &src, int nb, char *lds, int sr, int sh,
-                                            const int (&arow)[4], const int (&bcol)[4],
-                                            f4_t (&acc)[4][4])
+// s_waitcnt vmcnt(PER * later), later = 0 .. 6 blocks still in flight behind this one
+template <int PER>
+__device__ __forceinline__ void mg_wait(int later)
 {
-    using T = MfTile<KB>;
-    const int lane = threadIdx.x & (WAVE - 1);
-    // staging offsets: block b of this thread's row sr, chunks 4b + 2sh, +1
-    int w0[KB], w1[KB];
-#pragma unroll
-    for (int b = 0; b < KB; b++) {
-        w0[b] = T::off(sr, 4 * b + 2 * sh);
-        w1[b] = T::off(sr, 4 * b + 2 * sh + 1);
-    }
-    // fragment offsets: row base + lane%16, chunk 4b + lane/16
-    int ao[KB][4], bo[KB][4];
-#pragma unroll
-    for (int b = 0; b < KB; b++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            ao[b][i] = T::off(arow[i] + (lane & 15), 4 * b + (lane >> 4));
-            bo[b][i] = T::BYTES + T::off(bcol[i] + (lane & 15), 4 * b + (lane >> 4));
-        }
-
-    const char *ap = src.a;
-    const int8_t *qp = src.q;
-    const uint16_t *dp = src.d;
-    uint4 xa[KB], xb[KB], wv[KB];
-    uint16_t ws[KB];
-    auto load = [&]() {
-#pragma unroll
-        for (int b = 0; b < KB; b++) {
-            xa[b] = *reinterpret_cast<const uint4 *>(ap + b * QK * 2);
-            xb[b] = *reinterpret_cast<const uint4 *>(ap + b * QK * 2 + 16);
-            wv[b] = *reinterpret_cast<const uint4 *>(qp + b * src.qstep);
-            ws[b] = dp[b * src.dstep];
-        }
-        ap += KB * QK * 2;
-        qp += KB * src.qstep;
-        dp += KB * src.dstep;
-    };
-    auto store = [&](char *st) {
-#pragma unroll
-        for (int b = 0; b < KB; b++) {
-            *reinterpret_cast<uint4 *>(st + w0[b]) = xa[b];
-            *reinterpret_cast<uint4 *>(st + w1[b]) = xb[b];
-            uint4 lo, hi;
-            dequant16(wv[b], src.ok ? half_bits(ws[b]) : (_Float16)0.0f, lo, hi);
-            *reinterpret_cast<uint4 *>(st + T::BYTES + w0[b]) = lo;
-            *reinterpret_cast<uint4 *>(st + T::BYTES + w1[b]) = hi;
-        }
-    };
-    auto compute = [&](const char *st) {
-#pragma unroll
-        for (int b = 0; b < KB; b++) {
-            h8_t af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; i++) af[i] = *reinterpret_cast<const h8_t *>(st + ao[b][i]);
-#pragma unroll
-            for (int j = 0; j < 4; j++) bf[j] = *reinterpret_cast<const h8_t *>(st + bo[b][j]);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-    };
-
-    const int nst = nb / KB;
-    load();
-    store(lds);
-    __syncthreads();
-    for (int k = 0; k < nst; k++) {
-        char *cur = lds + (k & 1) * 2 * T::BYTES;
-        char *nxt = lds + ((k + 1) & 1) * 2 * T::BYTES;
-        const bool more = k + 1 < nst;
-        if (more) load();
-        compute(cur);
-        if (more) store(nxt);
-        __syncthreads();
+    switch (later) {
+    case 0: wait_vm<0>(); break;
+    case 1: wait_vm<PER>(); break;
+    case 2: wait_vm<2 * PER>(); break;
+    case 3: wait_vm<3 * PER>(); break;
+    case 4: wait_vm<4 * PER>(); break;
+    case 5: wait_vm<5 * PER>(); break;
+    default: wait_vm<6 * PER>(); break;
     }
 }
+static_assert(MG_AHEAD <= 6, "mg_wait covers up to 6 blocks in flight");
 
-// ---------------------------------------------------------------------------
-// gate/up: tile = MF_BM slots x 64 features (64 gate + 64 up columns).
-// Wave (wm, wn): slots wm*64 .. +64, features wn*32 .. +32 -> 4 x (2 gate +
-// 2 up) fragments of 16 x 16.
-// ---------------------------------------------------------------------------
-template <int KB>
-__global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_gateup_kernel(MfmaArgs a)
+template <int NFR>
+__device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds, int sc_off0, int sc_off1,
+                                            f16v_t (&acc)[4][2])
 {
-    __shared__ __align__(16) char lds[4 * MfTile<KB>::BYTES];
-    __shared__ int rowtok[MF_BM];
+    const int lane = threadIdx.x & (WAVE - 1);
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: SGPR operands
+    const uint32_t base = lds_u32(lds);
+    // copy destinations within a stage (wave-uniform)
+    const uint32_t da0 = base + (128 * wave) * 16, da1 = da0 + 64 * 16;
+    const uint32_t db0 = base + MG_A + (wave * 2) * 1024, db1 = db0 + 1024;
+    const uint32_t ds = base + MG_A + MG_B + wave * 256;
+    // fragment reads within a stage: row 32i + x has the swizzle of row x
+    // (s(r) depends on r mod 8 only), so fragment i is fragment 0 + 2048 i
+    int ao[2];
+#pragma unroll
+    for (int st = 0; st < 2; st++) ao[st] = 16 * mg_aslot(lane & 31, 2 * (lane >> 5) + st);
+    const int bo = MG_A + (wave * 2) * 1024 + 16 * mg_bslot(lane & 31, lane >> 5);
 
-    const int nft = (a.F + 63) / 64;
-    const int tile = blockIdx.x / nft, ft = blockIdx.x - tile * nft;
-    if (tile >= *a.n_tiles) return;
+    auto issue = [&](int b) {
+        const uint32_t so = (uint32_t)(b % MG_STAGES) * MG_STAGE;
+        const char *ab = src.abase + (size_t)b * 64;
+        dma16s(src.a0, ab, da0 + so);
+        dma16s(src.a1, ab, da1 + so);
+        dma16s(src.b0, src.bbase0 + (size_t)b * src.bstep, db0 + so);
+        dma16s(src.b1, src.bbase1 + (size_t)b * src.bstep, db1 + so);
+        if (wave < 2) dma4s(src.sc, src.sbase + (size_t)b * src.sstep, ds + so);
+    };
+    // per-wave copies per block: 5 (waves 0, 1) or 4.  Wait until block x's
+    // copies landed when blocks up to `upto` have been issued.
+    auto wait_block = [&](int x, int upto) {
+        const int later = min(nb - 1, upto) - x;
+        if (wave < 2) mg_wait<5>(later); else mg_wait<4>(later);
+    };
+    // Operands fetched one block ahead: B dequantised (both matrices, both
+    // MFMA steps) and the A fragments of MFMA step 0.
+    struct Frag {
+        h8_t b[2][2];
+        h8_t a0[NFR];
+    };
+    auto fetch = [&](int b, Frag &f) {
+        const char *st = lds + (b % MG_STAGES) * MG_STAGE;
+        const uint4 q0 = *reinterpret_cast<const uint4 *>(st + bo);
+        const uint4 q1 = *reinterpret_cast<const uint4 *>(st + bo + 1024);
+        const _Float16 d0 = *reinterpret_cast<const _Float16 *>(st + sc_off0);
+        const _Float16 d1 = *reinterpret_cast<const _Float16 *>(st + sc_off1);
+#pragma unroll
+        for (int i = 0; i < NFR; i++) f.a0[i] = *reinterpret_cast<const h8_t *>(st + ao[0] + 2048 * i);
+        uint4 lo0, hi0, lo1, hi1;
+        dequant16(q0, d0, lo0, hi0);
+        dequant16(q1, d1, lo1, hi1);
+        f.b[0][0] = __builtin_bit_cast(h8_t, lo0);
+        f.b[0][1] = __builtin_bit_cast(h8_t, hi0);
+        f.b[1][0] = __builtin_bit_cast(h8_t, lo1);
+        f.b[1][1] = __builtin_bit_cast(h8_t, hi1);
+    };
+    // block b's MFMAs; the step-1 A fragments are read here, under step 0's MFMAs
+    auto mma = [&](int b, const Frag &f) {
+        const char *st = lds + (b % MG_STAGES) * MG_STAGE;
+        h8_t a1[NFR];
+#pragma unroll
+        for (int i = 0; i < NFR; i++) a1[i] = *reinterpret_cast<const h8_t *>(st + ao[1] + 2048 * i);
+#pragma unroll
+        for (int i = 0; i < NFR; i++) {
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a0[i], f.b[0][0], acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a0[i], f.b[1][0], acc[i][1], 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < NFR; i++) {
+            acc[i][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i], f.b[0][1], acc[i][0], 0, 0, 0);
+            acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i], f.b[1][1], acc[i][1], 0, 0, 0);
+        }
+    };
+
+    // Software pipeline: block b+1's B operands and step-0 A fragments are
+    // read (and B dequantised) while block b's MFMAs run (two register sets,
+    // loop unrolled by two).
+#pragma unroll
+    for (int b = 0; b < MG_AHEAD; b++)
+        if (b < nb) issue(b);
+    Frag f0, f1;
+    wait_block(0, MG_AHEAD - 1);
+    __syncthreads();
+    fetch(0, f0);
+    int b = 0;
+    for (; b + 1 < nb; b += 2) {
+        // f0 holds block b
+        if (b + MG_AHEAD < nb) issue(b + MG_AHEAD);
+        wait_block(b + 1, b + MG_AHEAD);
+        __syncthreads();
+        fetch(b + 1, f1);
+        mma(b, f0);
+        // f1 holds block b + 1
+        if (b + 1 + MG_AHEAD < nb) issue(b + 1 + MG_AHEAD);
+        if (b + 2 < nb) {
+            wait_block(b + 2, b + 1 + MG_AHEAD);
+            __syncthreads();
+            fetch(b + 2, f0);
+        }
+        mma(b + 1, f1);
+    }
+    if (b < nb) mma(b, f0);   // odd block count: the last block, fetched above
+}
+
+// blockIdx -> (row tile, column tile): the dispatcher deals workgroups to the
+// 8 XCDs round robin, so XCD x runs blocks x, x+8, ...; each XCD takes a
+// contiguous run of the real work items (row-tile major), so the column
+// tiles of a row tile share its A rows, and the row tiles of an expert its
+// weights, in one L2.  False once past the real items.
+__device__ __forceinline__ bool mg_item(int n_tiles, int nct, int &tile, int &ct)
+{
+    const int R = n_tiles * nct;
+    const int per = (R + 7) >> 3;
+    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+    const int w = x * per + i;
+    if (i >= per || w >= R) return false;
+    tile = w / nct;
+    ct = w - tile * nct;
+    return true;
+}
+
+// MODE 0: gate/up -> SwiGLU -> act (column tile = 128 features: wave w takes
+//         features 32w..32w+31 of the gate and of the up tensor);
+// MODE 1: down -> y (column tile = 256 outputs: wave w takes 64w..64w+63).
+template <int MODE>
+__global__ __launch_bounds__(MG_THREADS, MG_OCC_CFG) void moe_mg_kernel(MfmaArgs a)
+{
+    __shared__ __align__(16) char lds[MG_STAGES * MG_STAGE];
+    __shared__ uint32_t rowoff[MG_BM];
+
+    const int ncols = MODE == 0 ? a.F : a.H;          // columns of a B matrix
+    const int tw = MODE == 0 ? 128 : 256;             // columns per column tile
+    const int nct = (ncols + tw - 1) / tw;
+    int tile, ct;
+    if (!mg_item(*a.n_tiles, nct, tile, ct)) return;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
-    const int n = min(MF_BM, a.counts[e] - m0);
+    const int n = min(MG_BM, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
-    const int f0 = ft * 64;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nb = MODE == 0 ? a.nbH : a.nbF;
+    const int kdim = MODE == 0 ? a.H : a.F;
 
-    if (tid < MF_BM) rowtok[tid] = a.perm[slot0 + min(tid, n - 1)] / a.K;
+    // A row offsets (bytes): gate/up gathers token rows of xh, down reads act rows
+    if (tid < MG_BM) {
+        const int r = min(tid, n - 1);
+        rowoff[tid] = (uint32_t)((MODE == 0 ? (size_t)(a.perm[slot0 + r] / a.K) : (size_t)(slot0 + r)) * kdim * 2);
+    }
     __syncthreads();
 
-    // staging: thread -> row / column tid/2, 16-value half tid&1
-    const int sr = tid >> 1, sh = tid & 1;
-    const int f = f0 + (sr & 63);
-    const int fc = min(f, a.F - 1);
-    MfSrc src;
-    src.a = reinterpret_cast<const char *>(a.xh + (size_t)rowtok[sr] * a.H) + sh * 32;
-    const size_t o = bm_index(e, a.nbH, 0, a.F, fc);
-    src.q = (sr < 64 ? a.gq : a.uq) + o * QK + sh * 16;
-    src.d = (sr < 64 ? a.gd : a.ud) + o;
-    src.qstep = (size_t)a.F * QK;
-    src.dstep = (size_t)a.F;
-    src.ok = f < a.F;
+    MgSrc src;
+    src.abase = MODE == 0 ? reinterpret_cast<const char *>(a.xh) : reinterpret_cast<const char *>(a.act);
+    {
+        const int s0 = 128 * wave + lane, s1 = s0 + 64;
+        const int r0 = s0 >> 2, r1 = s1 >> 2;
+        src.a0 = rowoff[r0] + 16 * ((s0 & 3) ^ (((r0 >> 1) ^ (r0 >> 2)) & 3));
+        src.a1 = rowoff[r1] + 16 * ((s1 & 3) ^ (((r1 >> 1) ^ (r1 >> 2)) & 3));
+    }
+    // this wave's two 32-column groups (clamped into range; stores are masked)
+    const int c0 = MODE == 0 ? ct * 128 + 32 * wave : ct * 256 + 64 * wave;
+    const int c1 = MODE == 0 ? c0 : c0 + 32;
+    const int8_t *q0 = MODE == 0 ? a.gq : a.dq;
+    const int8_t *q1 = MODE == 0 ? a.uq : a.dq;
+    const uint16_t *dd0 = MODE == 0 ? a.gd : a.dd;
+    const uint16_t *dd1 = MODE == 0 ? a.ud : a.dd;
+    {
+        const int f = (lane & 15) + 16 * (lane >> 5), h = (lane >> 4) & 1;   // inverse of mg_bslot
+        const int g0 = min(c0, ncols - 32) + f, g1 = min(c1, ncols - 32) + f;
+        src.bbase0 = reinterpret_cast<const char *>(q0 + bm_index(e, nb, 0, ncols, 0) * QK);
+        src.bbase1 = reinterpret_cast<const char *>(q1 + bm_index(e, nb, 0, ncols, 0) * QK);
+        src.b0 = (uint32_t)(g0 * QK + 16 * h);
+        src.b1 = (uint32_t)(g1 * QK + 16 * h);
+        // scales: wave 0 -> columns [cs, cs+128) of matrix 0, wave 1 -> of matrix 1
+        // (gate/up) or the next 128 (down); 2 per lane
+        const int cs = MODE == 0 ? ct * 128 : ct * 256 + 128 * (wave & 1);
+        const uint16_t *dsrc = (MODE == 0 && wave == 1) ? dd1 : dd0;
+        src.sbase = reinterpret_cast<const char *>(dsrc + bm_index(e, nb, 0, ncols, 0));
+        src.sc = (uint32_t)(2 * min(cs + 2 * lane, ncols - 2));
+        src.bstep = (size_t)ncols * QK;
+        src.sstep = (size_t)ncols * 2;
+    }
+    // scale offsets within a stage for this lane's columns of the two matrices
+    int so0, so1;
+    if (MODE == 0) {
+        so0 = MG_A + MG_B + (32 * wave + (lane & 31)) * 2;
+        so1 = so0 + 256;
+    } else {
+        const int l0 = 64 * wave + (lane & 31), l1 = l0 + 32;
+        so0 = MG_A + MG_B + (l0 >> 7) * 256 + (l0 & 127) * 2;
+        so1 = MG_A + MG_B + (l1 >> 7) * 256 + (l1 & 127) * 2;
+    }
 
-    const int arow[4] = {wm * 64, wm * 64 + 16, wm * 64 + 32, wm * 64 + 48};
-    const int bcol[4] = {wn * 32, wn * 32 + 16, 64 + wn * 32, 64 + wn * 32 + 16};
-    f4_t acc[4][4];
+    f16v_t acc[4][2];
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    mf_mainloop<KB>(src, a.nbH, lds, sr, sh, arow, bcol, acc);
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+    const int nfr = (n + 31) >> 5;
+    switch (nfr) {
+    case 1: mg_mainloop<1>(src, nb, lds, so0, so1, acc); break;
+    case 2: mg_mainloop<2>(src, nb, lds, so0, so1, acc); break;
+    case 3: mg_mainloop<3>(src, nb, lds, so0, so1, acc); break;
+    default: mg_mainloop<4>(src, nb, lds, so0, so1, acc); break;
+    }
 
-    // lane holds rows 4*(lane/16) + r, column lane % 16 of each fragment
-    const int cl = lane & 15, rq = 4 * (lane >> 4);
+    // lane holds column lane % 32 and rows 8*(r/4) + 4*(lane/32) + r%4 of each fragment
+    const int cl = lane & 31, rh = 4 * (lane >> 5);
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 4; i++) {
+        if (32 * i >= n) break;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-            const int ff = f0 + wn * 32 + j * 16 + cl;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = wm * 64 + i * 16 + rq + r;
-                if (row < n && ff < a.F) {
-                    const float g = acc[i][j][r], u = acc[i][j + 2][r];
+        for (int r = 0; r < 16; r++) {
+            const int row = 32 * i + 8 * (r >> 2) + rh + (r & 3);
+            if (row >= n) continue;
+            if (MODE == 0) {
+                const int ff = c0 + cl;
+                if (ff < a.F) {
+                    const float g = acc[i][0][r], u = acc[i][1][r];
                     // hardware exp and reciprocal (~1 ulp each), far inside the fp16 rounding
                     const float v = g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
                     a.act[(size_t)(slot0 + row) * a.F + ff] = (_Float16)v;
                 }
+            } else {
+                _Float16 *yr = a.y + (size_t)(slot0 + row) * a.H;
+                if (c0 + cl < a.H) yr[c0 + cl] = (_Float16)acc[i][0][r];
+                if (c1 + cl < a.H) yr[c1 + cl] = (_Float16)acc[i][1][r];
             }
         }
-}
-
-// ---------------------------------------------------------------------------
-// down: tile = MF_BM slots x 128 output columns; wave (wm, wn): slots
-// wm*64 .. +64, columns wn*64 .. +64 -> 4 x 4 fragments.
-// ---------------------------------------------------------------------------
-template <int KB>
-__global__ __launch_bounds__(MF_THREADS, 4) void moe_mfma_down_kernel(MfmaArgs a)
-{
-    __shared__ __align__(16) char lds[4 * MfTile<KB>::BYTES];
-
-    const int nht = (a.H + MF_BN - 1) / MF_BN;
-    const int tile = blockIdx.x / nht, ht = blockIdx.x - tile * nht;
-    if (tile >= *a.n_tiles) return;
-    const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
-    const int n = min(MF_BM, a.counts[e] - m0);
-    const int slot0 = a.offsets[e] + m0;
-    const int h0 = ht * MF_BN;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave & 1, wn = wave >> 1;
-
-    const int sr = tid >> 1, sh = tid & 1;
-    const int h = h0 + sr;
-    const int hc = min(h, a.H - 1);
-    MfSrc src;
-    src.a = reinterpret_cast<const char *>(a.act + (size_t)(slot0 + min(sr, n - 1)) * a.F) + sh * 32;
-    const size_t o = bm_index(e, a.nbF, 0, a.H, hc);
-    src.q = a.dq + o * QK + sh * 16;
-    src.d = a.dd + o;
-    src.qstep = (size_t)a.H * QK;
-    src.dstep = (size_t)a.H;
-    src.ok = h < a.H;
-
-    const int arow[4] = {wm * 64, wm * 64 + 16, wm * 64 + 32, wm * 64 + 48};
-    const int bcol[4] = {wn * 64, wn * 64 + 16, wn * 64 + 32, wn * 64 + 48};
-    f4_t acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) acc[i][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    mf_mainloop<KB>(src, a.nbF, lds, sr, sh, arow, bcol, acc);
-
-    const int cl = lane & 15, rq = 4 * (lane >> 4);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int hh = h0 + wn * 64 + j * 16 + cl;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int row = wm * 64 + i * 16 + rq + r;
-                if (row < n && hh < a.H) a.y[(size_t)(slot0 + row) * a.H + hh] = (_Float16)acc[i][j][r];
-            }
-        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -323,7 +393,7 @@ bool mfma_supported(const qq_moe *m) { return m->H % QK == 0 && m->F % QK == 0; 
 
 static size_t al256(size_t b) { return (b + 255) & ~(size_t)255; }
 
-static int tile_cap(const qq_moe *m, int T) { return T * m->K / MF_BM + m->E; }
+static int tile_cap(const qq_moe *m, int T) { return T * m->K / MG_BM + m->E; }
 
 size_t mfma_work_bytes(const qq_moe *m, int T)
 {
@@ -345,7 +415,7 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     int32_t *perm = reinterpret_cast<int32_t *>(p);    p += al256(P * 4);
     int32_t *inv = reinterpret_cast<int32_t *>(p);     p += al256(P * 4);
     DispatchTiles tiles;
-    tiles.bm = MF_BM;
+    tiles.bm = MG_BM;
     tiles.cap = cap;
     tiles.e = reinterpret_cast<int32_t *>(p);          p += al256((size_t)cap * 4);
     tiles.m0 = reinterpret_cast<int32_t *>(p);         p += al256((size_t)cap * 4);
@@ -386,15 +456,15 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     a.nbH = m->H / QK;
     a.nbF = m->F / QK;
 
-    // one Q8_0 block per pipeline stage: two per stage halve the barriers but
-    // double the LDS per workgroup, and the lost occupancy costs more
-    const dim3 g1((unsigned)cap * ((m->F + 63) / 64)), g2((unsigned)cap * ((m->H + MF_BN - 1) / MF_BN));
+    // XCD-aware grids (mg_item): 8 * ceil(items / 8) workgroups at most
+    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 127) / 128) + 7) / 8);
+    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 255) / 256) + 7) / 8);
     prof_begin(ctx, K_MFMA_GATEUP);
-    QQ_LAUNCH(ctx, moe_mfma_gateup_kernel<1>, g1, dim3(MF_THREADS), 0, a);
+    QQ_LAUNCH(ctx, moe_mg_kernel<0>, dim3(g1), dim3(MG_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_MFMA_DOWN);
-    QQ_LAUNCH(ctx, moe_mfma_down_kernel<1>, g2, dim3(MF_THREADS), 0, a);
+    QQ_LAUNCH(ctx, moe_mg_kernel<1>, dim3(g2), dim3(MG_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return launch_combine(ctx, m, T, y, true, inv, w, hidden);

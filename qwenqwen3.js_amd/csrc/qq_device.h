@@ -98,6 +98,18 @@ __device__ __forceinline__ void dma4(const void *g, uint32_t lds)
     asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
                  :: "v"(g), "s"(lds) : "memory");
 }
+// The same with a wave-uniform base address (SGPR pair) and a 32-bit
+// per-lane byte offset: one VGPR per lane instead of two.
+__device__ __forceinline__ void dma16s(uint32_t off, const void *base, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+                 :: "v"(off), "s"(base), "s"(lds) : "memory");
+}
+__device__ __forceinline__ void dma4s(uint32_t off, const void *base, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+                 :: "v"(off), "s"(base), "s"(lds) : "memory");
+}
 
 template <int N>
 __device__ __forceinline__ void wait_vm()
