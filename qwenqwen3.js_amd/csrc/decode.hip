@@ -448,22 +448,33 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     }
 }
 
-// 256 threads per 32 outputs: thread (group q, output jl) sums the slices
-// s = q, q+8, ... (NSP of them, NSP = ceil(NS/8)) of up to 4 ranks, with all
-// its loads in flight at once; the 8 groups are then summed in a fixed order.
-template <int NSP>
+// 256 threads per CW outputs: thread (group q, output jl) sums the slices
+// s = q, q + NG, ... (NSP of them, NG = 256 / CW groups) of up to 4 ranks,
+// with all its loads in flight at once; the NG groups are then summed in a
+// fixed order.
+template <int CW, int NSP>
 __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
     const float *__restrict__ partial, int H, int NS, int K, const int32_t *__restrict__ route_idx,
     const double *__restrict__ route_w, MaskBits mask, float *__restrict__ hidden,
     uint32_t *__restrict__ epoch_word)
 {
+    constexpr int NG = 256 / CW;
     // the experts kernel of this call has finished: the next call takes a new epoch
     if (blockIdx.x == 0 && threadIdx.x == 0) epoch_word[0] = epoch_word[0] + 1u;
-    __shared__ float red[MAX_K][8][32];
-    const int jl = threadIdx.x & 31;
-    const int q = threadIdx.x >> 5;
-    const int j = blockIdx.x * 32 + jl;
+    __shared__ float red[MAX_K][NG][CW];
+    __shared__ int sh_e[MAX_K];
+    __shared__ double sh_w[MAX_K];
+    const int jl = threadIdx.x % CW;
+    const int q = threadIdx.x / CW;
+    const int j = blockIdx.x * CW + jl;
     const int jc = min(j, H - 1);
+    // the routing and the residual row are loaded with the partial sums, in
+    // the same round trip
+    if (threadIdx.x >= CW && threadIdx.x < CW + K) {
+        sh_e[threadIdx.x - CW] = route_idx[threadIdx.x - CW];
+        sh_w[threadIdx.x - CW] = route_w[threadIdx.x - CW];
+    }
+    const float h_in = hidden[jc];
     for (int k0 = 0; k0 < K; k0 += 4) {
         float v[4][NSP];
 #pragma unroll
@@ -471,7 +482,7 @@ __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
             const int k = min(k0 + kk, K - 1);
 #pragma unroll
             for (int i = 0; i < NSP; i++) {
-                const int s = min(q + 8 * i, NS - 1);
+                const int s = min(q + NG * i, NS - 1);
                 v[kk][i] = partial[((size_t)k * NS + s) * H + jc];
             }
         }
@@ -481,22 +492,22 @@ __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
             float y = 0.0f;
 #pragma unroll
             for (int i = 0; i < NSP; i++)
-                if (q + 8 * i < NS) y += v[kk][i];
+                if (q + NG * i < NS) y += v[kk][i];
             if (k0 + kk < K) red[k0 + kk][q][jl] = y;
         }
     }
     __syncthreads();
-    if (threadIdx.x < 32 && j < H) {
+    if (threadIdx.x < CW && j < H) {
         float acc = 0.0f;
         for (int k = 0; k < K; k++) {
-            const int e = route_idx[k];
+            const int e = sh_e[k];
             if ((unsigned)e >= (unsigned)MAX_E || mask_has(mask, e)) continue;
             float y = red[k][0][jl];
 #pragma unroll
-            for (int p = 1; p < 8; p++) y += red[k][p][jl];
-            acc = (float)((double)acc + route_w[k] * (double)y);
+            for (int p = 1; p < NG; p++) y += red[k][p][jl];
+            acc = (float)((double)acc + sh_w[k] * (double)y);
         }
-        hidden[j] = hidden[j] + acc;
+        hidden[j] = h_in + acc;
     }
 }
 
@@ -572,17 +583,20 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
 
-    const int nsp = (a.NS + 7) / 8;
-    const dim3 cgrid((m->H + 31) / 32);
+    // 32 outputs per workgroup (16 or 8, with more workgroups, measured slower)
+    constexpr int CW = 32, NG = 256 / CW;
+    const int nsp = (a.NS + NG - 1) / NG;
+    const dim3 cgrid((m->H + CW - 1) / CW);
 #define QQ_CB(N)                                                                                 \
-    QQ_LAUNCH(ctx, moe_decode_combine_kernel<N>, cgrid, dim3(256), 0, a.partial, \
+    QQ_LAUNCH(ctx, (moe_decode_combine_kernel<CW, N>), cgrid, dim3(256), 0, a.partial, \
                        m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden, ctx->sync_epoch)
     prof_begin(ctx, K_DECODE_COMBINE);
     if (nsp <= 1) QQ_CB(1);
     else if (nsp <= 2) QQ_CB(2);
     else if (nsp <= 4) QQ_CB(4);
     else if (nsp <= 8) QQ_CB(8);
-    else QQ_CB(16);
+    else if (nsp <= 16) QQ_CB(16);
+    else QQ_CB(32);
     prof_end(ctx);
 #undef QQ_CB
     QQ_HIP(ctx, hipGetLastError());
