@@ -14,7 +14,8 @@ Other workloads (--workload): decode_b64 (64-token decode batch), prefill_2048
 (2048-token chunk, Zipf-skewed routing), stack22_decode / stack22_prefill (22
 independently seeded layers, rmsnorm + MoE per layer, 1 token resp. a
 4096-token chunk per step), matvec (one Q8_0 matvec 1024 -> 3072, rotating
-over 80 weights).
+over 80 weights), qwen3_decode_b1 / qwen3_prefill_2048 (one Qwen3-30B-A3B-shaped
+MoE layer, H=2048, F=768, E=128, K=8, softmax routing, no bias).
 
 Inputs are generated on the device before the timed region.  Times come from
 HIP events on the stream the kernels run on.  `value` times the steps
@@ -41,7 +42,13 @@ sys.path.insert(0, os.path.join(ROOT, "qwenqwen3.js_amd"))
 METRIC = "MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0"
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
-H, F, E, K = 2048, 1792, 32, 4
+H, F, E, K = 2048, 1792, 32, 4     # set per workload in main() from SHAPES
+GATING = "sigmoid"
+SHAPES = {
+    # name: (H, F, E, K, gating)
+    "lfm2": (2048, 1792, 32, 4, "sigmoid"),     # LFM2-8B-A1B MoE layer
+    "qwen3": (2048, 768, 128, 8, "softmax"),    # Qwen3-30B-A3B MoE layer
+}
 QBLK = 34
 STACK_LAYERS = 22
 MV_IN, MV_OUT = 1024, 3072
@@ -54,6 +61,8 @@ WORKLOADS = {
     "stack22_decode": ("stack", 1, "uniform", "moe_stack22_decode_batch1"),
     "stack22_prefill": ("stack", 4096, "uniform", "moe_stack22_prefill_4096"),
     "matvec": ("matvec", 1, None, "q8_0_matvec_1024x3072"),
+    "qwen3_decode_b1": ("layer", 1, None, "qwen3moe_layer_decode_batch1", "qwen3"),
+    "qwen3_prefill_2048": ("layer", 2048, None, "qwen3moe_layer_prefill_2048", "qwen3"),
 }
 MFMA_KERNELS = ("mfma_gateup", "mfma_down")
 
@@ -121,6 +130,9 @@ def make_layer(torch, ctx, seed, bias_kind):
         del blocks, qs, d
     rng = np.random.default_rng(seed)
     router = (rng.standard_normal((E, H)) * 0.02).astype(np.float32)
+    if GATING == "softmax":
+        layer = ctx.moe_create(router, qq_hip.TYPE_F32, None, *tensors, H, F, E, K)
+        return layer.set_gating(qq_hip.GATING_SOFTMAX)
     if bias_kind == "zipf":
         k = np.arange(1, E + 1, dtype=np.float64)
         pmf = k ** -1.1
@@ -155,7 +167,7 @@ def _node_bench(mode, seconds):
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
-def cpu_baseline(seconds, kind):
+def cpu_baseline(seconds, kind, shape="lfm2"):
     """The reference's CPU path restated for Node 12 (oracle/moe_ref.js: same loop
     order and float64 arithmetic as src/tensor.js / src/lfm2-engine.js, checked bit
     for bit against the C oracle by the tests), timed on one host thread on a
@@ -170,15 +182,18 @@ def cpu_baseline(seconds, kind):
                               "reference's JS CPU path restated for Node %s, 1 thread of %d host "
                               "cores" % (r["matvecs"], r["seconds"], r["node"], ncores)}
     per = STACK_LAYERS if kind == "stack" else 1
-    r = _node_bench("bench", seconds)
+    r = _node_bench("bench-qwen3" if shape == "qwen3" else "bench", seconds)
     if r:
+        what = ("Qwen3-MoE layer calls (H=2048, F=768, E=128, K=8, softmax routing, Q8_0 experts; "
+                "Qwen3Engine._moEFFN)" if shape == "qwen3" else
+                "MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts)")
         return {
             "value": round(r["tokens_per_s"] / per, 4), "unit": "tokens/s", "cores": 1,
             "kind": "port",
-            "sample": "%d single-token MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts) "
+            "sample": "%d single-token %s "
                       "in %.1f s: the reference's JS CPU path restated for Node %s, 1 thread of %d "
                       "host cores; tokens are independent, so tokens/s is the rate at any batch%s"
-                      % (r["tokens"], r["seconds"], r["node"], ncores,
+                      % (r["tokens"], what, r["seconds"], r["node"], ncores,
                          "; divided by %d layers for the stack" % per if per > 1 else ""),
         }
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -314,7 +329,10 @@ def main():
     import torch
     import qq_hip
 
-    kind, T, bias_kind, wname = WORKLOADS[args.workload]
+    kind, T, bias_kind, wname = WORKLOADS[args.workload][:4]
+    shape = WORKLOADS[args.workload][4] if len(WORKLOADS[args.workload]) > 4 else "lfm2"
+    global H, F, E, K, GATING
+    H, F, E, K, GATING = SHAPES[shape]
     torch.cuda.init()
     ctx = qq_hip.Context(0)
     # the library launches on this stream; every event below is recorded on it
@@ -385,6 +403,7 @@ def main():
         value, unit = T * args.steps / (total_ms / 1000.0), "tokens/s"
         config = {"workload": wname, "H": H, "F": F, "E": E, "K": K, "T": T,
                   "weights": "Q8_0", "activations": "f32", "router": "f32 (f64 accumulate)",
+                  "gating": "softmax (Qwen3-MoE)" if GATING == "softmax" else "sigmoid + bias (LFM2-MoE)",
                   "layer_instances": n_layers, "distinct_experts_per_layer_call": round(n_exp, 2)}
         if stack:
             config["per_layer"] = "rmsnorm(hidden) -> MoE -> hidden +="
@@ -423,7 +442,7 @@ def main():
     ctx.close()
 
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, kind)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, kind, shape)
     print(json.dumps(result), flush=True)
     return 0
 

@@ -301,8 +301,9 @@ function q8Tensor(next, inDim, outDim, nMats) {
     return u8.buffer;
 }
 
-function bench(seconds) {
-    const H = 2048, F = 1792, E = 32, K = 4;
+function bench(seconds, qwen3) {
+    // LFM2-8B-A1B MoE layer shape, or (qwen3) the Qwen3-30B-A3B one with softmax routing
+    const H = 2048, F = qwen3 ? 768 : 1792, E = qwen3 ? 128 : 32, K = qwen3 ? 8 : 4;
     const next = rng(12345);
     const router = new Float32Array(E * H);
     for (let i = 0; i < router.length; i++) router[i] = ((next() & 0xffff) / 65536 - 0.5) * 0.04;
@@ -314,13 +315,16 @@ function bench(seconds) {
         ffnGateExps: { buffer: q8Tensor(next, H, F, E), offset: 0, shape: [H, F, E], type: 8 },
         ffnUpExps: { buffer: q8Tensor(next, H, F, E), offset: 0, shape: [H, F, E], type: 8 },
         ffnDownExps: { buffer: q8Tensor(next, F, H, E), offset: 0, shape: [F, H, E], type: 8 },
+        nExpertsUsed: K,
     };
+    if (qwen3) layer.expProbsBias = null;
     const eng = { nExperts: E, nExpertsUsed: K, bufNormed: new Float32Array(H),
                   bufHidden: new Float32Array(H), bufMoEOut: new Float32Array(H),
                   expertMask: null, onRouterUpdate: null };
     const token = function () {
         for (let i = 0; i < H; i++) eng.bufNormed[i] = ((next() & 0xffff) / 65536 - 0.5) * 3.4;
-        moEFFN(eng, 0, layer);
+        if (qwen3) moEFFNSoftmax(eng, 0, layer);
+        else moEFFN(eng, 0, layer);
     };
     token();   // warm-up (JIT)
     let n = 0;
@@ -364,10 +368,12 @@ module.exports = { halfToNumber, matmulQ80xF32, matmulF32xF32, matmulGeneric, re
 if (require.main === module) {
     const cmd = process.argv[2];
     if (cmd === 'run') runJob(process.argv[3]);
-    else if (cmd === 'bench') bench(Number(process.argv[3] || 10));
+    else if (cmd === 'bench') bench(Number(process.argv[3] || 10), false);
+    else if (cmd === 'bench-qwen3') bench(Number(process.argv[3] || 10), true);
     else if (cmd === 'bench-matvec') benchMatvec(Number(process.argv[3] || 10));
     else {
-        process.stderr.write('usage: node moe_ref.js run <job.json> | bench <seconds> | bench-matvec <seconds>\n');
+        process.stderr.write('usage: node moe_ref.js run <job.json> | bench <seconds> | bench-qwen3 <seconds> | ' +
+                             'bench-matvec <seconds>\n');
         process.exit(2);
     }
 }

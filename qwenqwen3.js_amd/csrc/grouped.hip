@@ -65,8 +65,8 @@ __global__ __launch_bounds__(DISP_THREADS) void moe_dispatch_kernel(
     }
     __syncthreads();
     constexpr int STEP = DISP_THREADS * DISP_ROUND;
+    int ev[DISP_ROUND];
     for (int b0 = 0; b0 < P; b0 += STEP) {
-        int ev[DISP_ROUND];
 #pragma unroll
         for (int i = 0; i < DISP_ROUND; i++) {
             const int p = b0 + tid + DISP_THREADS * i;
@@ -114,11 +114,13 @@ __global__ __launch_bounds__(DISP_THREADS) void moe_dispatch_kernel(
     }
     __syncthreads();
     for (int b0 = 0; b0 < P; b0 += STEP) {
-        int ev[DISP_ROUND];
+        // one chunk (P <= STEP): the expert ids of the counting pass are still held
+        if (P > STEP) {
 #pragma unroll
-        for (int i = 0; i < DISP_ROUND; i++) {
-            const int p = b0 + tid + DISP_THREADS * i;
-            ev[i] = p < P ? idx[p] : -1;
+            for (int i = 0; i < DISP_ROUND; i++) {
+                const int p = b0 + tid + DISP_THREADS * i;
+                ev[i] = p < P ? idx[p] : -1;
+            }
         }
 #pragma unroll
         for (int i = 0; i < DISP_ROUND; i++) {
@@ -351,6 +353,7 @@ __global__ __launch_bounds__(GR_THREADS) void moe_grouped_down_kernel(GroupArgs 
 }
 
 // hidden[t][j] += sum_k fp32-rounded w[t,k] * y[inv[t,k]][j], ranks in order.
+template <int KM>
 __global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restrict__ y, int H, int K,
                                                           const int32_t *__restrict__ inv,
                                                           const double *__restrict__ w,
@@ -359,13 +362,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(const float *__restric
     const int t = blockIdx.y;
     const int j = blockIdx.x * 256 + threadIdx.x;
     if (j >= H) return;
-    float acc = 0.0f;
-    for (int k = 0; k < K; k++) {
-        const int p = t * K + k;
-        const int s = inv[p];
-        if (s < 0) continue;
-        acc = (float)((double)acc + w[p] * (double)y[(size_t)s * H + j]);
+    int sv[KM];
+    double wv[KM];
+#pragma unroll
+    for (int k = 0; k < KM; k++) {
+        sv[k] = k < K ? inv[t * K + k] : -1;
+        wv[k] = k < K ? w[t * K + k] : 0.0;
     }
+    float v[KM];
+#pragma unroll
+    for (int k = 0; k < KM; k++) v[k] = sv[k] >= 0 ? y[(size_t)sv[k] * H + j] : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KM; k++)
+        if (sv[k] >= 0) acc = (float)((double)acc + wv[k] * (double)v[k]);
     hidden[(size_t)t * H + j] = hidden[(size_t)t * H + j] + acc;
 }
 
@@ -383,7 +393,7 @@ int launch_dispatch(qq_ctx *ctx, const qq_moe *m, const int32_t *idx, int P, con
 
 // The same per element, four consecutive columns per thread (H % 4 == 0,
 // 16-byte aligned rows); y rows in fp32 or, from the fp16 MFMA path, fp16.
-template <typename YT>
+template <typename YT, int KM>
 __global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict__ y, int H, int K,
                                                            const int32_t *__restrict__ inv,
                                                            const double *__restrict__ w,
@@ -392,24 +402,35 @@ __global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict_
     const int t = blockIdx.y;
     const int j = 4 * (blockIdx.x * 256 + threadIdx.x);
     if (j >= H) return;
-    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k = 0; k < K; k++) {
-        const int p = t * K + k;
-        const int s = inv[p];
+    // slots and weights of every rank in one round trip, then every row
+    int sv[KM];
+    double wv[KM];
+#pragma unroll
+    for (int k = 0; k < KM; k++) {
+        sv[k] = k < K ? inv[t * K + k] : -1;
+        wv[k] = k < K ? w[t * K + k] : 0.0;
+    }
+    float v[KM][4];
+#pragma unroll
+    for (int k = 0; k < KM; k++) {
+        const int s = sv[k];
         if (s < 0) continue;
-        const double wk = w[p];
-        float v[4];
         if constexpr (sizeof(YT) == 4) {
             const float4 q = *reinterpret_cast<const float4 *>(y + (size_t)s * H + j);
-            v[0] = q.x; v[1] = q.y; v[2] = q.z; v[3] = q.w;
+            v[k][0] = q.x; v[k][1] = q.y; v[k][2] = q.z; v[k][3] = q.w;
         } else {
             const uint2 q = *reinterpret_cast<const uint2 *>(y + (size_t)s * H + j);
             const _Float16 *h = reinterpret_cast<const _Float16 *>(&q);
 #pragma unroll
-            for (int i = 0; i < 4; i++) v[i] = (float)h[i];
+            for (int i = 0; i < 4; i++) v[k][i] = (float)h[i];
         }
+    }
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-        for (int i = 0; i < 4; i++) acc[i] = (float)((double)acc[i] + wk * (double)v[i]);
+    for (int k = 0; k < KM; k++) {
+        if (sv[k] < 0) continue;
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[i] = (float)((double)acc[i] + wv[k] * (double)v[k][i]);
     }
     float4 *hp = reinterpret_cast<float4 *>(hidden + (size_t)t * H + j);
     float4 hv = *hp;
@@ -425,18 +446,24 @@ int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const void *y, bool y_f1
 {
     prof_begin(ctx, K_COMBINE);
     const bool vec = m->H % 4 == 0 && ((uintptr_t)hidden & 15) == 0 && ((uintptr_t)y & 15) == 0;
-    const dim3 g4((m->H / 4 + 255) / 256, T);
-    if (y_f16) {
-        if (!vec) return set_error(ctx, "combine: fp16 rows need H %% 4 == 0 and aligned buffers");
-        QQ_LAUNCH(ctx, moe_combine4_kernel<_Float16>, g4, dim3(256), 0,
-                  static_cast<const _Float16 *>(y), m->H, m->K, inv, w, hidden);
-    } else if (vec) {
-        QQ_LAUNCH(ctx, moe_combine4_kernel<float>, g4, dim3(256), 0, static_cast<const float *>(y),
+    if (y_f16 && !vec) return set_error(ctx, "combine: fp16 rows need H %% 4 == 0 and aligned buffers");
+    const dim3 g4((m->H / 4 + 255) / 256, T), g1((m->H + 255) / 256, T);
+    // every rank's slot, weight and row are loaded before the sum; KM ranks
+    // at most, so the registers stay few
+#define QQ_COMBINE(KM)                                                                            \
+    if (y_f16)                                                                                    \
+        QQ_LAUNCH(ctx, (moe_combine4_kernel<_Float16, KM>), g4, dim3(256), 0,                     \
+                  static_cast<const _Float16 *>(y), m->H, m->K, inv, w, hidden);                  \
+    else if (vec)                                                                                 \
+        QQ_LAUNCH(ctx, (moe_combine4_kernel<float, KM>), g4, dim3(256), 0,                        \
+                  static_cast<const float *>(y), m->H, m->K, inv, w, hidden);                     \
+    else                                                                                          \
+        QQ_LAUNCH(ctx, moe_combine_kernel<KM>, g1, dim3(256), 0, static_cast<const float *>(y),   \
                   m->H, m->K, inv, w, hidden);
-    } else {
-        QQ_LAUNCH(ctx, moe_combine_kernel, dim3((m->H + 255) / 256, T), dim3(256), 0,
-                  static_cast<const float *>(y), m->H, m->K, inv, w, hidden);
-    }
+    if (m->K <= 4) { QQ_COMBINE(4) }
+    else if (m->K <= 8) { QQ_COMBINE(8) }
+    else { QQ_COMBINE(MAX_K) }
+#undef QQ_COMBINE
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

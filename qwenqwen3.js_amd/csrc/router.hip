@@ -165,16 +165,23 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const int lane = threadIdx.x & (WAVE - 1);
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
     if (t >= T) return;
+    // every partial sum of this lane in flight at once, then added in slice order
+    double pv[EPL][ROUTER_MAX_SPLIT];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = min(lane + WAVE * i, E - 1);
+#pragma unroll
+        for (int ks = 0; ks < ROUTER_MAX_SPLIT; ks++)
+            pv[i][ks] = ks < KS ? part[((size_t)ks * T + t) * E + e] : 0.0;
+    }
     float lg[EPL];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
-        const int e = lane + WAVE * i;
-        double s = 0.0;
-        if (e < E) {
-            s = part[(size_t)t * E + e];
-            for (int ks = 1; ks < KS; ks++) s += part[((size_t)ks * T + t) * E + e];
-        }
-        lg[i] = (float)s;
+        double s = pv[i][0];
+#pragma unroll
+        for (int ks = 1; ks < ROUTER_MAX_SPLIT; ks++)
+            if (ks < KS) s += pv[i][ks];
+        lg[i] = (lane + WAVE * i < E) ? (float)s : 0.0f;
     }
     WaveRoute<EPL> R;
     wave_route<EPL>(lg, E, K, bias, softmax != 0, R);
