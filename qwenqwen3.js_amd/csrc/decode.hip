@@ -1,30 +1,35 @@
-// decode.hip -- batch-1 decode of one LFM2-MoE MoE layer in two launches.
+// decode.hip -- batch-1 decode of one MoE layer in two launches.
 //
-// Reference: Lfm2Engine._moEFFN, src/lfm2-engine.js:413-487, for one token.
+// Reference: Lfm2Engine._moEFFN, src/lfm2-engine.js:413-487 (sigmoid + bias
+// gating), and Qwen3Engine._moEFFN, src/qwen3-engine.js:304-363 (softmax
+// gating), for one token.
 //
 // Launch 1 (moe_decode_experts): 8 * ceil(E/8) router workgroups + K*NS
 // expert-unit workgroups (NS = ceil(F/32)).
 //   * router workgroup i (group g = i / 8): binary64 dots of x with router
-//     columns 8g .. 8g+7 (one per wave), fp32 logits, p_e = fp32 sigmoid (binary64 math) and
-//     selection scores s_e = fp32(p_e + bias_e), published as 64-bit words
-//     slot_s[e] = (epoch << 32) | s_e and slot_p[e] = (epoch << 32) | p_e.
+//     columns 8g .. 8g+7 (one per wave), fp32 logits, published
+//     as 64-bit words slot[e] = (epoch << 32) | value.  Sigmoid gating
+//     publishes the selection score s_e = fp32(p_e + bias_e) at slot[e] and
+//     p_e = fp32 sigmoid (binary64 math) at slot[SYNC_PROB + e]; softmax
+//     gating publishes the logit at slot[e] (the softmax needs all of them,
+//     so every waiter takes it itself).
 //     Workgroups are dealt to the 8 XCDs round robin, so the 8 copies of a
 //     group land on the 8 XCDs: each writes the table of its own XCD, which
 //     stays in that XCD's L2, and copy 0 also writes SYNC_REPLICAS
 //     device-coherent copies of the table.
 //   * expert-unit workgroup (k, s): stages x in LDS (and its 3-level int8
-//     decomposition), waits in wave 0 (bounded) until all E score
-//     slots carry this call's epoch -- polling its XCD's table through L2
-//     first, and the device-coherent copy u % SYNC_REPLICAS if that has not
-//     filled within DEC_LOCAL_TICKS (so progress never depends on where the
-//     dispatcher placed the router workgroups) -- ranks the experts itself
-//     (rank of e = number of experts ordered before it by (score desc, index
-//     asc): the order of a stable descending sort; identical in every
-//     workgroup), then streams one F-slice of the rank-k expert: gate and up
-//     rows f in [32s, 32s+32) (2 x 32 rows x H), SwiGLU, and the matching down
-//     block column s (H rows x 32), writing the partial down product
-//     partial[k][s][0..H).  Every weight load is issued before any
-//     arithmetic; dot products use v_dot4_i32_i8.
+//     decomposition), waits in wave 0 (bounded) until all E slots carry this
+//     call's epoch -- polling its XCD's table through L2 first, and the
+//     device-coherent copy u % SYNC_REPLICAS if that has not filled within
+//     DEC_LOCAL_TICKS (so progress never depends on where the dispatcher
+//     placed the router workgroups) -- takes the softmax if asked, ranks the
+//     experts itself (rank of e = number of experts ordered before it by
+//     (score desc, index asc): the order of a stable descending sort;
+//     identical in every workgroup), then streams one F-slice of the rank-k
+//     expert: gate and up rows f in [32s, 32s+32) (2 x 32 rows x H), SwiGLU,
+//     and the matching down block column s (H rows x 32), writing the partial
+//     down product partial[k][s][0..H).  Every weight load is issued before
+//     any arithmetic; dot products use v_dot4_i32_i8.
 //   Value and epoch travel together in one word, so no fence (and no cache
 //   write-back or invalidate) is needed on either side, and every expert has
 //   its own words, so nothing is contended.  The epoch is a device word that
@@ -49,6 +54,7 @@ constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the XCD's own table, 
 constexpr int RT_EPW = 8;                      // experts per router workgroup (one per wave)
 constexpr int RT_COPIES = 8;                   // router workgroups per expert group
 static_assert(RT_EPW == DEC_WAVES && RT_EPW * 8 == WAVE, "router lane layout");
+static_assert(MAX_E <= 4 * WAVE, "at most four experts per lane");
 
 // XCD (accelerator complex die) this wave runs on.
 __device__ __forceinline__ uint32_t xcc_id()
@@ -72,6 +78,7 @@ struct DecodeArgs {
     int router_q8;
     int router_vec4;      // F32 router, H % 4 == 0
     int n_router;         // router workgroups: RT_COPIES * ceil(E / RT_EPW)
+    int softmax;          // Qwen3-MoE gating: routers publish logits, waiters take the softmax
     const float *bias;
     const int8_t *gq;
     const __half *gd;
@@ -81,8 +88,9 @@ struct DecodeArgs {
     const __half *dd;
     MaskBits mask;
     const uint32_t *epoch_word;   // this call's epoch is *epoch_word + 1
-    // Slot tables, persistent across calls, each [0, 64) epoch << 32 | selection
-    // score bits, [64, 128) epoch << 32 | probability bits:
+    // Slot tables, persistent across calls, each [0, E) epoch << 32 | selection
+    // score bits (softmax gating: logit bits), [SYNC_PROB, SYNC_PROB + E)
+    // epoch << 32 | probability bits (sigmoid gating only):
     //   slots: SYNC_REPLICAS device-coherent copies, SYNC_REPLICA_WORDS apart;
     //   local: one table per XCD (SYNC_LOCAL_WORDS apart), kept in that XCD's L2
     uint64_t *slots;
@@ -96,24 +104,32 @@ struct DecodeArgs {
     uint32_t *err;
 };
 
-// Bounded wait until lanes < E of a slot table carry `epoch`; returns the
-// word.  Polls the XCD's own table (`loc`) while `use_loc` and for
-// DEC_LOCAL_TICKS, then the device-coherent copy `glob`; use_loc tells on
-// return which table answered.  Both are device-scope loads: for a line
-// written from the same XCD one is answered by that XCD's L2 in about
-// 0.2 us, against about 1-2 us for a line written from another XCD.
-__device__ __forceinline__ uint64_t wait_slots(const uint64_t *loc, const uint64_t *glob, int E,
-                                               uint32_t epoch, int lane, int &ok, bool &use_loc)
+// Bounded wait until words [0, E) of a slot table carry `epoch` (lane l
+// holds words l, l + 64, ...: EPL of them); returns them in v.  Polls the
+// XCD's own table (`loc`) while `use_loc` and for DEC_LOCAL_TICKS, then the
+// device-coherent copy `glob`; use_loc tells on return which table answered.
+// Both are device-scope loads: for a line written from the same XCD one is
+// answered by that XCD's L2 in about 0.2 us, against about 1-2 us for a line
+// written from another XCD.
+template <int EPL>
+__device__ __forceinline__ void wait_slots(const uint64_t *loc, const uint64_t *glob, int E,
+                                           uint32_t epoch, int lane, int &ok, bool &use_loc,
+                                           uint64_t (&v)[EPL])
 {
     const uint64_t t0 = wall_clock64();
-    uint64_t v;
     while (true) {
-        if (lane < E)
-            v = __hip_atomic_load(use_loc ? &loc[lane] : &glob[lane], __ATOMIC_RELAXED,
-                                  __HIP_MEMORY_SCOPE_AGENT);
-        else
-            v = (uint64_t)epoch << 32;
-        if (__all((uint32_t)(v >> 32) == epoch)) break;
+        bool all = true;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const int e = lane + WAVE * j;
+            if (e < E)
+                v[j] = __hip_atomic_load(use_loc ? &loc[e] : &glob[e], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+            else
+                v[j] = (uint64_t)epoch << 32;
+            all = all && (uint32_t)(v[j] >> 32) == epoch;
+        }
+        if (__all(all)) break;
         const uint64_t dt = wall_clock64() - t0;
         if (dt > DEC_LOCAL_TICKS) use_loc = false;
         if (dt > DEC_WAIT_TICKS) {
@@ -122,11 +138,11 @@ __device__ __forceinline__ uint64_t wait_slots(const uint64_t *loc, const uint64
         }
         __builtin_amdgcn_s_sleep(1);
     }
-    return v;
 }
 
-// NBW = blocks of H per wave (and 32-row chunks of H per wave) = ceil(ceil(H/32)/8).
-template <int NBW>
+// NBW = blocks of H per wave (and 32-row chunks of H per wave) = ceil(ceil(H/32)/8);
+// EPL = experts per lane of the waiting waves (1: E <= 64, 2: E <= 128, 4: E <= 256).
+template <int NBW, int EPL>
 __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeArgs a)
 {
     constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
@@ -141,10 +157,11 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     __shared__ float redu[DEC_WAVES][QK];
     __shared__ double rsum[DEC_WAVES];
     __shared__ int sh_ok;
-    __shared__ int rank_part[DEC_WAVES][WAVE];
+    __shared__ int rank_part[DEC_WAVES][EPL * WAVE];
     __shared__ int sh_rank_e[MAX_K];
     __shared__ float sh_rank_p[MAX_K];
-    __shared__ __align__(16) float sh_score[WAVE];
+    __shared__ __align__(16) float sh_score[EPL * WAVE];
+    __shared__ float sh_prob[EPL * WAVE];
 
     const int lane = threadIdx.x & (WAVE - 1);
     const int wave = threadIdx.x / WAVE;
@@ -152,13 +169,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     const uint32_t epoch = a.epoch_word[0] + 1u;
 
     const bool router = (int)blockIdx.x < a.n_router;
-    // router workgroup i: experts e0 .. e0+7 of group i / RT_COPIES, wave w takes e0 + w
-    const int e0 = (blockIdx.x / RT_COPIES) * RT_EPW;
+    // router workgroup i: experts 8g .. 8g + 7 of group g = i / RT_COPIES, one a wave
+    const int e_r = min((int)(blockIdx.x / RT_COPIES) * RT_EPW + wave, a.E - 1);
     const int H4 = a.H >> 2;
     float4 rw[NBW];
     if (router && a.router_vec4) {
         // issued before x is staged; columns past H meet the zero padding of xl
-        const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32) + (size_t)min(e0 + wave, a.E - 1) * H4;
+        const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32) + (size_t)e_r * H4;
 #pragma unroll
         for (int i = 0; i < NBW; i++) rw[i] = w4[min(lane + WAVE * i, H4 - 1)];
     }
@@ -196,13 +213,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     __syncthreads();
 
     if (router) {
-        // ---- router workgroup: logits, sigmoid, scores (lfm2-engine.js:418-431) ----
+        // ---- router workgroup: logits, then sigmoid and scores or softmax
+        // logits (lfm2-engine.js:418-431; qwen3-engine.js:306-307) ----
         // Workgroup i runs on XCD i % 8 (the dispatcher deals workgroups to the
         // XCDs round robin), so each XCD gets a full set of router workgroups
         // and its table fills from its own L2.  Nothing depends on that for
         // correctness: copy 0 of each group also fills the device-coherent
         // tables, which waiters fall back to.
-        const int ew = min(e0 + wave, a.E - 1);
         double acc = 0.0;
         if (a.router_vec4) {
             // four independent chains (one per float4 component), then joined
@@ -221,10 +238,10 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
             for (int k = lane; k < a.H; k += WAVE) {
                 double wv;
                 if (a.router_q8) {
-                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, ew);
+                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e_r);
                     wv = (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]);
                 } else {
-                    wv = (double)a.rf32[(size_t)ew * a.H + k];
+                    wv = (double)a.rf32[(size_t)e_r * a.H + k];
                 }
                 acc = fma((double)xl[k], wv, acc);
             }
@@ -233,25 +250,32 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
         if (lane == 0) rsum[wave] = acc;
         __syncthreads();
         if (wave == 0) {
-            // lane = 8 j + r: expert e0 + j; copies r and r + 8 of the device table
-            const int j = lane >> 3, r = lane & 7;
-            const int e = e0 + j;
+            // lane = 8 q + r: expert 8g + q; copies r and r + 8 of the device table
+            const int q = lane >> 3, r = lane & 7;
+            const int e = (blockIdx.x / RT_COPIES) * RT_EPW + q;
             if (e < a.E) {
-                // lfm2-engine.js:420-431
-                const float logit = (float)rsum[j];
-                const float p = (float)(1.0 / (1.0 + exp(-(double)logit)));
-                const float sc = p + a.bias[e];
+                const float logit = (float)rsum[q];
+                // sigmoid gating: probability and selection score; softmax
+                // gating: the logit (the softmax needs all of them and is taken
+                // by every waiter)
+                float p = 0.0f, sc = logit;
+                if (!a.softmax) {
+                    p = (float)(1.0 / (1.0 + exp(-(double)logit)));
+                    sc = p + a.bias[e];
+                }
                 const uint64_t ep = (uint64_t)epoch << 32;
+                uint64_t *ltab = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
                 if (r == 0) {
-                    uint64_t *tab = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
-                    __hip_atomic_store(&tab[WAVE + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    __hip_atomic_store(&tab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    if (!a.softmax)
+                        __hip_atomic_store(&ltab[SYNC_PROB + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                    __hip_atomic_store(&ltab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
                 }
                 if (blockIdx.x % RT_COPIES == 0) {
 #pragma unroll
                     for (int c = r; c < SYNC_REPLICAS; c += 8) {
                         uint64_t *tab = a.slots + (size_t)c * SYNC_REPLICA_WORDS;
-                        __hip_atomic_store(&tab[WAVE + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        if (!a.softmax)
+                            __hip_atomic_store(&tab[SYNC_PROB + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                         __hip_atomic_store(&tab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
                 }
@@ -282,12 +306,31 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
         if ((t & 3) == 0) xsig[t >> 2] = m * (1.0f / 127.0f);
     }
 
-    // ---- routing (lfm2-engine.js:433-447) ----
+    // ---- routing (lfm2-engine.js:433-447; qwen3-engine.js:306-321) ----
     bool use_loc = true;
     if (wave == 0) {
         int ok = 1;
-        const uint64_t v = wait_slots(loc, tab, a.E, epoch, lane, ok, use_loc);
-        sh_score[lane] = (lane < a.E) ? __uint_as_float((uint32_t)v) : -INFINITY;
+        uint64_t v[EPL];
+        wait_slots<EPL>(loc, tab, a.E, epoch, lane, ok, use_loc, v);
+        if (a.softmax) {
+            // every workgroup takes the same softmax of the same logits
+            float lg[EPL], pr[EPL];
+#pragma unroll
+            for (int j = 0; j < EPL; j++) lg[j] = __uint_as_float((uint32_t)v[j]);
+            softmax_probs<EPL>(lg, a.E, pr);
+#pragma unroll
+            for (int j = 0; j < EPL; j++) {
+                const int e = lane + WAVE * j;
+                sh_score[e] = (e < a.E) ? pr[j] : -INFINITY;
+                sh_prob[e] = pr[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < EPL; j++) {
+                const int e = lane + WAVE * j;
+                sh_score[e] = (e < a.E) ? __uint_as_float((uint32_t)v[j]) : -INFINITY;
+            }
+        }
         if (lane == 0) {
             sh_ok = ok;
             if (!ok) atomicOr(a.err, 1u);
@@ -295,48 +338,78 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeA
     }
     __syncthreads();
     if (!sh_ok) return;
-    // rank of expert `lane`: experts ordered before it by (score desc, index
-    // asc), so the rank-k expert is the k-th element of a stable descending
-    // sort.  Wave w counts over slots 8w .. 8w+7 (slots >= E hold -inf and
-    // never rank before a real expert); every wave then sums the counts.
+    // rank of expert e = lane + 64j: experts ordered before it by (score
+    // desc, index asc), so the rank-k expert is the k-th element of a stable
+    // descending sort.  Wave w counts over slots 8*EPL*w .. 8*EPL*(w+1) - 1
+    // (slots >= E hold -inf and never rank before a real expert); every wave
+    // then sums the counts.
     {
-        const float sc = sh_score[lane];
-        const float4 q0 = reinterpret_cast<const float4 *>(sh_score)[2 * wave];
-        const float4 q1 = reinterpret_cast<const float4 *>(sh_score)[2 * wave + 1];
-        const float qq[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-        int part = 0;
+        constexpr int NQ = 2 * EPL;   // float4 reads of the wave's 8*EPL slots
+        float qq[4 * NQ];
 #pragma unroll
-        for (int u = 0; u < 8; u++) {
-            const int i = 8 * wave + u;
-            part += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < lane));
+        for (int u = 0; u < NQ; u++) {
+            const float4 q4 = reinterpret_cast<const float4 *>(sh_score)[NQ * wave + u];
+            qq[4 * u] = q4.x;
+            qq[4 * u + 1] = q4.y;
+            qq[4 * u + 2] = q4.z;
+            qq[4 * u + 3] = q4.w;
         }
-        rank_part[wave][lane] = part;
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const int e = lane + WAVE * j;
+            const float sc = sh_score[e];
+            int part = 0;
+#pragma unroll
+            for (int u = 0; u < 4 * NQ; u++) {
+                const int i = 4 * NQ * wave + u;
+                part += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < e));
+            }
+            rank_part[wave][e] = part;
+        }
     }
     __syncthreads();
-    int rank = 0;
+    int rank[EPL];
+    int e = -1;
 #pragma unroll
-    for (int w = 0; w < DEC_WAVES; w++) rank += rank_part[w][lane];
-    if (lane >= a.E) rank = INT_MAX;
-    const uint64_t hit = __ballot(rank == kslot);   // the same in every wave
-    if (!hit) return;
-    const int e = (int)__builtin_ctzll(hit);
+    for (int j = 0; j < EPL; j++) {
+        rank[j] = 0;
+#pragma unroll
+        for (int w = 0; w < DEC_WAVES; w++) rank[j] += rank_part[w][lane + WAVE * j];
+        if (lane + WAVE * j >= a.E) rank[j] = INT_MAX;
+        const uint64_t hit = __ballot(rank[j] == kslot);   // the same in every wave
+        if (hit) e = WAVE * j + (int)__builtin_ctzll(hit);
+    }
+    if (e < 0) return;
     if (unit == 0 && wave == 0) {
-        // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457)
-        int okp = 1;
-        const uint64_t pv = wait_slots(loc + WAVE, tab + WAVE, a.E, epoch, lane, okp, use_loc);
-        if (!okp && lane == 0) atomicOr(a.err, 2u);
-        const float p = __uint_as_float((uint32_t)pv);
-        if (a.out_probs && lane < a.E) a.out_probs[lane] = p;
-        if (rank < a.K) {
-            sh_rank_e[rank] = lane;
-            sh_rank_p[rank] = p;
+        // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457;
+        // qwen3-engine.js:317-329: the sum starts at 0 and a zero sum gives zero weights)
+        float p[EPL];
+        if (a.softmax) {
+#pragma unroll
+            for (int j = 0; j < EPL; j++) p[j] = sh_prob[lane + WAVE * j];
+        } else {
+            int okp = 1;
+            uint64_t pv[EPL];
+            wait_slots<EPL>(loc + SYNC_PROB, tab + SYNC_PROB, a.E, epoch, lane, okp, use_loc, pv);
+            if (!okp && lane == 0) atomicOr(a.err, 2u);
+#pragma unroll
+            for (int j = 0; j < EPL; j++) p[j] = __uint_as_float((uint32_t)pv[j]);
+        }
+#pragma unroll
+        for (int j = 0; j < EPL; j++) {
+            const int ee = lane + WAVE * j;
+            if (a.out_probs && ee < a.E) a.out_probs[ee] = p[j];
+            if (rank[j] < a.K) {
+                sh_rank_e[rank[j]] = ee;
+                sh_rank_p[rank[j]] = p[j];
+            }
         }
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         if (lane == 0) {
-            double sumW = 1e-6;
+            double sumW = a.softmax ? 0.0 : 1e-6;
             for (int k = 0; k < a.K; k++) sumW = sumW + (double)sh_rank_p[k];
-            const double inv = 1.0 / sumW;
+            const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
             for (int k = 0; k < a.K; k++) {
                 const double wk = (double)sh_rank_p[k] * inv;
                 a.route_idx[k] = sh_rank_e[k];
@@ -513,10 +586,7 @@ __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
 
 bool decode_supported(const qq_moe *m, int T)
 {
-    // the decode kernel implements LFM2's sigmoid + bias gating; softmax
-    // layers take the batched path at T = 1 too
-    return T == 1 && m->gating == QQ_GATING_SIGMOID_BIAS && m->E <= WAVE && m->K <= m->E &&
-           m->H <= 8 * DEC_WAVES * QK;
+    return T == 1 && m->E <= MAX_E && m->K <= m->E && m->H <= 8 * DEC_WAVES * QK;
 }
 
 size_t decode_work_bytes(const qq_moe *m)
@@ -525,10 +595,19 @@ size_t decode_work_bytes(const qq_moe *m)
     return (size_t)m->K * NS * m->H * 4 + 256 + 256 + (size_t)m->K * 4 + 256;
 }
 
-template <int NBW>
+template <int NBW, int EPL>
 static void launch_experts(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
 {
-    QQ_LAUNCH(ctx, moe_decode_experts_kernel<NBW>, grid, dim3(DEC_THREADS), 0, a);
+    QQ_LAUNCH(ctx, (moe_decode_experts_kernel<NBW, EPL>), grid, dim3(DEC_THREADS), 0, a);
+}
+
+template <int EPL>
+static void launch_experts_nbw(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int nbw)
+{
+    if (nbw <= 1) launch_experts<1, EPL>(ctx, a, grid);
+    else if (nbw <= 2) launch_experts<2, EPL>(ctx, a, grid);
+    else if (nbw <= 4) launch_experts<4, EPL>(ctx, a, grid);
+    else launch_experts<8, EPL>(ctx, a, grid);
 }
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
@@ -562,6 +641,8 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.slots = ctx->sync_slots;
     a.local = ctx->sync_local;
     a.router_vec4 = !a.router_q8 && (m->H & 3) == 0;
+    a.softmax = m->gating == QQ_GATING_SOFTMAX;
+    const int epl = m->E <= WAVE ? 1 : m->E <= 2 * WAVE ? 2 : 4;
     a.n_router = RT_COPIES * ((m->E + RT_EPW - 1) / RT_EPW);
     a.epoch_word = ctx->sync_epoch;
     a.err = ctx->sync_err;
@@ -576,10 +657,9 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
     const dim3 grid(a.n_router + m->K * a.NS);
     prof_begin(ctx, K_DECODE_EXPERTS);
-    if (nbw <= 1) launch_experts<1>(ctx, a, grid);
-    else if (nbw <= 2) launch_experts<2>(ctx, a, grid);
-    else if (nbw <= 4) launch_experts<4>(ctx, a, grid);
-    else launch_experts<8>(ctx, a, grid);
+    if (epl == 1) launch_experts_nbw<1>(ctx, a, grid, nbw);
+    else if (epl == 2) launch_experts_nbw<2>(ctx, a, grid, nbw);
+    else launch_experts_nbw<4>(ctx, a, grid, nbw);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
 

@@ -298,8 +298,9 @@ __device__ __forceinline__ bool rank_before(float av, int ai, float bv, int bi)
 
 // Softmax gating (Qwen3-MoE, src/qwen3-engine.js:305-321 with softmaxInPlace,
 // src/tensor.js:150-164): probabilities p_e = fp32(fp32(exp(l_e - max)) * (1/S))
-// with S the binary64 sum of the fp32 exponentials in expert order (one lane
-// adds them in that order, as the reference does), selection by p_e itself,
+// with S the binary64 sum of the fp32 exponentials in expert order (as the
+// reference adds them; a tree sum where that is provably the same value),
+// selection by p_e itself,
 // and the weights renormalised from 0 (1/sum, or 0 when the sum is 0).
 template <int EPL>
 __device__ __forceinline__ void softmax_probs(const float (&logit)[EPL], int E, float (&prob)[EPL])
@@ -315,13 +316,28 @@ __device__ __forceinline__ void softmax_probs(const float (&logit)[EPL], int E, 
 #pragma unroll
     for (int i = 0; i < EPL; i++)
         ex[i] = (lane + WAVE * i < E) ? (float)exp((double)logit[i] - (double)mx) : 0.0f;
-    double sum = 0.0;
+    // When every term is 0 or in [2^-22, 1], all terms are multiples of 2^-45
+    // and every partial sum is at most E <= 2^8: each is exact in binary64
+    // (53 bits), so the sequential sum equals the exact sum and any order of
+    // addition gives it.  Otherwise one lane adds the terms in expert order.
+    static_assert(EPL * WAVE <= 256, "exact-sum bound");
+    bool exact = true;
 #pragma unroll
-    for (int i = 0; i < EPL; i++) {
-        const int n = min(WAVE, E - WAVE * i);
-        const int bits = __float_as_int(ex[i]);
-        for (int l = 0; l < n; l++)
-            sum = sum + (double)__int_as_float(__builtin_amdgcn_readlane(bits, l));
+    for (int i = 0; i < EPL; i++) exact = exact && (ex[i] == 0.0f || (ex[i] >= 0x1p-22f && ex[i] <= 1.0f));
+    double sum = 0.0;
+    if (__all(exact)) {
+        double part = 0.0;
+#pragma unroll
+        for (int i = 0; i < EPL; i++) part += (double)ex[i];   // zero past E
+        sum = wave_sum_dpp(part);
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int n = min(WAVE, E - WAVE * i);
+            const int bits = __float_as_int(ex[i]);
+            for (int l = 0; l < n; l++)
+                sum = sum + (double)__int_as_float(__builtin_amdgcn_readlane(bits, l));
+        }
     }
     const double inv = 1.0 / sum;
 #pragma unroll

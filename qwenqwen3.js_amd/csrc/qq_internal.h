@@ -19,13 +19,17 @@ constexpr int QBLK = 34;      // bytes per GGUF Q8_0 block {fp16 d, int8 qs[32]}
 constexpr int WAVE = 64;      // CDNA wavefront width
 constexpr int MAX_E = 256;    // experts supported by the router and the mask bitset
 constexpr int MAX_K = 16;     // experts used per token
-// Decode router exchange: copies of the per-expert slot table, each
-// 4352 B apart so that the copies start in different DRAM channels.
+// Decode router exchange: copies of the per-expert slot table (selection
+// scores or logits at [0, MAX_E), probabilities at [SYNC_PROB, SYNC_PROB +
+// MAX_E)), each 4608 B apart so that the copies start in different DRAM
+// channels ...
+constexpr int SYNC_PROB = MAX_E;
 constexpr int SYNC_REPLICAS = 16;
-constexpr int SYNC_REPLICA_WORDS = 544;
-// ... and one table per XCD (XCC_ID < 16), 1 KiB apart.
+constexpr int SYNC_REPLICA_WORDS = 576;
+// ... and one table per XCD (XCC_ID < 16), 4 KiB apart.
 constexpr int SYNC_LOCAL_TABLES = 16;
-constexpr int SYNC_LOCAL_WORDS = 128;
+constexpr int SYNC_LOCAL_WORDS = 2 * MAX_E;
+static_assert(SYNC_REPLICA_WORDS >= 2 * MAX_E, "slot table");
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
 struct MaskBits {

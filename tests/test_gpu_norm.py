@@ -40,18 +40,24 @@ def test_rmsnorm_matches_oracle(T, H):
     assert np.max(np.abs(gw - refw) / np.maximum(np.abs(refw), 1e-30)) < 3e-7
 
 
-@pytest.mark.parametrize("T,mfma,weighted", [(1, 0, False), (1, 0, True), (64, 0, True),
-                                             (96, 64, False)])
-def test_fused_norm_moe_matches_two_calls(T, mfma, weighted):
+@pytest.mark.parametrize("T,mfma,weighted,gating", [(1, 0, False, "sigmoid"),
+                                                    (1, 0, True, "sigmoid"),
+                                                    (64, 0, True, "sigmoid"),
+                                                    (96, 64, False, "sigmoid"),
+                                                    (1, 0, True, "softmax")])
+def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating):
     """qq_moe_forward_norm_dev == qq_rmsnorm_dev then qq_moe_forward_dev, bit for bit
     (a single row is normalised inside the decode kernel)."""
     import torch
     import synth
     from _util import upload_layer
-    print("fused norm+moe", T, mfma, weighted, flush=True)
+    print("fused norm+moe", T, mfma, weighted, gating, flush=True)
     ctx = gpu_context()
     ctx.set_mfma_min_tokens(mfma)
-    L = synth.moe_layer(41, H=512, F=256, E=16, K=4)
+    if gating == "softmax":
+        L = synth.moe_layer(41, H=512, F=256, E=128, K=4, bias=None, gating="softmax")
+    else:
+        L = synth.moe_layer(41, H=512, F=256, E=16, K=4)
     m = upload_layer(ctx, L)
     try:
         rng = np.random.default_rng(T + 7)

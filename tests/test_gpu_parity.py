@@ -144,6 +144,27 @@ def test_moe_small(case):
     _check_moe(L, x, hid)
 
 
+@pytest.mark.parametrize("case", [
+    dict(H=512, F=96, E=65, K=3),            # two experts a lane, the second lane ragged
+    dict(H=2048, F=768, E=128, K=8),         # two experts a lane, all full
+    dict(H=256, F=64, E=200, K=6),           # four experts a lane, ragged
+    dict(H=256, F=64, E=256, K=8),           # the largest expert count
+])
+def test_moe_decode_many_experts(case):
+    """Batch-1 decode (sigmoid + bias gating) with more experts than lanes in a wave."""
+    _say("moe decode many experts", case)
+    L = synth.moe_layer(13, **case)
+    x, hid = synth.activations(14, 1, case["H"])
+    _check_moe(L, x, hid)
+
+
+def test_moe_decode_q8_router_many_experts():
+    """Batch-1 decode with a Q8_0 router and 128 experts (the scalar router loop)."""
+    L = synth.moe_layer(15, H=256, F=64, E=128, K=8, router_type=synth.TYPE_Q8_0)
+    x, hid = synth.activations(16, 1, 256)
+    _check_moe(L, x, hid)
+
+
 def test_moe_no_bias_and_q8_router():
     L = synth.moe_layer(21, H=128, F=64, E=16, K=4, bias=None, router_type=synth.TYPE_Q8_0)
     x, hid = synth.activations(22, 7, 128)
@@ -162,17 +183,18 @@ def test_moe_mask():
     np.testing.assert_array_equal(out, hid)
 
 
-def test_moe_ties_lower_index():
+@pytest.mark.parametrize("E,tied,T", [(8, [1, 4, 6], 3), (8, [1, 4, 6], 1), (100, [5, 70, 71], 1)])
+def test_moe_ties_lower_index(E, tied, T):
     """Equal selection scores rank the lower expert first (stable sort)."""
-    L = synth.moe_layer(41, H=64, F=64, E=8, K=3)
-    router = np.zeros((8, 64), np.float32)
-    router[[1, 4, 6]] = 0.01
+    L = synth.moe_layer(41, H=64, F=64, E=E, K=3)
+    router = np.zeros((E, 64), np.float32)
+    router[tied] = 0.01
     L["router"] = router.view(np.uint8).ravel()
-    L["bias"] = np.zeros(8, np.float32)
-    x, hid = synth.activations(42, 3, 64)
+    L["bias"] = np.zeros(E, np.float32)
+    x, hid = synth.activations(42, T, 64)
     x[:] = np.abs(x)
     _, idx, _, _ = _check_moe(L, x, hid)
-    assert (idx == [1, 4, 6]).all()
+    assert (idx == tied).all()
 
 
 def test_moe_decode_batch1_full():
@@ -265,6 +287,9 @@ def test_moe_mfma_mask_and_unsupported_shape():
     dict(H=96, F=160, E=6, K=3, T=4),
     dict(H=2048, F=768, E=128, K=8, T=1),    # Qwen3-30B-A3B decode (E = 128: two experts a lane)
     dict(H=2048, F=768, E=128, K=8, T=9),
+    dict(H=512, F=96, E=65, K=3, T=1),       # second lane ragged
+    dict(H=256, F=64, E=200, K=4, T=1),      # four experts a lane, ragged
+    dict(H=256, F=64, E=256, K=8, T=1),      # the largest expert count
     dict(H=256, F=320, E=8, K=3, T=200),
 ])
 def test_moe_softmax_gating(case):
@@ -286,6 +311,68 @@ def test_moe_softmax_q8_router_mask_and_mfma():
     _check_moe(L, x, hid, mask={int(r_idx[0, 0])})
     with mfma_min_tokens(2):
         _check_moe(L, x, hid, tol=TOL_MFMA)
+
+
+def test_moe_softmax_decode_calls_in_a_row():
+    """Qwen3-30B-A3B-shaped layer (H=2048, F=768, E=128, K=8) at batch-1 decode: several
+    calls on one handle (each draws a fresh epoch), the last one with an expert mask."""
+    L = synth.moe_layer(77, H=2048, F=768, E=128, K=8, bias=None, gating="softmax",
+                        router_std=0.05)
+    x, hid = synth.activations(78, 5, 2048)
+    ctx = gpu_context()
+    m = upload_layer(ctx, L)
+    try:
+        for t in range(5):
+            mask = {int(oracle.moe_route(L, x[t:t + 1])[0][0, 2])} if t == 4 else None
+            out, idx, w, probs = m.forward(x[t:t + 1], hid[t:t + 1], mask=mask)
+            r_out, r_idx, r_w, r_probs = oracle.moe_ffn(L, x[t:t + 1], hid[t:t + 1], mask=mask)
+            np.testing.assert_array_equal(idx, r_idx)
+            np.testing.assert_array_equal(w, r_w)
+            np.testing.assert_array_equal(probs, r_probs)
+            err = rel_l2(moe_delta(out, hid[t:t + 1]), moe_delta(r_out, hid[t:t + 1]))
+            _say("softmax decode token", t, "rel_l2", err)
+            assert err < TOL_GEMV
+    finally:
+        for t in m._keep:
+            t.release()
+        m.release()
+
+
+def test_moe_softmax_decode_q8_router_and_ties():
+    """Batch-1 softmax decode with a Q8_0 router, and equal probabilities ranked by index."""
+    L = synth.moe_layer(79, H=256, F=64, E=128, K=8, bias=None, gating="softmax",
+                        router_type=synth.TYPE_Q8_0)
+    x, hid = synth.activations(80, 1, 256)
+    _check_moe(L, x, hid)
+    E, tied = 96, [3, 5, 70, 71]
+    L = synth.moe_layer(81, H=64, F=64, E=E, K=4, bias=None, gating="softmax")
+    router = np.zeros((E, 64), np.float32)
+    router[tied + [90]] = 0.01
+    L["router"] = router.view(np.uint8).ravel()
+    x, hid = synth.activations(82, 1, 64)
+    x[:] = np.abs(x)
+    _, idx, _, _ = _check_moe(L, x, hid)
+    assert (idx == tied).all()
+
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_moe_softmax_wide_logits(T):
+    """Router logits tens apart: exponentials below 2^-22 take the in-order sum, and a
+    dominant logit underflows the others to zero (probability 1, weight 1)."""
+    _say("moe softmax wide logits", T)
+    L = synth.moe_layer(83, H=256, F=64, E=128, K=8, bias=None, gating="softmax",
+                        router_std=1.0)
+    x, hid = synth.activations(84, T, 256)
+    _check_moe(L, x, hid)
+    E = 96
+    L = synth.moe_layer(85, H=64, F=64, E=E, K=2, bias=None, gating="softmax")
+    router = np.zeros((E, 64), np.float32)
+    router[77, 0] = 200.0
+    L["router"] = router.view(np.uint8).ravel()
+    x, hid = synth.activations(86, T, 64)
+    x[:, 0] = 1.0
+    _, idx, w, probs = _check_moe(L, x, hid)
+    assert (idx[:, 0] == 77).all() and (w[:, 0] == 1.0).all() and (probs[:, 77] == 1.0).all()
 
 
 def test_moe_softmax_set_gating_rejects_unknown():
