@@ -199,3 +199,99 @@ def moe_gguf(layers, arch="lfm2moe", K=None, alignment=None, extra_kvs=()):
         tensors.append((p + "ffn_up_exps.weight", [H, F, E], TYPE_Q8_0, L["up"]))
         tensors.append((p + "ffn_down_exps.weight", [F, H, E], TYPE_Q8_0, L["down"]))
     return gguf_file(kvs, tensors, alignment=alignment)
+
+
+# ---------------------------------------------------------------- LFM2 whole model
+
+TYPE_F16 = 1
+
+LFM2_TINY = dict(H=256, n_layers=6, attn_layers=(2, 4), n_dense=2, n_heads=4, n_head_kv=2,
+                 head_dim=64, n_ff=512, F=128, E=8, K=2, vocab=300, l_cache=3, ctx=64,
+                 rope_base=5000000.0, eps=1e-5)
+"""A small LFM2-MoE model: layers 0-1 dense, 2 and 4 attention, the rest short-conv."""
+
+LFM2_8B_A1B = dict(H=2048, n_layers=24, attn_layers=(2, 6, 10, 14, 18, 21), n_dense=2,
+                   n_heads=32, n_head_kv=8, head_dim=64, n_ff=7168, F=1792, E=32, K=4,
+                   vocab=65536, l_cache=3, ctx=4096, rope_base=5000000.0, eps=1e-5)
+"""LFM2-8B-A1B's shapes: 24 blocks (6 attention, 18 short-conv; 2 dense FFN,
+22 MoE with 32 experts, top-4), H 2048, 32 query / 8 KV heads of 64, vocab 65536."""
+
+
+def lfm2_tensors(seed, cfg, conv_type=TYPE_F32, tied=True, bias="uniform"):
+    """Seeded tensors of an LFM2-MoE model, named as Lfm2Engine binds them
+    (src/lfm2-engine.js:78-144): [(name, shape, type, bytes)].  Dense and
+    attention matrices are Q8_0; norms, router and expert bias F32; the conv
+    kernel [l_cache, H] F32, F16 or Q8_0 (one block per column)."""
+    rng = np.random.default_rng(seed)
+    H, L, hd = cfg["H"], cfg["l_cache"], cfg["head_dim"]
+    nq, nkv = cfg["n_heads"] * hd, cfg["n_head_kv"] * hd
+    t = []
+
+    def q8(name, i, o, n=1, scale=0.005):
+        t.append((name, [i, o] + ([n] if n > 1 else []), TYPE_Q8_0, q8_0_tensor(rng, i, o, n, scale)))
+
+    def f32(name, shape, v):
+        t.append((name, list(shape), TYPE_F32, np.asarray(v, np.float32)))
+
+    q8("token_embd.weight", H, cfg["vocab"], scale=0.01)
+    f32("token_embd_norm.weight", [H], rng.uniform(0.5, 1.5, H))
+    if not tied:
+        q8("output.weight", H, cfg["vocab"], scale=0.01)
+    for i in range(cfg["n_layers"]):
+        p = "blk.%d." % i
+        f32(p + "attn_norm.weight", [H], rng.uniform(0.5, 1.5, H))
+        f32(p + "ffn_norm.weight", [H], rng.uniform(0.5, 1.5, H))
+        if i in cfg["attn_layers"]:
+            q8(p + "attn_q.weight", H, nq)
+            q8(p + "attn_k.weight", H, nkv)
+            q8(p + "attn_v.weight", H, nkv)
+            q8(p + "attn_output.weight", nq, H)
+            f32(p + "attn_q_norm.weight", [hd], rng.uniform(0.5, 1.5, hd))
+            f32(p + "attn_k_norm.weight", [hd], rng.uniform(0.5, 1.5, hd))
+        else:
+            kern = (rng.standard_normal(L * H) * 0.5).astype(np.float32)   # index d * L + k
+            if conv_type == TYPE_F32:
+                t.append((p + "shortconv.conv.weight", [L, H], TYPE_F32, kern))
+            elif conv_type == TYPE_F16:
+                t.append((p + "shortconv.conv.weight", [L, H], TYPE_F16, kern.astype(np.float16)))
+            else:
+                t.append((p + "shortconv.conv.weight", [L, H], TYPE_Q8_0, q8_0_tensor(rng, L, H, 1, 0.01)))
+            q8(p + "shortconv.in_proj.weight", H, 3 * H)
+            q8(p + "shortconv.out_proj.weight", H, H)
+        if i < cfg["n_dense"]:
+            q8(p + "ffn_gate.weight", H, cfg["n_ff"])
+            q8(p + "ffn_up.weight", H, cfg["n_ff"])
+            q8(p + "ffn_down.weight", cfg["n_ff"], H)
+        else:
+            E, F = cfg["E"], cfg["F"]
+            f32(p + "ffn_gate_inp.weight", [H, E], rng.standard_normal(E * H) * 0.05)
+            if bias is not None:
+                f32(p + "exp_probs_b.bias", [E], rng.uniform(-0.01, 0.01, E))
+            q8(p + "ffn_gate_exps.weight", H, F, E)
+            q8(p + "ffn_up_exps.weight", H, F, E)
+            q8(p + "ffn_down_exps.weight", F, H, E)
+    return t
+
+
+def lfm2_gguf(seed, cfg, arch="lfm2moe", **kw):
+    """GGUF bytes of lfm2_tensors(seed, cfg) with the keys Lfm2Engine reads
+    (src/lfm2-engine.js:15-47; per-layer head_count_kv, 0 for short-conv
+    blocks).  Returns (bytes, {name: offset}, [(name, shape, type, bytes)])."""
+    p = arch + "."
+    kvs = [("general.architecture", GGUF_STRING, arch),
+           (p + "block_count", 4, cfg["n_layers"]),
+           (p + "embedding_length", 4, cfg["H"]),
+           (p + "attention.head_count", 4, cfg["n_heads"]),
+           (p + "attention.head_count_kv", GGUF_ARRAY,
+            (5, [cfg["n_head_kv"] if i in cfg["attn_layers"] else 0 for i in range(cfg["n_layers"])])),
+           (p + "attention.layer_norm_rms_epsilon", 6, cfg["eps"]),
+           (p + "expert_count", 4, cfg["E"]),
+           (p + "expert_used_count", 4, cfg["K"]),
+           (p + "expert_feed_forward_length", 4, cfg["F"]),
+           (p + "leading_dense_block_count", 4, cfg["n_dense"]),
+           (p + "shortconv.l_cache", 4, cfg["l_cache"]),
+           (p + "context_length", 4, cfg["ctx"]),
+           (p + "rope.freq_base", 6, cfg["rope_base"])]
+    tensors = lfm2_tensors(seed, cfg, **kw)
+    data, offs = gguf_file(kvs, tensors)
+    return data, offs, tensors

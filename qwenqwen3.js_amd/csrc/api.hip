@@ -57,7 +57,7 @@ int ensure_pinned(qq_ctx *ctx, size_t bytes)
 
 // Entry points that copy to or from the host, synchronise or allocate cannot
 // be recorded into a graph.
-static int no_capture(qq_ctx *ctx, const char *what)
+int no_capture(qq_ctx *ctx, const char *what)
 {
     if (ctx && ctx->capturing)
         return set_error(ctx, "%s cannot run while a graph capture is open", what);
@@ -68,12 +68,12 @@ static const char *const kKernelNames[K_COUNT] = {
     "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
     "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
     "cast_f16",         "mfma_gateup",    "mfma_down",      "stream_gateup", "stream_down",
-    "rmsnorm",
+    "rmsnorm", "lfm2_embed", "lfm2_matvec", "lfm2_attention",
 };
 
 // Read and clear the device error word; non-zero means a bounded device-side
 // wait expired (the results of that call are not valid).
-static int check_device_error(qq_ctx *ctx)
+int check_device_error(qq_ctx *ctx)
 {
     uint32_t e = 0;
     QQ_HIP(ctx, hipMemcpyAsync(&e, ctx->sync_err, 4, hipMemcpyDeviceToHost, ctx->stream));

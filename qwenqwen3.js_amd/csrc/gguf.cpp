@@ -595,3 +595,5 @@ int qq_gguf_moe_layer(qq_ctx *ctx, const qq_gguf *g, int block, int K, int gatin
 }
 
 }  // extern "C"
+
+const uint8_t *qq::gguf_base(const qq_gguf *g) { return g ? g->base : nullptr; }

@@ -1,0 +1,454 @@
+// lfm2.hip -- kernels of the LFM2 single-token device forward.
+//
+// Reference: Lfm2Engine.forward, src/lfm2-engine.js:228-280, and the blocks
+// it calls (_shortConv :282-327, _selfAttention :329-392, _denseFfn
+// :394-403); the MoE block runs through decode.hip.
+//
+// One token per call.  The matrix products are Q8_0 x fp32 matvecs
+// (matmulQ80xF32, src/tensor.js:26-53) over the repacked block-major panels
+// of q8_0.hip, and every elementwise step of the reference is folded into
+// the matvec that produces or consumes its operands:
+//   * the RMSNorm in front of a block (attn_norm, ffn_norm, the output norm:
+//     src/tensor.js:103-114) is formed by every workgroup of the matvec that
+//     reads it, from the residual row (binary64 sum of squares);
+//   * residual adds (addVec, src/tensor.js:181-185) are the epilogue of the
+//     matvec whose output is added (hidden = fp32(hidden + fp32(W x)));
+//   * short-conv: a workgroup owns 32 channels d and computes rows d, H + d
+//     and 2H + d of in_proj (B, C, x), then bx = B * x, the depthwise causal
+//     conv over its channels' state, the state shift and y = C * conv;
+//   * attention: a workgroup owns one head of q, k or v (64 rows): per-head
+//     RMSNorm, split-half RoPE and the KV-cache store are its epilogue;
+//   * dense FFN: rows f of gate and up in one workgroup, silu(g) * u.
+// Where the reference stores into a Float32Array the kernels round to fp32 at
+// the same step, and its binary64 expressions are kept in binary64 without
+// contraction into fused multiply-adds.
+#include "qq_device.h"
+
+// binary64 expressions of the reference stay separate multiplies and adds
+#pragma clang fp contract(off)
+
+namespace qq {
+
+constexpr int LM_WPG = 4;        // waves per 32-row group, splitting the blocks of a row
+constexpr int LM_MAX_IN = 8192;  // longest input row staged in LDS
+constexpr int LM_MAX_L = 4;      // short-conv kernel length (l_cache) supported
+constexpr int LM_HEAD = 64;      // head_dim supported by the QKV epilogue and attention
+constexpr int LM_MAX_CTX = 4096; // the reference caps the context at 4096 (lfm2-engine.js:33)
+constexpr int LM_ATTN_THREADS = 256;
+
+struct LmMat {
+    const int8_t *qs;
+    const __half *d;
+    int rows;
+};
+
+struct LmArgs {
+    const float *x;      // input row (in_dim floats)
+    int in_dim, nb;      // nb = ceil(in_dim / 32)
+    int norm;            // x = rmsnorm(x) * norm_w first
+    const float *norm_w;
+    double eps;
+    LmMat m[3];          // PLAIN/RESID/CONV: m[0]; SWIGLU: gate, up; QKV: q, k, v
+    float *y;            // output (RESID: added into)
+    // short-conv: state [L-1][H] (oldest first), kernel [H][L]
+    float *state;
+    const float *kern;
+    int L, H;
+    // attention: q out, KV cache of this layer [n_kv_heads][max_ctx][64]
+    float *q;
+    float *kc, *vc;
+    const float *qn, *kn;   // per-head norm weights [64]
+    int n_heads, n_kv_heads, pos, max_ctx;
+    const double *freq;     // RoPE frequencies 1 / base^(i / 32), i < 32
+};
+
+// Sum of one value per thread over a block of NW waves: waves by DPP, then
+// the wave sums in wave order.  Contains a __syncthreads.
+template <int NW>
+__device__ __forceinline__ double lm_block_sum(double v, double *red)
+{
+    return block_sum_f64<NW>(v, red);
+}
+
+template <int NW>
+__device__ __forceinline__ float lm_block_max(float v, float *red)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, WAVE));
+    if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
+    __syncthreads();
+    float m = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) m = fmaxf(m, red[w]);
+    return m;
+}
+
+// Row of matrix `mat` owned by 32-row group g of this workgroup, or -1.
+template <int MODE>
+__device__ __forceinline__ int lm_row(const LmArgs &a, int g, int &mat)
+{
+    const int j = blockIdx.x;
+    if (MODE == LM_PLAIN || MODE == LM_RESID) {
+        mat = 0;
+        return 64 * j + 32 * g;
+    }
+    if (MODE == LM_SWIGLU) {
+        mat = g;
+        return 32 * j;
+    }
+    if (MODE == LM_CONV) {
+        mat = 0;
+        return g * a.H + 32 * j;
+    }
+    // QKV: one head per workgroup, q heads first, then k, then v
+    if (j < a.n_heads) {
+        mat = 0;
+        return LM_HEAD * j + 32 * g;
+    }
+    mat = j < a.n_heads + a.n_kv_heads ? 1 : 2;
+    return LM_HEAD * (j - a.n_heads - (mat == 2 ? a.n_kv_heads : 0)) + 32 * g;
+}
+
+template <int MODE, int G>
+__global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
+{
+    constexpr int NT = G * LM_WPG * WAVE;
+    constexpr int NW = G * LM_WPG;
+    extern __shared__ __align__(16) float lm_lds[];
+    float *xl = lm_lds;                  // nb * 32 activations (zero padded)
+    float *xs = lm_lds + a.nb * QK;      // 2 * nb half-block sums
+    __shared__ float red[G][LM_WPG][32];
+    __shared__ double redd[NW];
+    __shared__ float hv[LM_HEAD];
+    __shared__ double hinv;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
+    const int kp = a.nb * QK;
+
+    // ---- input row -> LDS, normalised when asked (src/tensor.js:103-114) ----
+    double inv = 1.0;
+    if (a.norm) {
+        double ss = 0.0;
+        for (int k = tid; k < a.in_dim; k += NT) {
+            const double v = (double)a.x[k];
+            ss = fma(v, v, ss);
+        }
+        inv = rms_inv(lm_block_sum<NW>(ss, redd), a.in_dim, a.eps);
+    }
+    for (int k = tid; k < kp; k += NT) {
+        float v = k < a.in_dim ? a.x[k] : 0.0f;
+        if (a.norm && k < a.in_dim)
+            v = (float)((double)(a.norm_w ? a.norm_w[k] : 1.0f) * (double)v * inv);
+        xl[k] = v;
+    }
+    __syncthreads();
+    for (int i = tid; i < 2 * a.nb; i += NT) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 16; j++) s += xl[16 * i + j];
+        xs[i] = s;
+    }
+    __syncthreads();
+
+    // ---- 32-row groups: lane l takes row l/2, half l%2 of each block ----
+    const int g = wave / LM_WPG, wg = wave % LM_WPG;
+    int mat;
+    const int row0 = lm_row<MODE>(a, g, mat);
+    const LmMat M = a.m[mat];
+    const int row = row0 + lane / 2, h = lane & 1;
+    const bool row_ok = row < M.rows;
+    const int rc = min(row, M.rows - 1);
+    float acc = 0.0f;
+    for (int bb = wg; bb < a.nb; bb += 4 * LM_WPG) {
+        int4 q[4];
+        float dd[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {   // clamped addresses, zero scale out of range
+            const int b = min(bb + LM_WPG * u, a.nb - 1);
+            const size_t o = bm_index(0, a.nb, b, M.rows, rc);
+            q[u] = *reinterpret_cast<const int4 *>(M.qs + o * QK + 16 * h);
+            dd[u] = __half2float(M.d[o]);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; u++) dd[u] = (row_ok && bb + LM_WPG * u < a.nb) ? dd[u] : 0.0f;
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int b = bb + LM_WPG * u;
+            if (b < a.nb) acc = fmaf(dot16_q8_lds(q[u], &xl[b * QK + 16 * h], xs[2 * b + h]), dd[u], acc);
+        }
+    }
+    acc += __shfl_xor(acc, 1, WAVE);
+    if (h == 0) red[g][wg][lane / 2] = acc;
+    __syncthreads();
+
+    // ---- epilogues ----
+    auto rowsum = [&](int gg, int r) {
+        float v = red[gg][0][r];
+#pragma unroll
+        for (int w = 1; w < LM_WPG; w++) v += red[gg][w][r];
+        return v;
+    };
+    if (MODE == LM_PLAIN || MODE == LM_RESID) {
+        if (tid < G * 32) {
+            const int gg = tid / 32, r = tid % 32;
+            const int orow = 64 * blockIdx.x + 32 * gg + r;
+            if (orow < a.m[0].rows) {
+                const float v = rowsum(gg, r);
+                a.y[orow] = MODE == LM_RESID ? a.y[orow] + v : v;
+            }
+        }
+    } else if (MODE == LM_SWIGLU) {
+        // siluInPlace, mulInPlace (src/tensor.js:167-179)
+        const int f = 32 * blockIdx.x + tid;
+        if (tid < 32 && f < a.m[0].rows) {
+            const float gv = rowsum(0, tid), uv = rowsum(1, tid);
+            const double g64 = (double)gv;
+            const float s = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
+            a.y[f] = s * uv;
+        }
+    } else if (MODE == LM_CONV) {
+        // _shortConv steps 3-6 (src/lfm2-engine.js:297-322) for channel d
+        const int d = 32 * blockIdx.x + tid;
+        if (tid < 32 && d < a.H) {
+            const float B = rowsum(0, tid), C = rowsum(1, tid), X = rowsum(2, tid);
+            const float bx = B * X;
+            double s = 0.0;
+            float st[LM_MAX_L];
+#pragma unroll
+            for (int k = 0; k < LM_MAX_L - 1; k++)
+                if (k < a.L - 1) st[k] = a.state[(size_t)k * a.H + d];
+#pragma unroll
+            for (int k = 0; k < LM_MAX_L; k++) {
+                if (k >= a.L) break;
+                const double w = (double)a.kern[(size_t)d * a.L + k];
+                const double t = w * (double)(k < a.L - 1 ? st[k] : bx);
+                s = k == 0 ? t : s + t;
+            }
+            const float co = (float)s;
+#pragma unroll
+            for (int k = 0; k + 1 < LM_MAX_L - 1; k++)
+                if (k + 1 < a.L - 1) a.state[(size_t)k * a.H + d] = st[k + 1];
+            a.state[(size_t)(a.L - 2) * a.H + d] = bx;
+            a.y[d] = C * co;
+        }
+    } else {
+        // QKV: perHeadRMSNorm (src/tensor.js:117-129), applyRoPE (:132-147),
+        // KVCache.store (src/kv-cache.js:16-32)
+        if (tid < LM_HEAD) hv[tid] = rowsum(tid / 32, tid % 32);
+        __syncthreads();
+        const int j = blockIdx.x;
+        const int kind = j < a.n_heads ? 0 : (j < a.n_heads + a.n_kv_heads ? 1 : 2);
+        const int head = kind == 0 ? j : (kind == 1 ? j - a.n_heads : j - a.n_heads - a.n_kv_heads);
+        if (kind == 2) {
+            if (tid < LM_HEAD)
+                a.vc[((size_t)head * a.max_ctx + a.pos) * LM_HEAD + tid] = hv[tid];
+            return;
+        }
+        if (tid == 0) {
+            double ss = 0.0;   // in order, as the reference adds
+            for (int i = 0; i < LM_HEAD; i++) ss = ss + (double)hv[i] * (double)hv[i];
+            hinv = 1.0 / sqrt(ss / (double)LM_HEAD + a.eps);
+        }
+        __syncthreads();
+        const float *nw = kind == 0 ? a.qn : a.kn;
+        if (tid < LM_HEAD) hv[tid] = (float)((double)nw[tid] * (double)hv[tid] * hinv);
+        __syncthreads();
+        if (tid < LM_HEAD / 2) {
+            const int i = tid, half = LM_HEAD / 2;
+            const double th = (double)a.pos * a.freq[i];
+            const double c = cos(th), s = sin(th);
+            const double x0 = (double)hv[i], x1 = (double)hv[i + half];
+            const float r0 = (float)(x0 * c - x1 * s);
+            const float r1 = (float)(x0 * s + x1 * c);
+            if (kind == 0) {
+                a.q[(size_t)head * LM_HEAD + i] = r0;
+                a.q[(size_t)head * LM_HEAD + i + half] = r1;
+            } else {
+                float *kr = a.kc + ((size_t)head * a.max_ctx + a.pos) * LM_HEAD;
+                kr[i] = r0;
+                kr[i + half] = r1;
+            }
+        }
+    }
+}
+
+// GQA attention of one token (src/lfm2-engine.js:354-388), one workgroup
+// per query head h over kv head (h * n_kv_heads / n_heads) | 0 and positions
+// 0..n-1:
+//   score_p = fp32(dot(q, k_p) * scale)   dot in binary64, in dimension order
+//   softmaxInPlace (src/tensor.js:150-164): max, e_p = fp32(exp(s_p - max)),
+//     w_p = fp32(e_p * (1 / sum e))
+//   out[d] = fp32 sum of v_p[d] * w_p
+// The sum of the exponentials is a tree (not the reference's one-by-one
+// order) and out[d] is accumulated in four position classes joined at the
+// end, so those two steps agree with the reference to rounding, not bit for bit.
+__global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float *__restrict__ q,
+                                                                   const float *__restrict__ kc,
+                                                                   const float *__restrict__ vc,
+                                                                   int n_heads, int n_kv_heads,
+                                                                   int max_ctx, int n, double scale,
+                                                                   float *__restrict__ out)
+{
+    constexpr int NW = LM_ATTN_THREADS / WAVE;
+    __shared__ __align__(16) float qh[LM_HEAD];
+    __shared__ float sc[LM_MAX_CTX];
+    __shared__ float redf[NW];
+    __shared__ double redd[NW];
+    __shared__ float part[NW][LM_HEAD];
+    const int tid = threadIdx.x;
+    const int hq = blockIdx.x;
+    const int g = (int)(((long long)hq * n_kv_heads) / n_heads);
+    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
+    __syncthreads();
+    const float *K = kc + (size_t)g * max_ctx * LM_HEAD;
+    const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
+    float mx = -INFINITY;
+    for (int p = tid; p < n; p += LM_ATTN_THREADS) {
+        const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)p * LM_HEAD);
+        double dot = 0.0;
+#pragma unroll
+        for (int i = 0; i < LM_HEAD / 4; i++) {
+            const float4 kv = kr[i];
+            dot = fma((double)qh[4 * i], (double)kv.x, dot);
+            dot = fma((double)qh[4 * i + 1], (double)kv.y, dot);
+            dot = fma((double)qh[4 * i + 2], (double)kv.z, dot);
+            dot = fma((double)qh[4 * i + 3], (double)kv.w, dot);
+        }
+        const float s = (float)(dot * scale);
+        sc[p] = s;
+        mx = fmaxf(mx, s);
+    }
+    const float M = lm_block_max<NW>(mx, redf);
+    double ls = 0.0;
+    for (int p = tid; p < n; p += LM_ATTN_THREADS) {
+        const float e = (float)exp((double)sc[p] - (double)M);
+        sc[p] = e;
+        ls += (double)e;
+    }
+    const double inv = 1.0 / block_sum_f64<NW>(ls, redd);
+    for (int p = tid; p < n; p += LM_ATTN_THREADS) sc[p] = (float)((double)sc[p] * inv);
+    __syncthreads();
+    const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
+    float acc = 0.0f;
+    for (int p = cls; p < n; p += NW) {
+        const float w = sc[p];
+        if (w != 0.0f) acc = (float)fma((double)V[(size_t)p * LM_HEAD + d], (double)w, (double)acc);
+    }
+    part[cls][d] = acc;
+    __syncthreads();
+    if (tid < LM_HEAD) {
+        float o = part[0][tid];
+#pragma unroll
+        for (int c = 1; c < NW; c++) o = o + part[c][tid];
+        out[(size_t)hq * LM_HEAD + tid] = o;
+    }
+}
+
+// embeddingLookupQ80 (src/tensor.js:56-77) of column `token` of the repacked
+// [H, vocab] table: hidden[i] = q * d (exact in fp32).
+__global__ __launch_bounds__(256) void lfm2_embed_kernel(const int8_t *__restrict__ qs,
+                                                        const __half *__restrict__ d, int nb,
+                                                        int vocab, int token, int H,
+                                                        float *__restrict__ out)
+{
+    for (int i = threadIdx.x; i < H; i += 256) {
+        const size_t o = bm_index(0, nb, i / QK, vocab, token);
+        out[i] = (float)qs[o * QK + i % QK] * __half2float(d[o]);
+    }
+}
+
+__global__ __launch_bounds__(256) void lfm2_zero_kernel(float *__restrict__ p, size_t n)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0.0f;
+}
+
+// ---------------------------------------------------------------------------
+
+static LmMat lm_mat(const qq_tensor *t) { return LmMat{t->qs, t->d, t->out_dim}; }
+
+int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
+{
+    LmArgs a{};
+    a.x = l.x;
+    a.in_dim = l.mats[0]->in_dim;
+    a.nb = l.mats[0]->nb;
+    a.norm = l.norm;
+    a.norm_w = l.norm_w;
+    a.eps = l.eps;
+    for (int i = 0; i < 3; i++)
+        if (l.mats[i]) a.m[i] = lm_mat(l.mats[i]);
+    a.y = l.y;
+    a.state = l.state;
+    a.kern = l.kern;
+    a.L = l.L;
+    a.H = l.H;
+    a.q = l.q;
+    a.kc = l.kc;
+    a.vc = l.vc;
+    a.qn = l.qn;
+    a.kn = l.kn;
+    a.n_heads = l.n_heads;
+    a.n_kv_heads = l.n_kv_heads;
+    a.pos = l.pos;
+    a.max_ctx = l.max_ctx;
+    a.freq = l.freq;
+    if (a.in_dim > LM_MAX_IN) return set_error(ctx, "lfm2: input row of %d > %d", a.in_dim, LM_MAX_IN);
+    const size_t shm = (size_t)a.nb * QK * 4 + (size_t)2 * a.nb * 4;
+    prof_begin(ctx, K_LFM2_MV);
+    switch (mode) {
+    case LM_PLAIN:
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_PLAIN, 2>), dim3((a.m[0].rows + 63) / 64), dim3(2 * LM_WPG * WAVE), shm, a);
+        break;
+    case LM_RESID:
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 2>), dim3((a.m[0].rows + 63) / 64), dim3(2 * LM_WPG * WAVE), shm, a);
+        break;
+    case LM_SWIGLU:
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2>), dim3((a.m[0].rows + 31) / 32), dim3(2 * LM_WPG * WAVE), shm, a);
+        break;
+    case LM_CONV:
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3>), dim3((a.H + 31) / 32), dim3(3 * LM_WPG * WAVE), shm, a);
+        break;
+    default:
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 2>), dim3(a.n_heads + 2 * a.n_kv_heads), dim3(2 * LM_WPG * WAVE), shm, a);
+        break;
+    }
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
+                     int n_kv_heads, int max_ctx, int n, double scale, float *out)
+{
+    if (n < 1 || n > LM_MAX_CTX || n > max_ctx) return set_error(ctx, "lfm2: %d positions", n);
+    prof_begin(ctx, K_LFM2_ATTN);
+    QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, q, kc, vc, n_heads,
+              n_kv_heads, max_ctx, n, scale, out);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+int launch_lfm2_embed(qq_ctx *ctx, const qq_tensor *t, int token, float *out)
+{
+    prof_begin(ctx, K_LFM2_EMBED);
+    QQ_LAUNCH(ctx, lfm2_embed_kernel, dim3(1), dim3(256), 0, t->qs, t->d, t->nb, t->out_dim, token,
+              t->in_dim, out);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+int launch_lfm2_zero(qq_ctx *ctx, float *p, size_t n)
+{
+    if (!n) return QQ_OK;
+    const unsigned grid = (unsigned)std::min<size_t>((n + 255) / 256, 4096);
+    QQ_LAUNCH(ctx, lfm2_zero_kernel, dim3(grid), dim3(256), 0, p, n);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+}  // namespace qq

@@ -12,6 +12,8 @@
 
 #include "../../include/qq_moe.h"
 
+struct qq_gguf;
+
 namespace qq {
 
 constexpr int QK = 32;        // weights per Q8_0 block
@@ -135,6 +137,9 @@ enum KernelId {
     K_STREAM_GATEUP,
     K_STREAM_DOWN,
     K_RMSNORM,
+    K_LFM2_EMBED,
+    K_LFM2_MV,
+    K_LFM2_ATTN,
     K_COUNT
 };
 
@@ -157,6 +162,11 @@ void prof_slot(qq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop);
 
 int set_error(qq_ctx *ctx, const char *fmt, ...);
 int check_hip(qq_ctx *ctx, hipError_t e, const char *what);
+// Waits for the stream, then reads and clears the device error word (set by a
+// bounded device-side wait that expired).
+int check_device_error(qq_ctx *ctx);
+// QQ_E_ARG while a graph capture is open on the context's stream.
+int no_capture(qq_ctx *ctx, const char *what);
 int ensure_scratch(qq_ctx *ctx, size_t bytes);
 int ensure_pinned(qq_ctx *ctx, size_t bytes);
 
@@ -188,6 +198,33 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
                       char *work, const NormArgs *norm = nullptr);
 size_t grouped_work_bytes(const qq_moe *m, int T);
+
+// LFM2 single-token forward (lfm2.hip).  Matvec modes: y = W x; hidden +=
+// W x; silu(gate x) * (up x); in_proj + short-conv; q/k/v heads with norm,
+// RoPE and the KV-cache store.
+enum { LM_PLAIN = 0, LM_RESID = 1, LM_SWIGLU = 2, LM_CONV = 3, LM_QKV = 4 };
+struct LmLaunch {
+    const float *x = nullptr;
+    const qq_tensor *mats[3] = {nullptr, nullptr, nullptr};
+    int norm = 0;
+    const float *norm_w = nullptr;
+    double eps = 0.0;
+    float *y = nullptr;
+    float *state = nullptr;
+    const float *kern = nullptr;
+    int L = 0, H = 0;
+    float *q = nullptr, *kc = nullptr, *vc = nullptr;
+    const float *qn = nullptr, *kn = nullptr;
+    int n_heads = 0, n_kv_heads = 0, pos = 0, max_ctx = 0;
+    const double *freq = nullptr;
+};
+int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l);
+int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
+                     int n_kv_heads, int max_ctx, int n, double scale, float *out);
+int launch_lfm2_embed(qq_ctx *ctx, const qq_tensor *t, int token, float *out);
+int launch_lfm2_zero(qq_ctx *ctx, float *p, size_t n);
+// First byte of a GGUF reader's file (gguf.cpp).
+const uint8_t *gguf_base(const ::qq_gguf *g);
 // Optional row-tile table written by the dispatch kernel: tile i covers slots
 // [m0[i], m0[i] + bm) of expert e[i] (clipped to the expert's count); *n = tiles.
 struct DispatchTiles {

@@ -43,6 +43,20 @@ GGUF_EXPORTS = (
 )
 
 
+# ... and include/qq_lfm2.h
+LFM2_EXPORTS = (
+    "qq_lfm2_create", "qq_lfm2_get_info", "qq_lfm2_reset", "qq_lfm2_forward_dev", "qq_lfm2_forward",
+    "qq_lfm2_release",
+)
+
+
+class Lfm2Info(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int) for n in (
+        "n_layers", "n_embd", "n_heads", "n_head_kv", "head_dim", "n_vocab", "n_ff", "n_experts",
+        "n_experts_used", "n_dense_lead", "l_cache", "max_ctx", "n_attn_layers")] + [
+        ("eps", ctypes.c_double), ("rope_freq_base", ctypes.c_double)]
+
+
 class GgufHeader(ctypes.Structure):
     _fields_ = [("version", ctypes.c_uint32), ("tensor_count", ctypes.c_uint64),
                 ("kv_count", ctypes.c_uint64), ("file_size", ctypes.c_uint64),
@@ -122,6 +136,12 @@ def load():
                                         ctypes.POINTER(ctypes.c_double)]),
         "qq_gguf_moe_params": (I, [P, I, I, I, ctypes.POINTER(GgufMoeInfo)]),
         "qq_gguf_moe_layer": (I, [P, P, I, I, I, PP]),
+        "qq_lfm2_create": (I, [P, P, PP]),
+        "qq_lfm2_get_info": (I, [P, ctypes.POINTER(Lfm2Info)]),
+        "qq_lfm2_reset": (I, [P, P]),
+        "qq_lfm2_forward_dev": (I, [P, P, I, I, P, P]),
+        "qq_lfm2_forward": (I, [P, P, I, I, P]),
+        "qq_lfm2_release": (None, [P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -336,6 +356,38 @@ class Gguf:
         h = ctypes.c_void_p()
         ctx.check(self.L.qq_gguf_moe_layer(ctx.h, self.h, block, K, gating, ctypes.byref(h)), "qq_gguf_moe_layer")
         return MoeLayer(ctx, h, p["H"], p["F"], p["E"], p["K"], ())
+
+
+class Lfm2Model:
+    """The LFM2 single-token device forward (include/qq_lfm2.h), built from a Gguf."""
+
+    def __init__(self, ctx, gguf):
+        self.ctx, self.L = ctx, ctx.L
+        h = ctypes.c_void_p()
+        ctx.check(self.L.qq_lfm2_create(ctx.h, gguf.h, ctypes.byref(h)), "qq_lfm2_create")
+        self.h = h
+        info = Lfm2Info()
+        ctx.check(self.L.qq_lfm2_get_info(self.h, ctypes.byref(info)), "qq_lfm2_get_info")
+        self.info = {f: getattr(info, f) for f, _ in Lfm2Info._fields_}
+
+    def reset(self):
+        self.ctx.check(self.L.qq_lfm2_reset(self.ctx.h, self.h), "qq_lfm2_reset")
+
+    def forward(self, token, position, logits=True):
+        """Host logits (float32 [n_vocab]) or None."""
+        out = np.empty(self.info["n_vocab"], np.float32) if logits else None
+        self.ctx.check(self.L.qq_lfm2_forward(self.ctx.h, self.h, token, position, _ptr(out)),
+                       "qq_lfm2_forward")
+        return out
+
+    def forward_dev(self, token, position, logits_ptr=None, idx_ptr=None):
+        self.ctx.check(self.L.qq_lfm2_forward_dev(self.ctx.h, self.h, token, position, logits_ptr, idx_ptr),
+                       "qq_lfm2_forward_dev")
+
+    def release(self):
+        if self.h:
+            self.L.qq_lfm2_release(self.ctx.h, self.h)
+            self.h = None
 
 
 class Tensor:

@@ -12,12 +12,14 @@ from _util import ROOT
 
 HEADER = os.path.join(ROOT, "include", "qq_moe.h")
 GGUF_HEADER = os.path.join(ROOT, "include", "qq_gguf.h")
+LFM2_HEADER = os.path.join(ROOT, "include", "qq_lfm2.h")
 HAS_GPU = os.path.exists("/dev/kfd")
 
 
 def declared_functions(header=None):
     if header is None:
-        return sorted(set(declared_functions(HEADER)) | set(declared_functions(GGUF_HEADER)))
+        return sorted(set(declared_functions(HEADER)) | set(declared_functions(GGUF_HEADER)) |
+                      set(declared_functions(LFM2_HEADER)))
     text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(qq_[a-z0-9_]+)\s*\(", text)))
@@ -26,10 +28,11 @@ def declared_functions(header=None):
 def test_header_and_binding_agree():
     assert declared_functions(HEADER) == sorted(qq_hip.EXPORTS)
     assert declared_functions(GGUF_HEADER) == sorted(qq_hip.GGUF_EXPORTS)
+    assert declared_functions(LFM2_HEADER) == sorted(qq_hip.LFM2_EXPORTS)
 
 
 def test_every_header_is_covered():
-    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == ["qq_gguf.h", "qq_moe.h"]
+    assert sorted(os.listdir(os.path.join(ROOT, "include"))) == ["qq_gguf.h", "qq_lfm2.h", "qq_moe.h"]
 
 
 def test_library_exports_every_declared_symbol():

@@ -1,0 +1,102 @@
+"""The LFM2 single-token device forward (include/qq_lfm2.h) through the C ABI
+against the Node restatement of the reference's forward (oracle/lfm2_ref.js,
+pinned by tests/test_lfm2_oracle.py) on small synthetic model files: logits
+within 1e-4 relative L2 per token, every MoE block's expert choice equal."""
+import numpy as np
+import pytest
+
+import synth
+import _lfm2
+from _util import gpu_context, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOKENS = [5, 17, 250, 3, 99, 0, 42, 7]
+TOL = 1e-4
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _model(tmp_path, seed, cfg=synth.LFM2_TINY, **kw):
+    import qq_hip
+    path, offs, tensors = _lfm2.write_model(tmp_path, seed, cfg, **kw)
+    g = qq_hip.Gguf(path)
+    try:
+        m = qq_hip.Lfm2Model(gpu_context(), g)
+    finally:
+        g.close()
+    return m, path, offs, tensors
+
+
+def _check_tokens(tmp_path, seed, cfg=synth.LFM2_TINY, tokens=TOKENS, **kw):
+    import torch
+    m, path, offs, tensors = _model(tmp_path, seed, cfg, **kw)
+    try:
+        ref, routes = _lfm2.js_forward(tmp_path, path, offs, tensors, cfg, tokens)
+        T, V, nl, K = len(tokens), m.info["n_vocab"], m.info["n_layers"], m.info["n_experts_used"]
+        logits = torch.empty((T, V), dtype=torch.float32, device="cuda")
+        idx = torch.full((T, nl, K), -1, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        for t, tok in enumerate(tokens):
+            m.forward_dev(tok, t, logits[t].data_ptr(), idx[t].data_ptr())
+        gpu_context().synchronize()
+        got, gi = logits.cpu().numpy(), idx.cpu().numpy()
+        for t in range(T):
+            err = rel_l2(got[t], ref[t])
+            _say("token", t, "rel_l2", err)
+            assert err < TOL, (t, err)
+        moe = [l for l in range(nl) if l >= cfg["n_dense"]]
+        assert [gi[t, l].tolist() for t in range(T) for l in moe] == routes
+        return m, got
+    except BaseException:
+        m.release()
+        raise
+
+
+@pytest.mark.parametrize("seed,kw", [
+    (3, {}),
+    (4, dict(conv_type=synth.TYPE_F16, tied=False)),
+    (5, dict(conv_type=synth.TYPE_Q8_0, bias=None)),
+])
+def test_forward_matches_oracle(tmp_path, seed, kw):
+    _say("lfm2 forward", seed, kw)
+    m, _ = _check_tokens(tmp_path, seed, **kw)
+    m.release()
+
+
+def test_info_reset_and_host_entry_point(tmp_path):
+    _say("lfm2 info/reset")
+    cfg = synth.LFM2_TINY
+    m, got = _check_tokens(tmp_path, 3, tokens=TOKENS[:3])
+    try:
+        assert m.info["n_layers"] == cfg["n_layers"] and m.info["n_vocab"] == cfg["vocab"]
+        assert m.info["n_attn_layers"] == len(cfg["attn_layers"]) and m.info["head_dim"] == 64
+        assert m.info["max_ctx"] == cfg["ctx"] and m.info["n_ff"] == cfg["n_ff"]
+        # resetState: the same tokens again give the same logits, bit for bit
+        m.reset()
+        again = [m.forward(t, i) for i, t in enumerate(TOKENS[:3])]
+        for t in range(3):
+            np.testing.assert_array_equal(again[t], got[t])
+        # skipLogits
+        assert m.forward(TOKENS[3], 3, logits=False) is None
+    finally:
+        m.release()
+
+
+def test_bad_token_position_and_file(tmp_path):
+    import qq_hip
+    _say("lfm2 errors")
+    cfg = synth.LFM2_TINY
+    m, _, _, _ = _model(tmp_path, 3)
+    try:
+        with pytest.raises(qq_hip.QQError, match="token"):
+            m.forward(cfg["vocab"], 0)
+        with pytest.raises(qq_hip.QQError, match="position"):
+            m.forward(0, cfg["ctx"])
+    finally:
+        m.release()
+    bad = dict(cfg, l_cache=4)
+    with pytest.raises(qq_hip.QQError, match="l_cache"):
+        _model(tmp_path, 7, bad)
