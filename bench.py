@@ -15,7 +15,10 @@ Other workloads (--workload): decode_b64 (64-token decode batch), prefill_2048
 independently seeded layers, rmsnorm + MoE per layer, 1 token resp. a
 4096-token chunk per step), matvec (one Q8_0 matvec 1024 -> 3072, rotating
 over 80 weights), qwen3_decode_b1 / qwen3_prefill_2048 (one Qwen3-30B-A3B-shaped
-MoE layer, H=2048, F=768, E=128, K=8, softmax routing, no bias).
+MoE layer, H=2048, F=768, E=128, K=8, softmax routing, no bias), lfm2_decode
+(one token through a whole LFM2-8B-A1B-shaped model on the device -- 24
+blocks: 18 short-conv, 6 GQA attention, 2 dense FFN, 22 MoE; vocab 65536 --
+at positions 0, 1, 2, ... of one sequence; qq_lfm2_forward_dev).
 
 Inputs are generated on the device before the timed region.  Times come from
 HIP events on the stream the kernels run on.  `value` times the steps
@@ -40,6 +43,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(ROOT, "qwenqwen3.js_amd"))
 
 METRIC = "MoE-layer tokens/sec + HBM GB/s (% of peak), LFM2-8B-A1B-shape Q8_0"
+LFM2_METRIC = "whole-model decode tokens/sec, LFM2-8B-A1B-shape Q8_0"
 HBM_PEAK_GBPS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense fp16 MFMA
 H, F, E, K = 2048, 1792, 32, 4     # set per workload in main() from SHAPES
@@ -63,7 +67,10 @@ WORKLOADS = {
     "matvec": ("matvec", 1, None, "q8_0_matvec_1024x3072"),
     "qwen3_decode_b1": ("layer", 1, None, "qwen3moe_layer_decode_batch1", "qwen3"),
     "qwen3_prefill_2048": ("layer", 2048, None, "qwen3moe_layer_prefill_2048", "qwen3"),
+    "lfm2_decode": ("lfm2", 1, "uniform", "lfm2_8b_a1b_token_decode"),
 }
+LFM2_POS = 512        # positions cycle over 0 .. LFM2_POS - 1
+LFM2_BYTES = {}       # algorithmic bytes per launch of the lfm2 kernels (set by run_lfm2)
 MFMA_KERNELS = ("mfma_gateup", "mfma_down")
 
 
@@ -93,7 +100,7 @@ def kernel_bytes(name, T, n_experts):
         return 2 * T * H * 4
     if name == "q8_0_matvec":
         return MV_OUT * (MV_IN // 32) * QBLK + MV_IN * 4 + MV_OUT * 4
-    return None
+    return LFM2_BYTES.get(name)
 
 
 def kernel_flops(name, n_pairs):
@@ -181,6 +188,8 @@ def cpu_baseline(seconds, kind, shape="lfm2"):
                     "sample": "%d matmulQ80xF32 calls (1024 -> 3072 Q8_0) in %.1f s: the "
                               "reference's JS CPU path restated for Node %s, 1 thread of %d host "
                               "cores" % (r["matvecs"], r["seconds"], r["node"], ncores)}
+    if kind == "lfm2":
+        return lfm2_cpu_baseline(seconds)
     per = STACK_LAYERS if kind == "stack" else 1
     r = _node_bench("bench-qwen3" if shape == "qwen3" else "bench", seconds)
     if r:
@@ -210,6 +219,145 @@ def cpu_baseline(seconds, kind, shape="lfm2"):
     return {"value": round(n / el / per, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
             "sample": "%d single-token MoE-layer calls in %.1f s on the C oracle (node absent), "
                       "1 thread of %d host cores" % (n, el, ncores)}
+
+
+def lfm2_model_file(seed, cfg, tag):
+    """A synthetic LFM2-MoE GGUF file of shapes cfg (Q8_0 matrices sliced from
+    a seeded pool of random blocks) in the temp directory."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import synth
+    pool = synth.q8_0_pool(seed, 6 << 20)
+    d = tempfile.gettempdir()
+    if os.path.isdir("/dev/shm"):
+        st = os.statvfs("/dev/shm")
+        if st.f_bavail * st.f_frsize > (16 << 30):
+            d = "/dev/shm"      # memory-backed: the 8.9 GB file is written and mapped quickly
+    path = os.path.join(d, "qq_%s_%d.gguf" % (tag, os.getpid()))
+    _, offs, tensors = synth.lfm2_gguf(seed, cfg, path=path, pool=pool)
+    return path, offs, tensors
+
+
+def lfm2_cpu_baseline(seconds):
+    """oracle/lfm2_ref.js (the reference's Lfm2Engine.forward restated for Node)
+    timed on a 3-block model of the full widths -- one short-conv + dense
+    block, one attention + MoE block, one short-conv + MoE block, and the
+    65536-word head -- and scaled to the 24 blocks of LFM2-8B-A1B (2 / 6 / 16
+    of each kind).  The 24-block file (8.9 GB) does not fit Node 12's buffers."""
+    import shutil
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import synth
+    import _lfm2
+    node = shutil.which("node")
+    if not node:
+        return None
+    cfg = dict(synth.LFM2_8B_A1B, n_layers=3, attn_layers=(1,), n_dense=1)
+    path, offs, tensors = lfm2_model_file(11, cfg, "lfm2cpu")
+    try:
+        job = {"gguf": path, "kv": _lfm2.kv_dict(cfg), "tokens": [0], "start": 0,
+               "tensors": {n: {"offset": offs[n], "shape": sh, "type": t} for n, sh, t, _ in tensors}}
+        jp = path + ".json"
+        with open(jp, "w") as f:
+            json.dump(job, f)
+        p = subprocess.run([node, os.path.join(ROOT, "oracle", "lfm2_ref.js"), "bench", jp, str(seconds)],
+                           capture_output=True, text=True, timeout=seconds * 4 + 300, check=True)
+        r = json.loads(p.stdout.strip().splitlines()[-1])
+    finally:
+        for f in (path, path + ".json"):
+            if os.path.exists(f):
+                os.remove(f)
+    per = {b["kind"]: b["ms"] for b in r["blocks"]}
+    full = synth.LFM2_8B_A1B
+    n_attn = len(full["attn_layers"])
+    n_conv_dense = full["n_dense"]
+    ms = (n_conv_dense * per["conv+dense"] + n_attn * per["attn+moe"] +
+          (full["n_layers"] - n_attn - n_conv_dense) * per["conv+moe"] + r["head_ms"])
+    ncores = os.cpu_count() or 0
+    return {"value": round(1000.0 / ms, 4), "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": "%d tokens in %.1f s through a 3-block full-width LFM2 model (block ms: "
+                      "conv+dense %.0f, attn+moe %.0f, conv+moe %.0f; head %.0f) with "
+                      "oracle/lfm2_ref.js (the reference's Lfm2Engine.forward restated for Node %s), "
+                      "scaled to 2 + 6 + 16 blocks + head = %.0f ms per token; 1 thread of %d host "
+                      "cores" % (r["tokens"], r["seconds"], per["conv+dense"], per["attn+moe"],
+                                 per["conv+moe"], r["head_ms"], r["node"], ms, ncores)}
+
+
+def run_lfm2(args, torch, ctx, stream):
+    """The whole-model decode workload.  Returns (ms_per_step, kernels,
+    roofline, config, extra)."""
+    import qq_hip
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import synth
+    cfg = synth.LFM2_8B_A1B
+    t0 = time.time()
+    path, offs, tensors = lfm2_model_file(1, cfg, "lfm2gpu")
+    try:
+        g = qq_hip.Gguf(path)
+        try:
+            model = qq_hip.Lfm2Model(ctx, g)
+        finally:
+            g.close()
+    finally:
+        os.remove(path)
+    setup_s = time.time() - t0
+    info = model.info
+    V = info["n_vocab"]
+    logits = torch.empty(V, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        model.forward_dev((i * 7919) % V, i % LFM2_POS, logits.data_ptr())
+
+    total_ms = _time_steps(torch, ctx, stream, step, args.steps, args.warmup)
+    ms_per_step = total_ms / args.steps
+    # one pass with per-launch events over the first positions of a fresh sequence
+    n_prof = min(args.steps, 64)
+    model.reset()
+    ctx.profile_enable(n_prof * 160)
+    for i in range(n_prof):
+        step(i)
+    prof = ctx.profile_read()
+    ctx.profile_enable(0)
+    ctx.synchronize()
+
+    # algorithmic bytes per token (Q8_0: 34 bytes per 32 weights)
+    Hh, V, nq = info["n_embd"], info["n_vocab"], info["n_heads"] * info["head_dim"]
+    nkv = info["n_head_kv"] * info["head_dim"]
+    n_attn, nl, ndense = info["n_attn_layers"], info["n_layers"], info["n_dense_lead"]
+    n_conv = nl - n_attn
+    q8 = QBLK / 32.0
+    w_conv = (3 * Hh * Hh + Hh * Hh) * q8
+    w_attn = (2 * Hh * nq + 2 * Hh * nkv) * q8
+    w_dense = 3 * Hh * info["n_ff"] * q8
+    w_head = Hh * V * q8
+    mv_bytes = n_conv * w_conv + n_attn * w_attn + ndense * w_dense + w_head
+    mv_launches = 2 * n_conv + 2 * n_attn + 2 * ndense + 1
+    LFM2_BYTES["lfm2_matvec"] = mv_bytes / mv_launches
+    avg_n_prof = (n_prof + 1) / 2.0
+    LFM2_BYTES["lfm2_attention"] = info["n_head_kv"] * avg_n_prof * 64 * 4 * 2
+    LFM2_BYTES["lfm2_embed"] = Hh * q8 + Hh * 4
+    n_moe = nl - ndense
+    moe_bytes = n_moe * kernel_bytes("decode_experts", 1, K)
+    avg_n = (min(args.steps, LFM2_POS) + 1) / 2.0
+    kv_bytes = n_attn * info["n_head_kv"] * avg_n * 64 * 4 * 2
+    tok_bytes = mv_bytes + moe_bytes + kv_bytes
+    kernels = kernel_table(prof, 1, K, K)
+    dom, roofline = roofline_of(prof, kernels, args.workload)
+    config = {"workload": "lfm2_8b_a1b_token_decode", "blocks": nl, "attention_blocks": n_attn,
+              "dense_ffn_blocks": ndense, "moe_blocks": n_moe, "H": Hh, "heads": info["n_heads"],
+              "kv_heads": info["n_head_kv"], "head_dim": info["head_dim"], "n_ff": info["n_ff"],
+              "F": F, "E": E, "K": K, "vocab": V, "weights": "Q8_0", "activations": "f32",
+              "positions": "0..%d (step i at position i %% %d, one sequence)" % (LFM2_POS - 1, LFM2_POS),
+              "timed_positions": "0..%d" % (min(args.steps, LFM2_POS) - 1)}
+    extra = {"us_per_token": round(ms_per_step * 1000.0, 2),
+             "hbm_bytes_per_token": int(tok_bytes),
+             "hbm_gbps_token": round(tok_bytes / (ms_per_step * 1e6), 1),
+             "hbm_frac_token": round(tok_bytes / (ms_per_step * 1e6) / HBM_PEAK_GBPS, 4),
+             "launches_per_token": int(round(sum(c for _, c in prof.values()) / n_prof)),
+             "setup_s": round(setup_s, 1)}
+    model.release()
+    return ms_per_step, kernels, roofline, config, extra
 
 
 def copy_calibration(steps):
@@ -343,7 +491,11 @@ def main():
     gx.manual_seed(99)
     extra = {}
 
-    if kind == "matvec":
+    if kind == "lfm2":
+        keep = []
+        ms_per_step, kernels, roofline, config, extra = run_lfm2(args, torch, ctx, stream)
+        value, unit, dtype, graph_ms = 1000.0 / ms_per_step, "tokens/s", "f32", None
+    elif kind == "matvec":
         n_w = 80                      # 80 x 3.36 MB > the 256 MB Infinity Cache
         keep = [make_matvec_weight(torch, ctx, 500 + i) for i in range(n_w)]
         X = torch.randn((16, MV_IN), generator=gx, device="cuda", dtype=torch.float32)
@@ -416,7 +568,7 @@ def main():
             extra["us_per_token"] = round(ms_per_step * 1000.0, 2)
 
     result = {
-        "metric": METRIC,
+        "metric": LFM2_METRIC if kind == "lfm2" else METRIC,
         "value": round(value, 1),
         "unit": unit,
         "n_gpus": 1,
@@ -432,7 +584,7 @@ def main():
     }
     result.update(extra)
     # the same steps replayed from HIP graphs
-    result["graph_ms_per_step"] = round(graph_ms / args.steps, 5)
+    result["graph_ms_per_step"] = None if graph_ms is None else round(graph_ms / args.steps, 5)
     result["roofline"] = roofline
     result["kernels"] = kernels
     for obj in keep:

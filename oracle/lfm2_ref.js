@@ -235,9 +235,13 @@ function denseFfn(m, L) {
     M.addVec(m.hidden, M.matmulGeneric(L.down, g));
 }
 
-function forward(m, token, pos, skipLogits) {
+// tm (optional): { block(li, ms), head(ms) } receives the time of every block
+// and of the output head.
+function forward(m, token, pos, skipLogits, tm) {
+    const now = function () { return Number(process.hrtime.bigint()) / 1e6; };
     m.hidden.set(embedRow(m.tokEmbd, token));
     for (let li = 0; li < m.nLayers; li++) {
+        const ta = tm ? now() : 0;
         const L = m.layers[li];
         m.normed.set(m.hidden);
         rmsnormInPlace(m.normed, L.attnNorm, m.eps);
@@ -252,10 +256,14 @@ function forward(m, token, pos, skipLogits) {
                           onRouterUpdate: m.routes ? function (r) { m.routes.push(r.selected); } : null };
             M.moEFFN(eng, li, L);
         }
+        if (tm) tm.block(li, now() - ta);
     }
     if (skipLogits) return null;
+    const th = tm ? now() : 0;
     rmsnormInPlace(m.hidden, m.outputNorm, m.eps);
-    return M.matmulGeneric(m.output, m.hidden);
+    const out = M.matmulGeneric(m.output, m.hidden);
+    if (tm) tm.head(now() - th);
+    return out;
 }
 
 function loadJob(path) {
@@ -280,18 +288,26 @@ function run(path) {
     fs.writeFileSync(job.out_routes, JSON.stringify(m.routes));
 }
 
+// Times tokens through the model, per block and for the output head, so a
+// model of a few full-width blocks can stand for a deeper one.
 function bench(path, seconds) {
     const m = loadJob(path).model;
-    let n = 0;
+    const blockMs = new Array(m.nLayers).fill(0);
+    let headMs = 0, n = 0;
+    const tm = { block: function (li, ms) { blockMs[li] += ms; }, head: function (ms) { headMs += ms; } };
     const t0 = process.hrtime.bigint();
     let el = 0;
     while (el < seconds || n < 1) {
-        forward(m, (n * 7919) % m.nVocab, n % m.maxCtx, false);
+        forward(m, (n * 7919) % m.nVocab, n % m.maxCtx, false, tm);
         n++;
         el = Number(process.hrtime.bigint() - t0) / 1e9;
     }
-    process.stdout.write(JSON.stringify({ tokens: n, seconds: el, tokens_per_s: n / el, threads: 1,
-                                          node: process.version }) + '\n');
+    process.stdout.write(JSON.stringify({
+        tokens: n, seconds: el, tokens_per_s: n / el, threads: 1, node: process.version,
+        blocks: m.layers.map(function (L, i) {
+            return { kind: (L.rec ? 'conv' : 'attn') + '+' + (L.moe ? 'moe' : 'dense'), ms: blockMs[i] / n };
+        }),
+        head_ms: headMs / n }) + '\n');
 }
 
 module.exports = { buildModel, forward, embedRow, rmsnormInPlace, headNormInPlace, ropeInPlace,

@@ -173,6 +173,34 @@ def gguf_file(kvs, tensors, version=3, alignment=None):
     return bytes(out), {t[0]: start + r for t, r in zip(tensors, rel)}
 
 
+def gguf_write(path, kvs, tensors, version=3):
+    """gguf_file's layout (default alignment) written to `path` tensor by
+    tensor, without building the whole file in memory.  Returns {name: offset}."""
+    import struct
+    al = 32
+    head = b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(kvs))
+    head += b"".join(_gguf_str(k) + struct.pack("<I", t) + _gguf_value(t, v) for k, t, v in kvs)
+    sizes = [np.asarray(t[3]).nbytes for t in tensors]
+    rel, pos = [], 0
+    for n in sizes:
+        pos = -(-pos // al) * al
+        rel.append(pos)
+        pos += n
+    for (name, shape, typ, _), r in zip(tensors, rel):
+        head += _gguf_str(name) + struct.pack("<I", len(shape))
+        head += b"".join(struct.pack("<Q", d) for d in shape) + struct.pack("<IQ", typ, r)
+    start = -(-len(head) // al) * al
+    with open(path, "wb") as f:
+        f.write(head + bytes(start - len(head)))
+        at = 0
+        for t, r in zip(tensors, rel):
+            f.write(bytes(r - at))
+            data = np.ascontiguousarray(t[3])
+            f.write(memoryview(data.view(np.uint8).reshape(-1)))
+            at = r + data.nbytes
+    return {t[0]: start + r for t, r in zip(tensors, rel)}
+
+
 def moe_gguf(layers, arch="lfm2moe", K=None, alignment=None, extra_kvs=()):
     """A GGUF file holding MoE blocks 0..n-1 built from oracle-format layer
     dicts (moe_layer), with the tensor names the engines bind
@@ -217,18 +245,37 @@ LFM2_8B_A1B = dict(H=2048, n_layers=24, attn_layers=(2, 6, 10, 14, 18, 21), n_de
 22 MoE with 32 experts, top-4), H 2048, 32 query / 8 KV heads of 64, vocab 65536."""
 
 
-def lfm2_tensors(seed, cfg, conv_type=TYPE_F32, tied=True, bias="uniform"):
+def q8_0_pool(seed, n_blocks, scale=0.005):
+    """A pool of random Q8_0 blocks that lfm2_tensors(pool=...) slices its
+    matrices from (a fast way to fill a multi-GB model whose values only need
+    to be plausible, as for timing)."""
+    rng = np.random.default_rng(seed)
+    blocks = np.empty(n_blocks, Q8_DTYPE)
+    blocks["qs"] = rng.integers(-127, 128, size=(n_blocks, QK), dtype=np.int8)
+    blocks["d"] = (np.abs(rng.standard_normal(n_blocks)) * scale).astype(np.float16)
+    return blocks
+
+
+def lfm2_tensors(seed, cfg, conv_type=TYPE_F32, tied=True, bias="uniform", pool=None):
     """Seeded tensors of an LFM2-MoE model, named as Lfm2Engine binds them
     (src/lfm2-engine.js:78-144): [(name, shape, type, bytes)].  Dense and
     attention matrices are Q8_0; norms, router and expert bias F32; the conv
-    kernel [l_cache, H] F32, F16 or Q8_0 (one block per column)."""
+    kernel [l_cache, H] F32, F16 or Q8_0 (one block per column).  With a
+    q8_0_pool, every Q8_0 matrix is a seeded slice of the pool."""
     rng = np.random.default_rng(seed)
     H, L, hd = cfg["H"], cfg["l_cache"], cfg["head_dim"]
     nq, nkv = cfg["n_heads"] * hd, cfg["n_head_kv"] * hd
     t = []
 
     def q8(name, i, o, n=1, scale=0.005):
-        t.append((name, [i, o] + ([n] if n > 1 else []), TYPE_Q8_0, q8_0_tensor(rng, i, o, n, scale)))
+        shape = [i, o] + ([n] if n > 1 else [])
+        if pool is not None:
+            nblk = n * o * ((i + QK - 1) // QK)
+            assert i % QK == 0 and nblk <= len(pool)
+            off = int(rng.integers(0, len(pool) - nblk + 1))
+            t.append((name, shape, TYPE_Q8_0, pool[off:off + nblk].view(np.uint8)))
+            return
+        t.append((name, shape, TYPE_Q8_0, q8_0_tensor(rng, i, o, n, scale)))
 
     def f32(name, shape, v):
         t.append((name, list(shape), TYPE_F32, np.asarray(v, np.float32)))
@@ -273,10 +320,11 @@ def lfm2_tensors(seed, cfg, conv_type=TYPE_F32, tied=True, bias="uniform"):
     return t
 
 
-def lfm2_gguf(seed, cfg, arch="lfm2moe", **kw):
+def lfm2_gguf(seed, cfg, arch="lfm2moe", path=None, **kw):
     """GGUF bytes of lfm2_tensors(seed, cfg) with the keys Lfm2Engine reads
     (src/lfm2-engine.js:15-47; per-layer head_count_kv, 0 for short-conv
-    blocks).  Returns (bytes, {name: offset}, [(name, shape, type, bytes)])."""
+    blocks).  Returns (bytes, {name: offset}, [(name, shape, type, bytes)]);
+    with `path`, the file is written there and bytes is None."""
     p = arch + "."
     kvs = [("general.architecture", GGUF_STRING, arch),
            (p + "block_count", 4, cfg["n_layers"]),
@@ -293,5 +341,7 @@ def lfm2_gguf(seed, cfg, arch="lfm2moe", **kw):
            (p + "context_length", 4, cfg["ctx"]),
            (p + "rope.freq_base", 6, cfg["rope_base"])]
     tensors = lfm2_tensors(seed, cfg, **kw)
+    if path is not None:
+        return None, gguf_write(path, kvs, tensors), tensors
     data, offs = gguf_file(kvs, tensors)
     return data, offs, tensors

@@ -29,7 +29,6 @@
 
 namespace qq {
 
-constexpr int LM_WPG = 4;        // waves per 32-row group, splitting the blocks of a row
 constexpr int LM_MAX_IN = 8192;  // longest input row staged in LDS
 constexpr int LM_MAX_L = 4;      // short-conv kernel length (l_cache) supported
 constexpr int LM_HEAD = 64;      // head_dim supported by the QKV epilogue and attention
@@ -83,41 +82,75 @@ __device__ __forceinline__ float lm_block_max(float v, float *red)
     return m;
 }
 
-// Row of matrix `mat` owned by 32-row group g of this workgroup, or -1.
-template <int MODE>
+// First row of matrix `mat` owned by row group g (RPW rows) of this workgroup.
+template <int MODE, int G, int RPW>
 __device__ __forceinline__ int lm_row(const LmArgs &a, int g, int &mat)
 {
     const int j = blockIdx.x;
     if (MODE == LM_PLAIN || MODE == LM_RESID) {
         mat = 0;
-        return 64 * j + 32 * g;
+        return G * RPW * j + RPW * g;
     }
-    if (MODE == LM_SWIGLU) {
+    if (MODE == LM_SWIGLU) {   // group 0: gate rows, group 1: the same up rows
         mat = g;
-        return 32 * j;
+        return RPW * j;
     }
-    if (MODE == LM_CONV) {
+    if (MODE == LM_CONV) {     // group g: rows g*H + channels of the workgroup
         mat = 0;
-        return g * a.H + 32 * j;
+        return g * a.H + RPW * j;
     }
-    // QKV: one head per workgroup, q heads first, then k, then v
+    // QKV: one head (G * RPW = 64 rows) per workgroup, q heads, then k, then v
     if (j < a.n_heads) {
         mat = 0;
-        return LM_HEAD * j + 32 * g;
+        return LM_HEAD * j + RPW * g;
     }
     mat = j < a.n_heads + a.n_kv_heads ? 1 : 2;
-    return LM_HEAD * (j - a.n_heads - (mat == 2 ? a.n_kv_heads : 0)) + 32 * g;
+    return LM_HEAD * (j - a.n_heads - (mat == 2 ? a.n_kv_heads : 0)) + RPW * g;
 }
 
-template <int MODE, int G>
-__global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
+// BPL int8 weights (offset binary after the XOR) against BPL activations:
+// sum q_i x_i = sum (q_i + 128) x_i - 128 sum x_i, each byte converted by one
+// v_cvt_f32_ubyte.
+template <int BPL>
+__device__ __forceinline__ float lm_dot(const uint32_t (&w)[BPL / 4], const float *x, float xsum)
 {
-    constexpr int NT = G * LM_WPG * WAVE;
-    constexpr int NW = G * LM_WPG;
+    float xr[BPL];
+#pragma unroll
+    for (int i = 0; i < BPL / 4; i++) {
+        const float4 v = reinterpret_cast<const float4 *>(x)[i];
+        xr[4 * i] = v.x;
+        xr[4 * i + 1] = v.y;
+        xr[4 * i + 2] = v.z;
+        xr[4 * i + 3] = v.w;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < BPL / 4; i++) {
+        const uint32_t u = w[i] ^ 0x80808080u;
+#pragma unroll
+        for (int b = 0; b < 4; b++) acc = fmaf((float)((u >> (8 * b)) & 0xffu), xr[4 * i + b], acc);
+    }
+    return fmaf(-128.0f, xsum, acc);
+}
+
+// G row groups of RPW rows, WPG waves each.  In a wave, 64 / RPW lanes share
+// a row and each takes BPL = 32 * RPW / 64 bytes of a block; a wave keeps up to
+// NBW blocks of its rows in flight (blocks wg, wg + WPG, ... of a chunk of
+// WPG * NBW).  Fewer rows per wave spread a matrix over more workgroups
+// (CUs): one CU pulls only a few tens of GB/s.
+template <int MODE, int G, int WPG, int NBW, int RPW>
+__global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
+{
+    constexpr int NT = G * WPG * WAVE;
+    constexpr int NW = G * WPG;
+    constexpr int LPR = WAVE / RPW;       // lanes per row
+    constexpr int BPL = QK / LPR;         // bytes (weights) per lane per block
+    static_assert(LPR * BPL == QK && BPL % 4 == 0, "lane layout");
+    static_assert(MODE != LM_QKV || G * RPW == LM_HEAD, "one head per workgroup");
     extern __shared__ __align__(16) float lm_lds[];
     float *xl = lm_lds;                  // nb * 32 activations (zero padded)
-    float *xs = lm_lds + a.nb * QK;      // 2 * nb half-block sums
-    __shared__ float red[G][LM_WPG][32];
+    float *xs = lm_lds + a.nb * QK;      // sums of every BPL-value chunk
+    __shared__ float red[G][WPG][RPW];
     __shared__ double redd[NW];
     __shared__ float hv[LM_HEAD];
     __shared__ double hinv;
@@ -127,6 +160,42 @@ __global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     const int wave = tid / WAVE;
     const int kp = a.nb * QK;
 
+    // ---- row groups: lane l takes row l / LPR, bytes BPL * (l % LPR) of a block ----
+    const int g = wave / WPG, wg = wave % WPG;
+    int mat;
+    const int row0 = lm_row<MODE, G, RPW>(a, g, mat);
+    const LmMat M = a.m[mat];
+    const int row = row0 + lane / LPR, part = lane % LPR;
+    const bool row_ok = row < M.rows;
+    const int rc = min(row, M.rows - 1);
+    uint32_t q[NBW][BPL / 4];
+    float dd[NBW];
+    // NBW blocks from block bb on (stride WPG); clamped addresses, zero scale
+    // out of range
+    auto load = [&](int bb) {
+#pragma unroll
+        for (int u = 0; u < NBW; u++) {
+            const int b = min(bb + WPG * u, a.nb - 1);
+            const size_t o = bm_index(0, a.nb, b, M.rows, rc);
+            const int8_t *src = M.qs + o * QK + BPL * part;
+            if (BPL == 16) {
+                const int4 v = *reinterpret_cast<const int4 *>(src);
+                q[u][0] = v.x;
+                q[u][BPL / 4 > 1 ? 1 : 0] = v.y;
+                q[u][BPL / 4 > 2 ? 2 : 0] = v.z;
+                q[u][BPL / 4 > 3 ? 3 : 0] = v.w;
+            } else if (BPL == 8) {
+                const int2 v = *reinterpret_cast<const int2 *>(src);
+                q[u][0] = v.x;
+                q[u][BPL / 4 > 1 ? 1 : 0] = v.y;
+            } else {
+                q[u][0] = *reinterpret_cast<const uint32_t *>(src);
+            }
+            dd[u] = __half2float(M.d[o]);
+        }
+#pragma unroll
+        for (int u = 0; u < NBW; u++) dd[u] = (row_ok && bb + WPG * u < a.nb) ? dd[u] : 0.0f;
+    };
     // ---- input row -> LDS, normalised when asked (src/tensor.js:103-114) ----
     double inv = 1.0;
     if (a.norm) {
@@ -144,57 +213,43 @@ __global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         xl[k] = v;
     }
     __syncthreads();
-    for (int i = tid; i < 2 * a.nb; i += NT) {
+    for (int i = tid; i < kp / BPL; i += NT) {
         float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 16; j++) s += xl[16 * i + j];
+        for (int j = 0; j < BPL; j++) s += xl[BPL * i + j];
         xs[i] = s;
     }
     __syncthreads();
 
-    // ---- 32-row groups: lane l takes row l/2, half l%2 of each block ----
-    const int g = wave / LM_WPG, wg = wave % LM_WPG;
-    int mat;
-    const int row0 = lm_row<MODE>(a, g, mat);
-    const LmMat M = a.m[mat];
-    const int row = row0 + lane / 2, h = lane & 1;
-    const bool row_ok = row < M.rows;
-    const int rc = min(row, M.rows - 1);
     float acc = 0.0f;
-    for (int bb = wg; bb < a.nb; bb += 4 * LM_WPG) {
-        int4 q[4];
-        float dd[4];
+    for (int bb = wg; bb < a.nb; bb += NBW * WPG) {
+        load(bb);
+        __builtin_amdgcn_sched_barrier(0);   // every load of the chunk before its arithmetic
 #pragma unroll
-        for (int u = 0; u < 4; u++) {   // clamped addresses, zero scale out of range
-            const int b = min(bb + LM_WPG * u, a.nb - 1);
-            const size_t o = bm_index(0, a.nb, b, M.rows, rc);
-            q[u] = *reinterpret_cast<const int4 *>(M.qs + o * QK + 16 * h);
-            dd[u] = __half2float(M.d[o]);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; u++) dd[u] = (row_ok && bb + LM_WPG * u < a.nb) ? dd[u] : 0.0f;
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            const int b = bb + LM_WPG * u;
-            if (b < a.nb) acc = fmaf(dot16_q8_lds(q[u], &xl[b * QK + 16 * h], xs[2 * b + h]), dd[u], acc);
+        for (int u = 0; u < NBW; u++) {
+            const int b = bb + WPG * u;
+            if (b < a.nb) {
+                const int c = (b * QK + BPL * part) / BPL;
+                acc = fmaf(lm_dot<BPL>(q[u], &xl[b * QK + BPL * part], xs[c]), dd[u], acc);
+            }
         }
     }
-    acc += __shfl_xor(acc, 1, WAVE);
-    if (h == 0) red[g][wg][lane / 2] = acc;
+#pragma unroll
+    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (part == 0) red[g][wg][lane / LPR] = acc;
     __syncthreads();
 
     // ---- epilogues ----
     auto rowsum = [&](int gg, int r) {
         float v = red[gg][0][r];
 #pragma unroll
-        for (int w = 1; w < LM_WPG; w++) v += red[gg][w][r];
+        for (int w = 1; w < WPG; w++) v += red[gg][w][r];
         return v;
     };
     if (MODE == LM_PLAIN || MODE == LM_RESID) {
-        if (tid < G * 32) {
-            const int gg = tid / 32, r = tid % 32;
-            const int orow = 64 * blockIdx.x + 32 * gg + r;
+        if (tid < G * RPW) {
+            const int gg = tid / RPW, r = tid % RPW;
+            const int orow = G * RPW * blockIdx.x + RPW * gg + r;
             if (orow < a.m[0].rows) {
                 const float v = rowsum(gg, r);
                 a.y[orow] = MODE == LM_RESID ? a.y[orow] + v : v;
@@ -202,8 +257,8 @@ __global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         }
     } else if (MODE == LM_SWIGLU) {
         // siluInPlace, mulInPlace (src/tensor.js:167-179)
-        const int f = 32 * blockIdx.x + tid;
-        if (tid < 32 && f < a.m[0].rows) {
+        const int f = RPW * blockIdx.x + tid;
+        if (tid < RPW && f < a.m[0].rows) {
             const float gv = rowsum(0, tid), uv = rowsum(1, tid);
             const double g64 = (double)gv;
             const float s = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
@@ -211,8 +266,8 @@ __global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         }
     } else if (MODE == LM_CONV) {
         // _shortConv steps 3-6 (src/lfm2-engine.js:297-322) for channel d
-        const int d = 32 * blockIdx.x + tid;
-        if (tid < 32 && d < a.H) {
+        const int d = RPW * blockIdx.x + tid;
+        if (tid < RPW && d < a.H) {
             const float B = rowsum(0, tid), C = rowsum(1, tid), X = rowsum(2, tid);
             const float bx = B * X;
             double s = 0.0;
@@ -237,7 +292,7 @@ __global__ __launch_bounds__(G * LM_WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     } else {
         // QKV: perHeadRMSNorm (src/tensor.js:117-129), applyRoPE (:132-147),
         // KVCache.store (src/kv-cache.js:16-32)
-        if (tid < LM_HEAD) hv[tid] = rowsum(tid / 32, tid % 32);
+        if (tid < LM_HEAD) hv[tid] = rowsum(tid / RPW, tid % RPW);
         __syncthreads();
         const int j = blockIdx.x;
         const int kind = j < a.n_heads ? 0 : (j < a.n_heads + a.n_kv_heads ? 1 : 2);
@@ -301,13 +356,26 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
     const int tid = threadIdx.x;
     const int hq = blockIdx.x;
     const int g = (int)(((long long)hq * n_kv_heads) / n_heads);
-    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
-    __syncthreads();
     const float *K = kc + (size_t)g * max_ctx * LM_HEAD;
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
+    const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
+    // loads that depend on nothing are issued first: this thread's first K
+    // row, the first LM_VPRE values of its V column, the query
+    constexpr int LM_VPRE = 8;
+    float4 kr[LM_HEAD / 4];
+    auto load_k = [&](int p) {
+        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)min(p, n - 1) * LM_HEAD);
+#pragma unroll
+        for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = src[i];
+    };
+    load_k(tid);
+    float vpre[LM_VPRE];
+#pragma unroll
+    for (int u = 0; u < LM_VPRE; u++) vpre[u] = V[(size_t)min(cls + NW * u, n - 1) * LM_HEAD + d];
+    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
+    __syncthreads();
     float mx = -INFINITY;
     for (int p = tid; p < n; p += LM_ATTN_THREADS) {
-        const float4 *kr = reinterpret_cast<const float4 *>(K + (size_t)p * LM_HEAD);
         double dot = 0.0;
 #pragma unroll
         for (int i = 0; i < LM_HEAD / 4; i++) {
@@ -320,6 +388,7 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
         const float s = (float)(dot * scale);
         sc[p] = s;
         mx = fmaxf(mx, s);
+        if (p + LM_ATTN_THREADS < n) load_k(p + LM_ATTN_THREADS);
     }
     const float M = lm_block_max<NW>(mx, redf);
     double ls = 0.0;
@@ -331,11 +400,19 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
     const double inv = 1.0 / block_sum_f64<NW>(ls, redd);
     for (int p = tid; p < n; p += LM_ATTN_THREADS) sc[p] = (float)((double)sc[p] * inv);
     __syncthreads();
-    const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
     float acc = 0.0f;
-    for (int p = cls; p < n; p += NW) {
+    int u = 0;
+    for (int p = cls; p < n; p += NW, u++) {
         const float w = sc[p];
-        if (w != 0.0f) acc = (float)fma((double)V[(size_t)p * LM_HEAD + d], (double)w, (double)acc);
+        float v;
+        if (u < LM_VPRE) {
+            v = vpre[0];
+#pragma unroll
+            for (int k = 1; k < LM_VPRE; k++) v = u == k ? vpre[k] : v;
+        } else {
+            v = V[(size_t)p * LM_HEAD + d];
+        }
+        if (w != 0.0f) acc = (float)fma((double)v, (double)w, (double)acc);
     }
     part[cls][d] = acc;
     __syncthreads();
@@ -396,23 +473,26 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     a.max_ctx = l.max_ctx;
     a.freq = l.freq;
     if (a.in_dim > LM_MAX_IN) return set_error(ctx, "lfm2: input row of %d > %d", a.in_dim, LM_MAX_IN);
-    const size_t shm = (size_t)a.nb * QK * 4 + (size_t)2 * a.nb * 4;
+    // LDS: the activations and the chunk sums (BPL >= 4: at most nb * 8 of them)
+    const size_t shm = (size_t)a.nb * QK * 4 + (size_t)a.nb * 8 * 4;
     prof_begin(ctx, K_LFM2_MV);
+    // rows per wave and waves per row panel chosen so that a 2048-row matrix
+    // spreads over 256 workgroups with every block of a row in flight
     switch (mode) {
-    case LM_PLAIN:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_PLAIN, 2>), dim3((a.m[0].rows + 63) / 64), dim3(2 * LM_WPG * WAVE), shm, a);
+    case LM_PLAIN:   // the output head: 65536 rows
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_PLAIN, 1, 16, 4, 32>), dim3((a.m[0].rows + 31) / 32), dim3(16 * WAVE), shm, a);
         break;
     case LM_RESID:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 2>), dim3((a.m[0].rows + 63) / 64), dim3(2 * LM_WPG * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 4, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
         break;
     case LM_SWIGLU:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2>), dim3((a.m[0].rows + 31) / 32), dim3(2 * LM_WPG * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2, 8, 8, 16>), dim3((a.m[0].rows + 15) / 16), dim3(16 * WAVE), shm, a);
         break;
     case LM_CONV:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3>), dim3((a.H + 31) / 32), dim3(3 * LM_WPG * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3, 5, 13, 8>), dim3((a.H + 7) / 8), dim3(15 * WAVE), shm, a);
         break;
     default:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 2>), dim3(a.n_heads + 2 * a.n_kv_heads), dim3(2 * LM_WPG * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 2, 8, 8, 32>), dim3(a.n_heads + 2 * a.n_kv_heads), dim3(16 * WAVE), shm, a);
         break;
     }
     prof_end(ctx);
