@@ -13,6 +13,9 @@
 //   device.attachGGUF(path)   MoE blocks come from the file (memory-mapped,
 //                             repacked straight to the device) instead of from
 //                             the engine's ArrayBuffers
+//   device.attachLfm2Forward(engine)   Lfm2Engine.forward / resetState
+//                             (src/lfm2-engine.js:216-280) of one engine run the
+//                             whole token on the device from the attached file
 //
 // There is no CPU fallback: when the addon or the device is missing, the
 // constructor and install() throw.  Written for Node 12 (no `?.`, no `??`).
@@ -66,6 +69,7 @@ class MoEDevice {
         this._tensors = new WeakMap();   // ArrayBuffer -> Map(key -> device tensor)
         this.fallbackMatmul = null;
         this._gguf = null;
+        this._lfm2 = null;
     }
 
     // Bind MoE blocks from a GGUF file: the layer of block l is read from the
@@ -78,6 +82,30 @@ class MoEDevice {
         if (this._gguf) this.native.release(this._gguf);
         this._gguf = g;
         return this.native.ggufTensors(g);
+    }
+
+    // Whole-token forward on the device (include/qq_lfm2.h) for an engine
+    // whose model is the attached GGUF file: forward(tokenId, position,
+    // skipLogits), resetState and resetKVCache (src/lfm2-engine.js:216-280)
+    // are rebound on that engine object.  The logits land in
+    // engine.bufLogits and forward returns it, or null for skipLogits, as the
+    // reference does.  Returns the model's configuration (lfm2Info).
+    attachLfm2Forward(engine) {
+        if (!this._gguf) throw new Error('attachLfm2Forward: attachGGUF(path) first');
+        const model = this.native.lfm2Create(this.ctx, this._gguf);
+        if (this._lfm2) this.native.release(this._lfm2);
+        this._lfm2 = model;
+        const info = this.native.lfm2Info(model);
+        const dev = this;
+        if (!(engine.bufLogits instanceof Float32Array) || engine.bufLogits.length !== info.nVocab)
+            engine.bufLogits = new Float32Array(info.nVocab);
+        engine.forward = function (tokenId, position, skipLogits) {
+            dev.native.lfm2Forward(dev.ctx, model, tokenId | 0, position | 0, skipLogits ? null : this.bufLogits);
+            return skipLogits ? null : this.bufLogits;
+        };
+        engine.resetState = function () { dev.native.lfm2Reset(dev.ctx, model); };
+        engine.resetKVCache = function () { this.resetState(); };
+        return info;
     }
 
     // Device copy of a GGUF Q8_0 tensor, uploaded (and repacked) once per
@@ -196,6 +224,10 @@ class MoEDevice {
     }
 
     release() {
+        if (this._lfm2) {
+            this.native.release(this._lfm2);
+            this._lfm2 = null;
+        }
         if (this._gguf) {
             this.native.release(this._gguf);
             this._gguf = null;

@@ -24,6 +24,12 @@
  *   ggufTensors(gguf) -> [{name, shape, type, offset, nbytes}]
  *   ggufMoeParams(gguf, block, K, gating) -> {H, F, E, K, gating, routerType, hasBias}
  *   ggufMoeLayer(ctx, gguf, block, K, gating) -> moe (owns its expert tensors)
+ *   lfm2Create(ctx, gguf) -> lfm2      whole LFM2 model on the device (include/qq_lfm2.h)
+ *   lfm2Info(lfm2) -> {nLayers, nEmbd, nHeads, nHeadKV, headDim, nVocab, nFF, nExperts,
+ *                      nExpertsUsed, nDenseLead, lCache, maxCtx, nAttnLayers, eps, ropeFreqBase}
+ *   lfm2Forward(ctx, lfm2, token, position, logits: Float32Array|null)
+ *       one token through the model; logits (nVocab floats) or null (skipLogits)
+ *   lfm2Reset(ctx, lfm2)               zero the KV cache and conv states
  *   release(handle)    frees a tensor / moe / ctx / gguf now instead of at GC
  */
 #include <node_api.h>
@@ -33,18 +39,20 @@
 #include <string.h>
 
 #include "../../include/qq_gguf.h"
+#include "../../include/qq_lfm2.h"
 #include "../../include/qq_moe.h"
 
-enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3, H_GGUF = 4 };
+enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3, H_GGUF = 4, H_LFM2 = 5 };
 
 typedef struct handle {
     int kind;
-    void *ptr;           /* qq_ctx*, qq_tensor*, qq_moe* or qq_gguf* (NULL once released) */
+    void *ptr;           /* qq_ctx*, qq_tensor*, qq_moe*, qq_gguf* or qq_lfm2* (NULL once released) */
     struct handle *ctx;  /* owning context handle (tensor, moe) */
     napi_ref ctx_ref;    /* keeps the context alive while this handle lives */
     napi_ref keep[3];    /* moe: keeps gate/up/down tensors alive */
     int in_dim, out_dim, n_mats;
     int H, E, K;
+    int vocab;           /* lfm2 */
 } handle;
 
 #define CHECK_NAPI(env, call)                                                        \
@@ -72,6 +80,7 @@ static void release_handle(napi_env env, handle *h)
     case H_MOE: qq_moe_release(ctx, (qq_moe *)h->ptr); break;
     case H_CTX: qq_destroy((qq_ctx *)h->ptr); break;
     case H_GGUF: qq_gguf_close((qq_gguf *)h->ptr); break;
+    case H_LFM2: qq_lfm2_release(ctx, (qq_lfm2 *)h->ptr); break;
     }
     h->ptr = NULL;
     for (int i = 0; i < 3; i++)
@@ -557,6 +566,92 @@ static napi_value js_gguf_moe_layer(napi_env env, napi_callback_info info)
     return new_handle(env, h);
 }
 
+static napi_value js_lfm2_create(napi_env env, napi_callback_info info)
+{
+    ARGS(2);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *gh = get_handle(env, argv[1], H_GGUF);
+    if (!gh) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    qq_lfm2 *m = NULL;
+    int rc = qq_lfm2_create(ctx, (const qq_gguf *)gh->ptr, &m);
+    if (rc) return throw_qq(env, "qq_lfm2_create", rc, ctx);
+    handle *h = child_of(env, argv[0], ch, H_LFM2);
+    if (!h) {
+        qq_lfm2_release(ctx, m);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    qq_lfm2_info I;
+    qq_lfm2_get_info(m, &I);
+    h->ptr = m;
+    h->vocab = I.n_vocab;
+    return new_handle(env, h);
+}
+
+static napi_value js_lfm2_info(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    handle *mh = get_handle(env, argv[0], H_LFM2);
+    if (!mh) return NULL;
+    qq_lfm2_info I;
+    qq_lfm2_get_info((const qq_lfm2 *)mh->ptr, &I);
+    napi_value o;
+    CHECK_NAPI(env, napi_create_object(env, &o));
+    const struct {
+        const char *k;
+        double v;
+    } f[] = {{"nLayers", I.n_layers},         {"nEmbd", I.n_embd},         {"nHeads", I.n_heads},
+             {"nHeadKV", I.n_head_kv},        {"headDim", I.head_dim},     {"nVocab", I.n_vocab},
+             {"nFF", I.n_ff},                 {"nExperts", I.n_experts},   {"nExpertsUsed", I.n_experts_used},
+             {"nDenseLead", I.n_dense_lead},  {"lCache", I.l_cache},       {"maxCtx", I.max_ctx},
+             {"nAttnLayers", I.n_attn_layers}, {"eps", I.eps},             {"ropeFreqBase", I.rope_freq_base}};
+    for (size_t i = 0; i < sizeof f / sizeof f[0]; i++)
+        if (!set_num(env, o, f[i].k, f[i].v)) return NULL;
+    return o;
+}
+
+static napi_value js_lfm2_forward(napi_env env, napi_callback_info info)
+{
+    ARGS(5);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *mh = get_handle(env, argv[1], H_LFM2);
+    if (!mh) return NULL;
+    int32_t token, pos;
+    if (get_i32(env, argv[2], &token) || get_i32(env, argv[3], &pos)) {
+        napi_throw_type_error(env, NULL, "lfm2Forward(ctx, lfm2, token, position, logits | null)");
+        return NULL;
+    }
+    float *logits = NULL;
+    if (!is_nullish(env, argv[4])) {
+        size_t n;
+        if (get_typed(env, argv[4], napi_float32_array, (void **)&logits, &n) || n < (size_t)mh->vocab) {
+            napi_throw_type_error(env, NULL, "lfm2Forward: logits must be a Float32Array of nVocab floats or null");
+            return NULL;
+        }
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_lfm2_forward(ctx, (qq_lfm2 *)mh->ptr, token, pos, logits);
+    if (rc) return throw_qq(env, "qq_lfm2_forward", rc, ctx);
+    return NULL;
+}
+
+static napi_value js_lfm2_reset(napi_env env, napi_callback_info info)
+{
+    ARGS(2);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *mh = get_handle(env, argv[1], H_LFM2);
+    if (!mh) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_lfm2_reset(ctx, (qq_lfm2 *)mh->ptr);
+    if (!rc) rc = qq_synchronize(ctx);
+    if (rc) return throw_qq(env, "qq_lfm2_reset", rc, ctx);
+    return NULL;
+}
+
 static napi_value js_release(napi_env env, napi_callback_info info)
 {
     ARGS(1);
@@ -585,6 +680,10 @@ static napi_value module_init(napi_env env, napi_value exports)
         {"ggufTensors", NULL, js_gguf_tensors, NULL, NULL, NULL, napi_enumerable, NULL},
         {"ggufMoeParams", NULL, js_gguf_moe_params, NULL, NULL, NULL, napi_enumerable, NULL},
         {"ggufMoeLayer", NULL, js_gguf_moe_layer, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lfm2Create", NULL, js_lfm2_create, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lfm2Info", NULL, js_lfm2_info, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lfm2Forward", NULL, js_lfm2_forward, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"lfm2Reset", NULL, js_lfm2_reset, NULL, NULL, NULL, napi_enumerable, NULL},
         {"release", NULL, js_release, NULL, NULL, NULL, napi_enumerable, NULL},
     };
     if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;

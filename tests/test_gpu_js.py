@@ -46,3 +46,24 @@ def test_js_attach_gguf(tmp_path, arch):
     bad = [c for c in res["checks"] if not c["ok"]]
     assert res["ok"] and not bad, (bad, p.stderr[-2000:])
     assert res["max_rel_l2"] < 1e-4
+
+
+def test_js_lfm2_forward(tmp_path):
+    """MoEDevice.attachLfm2Forward: Lfm2Engine.forward / resetKVCache run the whole
+    token on the device from the attached file, against oracle/lfm2_ref.js."""
+    import synth
+    import _lfm2
+    print("js lfm2 forward", flush=True)
+    cfg = synth.LFM2_TINY
+    path, offs, tensors = _lfm2.write_model(tmp_path, 9, cfg)
+    job = {"gguf": path, "kv": _lfm2.kv_dict(cfg), "tokens": [3, 77, 250, 1, 9, 120],
+           "tensors": {n: {"offset": offs[n], "shape": s, "type": t} for n, s, t, _ in tensors}}
+    jp = tmp_path / "job.json"
+    jp.write_text(json.dumps(job))
+    p = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "lfm2_check.js"), str(jp)],
+                       capture_output=True, text=True, timeout=240)
+    assert p.stdout.strip(), p.stderr
+    res = json.loads(p.stdout.strip().splitlines()[-1])
+    bad = [c for c in res["checks"] if not c["ok"]]
+    assert res["ok"] and not bad, (bad, p.stderr[-2000:])
+    assert res["max_rel_l2"] < 1e-4
