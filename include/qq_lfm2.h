@@ -11,9 +11,10 @@
  * Supported files: the tensors Lfm2Engine binds (src/lfm2-engine.js:78-144),
  * with Q8_0 matrices (token_embd / output, in_proj, out_proj, attn_q/k/v/
  * output, ffn_gate/up/down, expert tensors), F32 or Q8_0 norm weights, an F32,
- * F16 or Q8_0 conv kernel with l_cache = 3, head_dim 64, at most 256 experts
- * and rows of at most 8192 inputs.  Anything else fails at creation with a
- * message naming the tensor or key.
+ * F16 or Q8_0 conv kernel with l_cache = 3, head_dim 64, rows of at most 8192
+ * inputs, and MoE blocks the batch-1 decode kernel takes (embedding length
+ * at most 2048, at most 256 experts).  Anything else fails at creation with a
+ * message naming the tensor, key or block.
  *
  * Numerics: matrix products accumulate in fp32 (the reference: binary64);
  * the elementwise steps round to fp32 where the reference stores into a
