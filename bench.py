@@ -306,8 +306,10 @@ def run_lfm2(args, torch, ctx, stream):
     logits = torch.empty(V, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
 
+    p0 = max(0, min(args.position0, info["max_ctx"] - LFM2_POS))
+
     def step(i):
-        model.forward_dev((i * 7919) % V, i % LFM2_POS, logits.data_ptr())
+        model.forward_dev((i * 7919) % V, p0 + i % LFM2_POS, logits.data_ptr())
 
     total_ms = _time_steps(torch, ctx, stream, step, args.steps, args.warmup)
     ms_per_step = total_ms / args.steps
@@ -334,12 +336,12 @@ def run_lfm2(args, torch, ctx, stream):
     mv_bytes = n_conv * w_conv + n_attn * w_attn + ndense * w_dense + w_head
     mv_launches = 2 * n_conv + 2 * n_attn + 2 * ndense + 1
     LFM2_BYTES["lfm2_matvec"] = mv_bytes / mv_launches
-    avg_n_prof = (n_prof + 1) / 2.0
+    avg_n_prof = p0 + (n_prof + 1) / 2.0
     LFM2_BYTES["lfm2_attention"] = info["n_head_kv"] * avg_n_prof * 64 * 4 * 2
     LFM2_BYTES["lfm2_embed"] = Hh * q8 + Hh * 4
     n_moe = nl - ndense
     moe_bytes = n_moe * kernel_bytes("decode_experts", 1, K)
-    avg_n = (min(args.steps, LFM2_POS) + 1) / 2.0
+    avg_n = p0 + (min(args.steps, LFM2_POS) + 1) / 2.0
     kv_bytes = n_attn * info["n_head_kv"] * avg_n * 64 * 4 * 2
     tok_bytes = mv_bytes + moe_bytes + kv_bytes
     kernels = kernel_table(prof, 1, K, K)
@@ -348,8 +350,9 @@ def run_lfm2(args, torch, ctx, stream):
               "dense_ffn_blocks": ndense, "moe_blocks": n_moe, "H": Hh, "heads": info["n_heads"],
               "kv_heads": info["n_head_kv"], "head_dim": info["head_dim"], "n_ff": info["n_ff"],
               "F": F, "E": E, "K": K, "vocab": V, "weights": "Q8_0", "activations": "f32",
-              "positions": "0..%d (step i at position i %% %d, one sequence)" % (LFM2_POS - 1, LFM2_POS),
-              "timed_positions": "0..%d" % (min(args.steps, LFM2_POS) - 1)}
+              "positions": "%d..%d (step i at position %d + i %% %d, one sequence)"
+                           % (p0, p0 + LFM2_POS - 1, p0, LFM2_POS),
+              "timed_positions": "%d..%d" % (p0, p0 + min(args.steps, LFM2_POS) - 1)}
     extra = {"us_per_token": round(ms_per_step * 1000.0, 2),
              "hbm_bytes_per_token": int(tok_bytes),
              "hbm_gbps_token": round(tok_bytes / (ms_per_step * 1e6), 1),
@@ -462,6 +465,9 @@ def main():
     ap.add_argument("--layers", type=int, default=16, help="distinct layer instances rotated over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--position0", type=int, default=0,
+                    help="lfm2_decode: first position of the timed sequence (step i runs at "
+                         "position0 + i %% 512)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only time a 1 GiB device-to-device copy (reference kernel for the "
                          "rocprof FETCH_SIZE / WRITE_SIZE scale factors)")

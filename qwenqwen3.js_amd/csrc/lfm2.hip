@@ -424,6 +424,96 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
     }
 }
 
+// Long contexts: the same attention split over chunks of LM_CHUNK positions
+// (one workgroup per head and chunk, so the K and V rows of a head are read
+// by many CUs at once).  Chunk c writes its score max m_c, the binary64 sum
+// l_c of fp32(exp(s - m_c)) and o_c[d] = sum fp32(exp(s - m_c)) * v[d]
+// (binary64); lfm2_attn_join_kernel then forms
+// out[d] = fp32(sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M)), M = max m_c,
+// over the chunks in order.  Equal to the one-workgroup form to rounding.
+constexpr int LM_CHUNK = 256;
+constexpr int LM_MAX_CHUNKS = LM_MAX_CTX / LM_CHUNK;
+constexpr int LM_PART = LM_HEAD + 2;   // doubles per (head, chunk): o[64], m, l
+
+__global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_chunk_kernel(
+    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc, int n_heads,
+    int n_kv_heads, int max_ctx, int n, double scale, double *__restrict__ part)
+{
+    constexpr int NW = LM_ATTN_THREADS / WAVE;
+    constexpr int VPT = LM_CHUNK / NW;   // V values per thread
+    static_assert(LM_ATTN_THREADS == LM_CHUNK, "one position per thread");
+    __shared__ __align__(16) float qh[LM_HEAD];
+    __shared__ float ex[LM_CHUNK];
+    __shared__ float redf[NW];
+    __shared__ double redd[NW];
+    __shared__ double po[NW][LM_HEAD];
+    const int tid = threadIdx.x;
+    const int hq = blockIdx.x, c = blockIdx.y;
+    const int g = (int)(((long long)hq * n_kv_heads) / n_heads);
+    const float *K = kc + (size_t)g * max_ctx * LM_HEAD;
+    const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
+    const int p0 = c * LM_CHUNK;
+    const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
+    // independent loads first: this thread's K row, its V column values, the query
+    float4 kr[LM_HEAD / 4];
+    {
+        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)min(p0 + tid, n - 1) * LM_HEAD);
+#pragma unroll
+        for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = src[i];
+    }
+    float vv[VPT];
+#pragma unroll
+    for (int u = 0; u < VPT; u++) vv[u] = V[(size_t)min(p0 + cls + NW * u, n - 1) * LM_HEAD + d];
+    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
+    __syncthreads();
+    const bool valid = p0 + tid < n;
+    double dot = 0.0;
+#pragma unroll
+    for (int i = 0; i < LM_HEAD / 4; i++) {
+        dot = fma((double)qh[4 * i], (double)kr[i].x, dot);
+        dot = fma((double)qh[4 * i + 1], (double)kr[i].y, dot);
+        dot = fma((double)qh[4 * i + 2], (double)kr[i].z, dot);
+        dot = fma((double)qh[4 * i + 3], (double)kr[i].w, dot);
+    }
+    const float sc = valid ? (float)(dot * scale) : -INFINITY;
+    const float m = lm_block_max<NW>(sc, redf);
+    const float e = valid ? (float)exp((double)sc - (double)m) : 0.0f;
+    ex[tid] = e;
+    const double l = block_sum_f64<NW>((double)e, redd);   // contains the barrier ex[] needs
+    double o = 0.0;
+#pragma unroll
+    for (int u = 0; u < VPT; u++) o = fma((double)vv[u], (double)ex[cls + NW * u], o);
+    po[cls][d] = o;
+    __syncthreads();
+    if (tid < LM_HEAD) {
+        double t = po[0][tid];
+#pragma unroll
+        for (int w = 1; w < NW; w++) t = t + po[w][tid];
+        double *pp = part + ((size_t)hq * LM_MAX_CHUNKS + c) * LM_PART;
+        pp[tid] = t;
+        if (tid == 0) {
+            pp[LM_HEAD] = (double)m;
+            pp[LM_HEAD + 1] = l;
+        }
+    }
+}
+
+__global__ __launch_bounds__(LM_HEAD) void lfm2_attn_join_kernel(const double *__restrict__ part, int nchunks,
+                                                                 float *__restrict__ out)
+{
+    const int hq = blockIdx.x, d = threadIdx.x;
+    const double *pp = part + (size_t)hq * LM_MAX_CHUNKS * LM_PART;
+    double M = -INFINITY;
+    for (int c = 0; c < nchunks; c++) M = fmax(M, pp[c * LM_PART + LM_HEAD]);
+    double L = 0.0, O = 0.0;
+    for (int c = 0; c < nchunks; c++) {
+        const double f = exp(pp[c * LM_PART + LM_HEAD] - M);
+        L = L + pp[c * LM_PART + LM_HEAD + 1] * f;
+        O = O + pp[c * LM_PART + d] * f;
+    }
+    out[(size_t)hq * LM_HEAD + d] = (float)(O / L);
+}
+
 // embeddingLookupQ80 (src/tensor.js:56-77) of column `token` of the repacked
 // [H, vocab] table: hidden[i] = q * d (exact in fp32).
 __global__ __launch_bounds__(256) void lfm2_embed_kernel(const int8_t *__restrict__ qs,
@@ -500,13 +590,22 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     return QQ_OK;
 }
 
+size_t lfm2_attn_work_bytes(int n_heads) { return (size_t)n_heads * LM_MAX_CHUNKS * LM_PART * 8; }
+
 int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
-                     int n_kv_heads, int max_ctx, int n, double scale, float *out)
+                     int n_kv_heads, int max_ctx, int n, double scale, float *out, double *work)
 {
     if (n < 1 || n > LM_MAX_CTX || n > max_ctx) return set_error(ctx, "lfm2: %d positions", n);
     prof_begin(ctx, K_LFM2_ATTN);
-    QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, q, kc, vc, n_heads,
-              n_kv_heads, max_ctx, n, scale, out);
+    if (n <= LM_CHUNK) {
+        QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, q, kc, vc, n_heads,
+                  n_kv_heads, max_ctx, n, scale, out);
+    } else {
+        const int nch = (n + LM_CHUNK - 1) / LM_CHUNK;
+        QQ_LAUNCH(ctx, lfm2_attn_chunk_kernel, dim3(n_heads, nch), dim3(LM_ATTN_THREADS), 0, q, kc, vc,
+                  n_heads, n_kv_heads, max_ctx, n, scale, work);
+        QQ_LAUNCH(ctx, lfm2_attn_join_kernel, dim3(n_heads), dim3(LM_HEAD), 0, work, nch, out);
+    }
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

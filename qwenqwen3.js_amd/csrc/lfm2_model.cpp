@@ -64,6 +64,7 @@ struct qq_lfm2 {
     float *hidden = nullptr, *ybuf = nullptr, *q = nullptr, *attn = nullptr, *ffn = nullptr,
           *logits = nullptr;
     double *freq = nullptr;
+    double *attn_work = nullptr;       // per-chunk attention partials (long contexts)
     std::vector<void *> dev;
     std::vector<qq_tensor *> tens;
     std::vector<qq_moe *> moes;
@@ -334,6 +335,8 @@ int bind(Binder &B)
         if (int rc = B.alloc(lens[i] * 4, &v)) return rc;
         *bufs[i] = static_cast<float *>(v);
     }
+    if (int rc = B.alloc(qq::lfm2_attn_work_bytes(I.n_heads), &v)) return rc;
+    m->attn_work = static_cast<double *>(v);
     // applyRoPE's frequencies 1 / base^(i / half) (src/tensor.js:135-137)
     double fr[kHeadDim / 2];
     for (int i = 0; i < kHeadDim / 2; i++) fr[i] = 1.0 / std::pow(I.rope_freq_base, (double)i / (kHeadDim / 2));
@@ -460,7 +463,7 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
             a.freq = m->freq;
             if (int rc = qq::launch_lfm2_mv(ctx, qq::LM_QKV, a)) return rc;
             if (int rc = qq::launch_lfm2_attn(ctx, m->q, kc, vc, I.n_heads, I.n_head_kv, I.max_ctx, position + 1,
-                                              1.0 / std::sqrt((double)kHeadDim), m->attn))
+                                              1.0 / std::sqrt((double)kHeadDim), m->attn, m->attn_work))
                 return rc;
             qq::LmLaunch r;
             r.x = m->attn;

@@ -219,8 +219,11 @@ struct LmLaunch {
     const double *freq = nullptr;
 };
 int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l);
+// Contexts beyond 256 positions run in chunks; `work` holds
+// lfm2_attn_work_bytes(n_heads) of per-chunk partials.
+size_t lfm2_attn_work_bytes(int n_heads);
 int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
-                     int n_kv_heads, int max_ctx, int n, double scale, float *out);
+                     int n_kv_heads, int max_ctx, int n, double scale, float *out, double *work);
 int launch_lfm2_embed(qq_ctx *ctx, const qq_tensor *t, int token, float *out);
 int launch_lfm2_zero(qq_ctx *ctx, float *p, size_t n);
 // First byte of a GGUF reader's file (gguf.cpp).

@@ -30,17 +30,17 @@ def _model(tmp_path, seed, cfg=synth.LFM2_TINY, **kw):
     return m, path, offs, tensors
 
 
-def _check_tokens(tmp_path, seed, cfg=synth.LFM2_TINY, tokens=TOKENS, **kw):
+def _check_tokens(tmp_path, seed, cfg=synth.LFM2_TINY, tokens=TOKENS, start=0, **kw):
     import torch
     m, path, offs, tensors = _model(tmp_path, seed, cfg, **kw)
     try:
-        ref, routes = _lfm2.js_forward(tmp_path, path, offs, tensors, cfg, tokens)
+        ref, routes = _lfm2.js_forward(tmp_path, path, offs, tensors, cfg, tokens, start)
         T, V, nl, K = len(tokens), m.info["n_vocab"], m.info["n_layers"], m.info["n_experts_used"]
         logits = torch.empty((T, V), dtype=torch.float32, device="cuda")
         idx = torch.full((T, nl, K), -1, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
         for t, tok in enumerate(tokens):
-            m.forward_dev(tok, t, logits[t].data_ptr(), idx[t].data_ptr())
+            m.forward_dev(tok, start + t, logits[t].data_ptr(), idx[t].data_ptr())
         gpu_context().synchronize()
         got, gi = logits.cpu().numpy(), idx.cpu().numpy()
         for t in range(T):
@@ -63,6 +63,16 @@ def _check_tokens(tmp_path, seed, cfg=synth.LFM2_TINY, tokens=TOKENS, **kw):
 def test_forward_matches_oracle(tmp_path, seed, kw):
     _say("lfm2 forward", seed, kw)
     m, _ = _check_tokens(tmp_path, seed, **kw)
+    m.release()
+
+
+@pytest.mark.parametrize("start", [253, 700])
+def test_forward_long_context(tmp_path, start):
+    """Positions past 256 take the chunked attention (chunks of 256 positions and a
+    join); the cache holds zeros below `start` on both sides."""
+    _say("lfm2 long context", start)
+    cfg = dict(synth.LFM2_TINY, ctx=1024)
+    m, _ = _check_tokens(tmp_path, 8, cfg=cfg, tokens=TOKENS[:6], start=start)
     m.release()
 
 
