@@ -16,8 +16,10 @@
 //   * short-conv: a workgroup owns 32 channels d and computes rows d, H + d
 //     and 2H + d of in_proj (B, C, x), then bx = B * x, the depthwise causal
 //     conv over its channels' state, the state shift and y = C * conv;
-//   * attention: a workgroup owns one head of q, k or v (64 rows): per-head
-//     RMSNorm, split-half RoPE and the KV-cache store are its epilogue;
+//   * attention: q, k and v are one matvec over their concatenated rows (v
+//     goes straight into the KV cache); each attention workgroup forms the
+//     per-head RMSNorm and split-half RoPE of its q head and of the new k row
+//     itself, and one workgroup per KV head stores that k row;
 //   * dense FFN: rows f of gate and up in one workgroup, silu(g) * u.
 // Where the reference stores into a Float32Array the kernels round to fp32 at
 // the same step, and its binary64 expressions are kept in binary64 without
@@ -53,8 +55,9 @@ struct LmArgs {
     float *state;
     const float *kern;
     int L, H;
-    // attention: q out, KV cache of this layer [n_kv_heads][max_ctx][64]
-    float *q;
+    // attention: raw q and k rows out, V into the KV cache of this layer
+    // [n_kv_heads][max_ctx][64]
+    float *q, *kraw;
     float *kc, *vc;
     const float *qn, *kn;   // per-head norm weights [64]
     int n_heads, n_kv_heads, pos, max_ctx;
@@ -99,13 +102,12 @@ __device__ __forceinline__ int lm_row(const LmArgs &a, int g, int &mat)
         mat = 0;
         return g * a.H + RPW * j;
     }
-    // QKV: one head (G * RPW = 64 rows) per workgroup, q heads, then k, then v
-    if (j < a.n_heads) {
-        mat = 0;
-        return LM_HEAD * j + RPW * g;
-    }
-    mat = j < a.n_heads + a.n_kv_heads ? 1 : 2;
-    return LM_HEAD * (j - a.n_heads - (mat == 2 ? a.n_kv_heads : 0)) + RPW * g;
+    // QKV: the rows of q, then k, then v, G * RPW of them per workgroup
+    // (head sizes are multiples of it, so a workgroup stays in one matrix)
+    const int r = G * RPW * j + RPW * g;
+    const int nq = a.n_heads * LM_HEAD, nkv = a.n_kv_heads * LM_HEAD;
+    mat = r < nq ? 0 : (r < nq + nkv ? 1 : 2);
+    return r - (mat >= 1 ? nq : 0) - (mat == 2 ? nkv : 0);
 }
 
 // BPL int8 weights (offset binary after the XOR) against BPL activations:
@@ -146,15 +148,12 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     constexpr int LPR = WAVE / RPW;       // lanes per row
     constexpr int BPL = QK / LPR;         // bytes (weights) per lane per block
     static_assert(LPR * BPL == QK && BPL % 4 == 0, "lane layout");
-    static_assert(MODE != LM_QKV || G * RPW == LM_HEAD, "one head per workgroup");
+    static_assert(MODE != LM_QKV || LM_HEAD % (G * RPW) == 0, "a workgroup within one head");
     extern __shared__ __align__(16) float lm_lds[];
     float *xl = lm_lds;                  // nb * 32 activations (zero padded)
     float *xs = lm_lds + a.nb * QK;      // sums of every BPL-value chunk
     __shared__ float red[G][WPG][RPW];
     __shared__ double redd[NW];
-    __shared__ float hv[LM_HEAD];
-    __shared__ double hinv;
-
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
     const int wave = tid / WAVE;
@@ -290,44 +289,68 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
             a.y[d] = C * co;
         }
     } else {
-        // QKV: perHeadRMSNorm (src/tensor.js:117-129), applyRoPE (:132-147),
-        // KVCache.store (src/kv-cache.js:16-32)
-        if (tid < LM_HEAD) hv[tid] = rowsum(tid / RPW, tid % RPW);
-        __syncthreads();
-        const int j = blockIdx.x;
-        const int kind = j < a.n_heads ? 0 : (j < a.n_heads + a.n_kv_heads ? 1 : 2);
-        const int head = kind == 0 ? j : (kind == 1 ? j - a.n_heads : j - a.n_heads - a.n_kv_heads);
-        if (kind == 2) {
-            if (tid < LM_HEAD)
-                a.vc[((size_t)head * a.max_ctx + a.pos) * LM_HEAD + tid] = hv[tid];
-            return;
-        }
-        if (tid == 0) {
-            double ss = 0.0;   // in order, as the reference adds
-            for (int i = 0; i < LM_HEAD; i++) ss = ss + (double)hv[i] * (double)hv[i];
-            hinv = 1.0 / sqrt(ss / (double)LM_HEAD + a.eps);
-        }
-        __syncthreads();
-        const float *nw = kind == 0 ? a.qn : a.kn;
-        if (tid < LM_HEAD) hv[tid] = (float)((double)nw[tid] * (double)hv[tid] * hinv);
-        __syncthreads();
-        if (tid < LM_HEAD / 2) {
-            const int i = tid, half = LM_HEAD / 2;
-            const double th = (double)a.pos * a.freq[i];
-            const double c = cos(th), s = sin(th);
-            const double x0 = (double)hv[i], x1 = (double)hv[i + half];
-            const float r0 = (float)(x0 * c - x1 * s);
-            const float r1 = (float)(x0 * s + x1 * c);
-            if (kind == 0) {
-                a.q[(size_t)head * LM_HEAD + i] = r0;
-                a.q[(size_t)head * LM_HEAD + i + half] = r1;
-            } else {
-                float *kr = a.kc + ((size_t)head * a.max_ctx + a.pos) * LM_HEAD;
-                kr[i] = r0;
-                kr[i + half] = r1;
+        // QKV: raw q and k rows; v rows straight into the cache (KVCache.store,
+        // src/kv-cache.js:16-32)
+        if (tid < G * RPW) {
+            const int r = G * RPW * blockIdx.x + tid;
+            const int nq = a.n_heads * LM_HEAD, nkv = a.n_kv_heads * LM_HEAD;
+            const float v = rowsum(tid / RPW, tid % RPW);
+            if (r < nq) a.q[r] = v;
+            else if (r < nq + nkv) a.kraw[r - nq] = v;
+            else if (r < nq + 2 * nkv) {
+                const int rv = r - nq - nkv;
+                a.vc[((size_t)(rv / LM_HEAD) * a.max_ctx + a.pos) * LM_HEAD + rv % LM_HEAD] = v;
             }
         }
     }
+}
+
+// perHeadRMSNorm (src/tensor.js:117-129) then applyRoPE (:132-147) of one
+// 64-value head `raw` into LDS `out`, by one wave (lane l holds value l):
+// the sum of squares in order in binary64 (every lane runs the same
+// sequence), (w * x) * inv, and x0' = fp32(x0 cos - x1 sin),
+// x1' = fp32(x0 sin + x1 cos) in binary64.
+__device__ __forceinline__ void lm_head_prep(const float *__restrict__ raw, const float *__restrict__ nw,
+                                             double eps, int pos, const double *__restrict__ freq,
+                                             float *out)
+{
+    static_assert(LM_HEAD == WAVE, "one value per lane");
+    const int l = threadIdx.x & (WAVE - 1);
+    const float x = raw[l];
+    const float w = nw[l];
+    const double fr = freq[l & (LM_HEAD / 2 - 1)];
+    const int xb = __float_as_int(x);
+    double ss = 0.0;
+    for (int i = 0; i < LM_HEAD; i++) {
+        const double v = (double)__int_as_float(__builtin_amdgcn_readlane(xb, i));
+        ss = ss + v * v;
+    }
+    const double inv = 1.0 / sqrt(ss / (double)LM_HEAD + eps);
+    const float t = (float)((double)w * (double)x * inv);
+    const float other = __shfl(t, (l + LM_HEAD / 2) & (WAVE - 1), WAVE);   // lane i < 32: value i + 32
+    if (l < LM_HEAD / 2) {
+        const double th = (double)pos * fr;
+        const double c = cos(th), s = sin(th);
+        const double x0 = (double)t, x1 = (double)other;
+        out[l] = (float)(x0 * c - x1 * s);
+        out[l + LM_HEAD / 2] = (float)(x0 * s + x1 * c);
+    }
+}
+
+// The query head hq and the new k row of its kv head g, normed and rotated,
+// into LDS; the first query head of each kv head (in the last chunk) stores
+// the k row into the cache, which nobody reads in this launch (position
+// n - 1 takes kpos).
+struct LmAttnIn {
+    const float *q, *kraw;
+    const float *qn, *kn;
+    const double *freq;
+    double eps;
+};
+
+__device__ __forceinline__ bool lm_first_of_group(int hq, int g, int n_heads, int n_kv_heads)
+{
+    return hq == 0 || (int)(((long long)(hq - 1) * n_kv_heads) / n_heads) != g;
 }
 
 // GQA attention of one token (src/lfm2-engine.js:354-388), one workgroup
@@ -340,8 +363,7 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
 // The sum of the exponentials is a tree (not the reference's one-by-one
 // order) and out[d] is accumulated in four position classes joined at the
 // end, so those two steps agree with the reference to rounding, not bit for bit.
-__global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float *__restrict__ q,
-                                                                   const float *__restrict__ kc,
+__global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in, float *__restrict__ kc,
                                                                    const float *__restrict__ vc,
                                                                    int n_heads, int n_kv_heads,
                                                                    int max_ctx, int n, double scale,
@@ -349,6 +371,7 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
 {
     constexpr int NW = LM_ATTN_THREADS / WAVE;
     __shared__ __align__(16) float qh[LM_HEAD];
+    __shared__ __align__(16) float kpos[LM_HEAD];
     __shared__ float sc[LM_MAX_CTX];
     __shared__ float redf[NW];
     __shared__ double redd[NW];
@@ -360,26 +383,35 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(const float 
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
     const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
     // loads that depend on nothing are issued first: this thread's first K
-    // row, the first LM_VPRE values of its V column, the query
+    // row (cached positions only: position n - 1 is this call's), the first
+    // LM_VPRE values of its V column
     constexpr int LM_VPRE = 8;
     float4 kr[LM_HEAD / 4];
     auto load_k = [&](int p) {
-        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)min(p, n - 1) * LM_HEAD);
+        if (p >= n - 1) return;
+        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)p * LM_HEAD);
 #pragma unroll
         for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = src[i];
     };
+#pragma unroll
+    for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     load_k(tid);
     float vpre[LM_VPRE];
 #pragma unroll
     for (int u = 0; u < LM_VPRE; u++) vpre[u] = V[(size_t)min(cls + NW * u, n - 1) * LM_HEAD + d];
-    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
+    // this query head (wave 0) and the new k row (wave 1), normed and rotated
+    if (tid / WAVE == 0) lm_head_prep(in.q + (size_t)hq * LM_HEAD, in.qn, in.eps, n - 1, in.freq, qh);
+    else if (tid / WAVE == 1) lm_head_prep(in.kraw + (size_t)g * LM_HEAD, in.kn, in.eps, n - 1, in.freq, kpos);
     __syncthreads();
+    if (lm_first_of_group(hq, g, n_heads, n_kv_heads) && tid < LM_HEAD)
+        kc[((size_t)g * max_ctx + n - 1) * LM_HEAD + tid] = kpos[tid];
     float mx = -INFINITY;
     for (int p = tid; p < n; p += LM_ATTN_THREADS) {
         double dot = 0.0;
+        const bool self = p == n - 1;
 #pragma unroll
         for (int i = 0; i < LM_HEAD / 4; i++) {
-            const float4 kv = kr[i];
+            const float4 kv = self ? reinterpret_cast<const float4 *>(kpos)[i] : kr[i];
             dot = fma((double)qh[4 * i], (double)kv.x, dot);
             dot = fma((double)qh[4 * i + 1], (double)kv.y, dot);
             dot = fma((double)qh[4 * i + 2], (double)kv.z, dot);
@@ -436,13 +468,14 @@ constexpr int LM_MAX_CHUNKS = LM_MAX_CTX / LM_CHUNK;
 constexpr int LM_PART = LM_HEAD + 2;   // doubles per (head, chunk): o[64], m, l
 
 __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_chunk_kernel(
-    const float *__restrict__ q, const float *__restrict__ kc, const float *__restrict__ vc, int n_heads,
+    LmAttnIn in, float *__restrict__ kc, const float *__restrict__ vc, int n_heads,
     int n_kv_heads, int max_ctx, int n, double scale, double *__restrict__ part)
 {
     constexpr int NW = LM_ATTN_THREADS / WAVE;
     constexpr int VPT = LM_CHUNK / NW;   // V values per thread
     static_assert(LM_ATTN_THREADS == LM_CHUNK, "one position per thread");
     __shared__ __align__(16) float qh[LM_HEAD];
+    __shared__ __align__(16) float kpos[LM_HEAD];
     __shared__ float ex[LM_CHUNK];
     __shared__ float redf[NW];
     __shared__ double redd[NW];
@@ -454,26 +487,35 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_chunk_kernel(
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
     const int p0 = c * LM_CHUNK;
     const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
-    // independent loads first: this thread's K row, its V column values, the query
+    // independent loads first: this thread's K row (cached positions only:
+    // position n - 1 is this call's) and its V column values
     float4 kr[LM_HEAD / 4];
-    {
-        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)min(p0 + tid, n - 1) * LM_HEAD);
+#pragma unroll
+    for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (p0 + tid < n - 1) {
+        const float4 *src = reinterpret_cast<const float4 *>(K + (size_t)(p0 + tid) * LM_HEAD);
 #pragma unroll
         for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = src[i];
     }
     float vv[VPT];
 #pragma unroll
     for (int u = 0; u < VPT; u++) vv[u] = V[(size_t)min(p0 + cls + NW * u, n - 1) * LM_HEAD + d];
-    if (tid < LM_HEAD) qh[tid] = q[(size_t)hq * LM_HEAD + tid];
+    // this query head (wave 0) and the new k row (wave 1), normed and rotated
+    if (tid / WAVE == 0) lm_head_prep(in.q + (size_t)hq * LM_HEAD, in.qn, in.eps, n - 1, in.freq, qh);
+    else if (tid / WAVE == 1) lm_head_prep(in.kraw + (size_t)g * LM_HEAD, in.kn, in.eps, n - 1, in.freq, kpos);
     __syncthreads();
+    if (c == (n - 1) / LM_CHUNK && lm_first_of_group(hq, g, n_heads, n_kv_heads) && tid < LM_HEAD)
+        kc[((size_t)g * max_ctx + n - 1) * LM_HEAD + tid] = kpos[tid];
     const bool valid = p0 + tid < n;
+    const bool self = p0 + tid == n - 1;
     double dot = 0.0;
 #pragma unroll
     for (int i = 0; i < LM_HEAD / 4; i++) {
-        dot = fma((double)qh[4 * i], (double)kr[i].x, dot);
-        dot = fma((double)qh[4 * i + 1], (double)kr[i].y, dot);
-        dot = fma((double)qh[4 * i + 2], (double)kr[i].z, dot);
-        dot = fma((double)qh[4 * i + 3], (double)kr[i].w, dot);
+        const float4 kv = self ? reinterpret_cast<const float4 *>(kpos)[i] : kr[i];
+        dot = fma((double)qh[4 * i], (double)kv.x, dot);
+        dot = fma((double)qh[4 * i + 1], (double)kv.y, dot);
+        dot = fma((double)qh[4 * i + 2], (double)kv.z, dot);
+        dot = fma((double)qh[4 * i + 3], (double)kv.w, dot);
     }
     const float sc = valid ? (float)(dot * scale) : -INFINITY;
     const float m = lm_block_max<NW>(sc, redf);
@@ -553,6 +595,7 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     a.L = l.L;
     a.H = l.H;
     a.q = l.q;
+    a.kraw = l.kraw;
     a.kc = l.kc;
     a.vc = l.vc;
     a.qn = l.qn;
@@ -582,7 +625,8 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
         QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3, 5, 13, 8>), dim3((a.H + 7) / 8), dim3(15 * WAVE), shm, a);
         break;
     default:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 2, 8, 8, 32>), dim3(a.n_heads + 2 * a.n_kv_heads), dim3(16 * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 1, 16, 4, 8>),
+                  dim3((a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 8), dim3(16 * WAVE), shm, a);
         break;
     }
     prof_end(ctx);
@@ -592,17 +636,19 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
 
 size_t lfm2_attn_work_bytes(int n_heads) { return (size_t)n_heads * LM_MAX_CHUNKS * LM_PART * 8; }
 
-int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
+int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kraw, const float *qn, const float *kn,
+                     const double *freq, double eps, float *kc, const float *vc, int n_heads,
                      int n_kv_heads, int max_ctx, int n, double scale, float *out, double *work)
 {
     if (n < 1 || n > LM_MAX_CTX || n > max_ctx) return set_error(ctx, "lfm2: %d positions", n);
+    const LmAttnIn in{q, kraw, qn, kn, freq, eps};
     prof_begin(ctx, K_LFM2_ATTN);
     if (n <= LM_CHUNK) {
-        QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, q, kc, vc, n_heads,
+        QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, in, kc, vc, n_heads,
                   n_kv_heads, max_ctx, n, scale, out);
     } else {
         const int nch = (n + LM_CHUNK - 1) / LM_CHUNK;
-        QQ_LAUNCH(ctx, lfm2_attn_chunk_kernel, dim3(n_heads, nch), dim3(LM_ATTN_THREADS), 0, q, kc, vc,
+        QQ_LAUNCH(ctx, lfm2_attn_chunk_kernel, dim3(n_heads, nch), dim3(LM_ATTN_THREADS), 0, in, kc, vc,
                   n_heads, n_kv_heads, max_ctx, n, scale, work);
         QQ_LAUNCH(ctx, lfm2_attn_join_kernel, dim3(n_heads), dim3(LM_HEAD), 0, work, nch, out);
     }

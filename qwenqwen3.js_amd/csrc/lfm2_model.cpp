@@ -61,8 +61,8 @@ struct qq_lfm2 {
     size_t conv_floats = 0;            // per short-conv block: (l_cache - 1) * H
     float *kc = nullptr, *vc = nullptr;
     size_t kv_floats = 0;              // per attention block: n_head_kv * max_ctx * 64
-    float *hidden = nullptr, *ybuf = nullptr, *q = nullptr, *attn = nullptr, *ffn = nullptr,
-          *logits = nullptr;
+    float *hidden = nullptr, *ybuf = nullptr, *q = nullptr, *kraw = nullptr, *attn = nullptr,
+          *ffn = nullptr, *logits = nullptr;
     double *freq = nullptr;
     double *attn_work = nullptr;       // per-chunk attention partials (long contexts)
     std::vector<void *> dev;
@@ -329,9 +329,10 @@ int bind(Binder &B)
     for (const LmLayer &L : m->layers)
         if (L.gate) max_ff = std::max(max_ff, L.gate->out_dim);
     const size_t nq = (size_t)I.n_heads * kHeadDim;
-    float **bufs[] = {&m->hidden, &m->ybuf, &m->q, &m->attn, &m->ffn, &m->logits};
-    const size_t lens[] = {(size_t)H, (size_t)H, nq, nq, (size_t)max_ff, (size_t)I.n_vocab};
-    for (int i = 0; i < 6; i++) {
+    float **bufs[] = {&m->hidden, &m->ybuf, &m->q, &m->kraw, &m->attn, &m->ffn, &m->logits};
+    const size_t lens[] = {(size_t)H, (size_t)H, nq, (size_t)I.n_head_kv * kHeadDim, nq, (size_t)max_ff,
+                           (size_t)I.n_vocab};
+    for (int i = 0; i < 7; i++) {
         if (int rc = B.alloc(lens[i] * 4, &v)) return rc;
         *bufs[i] = static_cast<float *>(v);
     }
@@ -452,6 +453,7 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
             a.norm_w = L.attn_norm;
             a.eps = I.eps;
             a.q = m->q;
+            a.kraw = m->kraw;
             a.kc = kc;
             a.vc = vc;
             a.qn = L.qn;
@@ -462,7 +464,8 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
             a.max_ctx = I.max_ctx;
             a.freq = m->freq;
             if (int rc = qq::launch_lfm2_mv(ctx, qq::LM_QKV, a)) return rc;
-            if (int rc = qq::launch_lfm2_attn(ctx, m->q, kc, vc, I.n_heads, I.n_head_kv, I.max_ctx, position + 1,
+            if (int rc = qq::launch_lfm2_attn(ctx, m->q, m->kraw, L.qn, L.kn, m->freq, I.eps, kc, vc, I.n_heads,
+                                              I.n_head_kv, I.max_ctx, position + 1,
                                               1.0 / std::sqrt((double)kHeadDim), m->attn, m->attn_work))
                 return rc;
             qq::LmLaunch r;

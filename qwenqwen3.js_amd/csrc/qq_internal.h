@@ -200,8 +200,8 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
 size_t grouped_work_bytes(const qq_moe *m, int T);
 
 // LFM2 single-token forward (lfm2.hip).  Matvec modes: y = W x; hidden +=
-// W x; silu(gate x) * (up x); in_proj + short-conv; q/k/v heads with norm,
-// RoPE and the KV-cache store.
+// W x; silu(gate x) * (up x); in_proj + short-conv; raw q and k rows with v
+// stored into the KV cache.
 enum { LM_PLAIN = 0, LM_RESID = 1, LM_SWIGLU = 2, LM_CONV = 3, LM_QKV = 4 };
 struct LmLaunch {
     const float *x = nullptr;
@@ -213,7 +213,7 @@ struct LmLaunch {
     float *state = nullptr;
     const float *kern = nullptr;
     int L = 0, H = 0;
-    float *q = nullptr, *kc = nullptr, *vc = nullptr;
+    float *q = nullptr, *kraw = nullptr, *kc = nullptr, *vc = nullptr;
     const float *qn = nullptr, *kn = nullptr;
     int n_heads = 0, n_kv_heads = 0, pos = 0, max_ctx = 0;
     const double *freq = nullptr;
@@ -222,7 +222,10 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l);
 // Contexts beyond 256 positions run in chunks; `work` holds
 // lfm2_attn_work_bytes(n_heads) of per-chunk partials.
 size_t lfm2_attn_work_bytes(int n_heads);
-int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kc, const float *vc, int n_heads,
+// q and kraw are the raw rows of this call (the attention forms the per-head
+// norms and RoPE and stores the new k row at position n - 1).
+int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kraw, const float *qn, const float *kn,
+                     const double *freq, double eps, float *kc, const float *vc, int n_heads,
                      int n_kv_heads, int max_ctx, int n, double scale, float *out, double *work);
 int launch_lfm2_embed(qq_ctx *ctx, const qq_tensor *t, int token, float *out);
 int launch_lfm2_zero(qq_ctx *ctx, float *p, size_t n);
