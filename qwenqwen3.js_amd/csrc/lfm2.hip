@@ -545,13 +545,26 @@ __global__ __launch_bounds__(LM_HEAD) void lfm2_attn_join_kernel(const double *_
 {
     const int hq = blockIdx.x, d = threadIdx.x;
     const double *pp = part + (size_t)hq * LM_MAX_CHUNKS * LM_PART;
+    // every chunk's values in flight at once, then the join in chunk order
+    double mv[LM_MAX_CHUNKS], lv[LM_MAX_CHUNKS], ov[LM_MAX_CHUNKS];
+#pragma unroll
+    for (int c = 0; c < LM_MAX_CHUNKS; c++) {
+        const int cc = min(c, nchunks - 1);
+        mv[c] = pp[cc * LM_PART + LM_HEAD];
+        lv[c] = pp[cc * LM_PART + LM_HEAD + 1];
+        ov[c] = pp[cc * LM_PART + d];
+    }
     double M = -INFINITY;
-    for (int c = 0; c < nchunks; c++) M = fmax(M, pp[c * LM_PART + LM_HEAD]);
+#pragma unroll
+    for (int c = 0; c < LM_MAX_CHUNKS; c++)
+        if (c < nchunks) M = fmax(M, mv[c]);
     double L = 0.0, O = 0.0;
-    for (int c = 0; c < nchunks; c++) {
-        const double f = exp(pp[c * LM_PART + LM_HEAD] - M);
-        L = L + pp[c * LM_PART + LM_HEAD + 1] * f;
-        O = O + pp[c * LM_PART + d] * f;
+#pragma unroll
+    for (int c = 0; c < LM_MAX_CHUNKS; c++) {
+        if (c >= nchunks) break;
+        const double f = exp(mv[c] - M);
+        L = L + lv[c] * f;
+        O = O + ov[c] * f;
     }
     out[(size_t)hq * LM_HEAD + d] = (float)(O / L);
 }
