@@ -9,7 +9,7 @@ import synth
 import _lfm2
 from _util import gpu_context, rel_l2
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(_lfm2.node() is None, reason="node is not installed")]
 
 TOKENS = [5, 17, 250, 3, 99, 0, 42, 7]
 TOL = 1e-4
