@@ -71,3 +71,37 @@ class _ConvStateNotShifted(_lfm2.F64Model):
 def test_planted_mistakes_are_far_outside(tmp_path, model):
     _, _, _, errs = _run(tmp_path, 3, model=model)
     assert max(errs[1:]) > 1e-3, errs
+
+
+def test_streamed_model_file_equals_in_memory_file(tmp_path):
+    """synth.gguf_write (used for the multi-GB bench model) lays a file out byte for
+    byte as synth.gguf_file does, and the pool-sliced model is well formed."""
+    data, offs, _ = synth.lfm2_gguf(3, synth.LFM2_TINY)
+    path = tmp_path / "s.gguf"
+    _, offs2, _ = synth.lfm2_gguf(3, synth.LFM2_TINY, path=str(path))
+    assert path.read_bytes() == data and offs2 == offs
+    pool = synth.q8_0_pool(1, 1 << 16)
+    _, offs3, tensors = synth.lfm2_gguf(4, synth.LFM2_TINY, path=str(tmp_path / "p.gguf"), pool=pool)
+    for name, shape, typ, arr in tensors:
+        if typ == synth.TYPE_Q8_0:
+            n = shape[2] if len(shape) > 2 else 1
+            assert len(arr) == n * shape[1] * (shape[0] // 32) * 34, name
+
+
+def test_cpu_baseline_bench_mode_runs(tmp_path):
+    """oracle/lfm2_ref.js bench: per-block and head times for the CPU baseline."""
+    import json
+    import os
+    import subprocess
+    cfg = synth.LFM2_TINY
+    path, offs, tensors = _lfm2.write_model(tmp_path, 3, cfg)
+    job = {"gguf": path, "kv": _lfm2.kv_dict(cfg), "tokens": [0], "start": 0,
+           "tensors": {n: {"offset": offs[n], "shape": s, "type": t} for n, s, t, _ in tensors}}
+    jp = tmp_path / "job.json"
+    jp.write_text(json.dumps(job))
+    p = subprocess.run([_lfm2.node(), os.path.join(_lfm2.ROOT, "oracle", "lfm2_ref.js"), "bench", str(jp), "0.2"],
+                       capture_output=True, text=True, timeout=120, check=True)
+    r = json.loads(p.stdout.strip().splitlines()[-1])
+    assert r["tokens"] >= 1 and r["head_ms"] > 0
+    kinds = [b["kind"] for b in r["blocks"]]
+    assert kinds == ["conv+dense", "conv+dense", "attn+moe", "conv+moe", "attn+moe", "conv+moe"]
