@@ -543,9 +543,10 @@ __global__ __launch_bounds__(256) void moe_decode_combine_kernel(
     const int jc = min(j, H - 1);
     // the routing and the residual row are loaded with the partial sums, in
     // the same round trip
-    if (threadIdx.x >= CW && threadIdx.x < CW + K) {
-        sh_e[threadIdx.x - CW] = route_idx[threadIdx.x - CW];
-        sh_w[threadIdx.x - CW] = route_w[threadIdx.x - CW];
+    const int tid = threadIdx.x;
+    if (tid >= CW && tid < CW + K) {
+        sh_e[tid - CW] = route_idx[tid - CW];
+        sh_w[tid - CW] = route_w[tid - CW];
     }
     const float h_in = hidden[jc];
     for (int k0 = 0; k0 < K; k0 += 4) {
