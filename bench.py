@@ -86,10 +86,9 @@ def kernel_bytes(name, T, n_experts):
     exchange (partial sums, grouped rows) are not counted."""
     gate, down = expert_bytes()
     router = E * H * 4 + E * 4
-    if name == "decode_experts":
-        return n_experts * (2 * gate + down) + router + T * H * 4
-    if name == "decode_combine":
-        return 2 * T * H * 4
+    if name == "moe_decode":
+        # experts, router and bias, x, hidden read and written
+        return n_experts * (2 * gate + down) + router + 3 * T * H * 4
     if name == "router_logits":
         return E * H * 4 + T * H * 4
     if name in ("grouped_gateup", "stream_gateup", "mfma_gateup"):
@@ -340,7 +339,7 @@ def run_lfm2(args, torch, ctx, stream):
     LFM2_BYTES["lfm2_attention"] = info["n_head_kv"] * avg_n_prof * 64 * 4 * 2
     LFM2_BYTES["lfm2_embed"] = Hh * q8 + Hh * 4
     n_moe = nl - ndense
-    moe_bytes = n_moe * kernel_bytes("decode_experts", 1, K)
+    moe_bytes = n_moe * kernel_bytes("moe_decode", 1, K)
     avg_n = p0 + (min(args.steps, LFM2_POS) + 1) / 2.0
     kv_bytes = n_attn * info["n_head_kv"] * avg_n * 64 * 4 * 2
     tok_bytes = mv_bytes + moe_bytes + kv_bytes
@@ -383,7 +382,9 @@ def copy_calibration(steps):
 
 
 def _time_steps(torch, ctx, stream, run, steps, warmup):
-    for i in range(warmup):
+    # warm-up steps are the ones just before step 0 in the rotation (-warmup .. -1),
+    # so the first timed steps do not meet the instances the warm-up has touched
+    for i in range(-warmup, 0):
         run(i)
     torch.cuda.synchronize()
     ev0 = torch.cuda.Event(enable_timing=True)

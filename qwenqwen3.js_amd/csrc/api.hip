@@ -65,8 +65,8 @@ int no_capture(qq_ctx *ctx, const char *what)
 }
 
 static const char *const kKernelNames[K_COUNT] = {
-    "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "decode_experts",
-    "decode_combine",   "dispatch",       "grouped_gateup", "grouped_down",  "combine",
+    "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "moe_decode",
+    "dispatch",       "grouped_gateup", "grouped_down",  "combine",
     "cast_f16",         "mfma_gateup",    "mfma_down",      "stream_gateup", "stream_down",
     "rmsnorm", "lfm2_embed", "lfm2_matvec", "lfm2_attention",
 };
@@ -135,12 +135,21 @@ static int tensor_alloc(qq_ctx *ctx, int in_dim, int out_dim, int n_mats, qq_ten
     t->nb = (in_dim + QK - 1) / QK;
     t->kp = t->nb * QK;
     const size_t rows = (size_t)n_mats * out_dim;
+    t->nbp = (t->nb + 7) & ~7;
     t->qs_bytes = rows * t->kp;
     t->d_bytes = rows * t->nb * sizeof(__half);
+    // + 128 bytes: a 16-byte scale load of the last row may start up to 56
+    // blocks past its end (the blocks it covers there are masked)
+    t->dcm_bytes = rows * t->nbp * sizeof(__half) + 128;
     hipError_t e = hipMalloc(&t->qs, t->qs_bytes);
     if (e == hipSuccess) e = hipMalloc(&t->d, t->d_bytes);
+    if (e == hipSuccess) e = hipMalloc(&t->dcm, t->dcm_bytes);
+    // the padding stays zero (same stream as the repack that fills the rest)
+    if (e == hipSuccess) e = hipMemsetAsync(t->dcm, 0, t->dcm_bytes, ctx->stream);
     if (e != hipSuccess) {
         if (t->qs) (void)hipFree(t->qs);
+        if (t->d) (void)hipFree(t->d);
+        if (t->dcm) (void)hipFree(t->dcm);
         delete t;
         return check_hip(ctx, e, "hipMalloc(Q8_0 tensor)");
     }
@@ -194,9 +203,10 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "hipEventCreate");
     }
     void *sync = nullptr;
-    const size_t sync_bytes =
-        ((size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS) *
-            sizeof(uint64_t) + 256;
+    const size_t sync_words = (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS +
+                              (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS + 2 * (size_t)SYNC_H_WORDS +
+                              SYNC_P_WORDS + SYNC_ARRIVE_WORDS;
+    const size_t sync_bytes = sync_words * sizeof(uint64_t) + 512;
     if ((e = hipMalloc(&sync, sync_bytes)) != hipSuccess || (e = hipMemset(sync, 0, sync_bytes)) != hipSuccess) {
         if (sync) (void)hipFree(sync);
         (void)hipEventDestroy(ctx->ev0);
@@ -207,8 +217,13 @@ int qq_init(int device, qq_ctx **out)
     }
     ctx->sync_slots = static_cast<uint64_t *>(sync);
     ctx->sync_local = ctx->sync_slots + SYNC_REPLICAS * SYNC_REPLICA_WORDS;
-    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_local + SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS);
-    ctx->sync_epoch = ctx->sync_err + 16;
+    ctx->sync_hloc = ctx->sync_local + SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS;
+    ctx->sync_hdev = ctx->sync_hloc + SYNC_H_WORDS;
+    ctx->sync_part = ctx->sync_hdev + SYNC_H_WORDS;
+    ctx->sync_arrive = ctx->sync_part + SYNC_P_WORDS;
+    // error word and epoch each on a 128-byte line of their own
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_arrive + SYNC_ARRIVE_WORDS);
+    ctx->sync_epoch = ctx->sync_err + 32;
     ctx->capturing = 0;
     *out = ctx;
     return QQ_OK;
@@ -330,6 +345,7 @@ int qq_tensor_release(qq_ctx *ctx, qq_tensor *t)
     }
     if (t->qs) (void)hipFree(t->qs);
     if (t->d) (void)hipFree(t->d);
+    if (t->dcm) (void)hipFree(t->dcm);
     delete t;
     return QQ_OK;
 }
@@ -476,7 +492,7 @@ static Path chunk_path(const qq_ctx *ctx, const qq_moe *m, int tn, const float *
 
 static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
 {
-    if (decode_supported(m, T)) return align256(decode_work_bytes(m));
+    if (decode_supported(ctx, m, T)) return 0;
     const int Tc = T < T_CHUNK ? T : T_CHUNK;
     size_t work = grouped_work_bytes(m, Tc);
     if (mfma_supported(m)) {
@@ -496,7 +512,7 @@ static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hid
     int rc = ensure_scratch(ctx, base + forward_scratch(ctx, m, T));
     if (rc) return rc;
     char *s = static_cast<char *>(ctx->scratch) + base;
-    if (decode_supported(m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs, s);
+    if (decode_supported(ctx, m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs);
     const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
     double *part = reinterpret_cast<double *>(s);
     int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(router_work_bytes(m, (int)Tc)));
@@ -552,11 +568,9 @@ int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev, con
     MaskBits mb;
     if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
     const NormArgs norm{norm_w_dev, eps};
-    if (decode_supported(m, T)) {
+    if (decode_supported(ctx, m, T)) {
         // every workgroup of the decode kernel normalises the row itself
-        if ((rc = ensure_scratch(ctx, forward_scratch(ctx, m, T)))) return rc;
-        return launch_moe_decode(ctx, m, hidden_dev, hidden_dev, mb, idx_dev, w_dev, probs_dev,
-                                 static_cast<char *>(ctx->scratch), &norm);
+        return launch_moe_decode(ctx, m, hidden_dev, hidden_dev, mb, idx_dev, w_dev, probs_dev, &norm);
     }
     // x = rmsnorm(hidden) at the start of the scratch, then the forward
     const size_t xb = align256((size_t)T * m->H * 4);

@@ -1,685 +1,807 @@
-// decode.hip -- batch-1 decode of one MoE layer in two launches.
+// decode.hip -- batch-1 decode of one MoE layer in one launch.
 //
 // Reference: Lfm2Engine._moEFFN, src/lfm2-engine.js:413-487 (sigmoid + bias
 // gating), and Qwen3Engine._moEFFN, src/qwen3-engine.js:304-363 (softmax
 // gating), for one token.
 //
-// Launch 1 (moe_decode_experts): 8 * ceil(E/8) router workgroups + K*NS
-// expert-unit workgroups (NS = ceil(F/32)).
-//   * router workgroup i (group g = i / 8): binary64 dots of x with router
-//     columns 8g .. 8g+7 (one per wave), fp32 logits, published
-//     as 64-bit words slot[e] = (epoch << 32) | value.  Sigmoid gating
-//     publishes the selection score s_e = fp32(p_e + bias_e) at slot[e] and
-//     p_e = fp32 sigmoid (binary64 math) at slot[SYNC_PROB + e]; softmax
-//     gating publishes the logit at slot[e] (the softmax needs all of them,
-//     so every waiter takes it itself).
-//     Workgroups are dealt to the 8 XCDs round robin, so the 8 copies of a
-//     group land on the 8 XCDs: each writes the table of its own XCD, which
-//     stays in that XCD's L2, and copy 0 also writes SYNC_REPLICAS
-//     device-coherent copies of the table.
-//   * expert-unit workgroup (k, s): stages x in LDS (and its 3-level int8
-//     decomposition), waits in wave 0 (bounded) until all E slots carry this
-//     call's epoch -- polling its XCD's table through L2 first, and the
-//     device-coherent copy u % SYNC_REPLICAS if that has not filled within
-//     DEC_LOCAL_TICKS (so progress never depends on where the dispatcher
-//     placed the router workgroups) -- takes the softmax if asked, ranks the
-//     experts itself (rank of e = number of experts ordered before it by
-//     (score desc, index asc): the order of a stable descending sort;
-//     identical in every workgroup), then streams one F-slice of the rank-k
-//     expert: gate and up rows f in [32s, 32s+32) (2 x 32 rows x H), SwiGLU,
-//     and the matching down block column s (H rows x 32), writing the partial
-//     down product partial[k][s][0..H).  Every weight load is issued before
-//     any arithmetic; dot products use v_dot4_i32_i8.
-//   Value and epoch travel together in one word, so no fence (and no cache
-//   write-back or invalidate) is needed on either side, and every expert has
-//   its own words, so nothing is contended.  The epoch is a device word that
-//   the combine launch of each call advances, so replaying a recorded graph
-//   of decode calls draws a fresh epoch every time.
-//   Workgroup (0, 0) also writes the routing outputs.
-// Launch 2 (moe_decode_combine): y_k = sum_s partial[k][s] in a fixed order,
-//   acc = fp32(acc + w_k * y_k) in rank order, hidden += acc.
+// The grid is G workgroups of 512 threads, one per CU (G = 256 on MI355X),
+// dealt by the dispatcher to the 8 XCDs round robin: workgroup j belongs to
+// group x = j % 8 (its XCD) as member i = j / 8 of M = G / 8.  Each group
+// runs the whole layer for its own eighth of the F features:
 //
-// Nothing waits on another workgroup except on the router slots, and the
-// router workgroups have the lowest ids, so they are dispatched first and never
-// wait themselves.  The wait is bounded by the wall clock; on expiry the
-// workgroup sets the context's error word and returns.
+//  1. Routing.  Member i forms the binary64 router dots of experts i, i + M,
+//     ... with x (forming x = rmsnorm(hidden) first when asked) and publishes
+//     the fp32 logits in its group's table; every workgroup waits for the E
+//     logits of its own table, takes the sigmoid + bias (or softmax) scores
+//     and ranks the experts itself (stable descending order, ties to the
+//     lower index), so every workgroup holds the same idx[K], p[K], w[K].
+//  2. Gate/up.  Group x owns F blocks [x nbF / 8, (x + 1) nbF / 8) of all K
+//     selected experts; its (rank, feature) columns are split evenly over the
+//     members (28 each at H=2048, F=1792, K=4).  A member issues every weight
+//     load of its share at once -- its gate and up columns and the down rows
+//     it needs in step 3 -- takes v_dot4 products of the int8 weights against
+//     a 3-level int8 split of x, SwiGLU, and publishes its h values.
+//  3. Down.  Every member waits for its group's h values (K x F/8), then
+//     forms the partial down products of its M-th of the H rows over the
+//     group's F blocks from the down weights already in its registers, and
+//     publishes them.
+//  4. Combine.  Workgroup j finishes rows [j H/G, (j+1) H/G): y_k = sum of the
+//     8 groups' partials in group order, acc = fp32(acc + w_k y_k) in rank
+//     order, hidden += acc.
+//
+// Every exchange is a table of 64-bit words (tag << 32) | value bits, written
+// once per call, so a reader knows a word is this call's from the word
+// itself: no fences, no cache write-back or invalidation.  The routing and h
+// tables of a group are written with workgroup-scope stores, which stay in
+// that XCD's L2, and read with device-scope loads that the L2 answers in about
+// 0.2 us; every word also goes to a device-coherent copy, which a reader falls
+// back to after DEC_LOCAL_TICKS (so progress never depends on where the
+// dispatcher put a workgroup).  Partials go to device-coherent words only.
+//
+// The tag of a call is the device epoch word + 1.  Every workgroup reads the
+// epoch first thing and publishes an arrival word once it has read the epoch,
+// x and hidden.  Workgroup 0 advances the epoch after its final wait, which
+// covers all G arrival words, so every workgroup has read the old epoch by
+// then.  A replayed graph of decode launches so draws a fresh tag every time.
+//
+// A workgroup writes its hidden rows only after all G arrival words carry the
+// tag, so hidden may be the input row itself (the fused ffn_norm).
+//
+// All G workgroups must be resident at once (one per CU; nothing else on the
+// device keeps a CU busy for long).  Every wait is bounded by the wall clock;
+// on expiry the workgroup sets the context's error word and skips the rest.
 #include "qq_device.h"
 
 namespace qq {
 
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * WAVE;
+constexpr int DEC_GROUPS = 8;                  // one per XCD
 constexpr uint64_t DEC_WAIT_TICKS = 5000000;   // 50 ms at the 100 MHz wall clock
-constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the XCD's own table, then the copies
-constexpr int RT_EPW = 8;                      // experts per router workgroup (one per wave)
-constexpr int RT_COPIES = 8;                   // router workgroups per expert group
-static_assert(RT_EPW == DEC_WAVES && RT_EPW * 8 == WAVE, "router lane layout");
-static_assert(MAX_E <= 4 * WAVE, "at most four experts per lane");
-
-// XCD (accelerator complex die) this wave runs on.
-__device__ __forceinline__ uint32_t xcc_id()
-{
-    uint32_t x;
-    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 4)" : "=s"(x));
-    return x;
-}
-
+constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the group's own table, then the copy
+constexpr int DEC_CCH = 32;                    // gate/up columns per chunk (two lanes each)
+constexpr int DEC_DCH = 8;                     // down loads per lane
+static_assert(DEC_THREADS == NORM_THREADS, "the decode kernel normalises like rmsnorm_kernel");
 
 struct DecodeArgs {
     const float *x;       // the MoE input, or the residual row when norm
     int norm;             // x = rmsnorm(x) * norm_w is formed in every workgroup
     const float *norm_w;  // NULL: unit weight
     double eps;
+    float *hidden;
     int H, F, E, K;
-    int nbH, nbF, NS;
-    const float *rf32;
-    const int8_t *rq;
+    int nbH, nbF;
+    const float *rf32;    // F32 router [E][H], or
+    const int8_t *rq;     // Q8_0 router (block-major)
     const __half *rd;
     int router_q8;
-    int router_vec4;      // F32 router, H % 4 == 0
-    int n_router;         // router workgroups: RT_COPIES * ceil(E / RT_EPW)
-    int softmax;          // Qwen3-MoE gating: routers publish logits, waiters take the softmax
+    int softmax;          // Qwen3-MoE gating
     const float *bias;
     const int8_t *gq;
-    const __half *gd;
+    const __half *gdcm;   // gate/up scales row by row (qq_tensor.dcm), nbpH per row
     const int8_t *uq;
-    const __half *ud;
+    const __half *udcm;
+    int nbpH;
     const int8_t *dq;
-    const __half *dd;
+    const __half *dd;     // down scales, block-major
     MaskBits mask;
-    const uint32_t *epoch_word;   // this call's epoch is *epoch_word + 1
-    // Slot tables, persistent across calls, each [0, E) epoch << 32 | selection
-    // score bits (softmax gating: logit bits), [SYNC_PROB, SYNC_PROB + E)
-    // epoch << 32 | probability bits (sigmoid gating only):
-    //   slots: SYNC_REPLICAS device-coherent copies, SYNC_REPLICA_WORDS apart;
-    //   local: one table per XCD (SYNC_LOCAL_WORDS apart), kept in that XCD's L2
-    uint64_t *slots;
-    uint64_t *local;
-    float *partial;       // [K][NS][H]
-    int32_t *route_idx;   // [K]
-    double *route_w;      // [K]
+    uint32_t *epoch_word;
+    // exchange tables (tag << 32 | bits):
+    uint64_t *rloc;       // per group: router logits [SYNC_LOCAL_WORDS apart]
+    uint64_t *rdev;       // SYNC_REPLICAS device-coherent copies of group 0's
+    uint64_t *hloc;       // h values [K][F] (each group writes its own features)
+    uint64_t *hdev;       // device-coherent copy
+    uint64_t *part;       // partial down sums [8][K][H], device-coherent
+    uint64_t *arrive;     // [G]
     int32_t *out_idx;     // optional outputs
     double *out_w;
     float *out_probs;
     uint32_t *err;
 };
 
-// Bounded wait until words [0, E) of a slot table carry `epoch` (lane l
-// holds words l, l + 64, ...: EPL of them); returns them in v.  Polls the
-// XCD's own table (`loc`) while `use_loc` and for DEC_LOCAL_TICKS, then the
-// device-coherent copy `glob`; use_loc tells on return which table answered.
-// Both are device-scope loads: for a line written from the same XCD one is
-// answered by that XCD's L2 in about 0.2 us, against about 1-2 us for a line
-// written from another XCD.
-template <int EPL>
-__device__ __forceinline__ void wait_slots(const uint64_t *loc, const uint64_t *glob, int E,
-                                           uint32_t epoch, int lane, int &ok, bool &use_loc,
-                                           uint64_t (&v)[EPL])
+__device__ __forceinline__ uint64_t tag_word(uint32_t tag, float v)
 {
-    const uint64_t t0 = wall_clock64();
-    while (true) {
-        bool all = true;
+    return ((uint64_t)tag << 32) | __float_as_uint(v);
+}
+
+__device__ __forceinline__ void store_local(uint64_t *p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__device__ __forceinline__ void store_dev(uint64_t *p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Bounded wait of the first NT threads for their words: thread t polls the
+// words of its items s < IPT with want[s] (loads issued together, each wave
+// on its own with wave votes), at pl[s] -- its group's table -- and after
+// DEC_LOCAL_TICKS at pd[s], the device-coherent copy (pd[s] = pl[s] when
+// there is none).  Once a word carries `tag` its low half goes to *dst[s]
+// (LDS; NULL: not kept).  The item addresses are worked out by the caller
+// once, so a poll round is only loads and compares.  The other waves go
+// straight to the closing barrier.  (Stores count in the same in-order
+// counter as loads here, so a wave that has just written device-scope words
+// would wait for their acknowledgement before every poll: the waves that
+// publish are kept out of the waits that follow.)  Returns false (in every
+// thread) when some wave's wait expired.
+template <int NT, int IPT>
+__device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uint64_t *(&pl)[IPT],
+                                           const uint64_t *(&pd)[IPT], bool (&want)[IPT],
+                                           float *(&dst)[IPT])
+{
+    bool fail = false;
+    if ((int)threadIdx.x < NT) {
+        const uint64_t t0 = wall_clock64();
+        bool loc = true;
+        while (true) {
+            uint64_t v[IPT];
 #pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            const int e = lane + WAVE * j;
-            if (e < E)
-                v[j] = __hip_atomic_load(use_loc ? &loc[e] : &glob[e], __ATOMIC_RELAXED,
-                                         __HIP_MEMORY_SCOPE_AGENT);
-            else
-                v[j] = (uint64_t)epoch << 32;
-            all = all && (uint32_t)(v[j] >> 32) == epoch;
+            for (int s = 0; s < IPT; s++)
+                v[s] = want[s] ? __hip_atomic_load(loc ? pl[s] : pd[s], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                               : 0;
+            bool mine = true;
+#pragma unroll
+            for (int s = 0; s < IPT; s++) {
+                if (!want[s]) continue;
+                if ((uint32_t)(v[s] >> 32) == tag) {
+                    want[s] = false;
+                    if (dst[s]) *dst[s] = __uint_as_float((uint32_t)v[s]);
+                } else {
+                    mine = false;
+                }
+            }
+            if (__all(mine)) break;
+            const uint64_t dt = wall_clock64() - t0;
+            if (dt > DEC_LOCAL_TICKS) loc = false;
+            if (dt > DEC_WAIT_TICKS) {
+                fail = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
         }
-        if (__all(all)) break;
-        const uint64_t dt = wall_clock64() - t0;
-        if (dt > DEC_LOCAL_TICKS) use_loc = false;
-        if (dt > DEC_WAIT_TICKS) {
-            ok = 0;
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
+    }
+    if (fail) *sh_fail = 1;
+    lds_barrier();
+    return *sh_fail == 0;
+}
+
+// 16-value chunks of the LDS row v[0, 16 * nch) -> three int8 levels and the
+// chunk scale, four lanes a chunk (lane 4c + q takes values 16c + 4q ..).
+__device__ __forceinline__ void decompose_row(const float *v, int nch, int4 *q1, int4 *q2, int4 *q3,
+                                              float *sig)
+{
+    for (int t = threadIdx.x; t < 4 * nch; t += DEC_THREADS) {
+        const float4 f = reinterpret_cast<const float4 *>(v)[t];
+        float m = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w)));
+        m = fmaxf(m, xor1_dpp(m));
+        m = fmaxf(m, xor2_dpp(m));
+        const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
+        uint32_t p1, p2, p3;
+        decompose4(f, inv, p1, p2, p3);
+        reinterpret_cast<uint32_t *>(q1)[t] = p1;
+        reinterpret_cast<uint32_t *>(q2)[t] = p2;
+        reinterpret_cast<uint32_t *>(q3)[t] = p3;
+        if ((t & 3) == 0) sig[t >> 2] = m * (1.0f / 127.0f);
     }
 }
 
-// NBW = blocks of H per wave (and 32-row chunks of H per wave) = ceil(ceil(H/32)/8);
-// EPL = experts per lane of the waiting waves (1: E <= 64, 2: E <= 128, 4: E <= 256).
-template <int NBW, int EPL>
-__global__ __launch_bounds__(DEC_THREADS) void moe_decode_experts_kernel(DecodeArgs a)
+__device__ __forceinline__ float f16_bits(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
+
+// q / d for 0 <= q < 2^20 and 1 <= d < 2^12 without an integer division:
+// the float product is within 2^-9 of the quotient, which is never that close
+// to the next integer.
+__device__ __forceinline__ int div_small(int q, float inv_d) { return (int)(((float)q + 0.5f) * inv_d); }
+
+// The NBW consecutive fp16 scales at p (2 NBW bytes, aligned to that size)
+// in one load: element i is (s[i / 2] >> 16 (i % 2)) & 0xffff.
+template <int NBW>
+struct ScaleRun {
+    uint32_t s[(NBW + 1) / 2];
+    __device__ __forceinline__ void load(const __half *p)
+    {
+        if constexpr (NBW == 8) {
+            const uint4 v = *reinterpret_cast<const uint4 *>(p);
+            s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
+        } else if constexpr (NBW == 4) {
+            const uint2 v = *reinterpret_cast<const uint2 *>(p);
+            s[0] = v.x; s[1] = v.y;
+        } else if constexpr (NBW == 2) {
+            s[0] = *reinterpret_cast<const uint32_t *>(p);
+        } else {
+            s[0] = *reinterpret_cast<const uint16_t *>(p);
+        }
+    }
+    __device__ __forceinline__ float get(int i) const { return f16_bits(s[i / 2] >> (16 * (i % 2))); }
+};
+
+// Limits of one launch (checked by decode_supported on the host).
+constexpr int DEC_MAX_HW = 2048;               // h values of one group (K x F-range)
+constexpr int DEC_MAX_RED = 4096;              // K x F blocks of a group x down rows of a member
+constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read by one workgroup
+
+// NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
+// experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64)).
+template <int NBW, int RE, int EPL>
+__global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 {
     constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
-    constexpr int NHB = XN / 16;                // 16-value chunks
+    constexpr int NHB = XN / 16;                // 16-value chunks of x
+    constexpr int XPT = (XN + DEC_THREADS - 1) / DEC_THREADS;
     __shared__ __align__(16) float xl[XN];
     __shared__ __align__(16) int4 xq1[NHB], xq2[NHB], xq3[NHB];
     __shared__ float xsig[NHB];
-    __shared__ __align__(16) float gl[QK];
-    __shared__ __align__(16) int4 gq1[2], gq2[2], gq3[2];
-    __shared__ float gsig[2];
-    __shared__ float redg[DEC_WAVES][QK];
-    __shared__ float redu[DEC_WAVES][QK];
-    __shared__ double rsum[DEC_WAVES];
-    __shared__ int sh_ok;
-    __shared__ int rank_part[DEC_WAVES][EPL * WAVE];
-    __shared__ int sh_rank_e[MAX_K];
-    __shared__ float sh_rank_p[MAX_K];
-    __shared__ __align__(16) float sh_score[EPL * WAVE];
-    __shared__ float sh_prob[EPL * WAVE];
+    __shared__ double rsum[RE][DEC_WAVES];
+    __shared__ double nsum[DEC_WAVES];
+    __shared__ float sh_lg[EPL * WAVE];
+    __shared__ int sh_idx[DEC_WAVES][MAX_K];     // each wave's own copy of the routing
+    __shared__ __align__(16) float sh_pr[DEC_WAVES][MAX_K];
+    __shared__ double sh_w[DEC_WAVES][MAX_K];
+    __shared__ __align__(16) uint64_t sh_key[DEC_WAVES][32 * RE];
+    __shared__ float redg[DEC_WAVES][DEC_CCH];
+    __shared__ float redu[DEC_WAVES][DEC_CCH];
+    __shared__ __align__(16) float hl[DEC_MAX_HW];
+    __shared__ __align__(16) int4 hq1[DEC_MAX_HW / 16], hq2[DEC_MAX_HW / 16], hq3[DEC_MAX_HW / 16];
+    __shared__ float hsig[DEC_MAX_HW / 16];
+    __shared__ float redd[DEC_MAX_RED];
+    __shared__ float pf[DEC_MAX_FIN];
+    __shared__ uint32_t sh_tag;
+    __shared__ int sh_fail;
 
-    const int lane = threadIdx.x & (WAVE - 1);
-    const int wave = threadIdx.x / WAVE;
-    // advanced by the previous call's combine kernel, so identical in every workgroup
-    const uint32_t epoch = a.epoch_word[0] + 1u;
+    const int tid = threadIdx.x;
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
+    const int G = gridDim.x;
+    const int j = blockIdx.x;
+    const int gx = j % DEC_GROUPS;   // group (XCD)
+    const int mi = j / DEC_GROUPS;   // member
+    const int M = G / DEC_GROUPS;
+    const uint16_t *dd16 = reinterpret_cast<const uint16_t *>(a.dd);
 
-    const bool router = (int)blockIdx.x < a.n_router;
-    // router workgroup i: experts 8g .. 8g + 7 of group g = i / RT_COPIES, one a wave
-    const int e_r = min((int)(blockIdx.x / RT_COPIES) * RT_EPW + wave, a.E - 1);
-    const int H4 = a.H >> 2;
-    float4 rw[NBW];
-    if (router && a.router_vec4) {
-        // issued before x is staged; columns past H meet the zero padding of xl
-        const float4 *w4 = reinterpret_cast<const float4 *>(a.rf32) + (size_t)e_r * H4;
+    // ---- every load of the routing phase, unconditional (clamped addresses) ----
+    const uint32_t epoch = __hip_atomic_load(a.epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // rows this workgroup finishes, and their residual values
+    const int RF = (a.H + G - 1) / G;
+    const int q0 = j * RF;
+    const int RFm = max(min(RF, a.H - q0), 0);
+    const float hin = a.hidden[min(q0 + tid, a.H - 1)];
+    float xv[XPT], wv[XPT];
+    const float *nw = a.norm_w ? a.norm_w : a.x;
 #pragma unroll
-        for (int i = 0; i < NBW; i++) rw[i] = w4[min(lane + WAVE * i, H4 - 1)];
+    for (int s = 0; s < XPT; s++) {
+        const int k = min(tid + DEC_THREADS * s, a.H - 1);
+        xv[s] = a.x[k];
+        wv[s] = nw[k];
+    }
+    // router rows of this member's experts e = mi + M t (F32 router)
+    float rw[RE][XPT];
+    if (!a.router_q8) {
+#pragma unroll
+        for (int t = 0; t < RE; t++) {
+            const int e = min(mi + M * t, a.E - 1);
+#pragma unroll
+            for (int s = 0; s < XPT; s++)
+                rw[t][s] = a.rf32[(size_t)e * a.H + min(tid + DEC_THREADS * s, a.H - 1)];
+        }
+    }
+    // selection bias of experts lane, lane + 64, ...
+    float bias_l[EPL];
+#pragma unroll
+    for (int t = 0; t < EPL; t++) bias_l[t] = a.bias[min(lane + WAVE * t, a.E - 1)];
+#pragma unroll
+    for (int s = 0; s < XPT; s++) {
+        const bool in = tid + DEC_THREADS * s < a.H;
+        xv[s] = in ? xv[s] : 0.0f;
+        wv[s] = (in && a.norm_w) ? wv[s] : 1.0f;
     }
 
     // ---- x -> LDS (ffn_norm first when asked: lfm2-engine.js:251-252) ----
-    {
-        static_assert(DEC_THREADS == NORM_THREADS, "the decode kernel normalises like rmsnorm_kernel");
-        constexpr int XPT = (XN + DEC_THREADS - 1) / DEC_THREADS;
-        float xv[XPT];
+    if (a.norm) {
+        double ss = 0.0;   // padding adds exact zeros
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int k = threadIdx.x + DEC_THREADS * i;
-            xv[i] = (k < a.H) ? a.x[k] : 0.0f;
-        }
-        if (a.norm) {
-            float wv[XPT];
+        for (int s = 0; s < XPT; s++) ss = fma((double)xv[s], (double)xv[s], ss);
+        const double inv = rms_inv(block_sum_f64<DEC_WAVES>(ss, nsum), a.H, a.eps);
 #pragma unroll
-            for (int i = 0; i < XPT; i++) {
-                const int k = threadIdx.x + DEC_THREADS * i;
-                wv[i] = (a.norm_w && k < a.H) ? a.norm_w[k] : 1.0f;
-            }
-            double ss = 0.0;   // padding adds exact zeros
-#pragma unroll
-            for (int i = 0; i < XPT; i++) ss = fma((double)xv[i], (double)xv[i], ss);
-            const double inv = rms_inv(block_sum_f64<DEC_WAVES>(ss, rsum), a.H, a.eps);
-#pragma unroll
-            for (int i = 0; i < XPT; i++) xv[i] = (float)((double)wv[i] * (double)xv[i] * inv);
-        }
-#pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int k = threadIdx.x + DEC_THREADS * i;
-            if (k < XN) xl[k] = xv[i];
-        }
+        for (int s = 0; s < XPT; s++) xv[s] = (float)((double)wv[s] * (double)xv[s] * inv);
     }
-    __syncthreads();
-
-    if (router) {
-        // ---- router workgroup: logits, then sigmoid and scores or softmax
-        // logits (lfm2-engine.js:418-431; qwen3-engine.js:306-307) ----
-        // Workgroup i runs on XCD i % 8 (the dispatcher deals workgroups to the
-        // XCDs round robin), so each XCD gets a full set of router workgroups
-        // and its table fills from its own L2.  Nothing depends on that for
-        // correctness: copy 0 of each group also fills the device-coherent
-        // tables, which waiters fall back to.
-        double acc = 0.0;
-        if (a.router_vec4) {
-            // four independent chains (one per float4 component), then joined
-            const float4 *x4 = reinterpret_cast<const float4 *>(xl);
-            double ax = 0.0, ay = 0.0, az = 0.0, aw = 0.0;
 #pragma unroll
-            for (int i = 0; i < NBW; i++) {
-                const float4 xv = x4[lane + WAVE * i];
-                ax = fma((double)xv.x, (double)rw[i].x, ax);
-                ay = fma((double)xv.y, (double)rw[i].y, ay);
-                az = fma((double)xv.z, (double)rw[i].z, az);
-                aw = fma((double)xv.w, (double)rw[i].w, aw);
+    for (int s = 0; s < XPT; s++) {
+        const int k = tid + DEC_THREADS * s;
+        if (k < XN) xl[k] = xv[s];
+    }
+    // ---- router dots (lfm2-engine.js:418, tensor.js:469-482): exact products, binary64 sums ----
+    const int re = (a.E > mi) ? (a.E - mi + M - 1) / M : 0;
+#pragma unroll
+    for (int t = 0; t < RE; t++) {
+        double acc = 0.0;
+        if (a.router_q8) {
+            const int e = min(mi + M * t, a.E - 1);
+#pragma unroll
+            for (int s = 0; s < XPT; s++) {
+                const int k = min(tid + DEC_THREADS * s, a.H - 1);
+                const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e);
+                acc = fma((double)xv[s], (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]), acc);
             }
-            acc = (ax + ay) + (az + aw);
         } else {
-            for (int k = lane; k < a.H; k += WAVE) {
-                double wv;
-                if (a.router_q8) {
-                    const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e_r);
-                    wv = (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]);
-                } else {
-                    wv = (double)a.rf32[(size_t)e_r * a.H + k];
-                }
-                acc = fma((double)xl[k], wv, acc);
-            }
+#pragma unroll
+            for (int s = 0; s < XPT; s++) acc = fma((double)xv[s], (double)rw[t][s], acc);
         }
         acc = wave_sum_dpp(acc);
-        if (lane == 0) rsum[wave] = acc;
-        __syncthreads();
-        if (wave == 0) {
-            // lane = 8 q + r: expert 8g + q; copies r and r + 8 of the device table
-            const int q = lane >> 3, r = lane & 7;
-            const int e = (blockIdx.x / RT_COPIES) * RT_EPW + q;
-            if (e < a.E) {
-                const float logit = (float)rsum[q];
-                // sigmoid gating: probability and selection score; softmax
-                // gating: the logit (the softmax needs all of them and is taken
-                // by every waiter)
-                float p = 0.0f, sc = logit;
-                if (!a.softmax) {
-                    p = (float)(1.0 / (1.0 + exp(-(double)logit)));
-                    sc = p + a.bias[e];
-                }
-                const uint64_t ep = (uint64_t)epoch << 32;
-                uint64_t *ltab = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
-                if (r == 0) {
-                    if (!a.softmax)
-                        __hip_atomic_store(&ltab[SYNC_PROB + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                    __hip_atomic_store(&ltab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-                }
-                if (blockIdx.x % RT_COPIES == 0) {
+        if (lane == 0) rsum[t][wave] = acc;
+    }
+    if (tid == 0) {
+        sh_tag = epoch + 1u;
+        sh_fail = 0;
+    }
+    lds_barrier();
+    const uint32_t tag = sh_tag;
+    // the last wave publishes (arrival: x and hidden have been read; the
+    // router logits); waves 0..3 poll
+    constexpr int PUB = (DEC_WAVES - 1) * WAVE;
+    if (tid == PUB) store_dev(&a.arrive[j], (uint64_t)tag << 32);
+    if (tid >= PUB && tid - PUB < re) {
+        const int t = tid - PUB;
+        const int e = mi + M * t;
+        double s = rsum[t][0];
 #pragma unroll
-                    for (int c = r; c < SYNC_REPLICAS; c += 8) {
-                        uint64_t *tab = a.slots + (size_t)c * SYNC_REPLICA_WORDS;
-                        if (!a.softmax)
-                            __hip_atomic_store(&tab[SYNC_PROB + e], ep | __float_as_uint(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                        __hip_atomic_store(&tab[e], ep | __float_as_uint(sc), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    }
-                }
-            }
+        for (int w = 1; w < DEC_WAVES; w++) s = s + rsum[t][w];
+        const uint64_t word = tag_word(tag, (float)s);
+        store_local(&a.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
+        if (gx == 0) {
+#pragma unroll
+            for (int c = 0; c < SYNC_REPLICAS; c++) store_dev(&a.rdev[(size_t)c * SYNC_REPLICA_WORDS + e], word);
         }
-        return;
+    }
+    // x -> three int8 levels for the v_dot4 products
+    decompose_row(xl, NHB, xq1, xq2, xq3, xsig);
+
+    bool ok;
+    {
+        const uint64_t *pl[1] = {&a.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, a.E - 1)]};
+        const uint64_t *pd[1] = {&a.rdev[(size_t)(j % SYNC_REPLICAS) * SYNC_REPLICA_WORDS + min(tid, a.E - 1)]};
+        bool want[1] = {tid < a.E};
+        float *dst[1] = {&sh_lg[min(tid, EPL * WAVE - 1)]};
+        ok = block_wait<4 * WAVE, 1>(tag, &sh_fail, pl, pd, want, dst);
     }
 
-    const int unit = blockIdx.x - a.n_router;
-    const uint64_t *tab = a.slots + (size_t)(unit % SYNC_REPLICAS) * SYNC_REPLICA_WORDS;
-    const uint64_t *loc = a.local + (size_t)xcc_id() * SYNC_LOCAL_WORDS;
-    const int kslot = unit / a.NS;
-    const int s = unit - kslot * a.NS;
-
-    // ---- x -> three int8 levels, four lanes per 16-value chunk ----
-    // (whole waves take part: 4 * NHB is a multiple of 64)
-    for (int t = threadIdx.x; t < 4 * NHB; t += DEC_THREADS) {
-        const float4 v = reinterpret_cast<const float4 *>(xl)[t];   // x[4t .. 4t+3]
-        float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-        m = fmaxf(m, __shfl_xor(m, 1, WAVE));
-        m = fmaxf(m, __shfl_xor(m, 2, WAVE));
-        const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
-        uint32_t p1, p2, p3;
-        decompose4(v, inv, p1, p2, p3);
-        reinterpret_cast<uint32_t *>(xq1)[t] = p1;
-        reinterpret_cast<uint32_t *>(xq2)[t] = p2;
-        reinterpret_cast<uint32_t *>(xq3)[t] = p3;
-        if ((t & 3) == 0) xsig[t >> 2] = m * (1.0f / 127.0f);
-    }
-
-    // ---- routing (lfm2-engine.js:433-447; qwen3-engine.js:306-321) ----
-    bool use_loc = true;
-    if (wave == 0) {
-        int ok = 1;
-        uint64_t v[EPL];
-        wait_slots<EPL>(loc, tab, a.E, epoch, lane, ok, use_loc, v);
-        if (a.softmax) {
-            // every workgroup takes the same softmax of the same logits
-            float lg[EPL], pr[EPL];
+    // ---- this workgroup's share (independent of the routing) ----
+    const int fb0 = gx * a.nbF / DEC_GROUPS, fb1 = (gx + 1) * a.nbF / DEC_GROUPS;
+    const int FRb = fb1 - fb0;                        // F blocks of the group (<= 8)
+    const int f0 = fb0 * QK;
+    const int FR = max(min(fb1 * QK, a.F) - f0, 0);   // features of the group
+    const float inv_fr = 1.0f / (float)max(FR, 1);
+    const float inv_frb = 1.0f / (float)max(FRb, 1);
+    const int NC = a.K * FR;                          // its (rank, feature) columns
+    const int CPM = (NC + M - 1) / M;
+    const int c0 = mi * CPM;
+    const int nc = max(min(CPM, NC - c0), 0);         // this member's columns (<= 32)
+    const int RM = (a.H + M - 1) / M;                 // down rows per member (<= 64)
+    const int r0 = mi * RM;
+    const int RMm = max(min(RM, a.H - r0), 0);
+    const int NRH = RM > 32 ? 2 : 1;                  // 32-row halves of the member's rows
+    const int RMP = NRH * 32;
+    const int NP2 = (FRb > 0 && RMm > 0) ? a.K * NRH : 0;   // (rank, row half) pairs
+    const int PPW = (NP2 + DEC_WAVES - 1) / DEC_WAVES;      // pairs per wave
+    const int NUW = PPW * FRb;                               // down units per lane (<= 8)
+    const int hh = lane & 1;
+    const int cs = lane >> 1;
+    // gate/up: lane 2c + h takes column c0 + c (lanes past the member's
+    // columns repeat its last one: no extra lines), bytes 16h .. 16h + 15 of
+    // blocks NBW w .. NBW w + NBW - 1; row offsets within an expert
+    const int cl = c0 + max(min(cs, nc - 1), 0);
+    const int ck = (nc > 0) ? div_small(cl, inv_fr) : 0;   // rank of the column
+    const int cf = (nc > 0) ? f0 + cl - ck * FR : 0;        // feature
+    uint32_t goff[NBW];
 #pragma unroll
-            for (int j = 0; j < EPL; j++) lg[j] = __uint_as_float((uint32_t)v[j]);
+    for (int i = 0; i < NBW; i++) goff[i] = (uint32_t)(min(NBW * wave + i, a.nbH - 1) * a.F + cf);
+    // down: wave w takes the (rank, row half) pairs w, w + 8 over the group's
+    // blocks, lane 2r + h row r of the half; row offsets within an expert
+    uint32_t doff[DEC_DCH];
+    bool dsec[DEC_DCH];   // unit of the second pair
+#pragma unroll
+    for (int i = 0; i < DEC_DCH; i++) {
+        const int t = min(div_small(i, inv_frb), 1);
+        const int bl = min(i - t * FRb, max(FRb - 1, 0));
+        const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
+        const int rh = (NRH == 2) ? (p & 1) : 0;
+        const int rl = min(rh * 32 + cs, max(RMm - 1, 0));
+        doff[i] = (uint32_t)(min(fb0 + bl, a.nbF - 1) * a.H + min(r0 + rl, a.H - 1));
+        dsec[i] = t != 0;
+    }
+    int pk2[2];   // ranks of this wave's two pairs
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
+        pk2[t] = min((NRH == 2) ? (p >> 1) : p, a.K - 1);
+    }
+
+    // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321), taken by
+    // every wave on its own (no workgroup barrier): scores, then the rank of
+    // each expert among them -- a stable descending sort, ties to the lower
+    // index -- from 64-bit keys (order-preserving score bits, complemented
+    // index), then the top K ----
+    constexpr int SLOTS = 32 * RE;   // >= E
+    float pr[EPL];
+    uint32_t mrank = 0;   // bit k: the rank-k expert is masked (lfm2-engine.js:464)
+    if (ok) {
+        float lg[EPL];
+#pragma unroll
+        for (int t = 0; t < EPL; t++) lg[t] = sh_lg[min(lane + WAVE * t, a.E - 1)];
+        if (a.softmax) {
             softmax_probs<EPL>(lg, a.E, pr);
-#pragma unroll
-            for (int j = 0; j < EPL; j++) {
-                const int e = lane + WAVE * j;
-                sh_score[e] = (e < a.E) ? pr[j] : -INFINITY;
-                sh_prob[e] = pr[j];
-            }
         } else {
 #pragma unroll
-            for (int j = 0; j < EPL; j++) {
-                const int e = lane + WAVE * j;
-                sh_score[e] = (e < a.E) ? __uint_as_float((uint32_t)v[j]) : -INFINITY;
+            for (int t = 0; t < EPL; t++) pr[t] = (float)(1.0 / (1.0 + exp(-(double)lg[t])));
+        }
+        uint64_t key[EPL];
+#pragma unroll
+        for (int t = 0; t < EPL; t++) {
+            const int e = lane + WAVE * t;
+            const float sc = (a.softmax ? pr[t] : pr[t] + bias_l[t]) + 0.0f;   // -0 -> +0
+            const uint32_t u = __float_as_uint(sc);
+            const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+            key[t] = (e < a.E) ? (((uint64_t)ord << 32) | (uint32_t)~e) : 0;
+            if (e < SLOTS) sh_key[wave][e] = key[t];
+        }
+        int rank[EPL];
+#pragma unroll
+        for (int t = 0; t < EPL; t++) rank[t] = 0;
+#pragma unroll 16
+        for (int u = 0; u < SLOTS / 2; u++) {
+            const ulonglong2 q = reinterpret_cast<const ulonglong2 *>(sh_key[wave])[u];
+#pragma unroll
+            for (int t = 0; t < EPL; t++) rank[t] += (int)(q.x > key[t]) + (int)(q.y > key[t]);
+        }
+#pragma unroll
+        for (int t = 0; t < EPL; t++) {
+            const int e = lane + WAVE * t;
+            if (e < a.E && rank[t] < a.K) {
+                sh_idx[wave][rank[t]] = e;
+                sh_pr[wave][rank[t]] = pr[t];
             }
         }
-        if (lane == 0) {
-            sh_ok = ok;
-            if (!ok) atomicOr(a.err, 1u);
-        }
+        const uint64_t mb = __ballot(lane < a.K && mask_has(a.mask, sh_idx[wave][min(lane, MAX_K - 1)]));
+        mrank = (uint32_t)mb;
     }
-    __syncthreads();
-    if (!sh_ok) return;
-    // rank of expert e = lane + 64j: experts ordered before it by (score
-    // desc, index asc), so the rank-k expert is the k-th element of a stable
-    // descending sort.  Wave w counts over slots 8*EPL*w .. 8*EPL*(w+1) - 1
-    // (slots >= E hold -inf and never rank before a real expert); every wave
-    // then sums the counts.
-    {
-        constexpr int NQ = 2 * EPL;   // float4 reads of the wave's 8*EPL slots
-        float qq[4 * NQ];
-#pragma unroll
-        for (int u = 0; u < NQ; u++) {
-            const float4 q4 = reinterpret_cast<const float4 *>(sh_score)[NQ * wave + u];
-            qq[4 * u] = q4.x;
-            qq[4 * u + 1] = q4.y;
-            qq[4 * u + 2] = q4.z;
-            qq[4 * u + 3] = q4.w;
-        }
-#pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            const int e = lane + WAVE * j;
-            const float sc = sh_score[e];
-            int part = 0;
-#pragma unroll
-            for (int u = 0; u < 4 * NQ; u++) {
-                const int i = 4 * NQ * wave + u;
-                part += (int)(qq[u] > sc) | ((int)(qq[u] == sc) & (int)(i < e));
-            }
-            rank_part[wave][e] = part;
-        }
-    }
-    __syncthreads();
-    int rank[EPL];
-    int e = -1;
-#pragma unroll
-    for (int j = 0; j < EPL; j++) {
-        rank[j] = 0;
-#pragma unroll
-        for (int w = 0; w < DEC_WAVES; w++) rank[j] += rank_part[w][lane + WAVE * j];
-        if (lane + WAVE * j >= a.E) rank[j] = INT_MAX;
-        const uint64_t hit = __ballot(rank[j] == kslot);   // the same in every wave
-        if (hit) e = WAVE * j + (int)__builtin_ctzll(hit);
-    }
-    if (e < 0) return;
-    if (unit == 0 && wave == 0) {
-        // probabilities (telemetry) and normalised weights (lfm2-engine.js:444-457;
-        // qwen3-engine.js:317-329: the sum starts at 0 and a zero sum gives zero weights)
-        float p[EPL];
-        if (a.softmax) {
-#pragma unroll
-            for (int j = 0; j < EPL; j++) p[j] = sh_prob[lane + WAVE * j];
-        } else {
-            int okp = 1;
-            uint64_t pv[EPL];
-            wait_slots<EPL>(loc + SYNC_PROB, tab + SYNC_PROB, a.E, epoch, lane, okp, use_loc, pv);
-            if (!okp && lane == 0) atomicOr(a.err, 2u);
-#pragma unroll
-            for (int j = 0; j < EPL; j++) p[j] = __uint_as_float((uint32_t)pv[j]);
-        }
-#pragma unroll
-        for (int j = 0; j < EPL; j++) {
-            const int ee = lane + WAVE * j;
-            if (a.out_probs && ee < a.E) a.out_probs[ee] = p[j];
-            if (rank[j] < a.K) {
-                sh_rank_e[rank[j]] = ee;
-                sh_rank_p[rank[j]] = p[j];
-            }
-        }
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        if (lane == 0) {
-            double sumW = a.softmax ? 0.0 : 1e-6;
-            for (int k = 0; k < a.K; k++) sumW = sumW + (double)sh_rank_p[k];
-            const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
-            for (int k = 0; k < a.K; k++) {
-                const double wk = (double)sh_rank_p[k] * inv;
-                a.route_idx[k] = sh_rank_e[k];
-                a.route_w[k] = wk;
-                if (a.out_idx) a.out_idx[k] = sh_rank_e[k];
-                if (a.out_w) a.out_w[k] = wk;
-            }
-        }
-    }
-    if (mask_has(a.mask, e)) return;   // the combine skips masked ranks
+    const int *idx_w = sh_idx[wave];   // this wave's copy
 
-    const int h = lane & 1;
-    const int f = s * QK + lane / 2;
-    const bool f_ok = f < a.F;
-
-    // ---- issue every weight load of this workgroup ----
-    // All addresses are clamped in bounds so every load is unconditional and
-    // the compiler issues them back to back; out-of-range rows / blocks get a
-    // zero scale afterwards.  One 64-bit base per tensor, uniform strides.
-    int4 gq[NBW], uq[NBW], dq[NBW];
-    __half gdh[NBW], udh[NBW], ddh[NBW];
+    // The loads are issued unconditionally (expert 0 stands in when the
+    // routing failed), so no control-flow join sits between them and their
+    // uses for the compiler to place conversions -- and waits -- at.
+    int4 gq[NBW], uq[NBW], dq[DEC_DCH];
+    ScaleRun<NBW> gs, us;
+    uint32_t ddb[DEC_DCH];
+    bool cok = false;
     {
-        const int fc = min(f, a.F - 1);
-        const int ilast = (a.nbH - 1 - wave) >= 0 ? (a.nbH - 1 - wave) / DEC_WAVES : 0;
-        const size_t row0 = ((size_t)e * a.nbH + min(wave, a.nbH - 1)) * a.F + fc;
-        const size_t rstride = (size_t)DEC_WAVES * a.F;
-        const int8_t *gp = a.gq + row0 * QK + 16 * h;
-        const int8_t *up = a.uq + row0 * QK + 16 * h;
+        const int eg = ok ? idx_w[ck] : 0;
+        cok = ok && cs < nc && !((mrank >> ck) & 1u);
+        const int8_t *gbase = a.gq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
+        const int8_t *ubase = a.uq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
 #pragma unroll
         for (int i = 0; i < NBW; i++) {
-            const size_t o = (size_t)min(i, ilast) * rstride;
-            gq[i] = *reinterpret_cast<const int4 *>(gp + o * QK);
-            uq[i] = *reinterpret_cast<const int4 *>(up + o * QK);
-            gdh[i] = a.gd[row0 + o];
-            udh[i] = a.ud[row0 + o];
+            gq[i] = *reinterpret_cast<const int4 *>(gbase + (size_t)goff[i] * QK);
+            uq[i] = *reinterpret_cast<const int4 *>(ubase + (size_t)goff[i] * QK);
         }
-        // down rows j = (wave + 8i)*32 + lane/2 of block column s
-        const size_t dsbase = ((size_t)e * a.nbF + s) * a.H;
-#pragma unroll
-        for (int i = 0; i < NBW; i++) {
-            const int j = min((wave + DEC_WAVES * i) * QK + lane / 2, a.H - 1);
-            dq[i] = *reinterpret_cast<const int4 *>(a.dq + (dsbase + j) * QK + 16 * h);
-            ddh[i] = a.dd[dsbase + j];
-        }
-    }
-    // every load above is issued before any of the work below
-    __builtin_amdgcn_sched_barrier(0);
-
-    // ---- gate / up rows, SwiGLU (tensor.js:167-178) ----
-    float ga = 0.0f, ua = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NBW; i++) {
-        // blocks past nbH: zero scale and zero activations (x is padded)
-        const int b = wave + DEC_WAVES * i;
-        const int c = 2 * b + h;
-        const bool bok = f_ok && b < a.nbH;
-        const float sg = bok ? __half2float(gdh[i]) : 0.0f;
-        const float su = bok ? __half2float(udh[i]) : 0.0f;
-        const int4 l1 = xq1[c], l2 = xq2[c], l3 = xq3[c];
-        const float sig = xsig[c];
-        ga = fmaf(dot16_lev3(gq[i], l1, l2, l3, sig), sg, ga);
-        ua = fmaf(dot16_lev3(uq[i], l1, l2, l3, sig), su, ua);
-    }
-    ga += __shfl_xor(ga, 1, WAVE);
-    ua += __shfl_xor(ua, 1, WAVE);
-    if (h == 0) {
-        redg[wave][lane / 2] = ga;
-        redu[wave][lane / 2] = ua;
-    }
-    __syncthreads();
-    if (threadIdx.x < QK) {
-        const int r = threadIdx.x;
-        float G = redg[0][r], U = redu[0][r];
-#pragma unroll
-        for (int w = 1; w < DEC_WAVES; w++) {
-            G += redg[w][r];
-            U += redu[w][r];
-        }
-        float gv = 0.0f;
-        if (s * QK + r < a.F) {
-            const double g64 = (double)G;
-            const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
-            gv = sg * U;
-        }
-        gl[r] = gv;
-    }
-    __syncthreads();
-    if (threadIdx.x < 2) {
-        Lev3 L;
-        decompose16(&gl[16 * threadIdx.x], L);
-        gq1[threadIdx.x] = L.l1;
-        gq2[threadIdx.x] = L.l2;
-        gq3[threadIdx.x] = L.l3;
-        gsig[threadIdx.x] = L.sig;
-    }
-    __syncthreads();
-
-    // ---- partial down product over this slice ----
-    float *part = a.partial + ((size_t)kslot * a.NS + s) * a.H;
-    const int4 m1 = gq1[h], m2 = gq2[h], m3 = gq3[h];
-    const float msig = gsig[h];
-#pragma unroll
-    for (int i = 0; i < NBW; i++) {
-        const int j = (wave + DEC_WAVES * i) * QK + lane / 2;
-        const float sdd = (j < a.H) ? __half2float(ddh[i]) : 0.0f;
-        float y = dot16_lev3(dq[i], m1, m2, m3, msig) * sdd;
-        y += __shfl_xor(y, 1, WAVE);
-        if (h == 0 && j < a.H) part[j] = y;
-    }
-}
-
-// 256 threads per CW outputs: thread (group q, output jl) sums the slices
-// s = q, q + NG, ... (NSP of them, NG = 256 / CW groups) of up to 4 ranks,
-// with all its loads in flight at once; the NG groups are then summed in a
-// fixed order.
-template <int CW, int NSP>
-__global__ __launch_bounds__(256) void moe_decode_combine_kernel(
-    const float *__restrict__ partial, int H, int NS, int K, const int32_t *__restrict__ route_idx,
-    const double *__restrict__ route_w, MaskBits mask, float *__restrict__ hidden,
-    uint32_t *__restrict__ epoch_word)
-{
-    constexpr int NG = 256 / CW;
-    // the experts kernel of this call has finished: the next call takes a new epoch
-    if (blockIdx.x == 0 && threadIdx.x == 0) epoch_word[0] = epoch_word[0] + 1u;
-    __shared__ float red[MAX_K][NG][CW];
-    __shared__ int sh_e[MAX_K];
-    __shared__ double sh_w[MAX_K];
-    const int jl = threadIdx.x % CW;
-    const int q = threadIdx.x / CW;
-    const int j = blockIdx.x * CW + jl;
-    const int jc = min(j, H - 1);
-    // the routing and the residual row are loaded with the partial sums, in
-    // the same round trip
-    const int tid = threadIdx.x;
-    if (tid >= CW && tid < CW + K) {
-        sh_e[tid - CW] = route_idx[tid - CW];
-        sh_w[tid - CW] = route_w[tid - CW];
-    }
-    const float h_in = hidden[jc];
-    for (int k0 = 0; k0 < K; k0 += 4) {
-        float v[4][NSP];
-#pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
-            const int k = min(k0 + kk, K - 1);
-#pragma unroll
-            for (int i = 0; i < NSP; i++) {
-                const int s = min(q + NG * i, NS - 1);
-                v[kk][i] = partial[((size_t)k * NS + s) * H + jc];
-            }
-        }
+        // the scales: the pair's gate scales come with the even lane, its up
+        // scales with the odd one (applied after the block products)
+        const size_t grow = (size_t)eg * a.F + cf;
+        gs.load((hh ? a.udcm : a.gdcm) + grow * a.nbpH + NBW * wave);
         __builtin_amdgcn_sched_barrier(0);
+    }
+    // Every wave's gate/up requests go out before any down request: a CU's
+    // requests are served about in issue order, so the workgroup receives
+    // all its gate/up bytes first (its h is ready early) and the down bytes
+    // arrive while the h values are exchanged.  (Loads also complete in
+    // issue order within a wave, so the gate/up products never wait for the
+    // down rows.)
+    lds_barrier();
+    {
+        const int ed0 = ok ? idx_w[pk2[0]] : 0, ed1 = ok ? idx_w[pk2[1]] : 0;
+        const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
 #pragma unroll
-        for (int kk = 0; kk < 4; kk++) {
+        for (int i = 0; i < DEC_DCH; i++)
+            dq[i] = *reinterpret_cast<const int4 *>(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
+#pragma unroll
+        for (int i = 0; i < DEC_DCH; i++) ddb[i] = dd16[(dsec[i] ? dst1 : dst0) + doff[i]];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // ---- weights (lfm2-engine.js:444-447; qwen3-engine.js:317-321), worked
+    // out while the weight bytes stream in ----
+    double wk[MAX_K];
+    if (ok) {
+        float pk[MAX_K];
+#pragma unroll
+        for (int u = 0; u < MAX_K / 4; u++) {
+            const float4 v = reinterpret_cast<const float4 *>(sh_pr[wave])[u];
+            pk[4 * u] = v.x;
+            pk[4 * u + 1] = v.y;
+            pk[4 * u + 2] = v.z;
+            pk[4 * u + 3] = v.w;
+        }
+        double sumW = a.softmax ? 0.0 : 1e-6;
+#pragma unroll
+        for (int k = 0; k < MAX_K; k++)
+            if (k < a.K) sumW = sumW + (double)pk[k];
+        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
+#pragma unroll
+        for (int k = 0; k < MAX_K; k++) wk[k] = (k < a.K) ? (double)pk[k] * inv : 0.0;
+#pragma unroll
+        for (int k = 0; k < MAX_K; k++)
+            if (lane == k) sh_w[wave][k] = wk[k];
+        if (j == 0 && wave == 0) {
+            if (lane < a.K) {
+                if (a.out_idx) a.out_idx[lane] = idx_w[lane];
+                if (a.out_w) a.out_w[lane] = sh_w[0][lane];
+            }
+            if (a.out_probs) {
+#pragma unroll
+                for (int t = 0; t < EPL; t++)
+                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
+            }
+        }
+    }
+
+    // ---- gate / up columns, SwiGLU (tensor.js:167-178), h out ----
+    if (ok) {
+        float dg[NBW], du[NBW];
+#pragma unroll
+        for (int i = 0; i < NBW; i++) {
+            const int c = 2 * (NBW * wave + i) + hh;
+            const int4 l1 = xq1[c], l2 = xq2[c], l3 = xq3[c];
+            const float sig = xsig[c];
+            dg[i] = dot16_lev3(gq[i], l1, l2, l3, sig);
+            du[i] = dot16_lev3(uq[i], l1, l2, l3, sig);
+        }
+#pragma unroll
+        for (int i = 0; i < (NBW + 1) / 2; i++) {
+            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)gs.s[i], 0xB1, 0xf, 0xf, false);
+            us.s[i] = hh ? gs.s[i] : other;
+            gs.s[i] = hh ? other : gs.s[i];
+        }
+        float ga = 0.0f, ua = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NBW; i++) {
+            const int b = NBW * wave + i;
+            const bool bok = cok && b < a.nbH;
+            ga = fmaf(dg[i], bok ? gs.get(i) : 0.0f, ga);
+            ua = fmaf(du[i], bok ? us.get(i) : 0.0f, ua);
+        }
+        ga += xor1_dpp(ga);
+        ua += xor1_dpp(ua);
+        if (hh == 0) {
+            redg[wave][cs] = ga;
+            redu[wave][cs] = ua;
+        }
+        lds_barrier();
+        if (tid >= PUB && tid - PUB < nc) {
+            const int cc = tid - PUB;
+            const int c = c0 + cc;
+            const int k = div_small(c, inv_fr);
+            const int f = f0 + c - k * FR;
+            if (!((mrank >> k) & 1u)) {
+                float G = redg[0][cc], U = redu[0][cc];
+#pragma unroll
+                for (int w = 1; w < DEC_WAVES; w++) {
+                    G += redg[w][cc];
+                    U += redu[w][cc];
+                }
+                const double g64 = (double)G;
+                const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
+                const uint64_t word = tag_word(tag, sg * U);
+                store_local(&a.hloc[(size_t)k * a.F + f], word);
+                store_dev(&a.hdev[(size_t)k * a.F + f], word);
+            }
+        }
+    }
+
+    // ---- the group's h values -> LDS (zero for masked ranks and padding) ----
+    const int HW = a.K * FRb * QK;
+    for (int i = tid; i < HW; i += DEC_THREADS) hl[i] = 0.0f;
+    // partials of groups without blocks and of masked ranks read as zero
+    for (int i = tid; i < DEC_MAX_FIN; i += DEC_THREADS) pf[i] = 0.0f;
+    lds_barrier();
+    if (ok && NP2 > 0) {
+        constexpr int IPT = (DEC_MAX_HW + PUB - 1) / PUB;
+        const uint64_t *pl[IPT], *pd[IPT];
+        bool want[IPT];
+        float *dst[IPT];
+#pragma unroll
+        for (int s2 = 0; s2 < IPT; s2++) {
+            const int i = min(tid + PUB * s2, NC - 1);
+            const int k = div_small(i, inv_fr);
+            const int f = f0 + i - k * FR;
+            pl[s2] = &a.hloc[(size_t)k * a.F + f];
+            pd[s2] = &a.hdev[(size_t)k * a.F + f];
+            want[s2] = tid + PUB * s2 < NC && !((mrank >> k) & 1u);
+            dst[s2] = &hl[k * FRb * QK + (i - k * FR)];
+        }
+        ok = block_wait<PUB, IPT>(tag, &sh_fail, pl, pd, want, dst);
+    }
+    if (ok && NP2 > 0) {
+        decompose_row(hl, 2 * a.K * FRb, hq1, hq2, hq3, hsig);
+        lds_barrier();
+        // ---- partial down products over the group's blocks ----
+#pragma unroll
+        for (int i = 0; i < DEC_DCH; i++) {
+            if (i >= NUW) continue;
+            const int t = div_small(i, inv_frb);
+            const int bl = i - t * FRb;
+            const int p = wave + DEC_WAVES * t;
+            if (p >= NP2) continue;
+            const int k = (NRH == 2) ? (p >> 1) : p;
+            const int rh = (NRH == 2) ? (p & 1) : 0;
+            const int rl = rh * 32 + cs;
+            const int hc = (k * FRb + bl) * 2 + hh;
+            // the scale bits pass an empty asm here (ordered after the
+            // barriers above), so the compiler cannot convert them -- and wait
+            // for the down loads -- before the gate/up products
+            uint32_t db = ddb[i];
+            asm volatile("" : "+v"(db));
+            const float sd = (rl < RMm) ? f16_bits(db) : 0.0f;
+            float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * sd;
+            y += xor1_dpp(y);
+            if (hh == 0) redd[(k * FRb + bl) * RMP + rl] = y;
+        }
+        lds_barrier();
+        for (int t = tid - DEC_THREADS / 2; t >= 0 && t < a.K * RMm; t += DEC_THREADS / 2) {
+            const int k = t / RMm;
+            const int rl = t - k * RMm;
+            if ((mrank >> k) & 1u) continue;
+            float v[8];
+#pragma unroll
+            for (int bl = 0; bl < 8; bl++) v[bl] = redd[(k * FRb + min(bl, FRb - 1)) * RMP + rl];
+            float s = 0.0f;
+#pragma unroll
+            for (int bl = 0; bl < 8; bl++) s += (bl < FRb) ? v[bl] : 0.0f;
+            store_dev(&a.part[((size_t)gx * a.K + k) * a.H + r0 + rl], tag_word(tag, s));
+        }
+    }
+
+    // ---- combine (lfm2-engine.js:459-486): y_k = sum of the groups' partials,
+    // acc = fp32(acc + w_k y_k) in rank order, hidden += acc ----
+    const int NP = DEC_GROUPS * a.K * RF;
+    if (ok) {
+        constexpr int NT = DEC_THREADS / 2;
+        constexpr int IPT = DEC_MAX_FIN / NT;
+        const uint64_t *pl[IPT];
+        bool want[IPT];
+        float *dst[IPT];
+#pragma unroll
+        for (int s2 = 0; s2 < IPT; s2++) {
+            const int i = tid + NT * s2;
+            if (i >= NP) {
+                pl[s2] = &a.arrive[min(i - NP, G - 1)];
+                want[s2] = i < NP + G;
+                dst[s2] = nullptr;
+            } else {
+                const int x = i / (a.K * RF);
+                const int r = i - x * a.K * RF;
+                const int k = r / RF;
+                const int q = r - k * RF;
+                const int xb0 = x * a.nbF / DEC_GROUPS, xb1 = (x + 1) * a.nbF / DEC_GROUPS;
+                pl[s2] = &a.part[((size_t)x * a.K + k) * a.H + min(q0 + q, a.H - 1)];
+                want[s2] = q < RFm && xb1 > xb0 && !((mrank >> k) & 1u);
+                dst[s2] = &pf[i];
+            }
+        }
+        ok = block_wait<NT, IPT>(tag, &sh_fail, pl, pl, want, dst);
+    }
+    if (ok && tid < RFm) {
+        float acc = 0.0f;
+        for (int k = 0; k < a.K; k++) {
+            float v[DEC_GROUPS];
+#pragma unroll
+            for (int x = 0; x < DEC_GROUPS; x++) v[x] = pf[(x * a.K + k) * RF + tid];
             float y = 0.0f;
 #pragma unroll
-            for (int i = 0; i < NSP; i++)
-                if (q + NG * i < NS) y += v[kk][i];
-            if (k0 + kk < K) red[k0 + kk][q][jl] = y;
+            for (int x = 0; x < DEC_GROUPS; x++) y += v[x];
+            if (!((mrank >> k) & 1u)) acc = (float)((double)acc + sh_w[wave][k] * (double)y);
         }
+        a.hidden[q0 + tid] = hin + acc;
     }
-    __syncthreads();
-    if (threadIdx.x < CW && j < H) {
-        float acc = 0.0f;
-        for (int k = 0; k < K; k++) {
-            const int e = sh_e[k];
-            if ((unsigned)e >= (unsigned)MAX_E || mask_has(mask, e)) continue;
-            float y = red[k][0][jl];
-#pragma unroll
-            for (int p = 1; p < NG; p++) y += red[k][p][jl];
-            acc = (float)((double)acc + sh_w[k] * (double)y);
-        }
-        hidden[j] = h_in + acc;
+    if (tid == 0) {
+        if (!ok) atomicOr(a.err, 1u);
+        // workgroup 0 has seen every arrival word carry this tag (or gave up
+        // waiting), so every workgroup has read the epoch: the next call draws
+        // the next tag
+        if (j == 0) __hip_atomic_store(a.epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-bool decode_supported(const qq_moe *m, int T)
+static int decode_grid(const qq_ctx *ctx)
 {
-    return T == 1 && m->E <= MAX_E && m->K <= m->E && m->H <= 8 * DEC_WAVES * QK;
+    return (std::min(ctx->num_cus, SYNC_ARRIVE_WORDS) / DEC_GROUPS) * DEC_GROUPS;
 }
 
-size_t decode_work_bytes(const qq_moe *m)
+bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T)
 {
-    const int NS = (m->F + QK - 1) / QK;
-    return (size_t)m->K * NS * m->H * 4 + 256 + 256 + (size_t)m->K * 4 + 256;
+    if (T != 1 || m->E > MAX_E || m->K > m->E || m->H > 8 * DEC_WAVES * QK) return false;
+    const int G = decode_grid(ctx);
+    if (G < DEC_GROUPS) return false;
+    const int M = G / DEC_GROUPS;
+    const int nbF = (m->F + QK - 1) / QK;
+    const int frb = (nbF + DEC_GROUPS - 1) / DEC_GROUPS;   // blocks of the largest group
+    const int cpm = (m->K * frb * QK + M - 1) / M;
+    const int RM = (m->H + M - 1) / M;
+    const int nrh = RM > 32 ? 2 : 1;
+    const int RF = (m->H + G - 1) / G;
+    const int ppw = (m->K * nrh + DEC_WAVES - 1) / DEC_WAVES;
+    return (m->E + M - 1) / M <= 8 && RM <= 64 && cpm <= DEC_CCH && ppw <= 2 && ppw * frb <= DEC_DCH &&
+           m->K * frb * QK <= DEC_MAX_HW &&
+           m->K * frb * nrh * 32 <= DEC_MAX_RED && DEC_GROUPS * m->K * RF + G <= DEC_MAX_FIN &&
+           (size_t)m->K * m->F <= SYNC_H_WORDS && (size_t)m->K * m->H * DEC_GROUPS <= SYNC_P_WORDS;
 }
 
-template <int NBW, int EPL>
-static void launch_experts(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
+template <int NBW, int RE, int EPL>
+static void launch_t(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
 {
-    QQ_LAUNCH(ctx, (moe_decode_experts_kernel<NBW, EPL>), grid, dim3(DEC_THREADS), 0, a);
+    QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL>), grid, dim3(DEC_THREADS), 0, a);
 }
 
-template <int EPL>
-static void launch_experts_nbw(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int nbw)
+// (RE, EPL) pairs: with M <= 32 members per group, ceil(E / M) <= RE implies
+// ceil(E / 64) <= EPL for these four
+template <int NBW>
+static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re)
 {
-    if (nbw <= 1) launch_experts<1, EPL>(ctx, a, grid);
-    else if (nbw <= 2) launch_experts<2, EPL>(ctx, a, grid);
-    else if (nbw <= 4) launch_experts<4, EPL>(ctx, a, grid);
-    else launch_experts<8, EPL>(ctx, a, grid);
+    if (re <= 1) launch_t<NBW, 1, 1>(ctx, a, grid);
+    else if (re <= 2) launch_t<NBW, 2, 1>(ctx, a, grid);
+    else if (re <= 4) launch_t<NBW, 4, 2>(ctx, a, grid);
+    else launch_t<NBW, 8, 4>(ctx, a, grid);
 }
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      char *work, const NormArgs *norm)
+                      const NormArgs *norm)
 {
     DecodeArgs a;
     a.x = x;
     a.norm = norm != nullptr;
     a.norm_w = norm ? norm->w : nullptr;
     a.eps = norm ? norm->eps : 0.0;
+    a.hidden = hidden;
     a.H = m->H;
     a.F = m->F;
     a.E = m->E;
     a.K = m->K;
     a.nbH = (m->H + QK - 1) / QK;
     a.nbF = (m->F + QK - 1) / QK;
-    a.NS = a.nbF;
     a.router_q8 = m->router_type == QQ_TYPE_Q8_0;
     a.rf32 = m->router_f32;
     a.rq = a.router_q8 ? m->router_q8->qs : nullptr;
     a.rd = a.router_q8 ? m->router_q8->d : nullptr;
+    a.softmax = m->gating == QQ_GATING_SOFTMAX;
     a.bias = m->bias;
     a.gq = m->gate->qs;
-    a.gd = m->gate->d;
+    a.gdcm = m->gate->dcm;
     a.uq = m->up->qs;
-    a.ud = m->up->d;
+    a.udcm = m->up->dcm;
+    a.nbpH = m->gate->nbp;
     a.dq = m->down->qs;
     a.dd = m->down->d;
     a.mask = mask;
-    a.slots = ctx->sync_slots;
-    a.local = ctx->sync_local;
-    a.router_vec4 = !a.router_q8 && (m->H & 3) == 0;
-    a.softmax = m->gating == QQ_GATING_SOFTMAX;
-    const int epl = m->E <= WAVE ? 1 : m->E <= 2 * WAVE ? 2 : 4;
-    a.n_router = RT_COPIES * ((m->E + RT_EPW - 1) / RT_EPW);
     a.epoch_word = ctx->sync_epoch;
-    a.err = ctx->sync_err;
-    const size_t part_b = ((size_t)m->K * a.NS * m->H * 4 + 255) & ~(size_t)255;
-    a.partial = reinterpret_cast<float *>(work);
-    a.route_w = reinterpret_cast<double *>(work + part_b);
-    a.route_idx = reinterpret_cast<int32_t *>(reinterpret_cast<char *>(a.route_w) + 256);
+    a.rloc = ctx->sync_local;
+    a.rdev = ctx->sync_slots;
+    a.hloc = ctx->sync_hloc;
+    a.hdev = ctx->sync_hdev;
+    a.part = ctx->sync_part;
+    a.arrive = ctx->sync_arrive;
     a.out_idx = out_idx;
     a.out_w = out_w;
     a.out_probs = out_probs;
+    a.err = ctx->sync_err;
 
+    const int G = decode_grid(ctx);
+    const int re = (m->E + G / DEC_GROUPS - 1) / (G / DEC_GROUPS);
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
-    const dim3 grid(a.n_router + m->K * a.NS);
-    prof_begin(ctx, K_DECODE_EXPERTS);
-    if (epl == 1) launch_experts_nbw<1>(ctx, a, grid, nbw);
-    else if (epl == 2) launch_experts_nbw<2>(ctx, a, grid, nbw);
-    else launch_experts_nbw<4>(ctx, a, grid, nbw);
+    const dim3 grid(G);
+    prof_begin(ctx, K_DECODE);
+    if (nbw <= 1) launch_re<1>(ctx, a, grid, re);
+    else if (nbw <= 2) launch_re<2>(ctx, a, grid, re);
+    else if (nbw <= 4) launch_re<4>(ctx, a, grid, re);
+    else launch_re<8>(ctx, a, grid, re);
     prof_end(ctx);
-    QQ_HIP(ctx, hipGetLastError());
-
-    // 32 outputs per workgroup (16 or 8, with more workgroups, measured slower)
-    constexpr int CW = 32, NG = 256 / CW;
-    const int nsp = (a.NS + NG - 1) / NG;
-    const dim3 cgrid((m->H + CW - 1) / CW);
-#define QQ_CB(N)                                                                                 \
-    QQ_LAUNCH(ctx, (moe_decode_combine_kernel<CW, N>), cgrid, dim3(256), 0, a.partial, \
-                       m->H, a.NS, m->K, a.route_idx, a.route_w, mask, hidden, ctx->sync_epoch)
-    prof_begin(ctx, K_DECODE_COMBINE);
-    if (nsp <= 1) QQ_CB(1);
-    else if (nsp <= 2) QQ_CB(2);
-    else if (nsp <= 4) QQ_CB(4);
-    else if (nsp <= 8) QQ_CB(8);
-    else if (nsp <= 16) QQ_CB(16);
-    else QQ_CB(32);
-    prof_end(ctx);
-#undef QQ_CB
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
 }

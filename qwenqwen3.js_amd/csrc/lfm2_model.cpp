@@ -299,7 +299,7 @@ int bind(Binder &B)
         if (L.moe) {
             if (int rc = qq_gguf_moe_layer(B.ctx, B.g, i, 0, -1, &L.ffn_moe)) return rc;
             m->moes.push_back(L.ffn_moe);
-            if (!qq::decode_supported(L.ffn_moe, 1))
+            if (!qq::decode_supported(B.ctx, L.ffn_moe, 1))
                 return set_error(B.ctx, "lfm2: MoE block %d is outside the batch-1 decode kernel's shapes", i);
         } else {
             qq_gguf_tensor tg;

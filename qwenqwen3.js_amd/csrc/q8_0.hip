@@ -8,7 +8,8 @@
 // quants of every row r are contiguous, rows in order:
 //   qs[((m*nb + b)*rows + r)*32 + i],   d[(m*nb + b)*rows + r]
 // A wavefront load of 64 lanes x 16 bytes is then 32 rows x one block: 1 KiB
-// contiguous, whichever rows a kernel owns.
+// contiguous, whichever rows a kernel owns.  The scales are also kept row by
+// row, dcm[(m*rows + r)*nbp + b] (nbp = nb rounded up to 8, zero padded).
 #include "qq_device.h"
 
 namespace qq {
@@ -18,8 +19,9 @@ namespace qq {
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t *__restrict__ src,
                                                           int8_t *__restrict__ qs,
-                                                          __half *__restrict__ d, size_t nblocks,
-                                                          int rows, int nb)
+                                                          __half *__restrict__ d,
+                                                          __half *__restrict__ dcm, size_t nblocks,
+                                                          int rows, int nb, int nbp)
 {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= nblocks) return;
@@ -36,6 +38,7 @@ __global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t *__restr
     dst[0] = make_int4((int)w[0], (int)w[1], (int)w[2], (int)w[3]);
     dst[1] = make_int4((int)w[4], (int)w[5], (int)w[6], (int)w[7]);
     d[o] = __ushort_as_half(s16[0]);
+    dcm[col * nbp + b] = __ushort_as_half(s16[0]);
 }
 
 int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t)
@@ -44,7 +47,7 @@ int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t)
     const unsigned grid = (unsigned)((nblocks + 255) / 256);
     prof_begin(ctx, K_REPACK);
     QQ_LAUNCH(ctx, repack_q8_0_kernel, dim3(grid), dim3(256), 0, gguf_dev,
-                       t->qs, t->d, nblocks, t->out_dim, t->nb);
+                       t->qs, t->d, t->dcm, nblocks, t->out_dim, t->nb, t->nbp);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

@@ -111,6 +111,81 @@ __device__ __forceinline__ void dma4s(uint32_t off, const void *base, uint32_t l
                  :: "v"(off), "s"(base), "s"(lds) : "memory");
 }
 
+// Value of lane ^ 1 (resp. lane ^ 2) by a DPP quad permutation: a VALU
+// operation, where __shfl_xor goes through the LDS permute unit.
+__device__ __forceinline__ float xor1_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float xor2_dpp(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
+}
+
+// Maximum over the 64 lanes of a wavefront (all lanes active), the same value
+// in every lane: quads and rows of 16 by DPP, then the four row maxima.
+__device__ __forceinline__ float wave_max_dpp(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Stable top-K of E scores held by one wavefront (score of expert lane + 64 t
+// in sc[t]; slots past E must hold -inf): K rounds of a DPP maximum and a
+// ballot for the lowest expert holding it, so ties go to the lower index --
+// the order of a stable descending sort.  idx[k] / p[k] get the rank-k expert
+// and pr[] of it, the same in every lane.  Scores must not be NaN.
+template <int EPL>
+__device__ __forceinline__ void wave_topk(const float (&sc)[EPL], const float (&pr)[EPL], int K,
+                                          int (&idx)[MAX_K], float (&p)[MAX_K])
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    float v[EPL];
+#pragma unroll
+    for (int t = 0; t < EPL; t++) v[t] = sc[t];
+#pragma unroll
+    for (int k = 0; k < MAX_K; k++) {
+        idx[k] = 0;
+        p[k] = 0.0f;
+        if (k >= K) continue;
+        float m = v[0];
+#pragma unroll
+        for (int t = 1; t < EPL; t++) m = fmaxf(m, v[t]);
+        m = wave_max_dpp(m);
+        int win = -1;
+        float pw = 0.0f;
+#pragma unroll
+        for (int t = EPL - 1; t >= 0; t--) {
+            const uint64_t hit = __ballot(v[t] == m);
+            if (hit) {
+                const int l = (int)__builtin_ctzll(hit);
+                win = WAVE * t + l;
+                pw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pr[t]), l));
+            }
+        }
+        idx[k] = win;
+        p[k] = pw;
+#pragma unroll
+        for (int t = 0; t < EPL; t++)
+            if (WAVE * t + lane == win) v[t] = -INFINITY;
+    }
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS
+// operations, not for its global loads and stores (words exchanged with other
+// workgroups carry their own tags and need no fence).
+__device__ __forceinline__ void lds_barrier()
+{
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vm()
 {
@@ -345,10 +420,10 @@ __device__ __forceinline__ void softmax_probs(const float (&logit)[EPL], int E, 
 }
 
 // softmax: Qwen3 gating (bias unused); otherwise LFM2's sigmoid + bias.
+// bias[i] is the selection bias of expert lane + 64 i (any value past E).
 template <int EPL>
-__device__ __forceinline__ void wave_route(const float (&logit)[EPL], int E, int K,
-                                           const float *__restrict__ bias, bool softmax,
-                                           WaveRoute<EPL> &out)
+__device__ __forceinline__ void wave_route(const float (&logit)[EPL], const float (&bias)[EPL], int E,
+                                           int K, bool softmax, WaveRoute<EPL> &out)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     float s[EPL];
@@ -364,7 +439,7 @@ __device__ __forceinline__ void wave_route(const float (&logit)[EPL], int E, int
             s[i] = 0.0f;
             if (e < E) {
                 out.prob[i] = (float)(1.0 / (1.0 + exp(-(double)logit[i])));
-                s[i] = out.prob[i] + bias[e];
+                s[i] = out.prob[i] + bias[i];
             }
         }
     }

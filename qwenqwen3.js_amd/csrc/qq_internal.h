@@ -21,17 +21,21 @@ constexpr int QBLK = 34;      // bytes per GGUF Q8_0 block {fp16 d, int8 qs[32]}
 constexpr int WAVE = 64;      // CDNA wavefront width
 constexpr int MAX_E = 256;    // experts supported by the router and the mask bitset
 constexpr int MAX_K = 16;     // experts used per token
-// Decode router exchange: copies of the per-expert slot table (selection
-// scores or logits at [0, MAX_E), probabilities at [SYNC_PROB, SYNC_PROB +
-// MAX_E)), each 4608 B apart so that the copies start in different DRAM
-// channels ...
-constexpr int SYNC_PROB = MAX_E;
+// Decode router exchange: SYNC_REPLICAS device-coherent copies of the router
+// logit table [MAX_E], each 4608 B apart so that the copies start in
+// different DRAM channels ...
 constexpr int SYNC_REPLICAS = 16;
 constexpr int SYNC_REPLICA_WORDS = 576;
 // ... and one table per XCD (XCC_ID < 16), 4 KiB apart.
 constexpr int SYNC_LOCAL_TABLES = 16;
 constexpr int SYNC_LOCAL_WORDS = 2 * MAX_E;
 static_assert(SYNC_REPLICA_WORDS >= 2 * MAX_E, "slot table");
+// Batch-1 decode exchange tables (64-bit tagged words): h values [K][F] in a
+// group-local and a device-coherent copy, partial down sums [8][K][H], and
+// one arrival word per workgroup.
+constexpr int SYNC_H_WORDS = MAX_K * 4096;
+constexpr int SYNC_P_WORDS = 8 * MAX_K * 2048;
+constexpr int SYNC_ARRIVE_WORDS = 256;
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
 struct MaskBits {
@@ -58,15 +62,20 @@ __host__ __device__ inline bool mask_has(const MaskBits &m, int e)
 // The repack keeps 34 bytes per 32 weights (the GGUF byte count) but splits
 // the 2-byte scale out of each block so that every row of qs is 32-byte
 // aligned and a wavefront reads it as 64 lanes x 16 contiguous bytes.
+//   dcm: fp16 [n_mats][rows][nbp]  the same scales row by row (nbp = nb
+//        rounded up to 8, zero padded), so that one lane reads the scales of
+//        8 consecutive blocks of its row in one 16-byte load (decode kernel)
 struct qq_tensor {
     int in_dim;     // k (GGUF shape[0])
     int out_dim;    // rows (GGUF shape[1])
     int n_mats;     // experts (GGUF shape[2], 1 for a 2-D tensor)
     int nb;         // blocks per row = ceil(in_dim/32)
     int kp;         // nb*32
+    int nbp;        // nb rounded up to a multiple of 8
     int8_t *qs;
     __half *d;
-    size_t qs_bytes, d_bytes;
+    __half *dcm;
+    size_t qs_bytes, d_bytes, dcm_bytes;
 };
 
 struct qq_moe {
@@ -95,16 +104,17 @@ struct qq_ctx {
     size_t pinned_bytes;
     // timing events of the bench entry points
     hipEvent_t ev0, ev1;
-    // device words shared by the kernels of this context: the decode router's
-    // SYNC_REPLICAS device-coherent tables and SYNC_LOCAL_TABLES per-XCD
-    // tables of per-expert (epoch, score) and (epoch, probability) slots,
-    // then the error word and the decode epoch (advanced
-    // on the device by every decode combine, so a replayed graph of decode
-    // launches sees a fresh epoch each time)
+    // device words shared by the kernels of this context: the decode
+    // kernel's exchange tables (router logits: SYNC_REPLICAS device-coherent
+    // copies and one table per XCD group; h values, partial sums, arrivals),
+    // the error word and the decode epoch (advanced on the device by every
+    // decode call, so a replayed graph of decode launches sees a fresh epoch
+    // each time)
     uint64_t *sync_slots;
     uint64_t *sync_local;
     uint32_t *sync_err;
     uint32_t *sync_epoch;
+    uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive;
     // a graph capture on `stream` is open (qq_capture_begin)
     int capturing;
     // token batches of at least this many rows take the fp16 MFMA path (0: never)
@@ -125,8 +135,7 @@ enum KernelId {
     K_MATVEC,
     K_ROUTER_LOGITS,
     K_ROUTER_TOPK,
-    K_DECODE_EXPERTS,
-    K_DECODE_COMBINE,
+    K_DECODE,
     K_DISPATCH,
     K_GROUPED_GATEUP,
     K_GROUPED_DOWN,
@@ -186,8 +195,9 @@ constexpr int ROUTER_MAX_SPLIT = 8;
 size_t router_work_bytes(const qq_moe *m, int T);
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
                        int32_t *idx, double *w, float *probs);
-bool decode_supported(const qq_moe *m, int T);
-size_t decode_work_bytes(const qq_moe *m);
+// Batch-1 decode in one launch (decode.hip); its exchange tables live in the
+// context's sync area, so it needs no scratch.
+bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T);
 // ffn_norm folded into a forward: x = rmsnorm(x) * w (w NULL: unit weight).
 struct NormArgs {
     const float *w;
@@ -196,7 +206,7 @@ struct NormArgs {
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      char *work, const NormArgs *norm = nullptr);
+                      const NormArgs *norm = nullptr);
 size_t grouped_work_bytes(const qq_moe *m, int T);
 
 // LFM2 single-token forward (lfm2.hip).  Matvec modes: y = W x; hidden +=

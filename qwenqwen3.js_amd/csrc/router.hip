@@ -183,8 +183,11 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
             if (ks < KS) s += pv[i][ks];
         lg[i] = (lane + WAVE * i < E) ? (float)s : 0.0f;
     }
+    float bl[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) bl[i] = bias[min(lane + WAVE * i, E - 1)];
     WaveRoute<EPL> R;
-    wave_route<EPL>(lg, E, K, bias, softmax != 0, R);
+    wave_route<EPL>(lg, bl, E, K, softmax != 0, R);
     if (probs) {
 #pragma unroll
         for (int i = 0; i < EPL; i++) {

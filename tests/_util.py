@@ -43,3 +43,40 @@ def upload_layer(ctx, L):
         import qq_hip
         m.set_gating(qq_hip.GATING_SOFTMAX)
     return m
+
+
+def dense_moe_f64(L, x, hidden, idx, w, mask=None):
+    """The expert products of an MoE layer in float64 over the dequantised
+    weights, written independently of the C oracle's loops (dense matrices,
+    BLAS products, no fp32 rounding anywhere):
+
+        out[t] = hidden[t] + sum_k w[t,k] * down_e (silu(gate_e x_t) * up_e x_t),  e = idx[t,k]
+
+    with the routing (idx, w) taken as given -- the tests check it bit for
+    bit against the oracle first.  Experts in `mask` are skipped (their
+    weights are not renormalised, src/lfm2-engine.js:464).  It differs from
+    the reference only by the reference's fp32 roundings (~1e-7 relative)."""
+    import synth
+    H, F, E = L["H"], L["F"], L["E"]
+    x64 = np.asarray(x, np.float64).reshape(-1, H)
+    out = np.array(hidden, np.float64).reshape(-1, H)
+    idx = np.asarray(idx).reshape(x64.shape[0], -1)
+    w = np.asarray(w, np.float64).reshape(idx.shape)
+    nbH, nbF = (H + 31) // 32, (F + 31) // 32
+    gsz, dsz = F * nbH * 34, H * nbF * 34
+    for e in range(E):
+        if mask is not None and e in mask:
+            continue
+        t, k = np.nonzero(idx == e)
+        if t.size == 0:
+            continue
+        wg = synth.q8_0_dequant(L["gate"][e * gsz:(e + 1) * gsz], H, F)[0]   # [F, H]
+        wu = synth.q8_0_dequant(L["up"][e * gsz:(e + 1) * gsz], H, F)[0]
+        wd = synth.q8_0_dequant(L["down"][e * dsz:(e + 1) * dsz], F, H)[0]   # [H, F]
+        xs = x64[t]
+        g = xs @ wg.T
+        u = xs @ wu.T
+        h = g / (1.0 + np.exp(-g)) * u
+        y = h @ wd.T
+        np.add.at(out, t, w[t, k][:, None] * y)
+    return out

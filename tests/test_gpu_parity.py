@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 import synth
-from _util import full_layer, gpu_context, moe_delta, rel_l2, upload_layer
+from _util import dense_moe_f64, full_layer, gpu_context, moe_delta, rel_l2, upload_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -232,21 +232,33 @@ def test_moe_decode_batch64_full():
 
 @pytest.mark.parametrize("path", ["mfma", "fp32"])
 def test_moe_prefill_2048_skewed(path):
-    """2048-token chunk with Zipf-skewed routing: all top-K bit-exact, sampled rows checked
-    (MFMA path at 1e-2, fp32 grouped path at 1e-4)."""
+    """2048-token chunk with Zipf-skewed routing: all top-K bit-exact; sampled rows against
+    the oracle and every row against the float64 dense restatement (MFMA path at 1e-2,
+    fp32 path at 1e-4), so cold experts (< 10 rows) and the partial last fragments of hot
+    groups are all compared."""
     _say("prefill 2048", path)
     L = full_layer(2, bias="zipf")
     x, hid = synth.activations(303, 2048, 2048)
     rows = np.random.default_rng(0).choice(2048, 24, replace=False)
+    tol = TOL_MFMA if path == "mfma" else TOL_GEMV
     with mfma_min_tokens(512 if path == "mfma" else 0):
-        _, idx, w, probs = _check_moe(L, x, hid, rows=rows,
-                                      tol=TOL_MFMA if path == "mfma" else TOL_GEMV)
+        out, idx, w, probs = _check_moe(L, x, hid, rows=rows, tol=tol)
     r_idx, r_w, r_probs = oracle.moe_route(L, x)
     np.testing.assert_array_equal(idx, r_idx)
     np.testing.assert_array_equal(w, r_w)
     np.testing.assert_array_equal(probs, r_probs)
     counts = np.bincount(idx.ravel(), minlength=32)
     assert counts.max() >= 300 and counts.min() < 10, counts
+    dense = dense_moe_f64(L, x, hid, r_idx, r_w)
+    err = rel_l2(moe_delta(out, hid), dense - hid)
+    per_row = [rel_l2(moe_delta(out[t], hid[t]), dense[t] - hid[t]) for t in range(2048)]
+    _say("all rows rel_l2", err, "worst row", int(np.argmax(per_row)), max(per_row))
+    assert err < tol, err
+    assert max(per_row) < 2 * tol
+    # the coldest expert's rows on their own
+    cold = int(np.argmin(np.where(counts > 0, counts, 1 << 30)))
+    ct = np.nonzero((idx == cold).any(axis=1))[0]
+    assert rel_l2(moe_delta(out[ct], hid[ct]), dense[ct] - hid[ct]) < tol
 
 
 @pytest.mark.parametrize("case", [
