@@ -187,6 +187,15 @@ __device__ __forceinline__ void decompose_row(const float *v, int nch, int4 *q1,
     }
 }
 
+// 16 weight bytes read once per call: a non-temporal load, so the stream of
+// expert weights does not push the exchange tables and activations out of L2.
+__device__ __forceinline__ int4 load_stream16(const int8_t *p)
+{
+    typedef int v4i __attribute__((ext_vector_type(4)));
+    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ float f16_bits(uint32_t b) { return __half2float(__ushort_as_half((uint16_t)b)); }
 
 // q / d for 0 <= q < 2^20 and 1 <= d < 2^12 without an integer division:
@@ -218,7 +227,6 @@ struct ScaleRun {
 
 // Limits of one launch (checked by decode_supported on the host).
 constexpr int DEC_MAX_HW = 2048;               // h values of one group (K x F-range)
-constexpr int DEC_MAX_RED = 4096;              // K x F blocks of a group x down rows of a member
 constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read by one workgroup
 
 // NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
@@ -244,7 +252,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     __shared__ __align__(16) float hl[DEC_MAX_HW];
     __shared__ __align__(16) int4 hq1[DEC_MAX_HW / 16], hq2[DEC_MAX_HW / 16], hq3[DEC_MAX_HW / 16];
     __shared__ float hsig[DEC_MAX_HW / 16];
-    __shared__ float redd[DEC_MAX_RED];
+    __shared__ float sh_pd[2 * DEC_WAVES][32];   // sums of the (rank, row half) pairs
     __shared__ float pf[DEC_MAX_FIN];
     __shared__ uint32_t sh_tag;
     __shared__ int sh_fail;
@@ -397,8 +405,16 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     for (int i = 0; i < NBW; i++) goff[i] = (uint32_t)(min(NBW * wave + i, a.nbH - 1) * a.F + cf);
     // down: wave w takes the (rank, row half) pairs w, w + 8 over the group's
     // blocks, lane 2r + h row r of the half; row offsets within an expert
+    int pk2[2];   // ranks of this wave's two pairs
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
+        pk2[t] = min((NRH == 2) ? (p >> 1) : p, a.K - 1);
+    }
     uint32_t doff[DEC_DCH];
     bool dsec[DEC_DCH];   // unit of the second pair
+    bool don[DEC_DCH];    // unit in use (pair, block and row exist)
+    int dhc[DEC_DCH];     // its 16-value chunk of the group's h values
 #pragma unroll
     for (int i = 0; i < DEC_DCH; i++) {
         const int t = min(div_small(i, inv_frb), 1);
@@ -408,12 +424,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const int rl = min(rh * 32 + cs, max(RMm - 1, 0));
         doff[i] = (uint32_t)(min(fb0 + bl, a.nbF - 1) * a.H + min(r0 + rl, a.H - 1));
         dsec[i] = t != 0;
-    }
-    int pk2[2];   // ranks of this wave's two pairs
-#pragma unroll
-    for (int t = 0; t < 2; t++) {
-        const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
-        pk2[t] = min((NRH == 2) ? (p >> 1) : p, a.K - 1);
+        don[i] = i < NUW && wave + DEC_WAVES * t < NP2 && rh * 32 + cs < RMm;
+        dhc[i] = (pk2[t] * FRb + bl) * 2 + hh;
     }
 
     // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321), taken by
@@ -473,37 +485,39 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     ScaleRun<NBW> gs, us;
     uint32_t ddb[DEC_DCH];
     bool cok = false;
+    const int eg = ok ? idx_w[ck] : 0;
+    const int ed0 = ok ? idx_w[pk2[0]] : 0, ed1 = ok ? idx_w[pk2[1]] : 0;
+    const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
     {
-        const int eg = ok ? idx_w[ck] : 0;
+        // The scales go out first: small requests to pages the weight rows do
+        // not touch are otherwise served after the whole stream.  The pair's
+        // gate scales come with the even lane, its up scales with the odd one
+        // (applied after the block products).
+        const size_t grow = (size_t)eg * a.F + cf;
+        gs.load((hh ? a.udcm : a.gdcm) + grow * a.nbpH + NBW * wave);
+#pragma unroll
+        for (int i = 0; i < DEC_DCH; i++) ddb[i] = dd16[(dsec[i] ? dst1 : dst0) + doff[i]];
         cok = ok && cs < nc && !((mrank >> ck) & 1u);
         const int8_t *gbase = a.gq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
         const int8_t *ubase = a.uq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
 #pragma unroll
         for (int i = 0; i < NBW; i++) {
-            gq[i] = *reinterpret_cast<const int4 *>(gbase + (size_t)goff[i] * QK);
-            uq[i] = *reinterpret_cast<const int4 *>(ubase + (size_t)goff[i] * QK);
+            gq[i] = load_stream16(gbase + (size_t)goff[i] * QK);
+            uq[i] = load_stream16(ubase + (size_t)goff[i] * QK);
         }
-        // the scales: the pair's gate scales come with the even lane, its up
-        // scales with the odd one (applied after the block products)
-        const size_t grow = (size_t)eg * a.F + cf;
-        gs.load((hh ? a.udcm : a.gdcm) + grow * a.nbpH + NBW * wave);
         __builtin_amdgcn_sched_barrier(0);
     }
     // Every wave's gate/up requests go out before any down request: a CU's
     // requests are served about in issue order, so the workgroup receives
-    // all its gate/up bytes first (its h is ready early) and the down bytes
+    // its gate/up bytes first (its h is ready early) and the down bytes
     // arrive while the h values are exchanged.  (Loads also complete in
     // issue order within a wave, so the gate/up products never wait for the
     // down rows.)
     lds_barrier();
     {
-        const int ed0 = ok ? idx_w[pk2[0]] : 0, ed1 = ok ? idx_w[pk2[1]] : 0;
-        const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++)
-            dq[i] = *reinterpret_cast<const int4 *>(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
-#pragma unroll
-        for (int i = 0; i < DEC_DCH; i++) ddb[i] = dd16[(dsec[i] ? dst1 : dst0) + doff[i]];
+            dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
         __builtin_amdgcn_sched_barrier(0);
     }
     // ---- weights (lfm2-engine.js:444-447; qwen3-engine.js:317-321), worked
@@ -621,40 +635,41 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     if (ok && NP2 > 0) {
         decompose_row(hl, 2 * a.K * FRb, hq1, hq2, hq3, hsig);
         lds_barrier();
-        // ---- partial down products over the group's blocks ----
+        // ---- partial down products: lane 2r + h of wave w adds up the
+        // products of its row r of pairs w and w + 8 over the group's blocks
+        // (in block order), straight from registers ----
+        float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++) {
-            if (i >= NUW) continue;
-            const int t = div_small(i, inv_frb);
-            const int bl = i - t * FRb;
-            const int p = wave + DEC_WAVES * t;
-            if (p >= NP2) continue;
-            const int k = (NRH == 2) ? (p >> 1) : p;
-            const int rh = (NRH == 2) ? (p & 1) : 0;
-            const int rl = rh * 32 + cs;
-            const int hc = (k * FRb + bl) * 2 + hh;
+            const int hc = dhc[i];
             // the scale bits pass an empty asm here (ordered after the
             // barriers above), so the compiler cannot convert them -- and wait
             // for the down loads -- before the gate/up products
             uint32_t db = ddb[i];
             asm volatile("" : "+v"(db));
-            const float sd = (rl < RMm) ? f16_bits(db) : 0.0f;
-            float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * sd;
-            y += xor1_dpp(y);
-            if (hh == 0) redd[(k * FRb + bl) * RMP + rl] = y;
+            const float sd = don[i] ? f16_bits(db) : 0.0f;
+            const float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * sd;
+            acc0 += dsec[i] ? 0.0f : y;
+            acc1 += dsec[i] ? y : 0.0f;
         }
-        lds_barrier();
-        for (int t = tid - DEC_THREADS / 2; t >= 0 && t < a.K * RMm; t += DEC_THREADS / 2) {
-            const int k = t / RMm;
-            const int rl = t - k * RMm;
-            if ((mrank >> k) & 1u) continue;
-            float v[8];
-#pragma unroll
-            for (int bl = 0; bl < 8; bl++) v[bl] = redd[(k * FRb + min(bl, FRb - 1)) * RMP + rl];
-            float s = 0.0f;
-#pragma unroll
-            for (int bl = 0; bl < 8; bl++) s += (bl < FRb) ? v[bl] : 0.0f;
-            store_dev(&a.part[((size_t)gx * a.K + k) * a.H + r0 + rl], tag_word(tag, s));
+        acc0 += xor1_dpp(acc0);
+        acc1 += xor1_dpp(acc1);
+        if (hh == 0) {
+            sh_pd[wave][cs] = acc0;
+            sh_pd[DEC_WAVES + wave][cs] = acc1;
+        }
+    }
+    lds_barrier();
+    // waves 4..7 publish the pairs' sums (the polling waves 0..3 then hold no
+    // device stores to wait for)
+    if (ok && NP2 > 0) {
+        for (int t = tid - DEC_THREADS / 2; t >= 0 && t < NP2 * 32; t += DEC_THREADS / 2) {
+            const int p = t >> 5;
+            const int r = t & 31;
+            const int k = (NRH == 2) ? (p >> 1) : p;
+            const int rl = ((NRH == 2) ? (p & 1) : 0) * 32 + r;
+            if (rl < RMm && !((mrank >> k) & 1u))
+                store_dev(&a.part[((size_t)gx * a.K + k) * a.H + r0 + rl], tag_word(tag, sh_pd[p][r]));
         }
     }
 
@@ -689,14 +704,24 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     }
     if (ok && tid < RFm) {
         float acc = 0.0f;
-        for (int k = 0; k < a.K; k++) {
-            float v[DEC_GROUPS];
+        for (int k0 = 0; k0 < a.K; k0 += 4) {   // four ranks' reads issued together
+            float v[4][DEC_GROUPS];
+            double w4[4];
 #pragma unroll
-            for (int x = 0; x < DEC_GROUPS; x++) v[x] = pf[(x * a.K + k) * RF + tid];
-            float y = 0.0f;
+            for (int kk = 0; kk < 4; kk++) {
+                const int k = min(k0 + kk, a.K - 1);
 #pragma unroll
-            for (int x = 0; x < DEC_GROUPS; x++) y += v[x];
-            if (!((mrank >> k) & 1u)) acc = (float)((double)acc + sh_w[wave][k] * (double)y);
+                for (int x = 0; x < DEC_GROUPS; x++) v[kk][x] = pf[(x * a.K + k) * RF + tid];
+                w4[kk] = sh_w[0][k];
+            }
+#pragma unroll
+            for (int kk = 0; kk < 4; kk++) {
+                float y = 0.0f;
+#pragma unroll
+                for (int x = 0; x < DEC_GROUPS; x++) y += v[kk][x];
+                const int k = k0 + kk;
+                if (k < a.K && !((mrank >> k) & 1u)) acc = (float)((double)acc + w4[kk] * (double)y);
+            }
         }
         a.hidden[q0 + tid] = hin + acc;
     }
@@ -729,7 +754,7 @@ bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T)
     const int ppw = (m->K * nrh + DEC_WAVES - 1) / DEC_WAVES;
     return (m->E + M - 1) / M <= 8 && RM <= 64 && cpm <= DEC_CCH && ppw <= 2 && ppw * frb <= DEC_DCH &&
            m->K * frb * QK <= DEC_MAX_HW &&
-           m->K * frb * nrh * 32 <= DEC_MAX_RED && DEC_GROUPS * m->K * RF + G <= DEC_MAX_FIN &&
+           DEC_GROUPS * m->K * RF + G <= DEC_MAX_FIN &&
            (size_t)m->K * m->F <= SYNC_H_WORDS && (size_t)m->K * m->H * DEC_GROUPS <= SYNC_P_WORDS;
 }
 

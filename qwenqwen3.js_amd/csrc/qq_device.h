@@ -122,6 +122,16 @@ __device__ __forceinline__ float xor2_dpp(float v)
     return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf, false));
 }
 
+// Maximum over each row of 16 lanes (all 16 active), the same value in every
+// lane of the row: rotations by 8, 4, 2 and 1 within the row.
+__device__ __forceinline__ float row_max16(float v)
+{
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x128, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x124, 0xf, 0xf, false)));
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x122, 0xf, 0xf, false)));
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x121, 0xf, 0xf, false)));
+}
+
 // Maximum over the 64 lanes of a wavefront (all lanes active), the same value
 // in every lane: quads and rows of 16 by DPP, then the four row maxima.
 __device__ __forceinline__ float wave_max_dpp(float v)
@@ -283,6 +293,19 @@ __device__ __forceinline__ uint32_t pack4_i8(int a, int b, int c, int d)
            ((uint32_t)(d & 0xff) << 24);
 }
 
+// t (|t| <= 127) -> three int8 levels, t ~ a1 + a2 / 254 + a3 / 254^2.
+__device__ __forceinline__ void decompose1(float t, int &q1, int &q2, int &q3)
+{
+    const float a1 = fminf(fmaxf(rintf(t), -127.0f), 127.0f);
+    const float t2 = (t - a1) * 254.0f;
+    const float a2 = fminf(fmaxf(rintf(t2), -127.0f), 127.0f);
+    const float t3 = (t2 - a2) * 254.0f;
+    const float a3 = fminf(fmaxf(rintf(t3), -127.0f), 127.0f);
+    q1 = (int)a1;
+    q2 = (int)a2;
+    q3 = (int)a3;
+}
+
 // Three levels of four values, packed as they are formed (few live registers).
 __device__ __forceinline__ void decompose4(const float4 v, float inv, uint32_t &p1, uint32_t &p2,
                                            uint32_t &p3)
@@ -290,17 +313,7 @@ __device__ __forceinline__ void decompose4(const float4 v, float inv, uint32_t &
     const float vv[4] = {v.x, v.y, v.z, v.w};
     int q1[4], q2[4], q3[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float t = vv[i] * inv;
-        const float a1 = fminf(fmaxf(rintf(t), -127.0f), 127.0f);
-        const float t2 = (t - a1) * 254.0f;
-        const float a2 = fminf(fmaxf(rintf(t2), -127.0f), 127.0f);
-        const float t3 = (t2 - a2) * 254.0f;
-        const float a3 = fminf(fmaxf(rintf(t3), -127.0f), 127.0f);
-        q1[i] = (int)a1;
-        q2[i] = (int)a2;
-        q3[i] = (int)a3;
-    }
+    for (int i = 0; i < 4; i++) decompose1(vv[i] * inv, q1[i], q2[i], q3[i]);
     p1 = pack4_i8(q1[0], q1[1], q1[2], q1[3]);
     p2 = pack4_i8(q2[0], q2[1], q2[2], q2[3]);
     p3 = pack4_i8(q3[0], q3[1], q3[2], q3[3]);
