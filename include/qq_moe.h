@@ -130,6 +130,22 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
                        int T, const uint8_t *mask, int32_t *idx_dev, double *w_dev,
                        float *probs_dev);
 
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The same as qq_moe_forward_dev, but the forward's
+ * scratch is a fixed array of QQ_NOALLOC_SCRATCH_BYTES per GPU (32 MiB,
+ * held until the process ends) instead of the context's arena, so the call
+ * allocates nothing.  A T whose scratch does not fit (about 500 rows at
+ * LFM2-8B-A1B shapes; batch-1 decode needs none) is rejected with
+ * QQ_E_ARG before anything is enqueued.  Every call on one GPU shares that
+ * GPU's array (the kernels write all of it that they read, so nothing needs
+ * clearing between calls): calls that overlap on one GPU -- two streams, two
+ * contexts -- race. */
+#define QQ_NOALLOC_SCRATCH_BYTES (32u << 20)
+int qq_moe_forward_noalloc_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev,
+                               int T, const uint8_t *mask, int32_t *idx_dev, double *w_dev,
+                               float *probs_dev);
+
 /* The FFN sub-block of an MoE layer (src/lfm2-engine.js:250-257): the
  * ffn_norm RMSNorm of the residual row (src/tensor.js:103-114), then the MoE
  * block on it:

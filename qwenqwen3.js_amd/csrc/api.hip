@@ -4,6 +4,11 @@
 #include <cstdlib>
 #include <new>
 
+// Scratch of qq_moe_forward_noalloc_dev: one array per GPU, held until the
+// process ends.  Host code reaches it only through the address that
+// hipGetSymbolAddress gave for that device (qq_ctx::noalloc_scratch).
+static __device__ __align__(256) char scratch[QQ_NOALLOC_SCRATCH_BYTES];
+
 namespace qq {
 
 static thread_local char g_init_err[512] = "";
@@ -190,6 +195,13 @@ int qq_init(int device, qq_ctx **out)
     if (!ctx) return set_error(nullptr, "host allocation failed");
     ctx->device = device;
     ctx->num_cus = prop.multiProcessorCount;
+    // this device's copy of the fixed scratch array (the device is current)
+    void *fixed = nullptr;
+    if ((e = hipGetSymbolAddress(&fixed, HIP_SYMBOL(scratch))) != hipSuccess || !fixed) {
+        delete ctx;
+        return check_hip(nullptr, e != hipSuccess ? e : hipErrorInvalidSymbol, "hipGetSymbolAddress(scratch)");
+    }
+    ctx->noalloc_scratch = static_cast<char *>(fixed);
     if ((e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking)) != hipSuccess) {
         delete ctx;
         return check_hip(nullptr, e, "hipStreamCreate");
@@ -505,13 +517,12 @@ static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
            align256((size_t)Tc * m->K * 8) + align256(work);
 }
 
-// x, hidden (and the optional outputs) are device pointers; scratch starts at `base`.
-static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                        const MaskBits &mask, int32_t *idx, double *w, float *probs, size_t base)
+// x, hidden (and the optional outputs) are device pointers; s holds
+// forward_scratch(ctx, m, T) bytes (256-byte aligned).  Allocates nothing.
+static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                       const MaskBits &mask, int32_t *idx, double *w, float *probs, char *s)
 {
-    int rc = ensure_scratch(ctx, base + forward_scratch(ctx, m, T));
-    if (rc) return rc;
-    char *s = static_cast<char *>(ctx->scratch) + base;
+    int rc = QQ_OK;
     if (decode_supported(ctx, m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs);
     const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
     double *part = reinterpret_cast<double *>(s);
@@ -536,6 +547,15 @@ static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hid
     return QQ_OK;
 }
 
+// The same with the context's arena as scratch, from `base` on.
+static int forward_impl(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
+                        const MaskBits &mask, int32_t *idx, double *w, float *probs, size_t base)
+{
+    const int rc = ensure_scratch(ctx, base + forward_scratch(ctx, m, T));
+    if (rc) return rc;
+    return forward_run(ctx, m, x, hidden, T, mask, idx, w, probs, static_cast<char *>(ctx->scratch) + base);
+}
+
 static int forward_check(qq_ctx *ctx, const qq_moe *m, int T)
 {
     if (!ctx) return QQ_E_ARG;
@@ -554,6 +574,22 @@ int qq_moe_forward_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *
     MaskBits mb;
     if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
     return forward_impl(ctx, m, x_dev, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, 0);
+}
+
+int qq_moe_forward_noalloc_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev, int T,
+                               const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev)
+{
+    int rc = forward_check(ctx, m, T);
+    if (rc || T == 0) return rc;
+    if (!x_dev || !hidden_dev) return set_error(ctx, "moe_forward_noalloc: NULL buffer");
+    const size_t need = forward_scratch(ctx, m, T);
+    if (need > QQ_NOALLOC_SCRATCH_BYTES)
+        return set_error(ctx, "moe_forward_noalloc: T=%d needs %zu scratch bytes, the fixed array holds %zu", T,
+                         need, (size_t)QQ_NOALLOC_SCRATCH_BYTES);
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
+    return forward_run(ctx, m, x_dev, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, ctx->noalloc_scratch);
 }
 
 int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev, const float *norm_w_dev,

@@ -99,6 +99,9 @@ struct qq_ctx {
     // device scratch arena (grown on demand; one arena per context)
     void *scratch;
     size_t scratch_bytes;
+    // this device's fixed scratch array (qq_moe_forward_noalloc_dev), from
+    // hipGetSymbolAddress at qq_init
+    char *noalloc_scratch;
     // pinned host staging for the host-pointer entry points
     void *pinned;
     size_t pinned_bytes;

@@ -29,7 +29,7 @@ EXPORTS = (
     "qq_q8_0_upload", "qq_q8_0_upload_dev", "qq_tensor_release",
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
-    "qq_moe_forward_norm_dev", "qq_moe_set_gating",
+    "qq_moe_forward_norm_dev", "qq_moe_forward_noalloc_dev", "qq_moe_set_gating",
     "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
@@ -103,6 +103,7 @@ def load():
         "qq_moe_release": (I, [P, P]),
         "qq_moe_forward": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_dev": (I, [P, P, P, P, I, P, P, P, P]),
+        "qq_moe_forward_noalloc_dev": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_norm_dev": (I, [P, P, P, P, ctypes.c_double, I, P, P, P, P]),
         "qq_moe_set_gating": (I, [P, P, I]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
@@ -452,6 +453,19 @@ class MoeLayer:
         self.ctx.check(self.ctx.L.qq_moe_forward_dev(self.ctx.h, self.h, ctypes.c_void_p(x_ptr),
                                                      ctypes.c_void_p(hidden_ptr), T, _ptr(m), vp(idx_ptr),
                                                      vp(w_ptr), vp(probs_ptr)), "qq_moe_forward_dev")
+
+    def forward_noalloc_dev(self, x_ptr, hidden_ptr, T, mask=None, idx_ptr=None, w_ptr=None, probs_ptr=None):
+        """forward_dev with the fixed per-GPU scratch array (qq_moe_forward_noalloc_dev)."""
+        m = None
+        if mask is not None:
+            m = np.zeros(self.E, np.uint8)
+            for e in mask:
+                m[e] = 1
+        vp = lambda p: None if p is None else ctypes.c_void_p(p)
+        self.ctx.check(self.ctx.L.qq_moe_forward_noalloc_dev(self.ctx.h, self.h, ctypes.c_void_p(x_ptr),
+                                                             ctypes.c_void_p(hidden_ptr), T, _ptr(m),
+                                                             vp(idx_ptr), vp(w_ptr), vp(probs_ptr)),
+                       "qq_moe_forward_noalloc_dev")
 
     def forward_norm_dev(self, hidden_ptr, T, norm_w_ptr=None, eps=1e-5, mask=None, idx_ptr=None,
                          w_ptr=None, probs_ptr=None):
