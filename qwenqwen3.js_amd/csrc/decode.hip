@@ -230,8 +230,9 @@ constexpr int DEC_MAX_HW = 2048;               // h values of one group (K x F-r
 constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read by one workgroup
 
 // NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
-// experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64)).
-template <int NBW, int RE, int EPL>
+// experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64));
+// PP2: a wave takes two (rank, row half) pairs of down rows (K x halves > 8).
+template <int NBW, int RE, int EPL, bool PP2>
 __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 {
     constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
@@ -243,15 +244,17 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     __shared__ double rsum[RE][DEC_WAVES];
     __shared__ double nsum[DEC_WAVES];
     __shared__ float sh_lg[EPL * WAVE];
-    __shared__ int sh_idx[DEC_WAVES][MAX_K];     // each wave's own copy of the routing
-    __shared__ __align__(16) float sh_pr[DEC_WAVES][MAX_K];
-    __shared__ double sh_w[DEC_WAVES][MAX_K];
-    __shared__ __align__(16) uint64_t sh_key[DEC_WAVES][32 * RE];
+    __shared__ int sh_idx[MAX_K];                // the routing, formed by wave 0
+    __shared__ __align__(16) float sh_pr[MAX_K];
+    __shared__ double sh_w[MAX_K];
+    __shared__ uint32_t sh_mrank;
+    __shared__ __align__(16) uint64_t sh_key[32 * RE];
     __shared__ float redg[DEC_WAVES][DEC_CCH];
     __shared__ float redu[DEC_WAVES][DEC_CCH];
     __shared__ __align__(16) float hl[DEC_MAX_HW];
-    __shared__ __align__(16) int4 hq1[DEC_MAX_HW / 16], hq2[DEC_MAX_HW / 16], hq3[DEC_MAX_HW / 16];
-    __shared__ float hsig[DEC_MAX_HW / 16];
+    // (16 chunks of padding: the down units past a pair's blocks read there)
+    __shared__ __align__(16) int4 hq1[DEC_MAX_HW / 16 + 16], hq2[DEC_MAX_HW / 16 + 16], hq3[DEC_MAX_HW / 16 + 16];
+    __shared__ float hsig[DEC_MAX_HW / 16 + 16];
     __shared__ float sh_pd[2 * DEC_WAVES][32];   // sums of the (rank, row half) pairs
     __shared__ float pf[DEC_MAX_FIN];
     __shared__ uint32_t sh_tag;
@@ -388,7 +391,6 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int r0 = mi * RM;
     const int RMm = max(min(RM, a.H - r0), 0);
     const int NRH = RM > 32 ? 2 : 1;                  // 32-row halves of the member's rows
-    const int RMP = NRH * 32;
     const int NP2 = (FRb > 0 && RMm > 0) ? a.K * NRH : 0;   // (rank, row half) pairs
     const int PPW = (NP2 + DEC_WAVES - 1) / DEC_WAVES;      // pairs per wave
     const int NUW = PPW * FRb;                               // down units per lane (<= 8)
@@ -417,7 +419,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     int dhc[DEC_DCH];     // its 16-value chunk of the group's h values
 #pragma unroll
     for (int i = 0; i < DEC_DCH; i++) {
-        const int t = min(div_small(i, inv_frb), 1);
+        const int t = PP2 ? min(div_small(i, inv_frb), 1) : 0;
         const int bl = min(i - t * FRb, max(FRb - 1, 0));
         const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
         const int rh = (NRH == 2) ? (p & 1) : 0;
@@ -425,19 +427,20 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         doff[i] = (uint32_t)(min(fb0 + bl, a.nbF - 1) * a.H + min(r0 + rl, a.H - 1));
         dsec[i] = t != 0;
         don[i] = i < NUW && wave + DEC_WAVES * t < NP2 && rh * 32 + cs < RMm;
-        dhc[i] = (pk2[t] * FRb + bl) * 2 + hh;
+        // one pair: the units' chunks are consecutive (immediate LDS offsets)
+        dhc[i] = PP2 ? (pk2[t] * FRb + bl) * 2 + hh : (pk2[0] * FRb + i) * 2 + hh;
     }
 
-    // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321), taken by
-    // every wave on its own (no workgroup barrier): scores, then the rank of
-    // each expert among them -- a stable descending sort, ties to the lower
-    // index -- from 64-bit keys (order-preserving score bits, complemented
-    // index), then the top K ----
+    // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321) and the
+    // weights (lfm2-engine.js:444-447; qwen3-engine.js:317-321), formed by
+    // wave 0 alone (one wave per SIMD runs faster than eight sharing four):
+    // scores, then the rank of each expert among them -- a stable descending
+    // sort, ties to the lower index -- from 64-bit keys (order-preserving
+    // score bits, complemented index), the top K, and w_k = p_k / S in rank
+    // order ----
     constexpr int SLOTS = 32 * RE;   // >= E
-    float pr[EPL];
-    uint32_t mrank = 0;   // bit k: the rank-k expert is masked (lfm2-engine.js:464)
-    if (ok) {
-        float lg[EPL];
+    if (ok && wave == 0) {
+        float lg[EPL], pr[EPL];
 #pragma unroll
         for (int t = 0; t < EPL; t++) lg[t] = sh_lg[min(lane + WAVE * t, a.E - 1)];
         if (a.softmax) {
@@ -454,14 +457,16 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const uint32_t u = __float_as_uint(sc);
             const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
             key[t] = (e < a.E) ? (((uint64_t)ord << 32) | (uint32_t)~e) : 0;
-            if (e < SLOTS) sh_key[wave][e] = key[t];
+            if (e < SLOTS) sh_key[e] = key[t];
         }
+        // (a wave's LDS accesses are done in order, so its lanes read what
+        // its other lanes wrote above without a barrier)
         int rank[EPL];
 #pragma unroll
         for (int t = 0; t < EPL; t++) rank[t] = 0;
 #pragma unroll 16
         for (int u = 0; u < SLOTS / 2; u++) {
-            const ulonglong2 q = reinterpret_cast<const ulonglong2 *>(sh_key[wave])[u];
+            const ulonglong2 q = reinterpret_cast<const ulonglong2 *>(sh_key)[u];
 #pragma unroll
             for (int t = 0; t < EPL; t++) rank[t] += (int)(q.x > key[t]) + (int)(q.y > key[t]);
         }
@@ -469,14 +474,43 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         for (int t = 0; t < EPL; t++) {
             const int e = lane + WAVE * t;
             if (e < a.E && rank[t] < a.K) {
-                sh_idx[wave][rank[t]] = e;
-                sh_pr[wave][rank[t]] = pr[t];
+                sh_idx[rank[t]] = e;
+                sh_pr[rank[t]] = pr[t];
             }
         }
-        const uint64_t mb = __ballot(lane < a.K && mask_has(a.mask, sh_idx[wave][min(lane, MAX_K - 1)]));
-        mrank = (uint32_t)mb;
+        // bit k: the rank-k expert is masked (lfm2-engine.js:464)
+        const uint64_t mb = __ballot(lane < a.K && mask_has(a.mask, sh_idx[min(lane, MAX_K - 1)]));
+        float pk[MAX_K];
+#pragma unroll
+        for (int u = 0; u < MAX_K / 4; u++) {
+            const float4 v = reinterpret_cast<const float4 *>(sh_pr)[u];
+            pk[4 * u] = v.x;
+            pk[4 * u + 1] = v.y;
+            pk[4 * u + 2] = v.z;
+            pk[4 * u + 3] = v.w;
+        }
+        double sumW = a.softmax ? 0.0 : 1e-6;
+#pragma unroll
+        for (int k = 0; k < MAX_K; k++)
+            if (k < a.K) sumW = sumW + (double)pk[k];
+        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
+        const double wl = (double)sh_pr[min(lane, MAX_K - 1)] * inv;   // w of rank `lane`
+        if (lane < a.K) sh_w[lane] = wl;
+        if (lane == 0) sh_mrank = (uint32_t)mb;
+        if (j == 0) {
+            if (lane < a.K) {
+                if (a.out_idx) a.out_idx[lane] = sh_idx[lane];
+                if (a.out_w) a.out_w[lane] = wl;
+            }
+            if (a.out_probs) {
+#pragma unroll
+                for (int t = 0; t < EPL; t++)
+                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
+            }
+        }
     }
-    const int *idx_w = sh_idx[wave];   // this wave's copy
+    lds_barrier();
+    const uint32_t mrank = ok ? sh_mrank : 0u;
 
     // The loads are issued unconditionally (expert 0 stands in when the
     // routing failed), so no control-flow join sits between them and their
@@ -485,8 +519,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     ScaleRun<NBW> gs, us;
     uint32_t ddb[DEC_DCH];
     bool cok = false;
-    const int eg = ok ? idx_w[ck] : 0;
-    const int ed0 = ok ? idx_w[pk2[0]] : 0, ed1 = ok ? idx_w[pk2[1]] : 0;
+    const int eg = ok ? sh_idx[ck] : 0;
+    const int ed0 = ok ? sh_idx[pk2[0]] : 0, ed1 = ok ? sh_idx[pk2[1]] : 0;
     const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
     {
         // The scales go out first: small requests to pages the weight rows do
@@ -520,42 +554,6 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
         __builtin_amdgcn_sched_barrier(0);
     }
-    // ---- weights (lfm2-engine.js:444-447; qwen3-engine.js:317-321), worked
-    // out while the weight bytes stream in ----
-    double wk[MAX_K];
-    if (ok) {
-        float pk[MAX_K];
-#pragma unroll
-        for (int u = 0; u < MAX_K / 4; u++) {
-            const float4 v = reinterpret_cast<const float4 *>(sh_pr[wave])[u];
-            pk[4 * u] = v.x;
-            pk[4 * u + 1] = v.y;
-            pk[4 * u + 2] = v.z;
-            pk[4 * u + 3] = v.w;
-        }
-        double sumW = a.softmax ? 0.0 : 1e-6;
-#pragma unroll
-        for (int k = 0; k < MAX_K; k++)
-            if (k < a.K) sumW = sumW + (double)pk[k];
-        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
-#pragma unroll
-        for (int k = 0; k < MAX_K; k++) wk[k] = (k < a.K) ? (double)pk[k] * inv : 0.0;
-#pragma unroll
-        for (int k = 0; k < MAX_K; k++)
-            if (lane == k) sh_w[wave][k] = wk[k];
-        if (j == 0 && wave == 0) {
-            if (lane < a.K) {
-                if (a.out_idx) a.out_idx[lane] = idx_w[lane];
-                if (a.out_w) a.out_w[lane] = sh_w[0][lane];
-            }
-            if (a.out_probs) {
-#pragma unroll
-                for (int t = 0; t < EPL; t++)
-                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
-            }
-        }
-    }
-
     // ---- gate / up columns, SwiGLU (tensor.js:167-178), h out ----
     if (ok) {
         float dg[NBW], du[NBW];
@@ -647,10 +645,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             // for the down loads -- before the gate/up products
             uint32_t db = ddb[i];
             asm volatile("" : "+v"(db));
-            const float sd = don[i] ? f16_bits(db) : 0.0f;
-            const float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * sd;
-            acc0 += dsec[i] ? 0.0f : y;
-            acc1 += dsec[i] ? y : 0.0f;
+            const float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * f16_bits(db);
+            if (PP2) {
+                acc0 += (don[i] && !dsec[i]) ? y : 0.0f;
+                acc1 += (don[i] && dsec[i]) ? y : 0.0f;
+            } else {
+                acc0 += don[i] ? y : 0.0f;
+            }
         }
         acc0 += xor1_dpp(acc0);
         acc1 += xor1_dpp(acc1);
@@ -712,7 +713,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
                 const int k = min(k0 + kk, a.K - 1);
 #pragma unroll
                 for (int x = 0; x < DEC_GROUPS; x++) v[kk][x] = pf[(x * a.K + k) * RF + tid];
-                w4[kk] = sh_w[0][k];
+                w4[kk] = sh_w[k];
             }
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
@@ -759,20 +760,21 @@ bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T)
 }
 
 template <int NBW, int RE, int EPL>
-static void launch_t(qq_ctx *ctx, const DecodeArgs &a, dim3 grid)
+static void launch_t(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, bool pp2)
 {
-    QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL>), grid, dim3(DEC_THREADS), 0, a);
+    if (pp2) QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, true>), grid, dim3(DEC_THREADS), 0, a);
+    else QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, false>), grid, dim3(DEC_THREADS), 0, a);
 }
 
 // (RE, EPL) pairs: with M <= 32 members per group, ceil(E / M) <= RE implies
 // ceil(E / 64) <= EPL for these four
 template <int NBW>
-static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re)
+static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re, bool pp2)
 {
-    if (re <= 1) launch_t<NBW, 1, 1>(ctx, a, grid);
-    else if (re <= 2) launch_t<NBW, 2, 1>(ctx, a, grid);
-    else if (re <= 4) launch_t<NBW, 4, 2>(ctx, a, grid);
-    else launch_t<NBW, 8, 4>(ctx, a, grid);
+    if (re <= 1) launch_t<NBW, 1, 1>(ctx, a, grid, pp2);
+    else if (re <= 2) launch_t<NBW, 2, 1>(ctx, a, grid, pp2);
+    else if (re <= 4) launch_t<NBW, 4, 2>(ctx, a, grid, pp2);
+    else launch_t<NBW, 8, 4>(ctx, a, grid, pp2);
 }
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
@@ -820,12 +822,14 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     const int G = decode_grid(ctx);
     const int re = (m->E + G / DEC_GROUPS - 1) / (G / DEC_GROUPS);
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
+    const int RM = (m->H + G / DEC_GROUPS - 1) / (G / DEC_GROUPS);
+    const bool pp2 = m->K * (RM > 32 ? 2 : 1) > DEC_WAVES;
     const dim3 grid(G);
     prof_begin(ctx, K_DECODE);
-    if (nbw <= 1) launch_re<1>(ctx, a, grid, re);
-    else if (nbw <= 2) launch_re<2>(ctx, a, grid, re);
-    else if (nbw <= 4) launch_re<4>(ctx, a, grid, re);
-    else launch_re<8>(ctx, a, grid, re);
+    if (nbw <= 1) launch_re<1>(ctx, a, grid, re, pp2);
+    else if (nbw <= 2) launch_re<2>(ctx, a, grid, re, pp2);
+    else if (nbw <= 4) launch_re<4>(ctx, a, grid, re, pp2);
+    else launch_re<8>(ctx, a, grid, re, pp2);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
