@@ -57,6 +57,7 @@ namespace qq {
 constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * WAVE;
 constexpr int DEC_GROUPS = 8;                  // one per XCD
+static_assert(DEC_GROUPS == 8, "group blocks are found with shifts by 3");
 constexpr uint64_t DEC_WAIT_TICKS = 5000000;   // 50 ms at the 100 MHz wall clock
 constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the group's own table, then the copy
 constexpr int DEC_CCH = 32;                    // gate/up columns per chunk (two lanes each)
@@ -167,24 +168,47 @@ __device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uin
     return *sh_fail == 0;
 }
 
-// 16-value chunks of the LDS row v[0, 16 * nch) -> three int8 levels and the
-// chunk scale, four lanes a chunk (lane 4c + q takes values 16c + 4q ..).
-__device__ __forceinline__ void decompose_row(const float *v, int nch, int4 *q1, int4 *q2, int4 *q3,
-                                              float *sig)
+// 32-value blocks of the LDS row v[0, 32 nblk) -> three int8 levels (row l of
+// lev, LS bytes apart, holds level l at the values' positions) and the block
+// scale, eight lanes a block (lane 8b + q takes values 32b + 4q .. 32b + 4q + 3).
+template <int LS>
+__device__ __forceinline__ void decompose32(const float *v, int nblk, int8_t *lev, float *sig)
 {
-    for (int t = threadIdx.x; t < 4 * nch; t += DEC_THREADS) {
+    for (int t = threadIdx.x; t < 8 * nblk; t += DEC_THREADS) {
         const float4 f = reinterpret_cast<const float4 *>(v)[t];
         float m = fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w)));
         m = fmaxf(m, xor1_dpp(m));
         m = fmaxf(m, xor2_dpp(m));
+        m = fmaxf(m, __shfl_xor(m, 4));
         const float inv = (m > 0.0f) ? 127.0f / m : 0.0f;
         uint32_t p1, p2, p3;
         decompose4(f, inv, p1, p2, p3);
-        reinterpret_cast<uint32_t *>(q1)[t] = p1;
-        reinterpret_cast<uint32_t *>(q2)[t] = p2;
-        reinterpret_cast<uint32_t *>(q3)[t] = p3;
-        if ((t & 3) == 0) sig[t >> 2] = m * (1.0f / 127.0f);
+        reinterpret_cast<uint32_t *>(lev)[t] = p1;
+        reinterpret_cast<uint32_t *>(lev + LS)[t] = p2;
+        reinterpret_cast<uint32_t *>(lev + 2 * LS)[t] = p3;
+        if ((t & 7) == 0) sig[t >> 3] = m * (1.0f / 127.0f);
     }
+}
+
+typedef int mf_v4i __attribute__((ext_vector_type(4)));
+typedef int mf_v16i __attribute__((ext_vector_type(16)));
+
+// One 32 x 32 x 32 int8 product on the matrix cores, C[m][n] = sum_k A[m][k]
+// B[k][n]: lane l holds 16 bytes of row l % 32 of A and the same 16 k of
+// column l % 32 of B (any split of k that A and B share gives the same sum);
+// C[m][n] comes back in lane n + 32 ((m / 4) % 2), element 4 (m / 8) + m % 4.
+__device__ __forceinline__ mf_v16i mfma_i8(const int4 a, const int4 b)
+{
+    const mf_v4i av = {a.x, a.y, a.z, a.w};
+    const mf_v4i bv = {b.x, b.y, b.z, b.w};
+    const mf_v16i z = {};
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z, 0, 0, 0);
+}
+
+// The three levels' sums in rows 0..2 of C (lanes 0..31): c0 + c1/254 + c2/254^2.
+__device__ __forceinline__ float lev3_sum(const mf_v16i c)
+{
+    return fmaf(fmaf((float)c[2], 1.0f / 254.0f, (float)c[1]), 1.0f / 254.0f, (float)c[0]);
 }
 
 // 16 weight bytes read once per call: a non-temporal load, so the stream of
@@ -236,11 +260,12 @@ template <int NBW, int RE, int EPL, bool PP2>
 __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 {
     constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
-    constexpr int NHB = XN / 16;                // 16-value chunks of x
     constexpr int XPT = (XN + DEC_THREADS - 1) / DEC_THREADS;
     __shared__ __align__(16) float xl[XN];
-    __shared__ __align__(16) int4 xq1[NHB], xq2[NHB], xq3[NHB];
-    __shared__ float xsig[NHB];
+    // x and h in three int8 levels (rows 0..2) and a row of zeros (row 3):
+    // lane l of an MFMA reads row min(l % 32, 3)
+    __shared__ __align__(16) int8_t xlev[4][XN];
+    __shared__ float xsig[XN / QK];
     __shared__ double rsum[RE][DEC_WAVES];
     __shared__ double nsum[DEC_WAVES];
     __shared__ float sh_lg[EPL * WAVE];
@@ -252,9 +277,9 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     __shared__ float redg[DEC_WAVES][DEC_CCH];
     __shared__ float redu[DEC_WAVES][DEC_CCH];
     __shared__ __align__(16) float hl[DEC_MAX_HW];
-    // (16 chunks of padding: the down units past a pair's blocks read there)
-    __shared__ __align__(16) int4 hq1[DEC_MAX_HW / 16 + 16], hq2[DEC_MAX_HW / 16 + 16], hq3[DEC_MAX_HW / 16 + 16];
-    __shared__ float hsig[DEC_MAX_HW / 16 + 16];
+    // (8 blocks of padding: the down units past a pair's blocks read there)
+    __shared__ __align__(16) int8_t hlev[4][DEC_MAX_HW + 8 * QK];
+    __shared__ float hsig[DEC_MAX_HW / QK + 8];
     __shared__ float sh_pd[2 * DEC_WAVES][32];   // sums of the (rank, row half) pairs
     __shared__ float pf[DEC_MAX_FIN];
     __shared__ uint32_t sh_tag;
@@ -364,8 +389,11 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             for (int c = 0; c < SYNC_REPLICAS; c++) store_dev(&a.rdev[(size_t)c * SYNC_REPLICA_WORDS + e], word);
         }
     }
-    // x -> three int8 levels for the v_dot4 products
-    decompose_row(xl, NHB, xq1, xq2, xq3, xsig);
+    // x -> three int8 levels for the MFMA products; the rows of zeros
+    decompose32<XN>(xl, XN / QK, &xlev[0][0], xsig);
+    for (int i = tid; i < XN / 16; i += DEC_THREADS) reinterpret_cast<int4 *>(xlev[3])[i] = make_int4(0, 0, 0, 0);
+    for (int i = tid; i < (DEC_MAX_HW + 8 * QK) / 16; i += DEC_THREADS)
+        reinterpret_cast<int4 *>(hlev[3])[i] = make_int4(0, 0, 0, 0);
 
     bool ok;
     {
@@ -394,9 +422,9 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int NP2 = (FRb > 0 && RMm > 0) ? a.K * NRH : 0;   // (rank, row half) pairs
     const int PPW = (NP2 + DEC_WAVES - 1) / DEC_WAVES;      // pairs per wave
     const int NUW = PPW * FRb;                               // down units per lane (<= 8)
-    const int hh = lane & 1;
-    const int cs = lane >> 1;
-    // gate/up: lane 2c + h takes column c0 + c (lanes past the member's
+    const int hh = lane >> 5;
+    const int cs = lane & 31;
+    // gate/up: lane c + 32h takes column c0 + c (lanes past the member's
     // columns repeat its last one: no extra lines), bytes 16h .. 16h + 15 of
     // blocks NBW w .. NBW w + NBW - 1; row offsets within an expert
     const int cl = c0 + max(min(cs, nc - 1), 0);
@@ -406,7 +434,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 #pragma unroll
     for (int i = 0; i < NBW; i++) goff[i] = (uint32_t)(min(NBW * wave + i, a.nbH - 1) * a.F + cf);
     // down: wave w takes the (rank, row half) pairs w, w + 8 over the group's
-    // blocks, lane 2r + h row r of the half; row offsets within an expert
+    // blocks, lane r + 32h row r of the half; row offsets within an expert
     int pk2[2];   // ranks of this wave's two pairs
 #pragma unroll
     for (int t = 0; t < 2; t++) {
@@ -416,7 +444,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     uint32_t doff[DEC_DCH];
     bool dsec[DEC_DCH];   // unit of the second pair
     bool don[DEC_DCH];    // unit in use (pair, block and row exist)
-    int dhc[DEC_DCH];     // its 16-value chunk of the group's h values
+    int dhb[DEC_DCH];     // its 32-value block of the group's h values
 #pragma unroll
     for (int i = 0; i < DEC_DCH; i++) {
         const int t = PP2 ? min(div_small(i, inv_frb), 1) : 0;
@@ -427,20 +455,21 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         doff[i] = (uint32_t)(min(fb0 + bl, a.nbF - 1) * a.H + min(r0 + rl, a.H - 1));
         dsec[i] = t != 0;
         don[i] = i < NUW && wave + DEC_WAVES * t < NP2 && rh * 32 + cs < RMm;
-        // one pair: the units' chunks are consecutive (immediate LDS offsets)
-        dhc[i] = PP2 ? (pk2[t] * FRb + bl) * 2 + hh : (pk2[0] * FRb + i) * 2 + hh;
+        // one pair: the units' blocks are consecutive (immediate LDS offsets)
+        dhb[i] = PP2 ? pk2[t] * FRb + bl : pk2[0] * FRb + i;
     }
 
-    // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321) and the
-    // weights (lfm2-engine.js:444-447; qwen3-engine.js:317-321), formed by
+    // ---- routing (lfm2-engine.js:420-447; qwen3-engine.js:305-321), formed by
     // wave 0 alone (one wave per SIMD runs faster than eight sharing four):
     // scores, then the rank of each expert among them -- a stable descending
     // sort, ties to the lower index -- from 64-bit keys (order-preserving
-    // score bits, complemented index), the top K, and w_k = p_k / S in rank
-    // order ----
+    // score bits, complemented index), and the top K.  The weights w_k =
+    // p_k / S (lfm2-engine.js:444-447; qwen3-engine.js:317-321) follow once
+    // the weight loads are out ----
     constexpr int SLOTS = 32 * RE;   // >= E
+    float pr[EPL];
     if (ok && wave == 0) {
-        float lg[EPL], pr[EPL];
+        float lg[EPL];
 #pragma unroll
         for (int t = 0; t < EPL; t++) lg[t] = sh_lg[min(lane + WAVE * t, a.E - 1)];
         if (a.softmax) {
@@ -480,34 +509,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         }
         // bit k: the rank-k expert is masked (lfm2-engine.js:464)
         const uint64_t mb = __ballot(lane < a.K && mask_has(a.mask, sh_idx[min(lane, MAX_K - 1)]));
-        float pk[MAX_K];
-#pragma unroll
-        for (int u = 0; u < MAX_K / 4; u++) {
-            const float4 v = reinterpret_cast<const float4 *>(sh_pr)[u];
-            pk[4 * u] = v.x;
-            pk[4 * u + 1] = v.y;
-            pk[4 * u + 2] = v.z;
-            pk[4 * u + 3] = v.w;
-        }
-        double sumW = a.softmax ? 0.0 : 1e-6;
-#pragma unroll
-        for (int k = 0; k < MAX_K; k++)
-            if (k < a.K) sumW = sumW + (double)pk[k];
-        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
-        const double wl = (double)sh_pr[min(lane, MAX_K - 1)] * inv;   // w of rank `lane`
-        if (lane < a.K) sh_w[lane] = wl;
         if (lane == 0) sh_mrank = (uint32_t)mb;
-        if (j == 0) {
-            if (lane < a.K) {
-                if (a.out_idx) a.out_idx[lane] = sh_idx[lane];
-                if (a.out_w) a.out_w[lane] = wl;
-            }
-            if (a.out_probs) {
-#pragma unroll
-                for (int t = 0; t < EPL; t++)
-                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
-            }
-        }
     }
     lds_barrier();
     const uint32_t mrank = ok ? sh_mrank : 0u;
@@ -524,11 +526,10 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
     {
         // The scales go out first: small requests to pages the weight rows do
-        // not touch are otherwise served after the whole stream.  The pair's
-        // gate scales come with the even lane, its up scales with the odd one
-        // (applied after the block products).
+        // not touch are otherwise served after the whole stream.
         const size_t grow = (size_t)eg * a.F + cf;
-        gs.load((hh ? a.udcm : a.gdcm) + grow * a.nbpH + NBW * wave);
+        gs.load(a.gdcm + grow * a.nbpH + NBW * wave);
+        us.load(a.udcm + grow * a.nbpH + NBW * wave);
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++) ddb[i] = dd16[(dsec[i] ? dst1 : dst0) + doff[i]];
         cok = ok && cs < nc && !((mrank >> ck) & 1u);
@@ -554,33 +555,54 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
         __builtin_amdgcn_sched_barrier(0);
     }
+    // ---- the weights, by wave 0 while the weight bytes stream in ----
+    if (ok && wave == 0) {
+        float pk[MAX_K];
+#pragma unroll
+        for (int u = 0; u < MAX_K / 4; u++) {
+            const float4 v = reinterpret_cast<const float4 *>(sh_pr)[u];
+            pk[4 * u] = v.x;
+            pk[4 * u + 1] = v.y;
+            pk[4 * u + 2] = v.z;
+            pk[4 * u + 3] = v.w;
+        }
+        double sumW = a.softmax ? 0.0 : 1e-6;
+#pragma unroll
+        for (int k = 0; k < MAX_K; k++)
+            if (k < a.K) sumW = sumW + (double)pk[k];
+        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
+        const double wl = (double)sh_pr[min(lane, MAX_K - 1)] * inv;   // w of rank `lane`
+        if (lane < a.K) sh_w[lane] = wl;
+        if (j == 0) {
+            if (lane < a.K) {
+                if (a.out_idx) a.out_idx[lane] = sh_idx[lane];
+                if (a.out_w) a.out_w[lane] = wl;
+            }
+            if (a.out_probs) {
+#pragma unroll
+                for (int t = 0; t < EPL; t++)
+                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
+            }
+        }
+    }
+
     // ---- gate / up columns, SwiGLU (tensor.js:167-178), h out ----
     if (ok) {
-        float dg[NBW], du[NBW];
-#pragma unroll
-        for (int i = 0; i < NBW; i++) {
-            const int c = 2 * (NBW * wave + i) + hh;
-            const int4 l1 = xq1[c], l2 = xq2[c], l3 = xq3[c];
-            const float sig = xsig[c];
-            dg[i] = dot16_lev3(gq[i], l1, l2, l3, sig);
-            du[i] = dot16_lev3(uq[i], l1, l2, l3, sig);
-        }
-#pragma unroll
-        for (int i = 0; i < (NBW + 1) / 2; i++) {
-            const uint32_t other = (uint32_t)__builtin_amdgcn_mov_dpp((int)gs.s[i], 0xB1, 0xf, 0xf, false);
-            us.s[i] = hh ? gs.s[i] : other;
-            gs.s[i] = hh ? other : gs.s[i];
-        }
+        // block b of the wave: C = (x levels of b) x (b's bytes of the 32
+        // columns) on the matrix cores, column c's three level sums in lane c
+        const int8_t *xa = &xlev[min(cs, 3)][16 * hh];
         float ga = 0.0f, ua = 0.0f;
 #pragma unroll
         for (int i = 0; i < NBW; i++) {
             const int b = NBW * wave + i;
+            const int4 av = *reinterpret_cast<const int4 *>(xa + QK * b);
+            const float fg = lev3_sum(mfma_i8(av, gq[i]));
+            const float fu = lev3_sum(mfma_i8(av, uq[i]));
             const bool bok = cok && b < a.nbH;
-            ga = fmaf(dg[i], bok ? gs.get(i) : 0.0f, ga);
-            ua = fmaf(du[i], bok ? us.get(i) : 0.0f, ua);
+            const float sx = xsig[b];
+            ga = fmaf(fg, bok ? sx * gs.get(i) : 0.0f, ga);
+            ua = fmaf(fu, bok ? sx * us.get(i) : 0.0f, ua);
         }
-        ga += xor1_dpp(ga);
-        ua += xor1_dpp(ua);
         if (hh == 0) {
             redg[wave][cs] = ga;
             redu[wave][cs] = ua;
@@ -631,21 +653,24 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         ok = block_wait<PUB, IPT>(tag, &sh_fail, pl, pd, want, dst);
     }
     if (ok && NP2 > 0) {
-        decompose_row(hl, 2 * a.K * FRb, hq1, hq2, hq3, hsig);
+        decompose32<DEC_MAX_HW + 8 * QK>(hl, a.K * FRb, &hlev[0][0], hsig);
         lds_barrier();
-        // ---- partial down products: lane 2r + h of wave w adds up the
-        // products of its row r of pairs w and w + 8 over the group's blocks
-        // (in block order), straight from registers ----
+        // ---- partial down products: lane r of wave w adds up the products
+        // of its row r of pairs w and w + 8 over the group's blocks (in block
+        // order), one MFMA a block: C = (h levels of the block) x (the block's
+        // bytes of the 32 rows) ----
+        const int8_t *ha = &hlev[min(cs, 3)][16 * hh];
         float acc0 = 0.0f, acc1 = 0.0f;
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++) {
-            const int hc = dhc[i];
+            const int hb = dhb[i];
             // the scale bits pass an empty asm here (ordered after the
             // barriers above), so the compiler cannot convert them -- and wait
             // for the down loads -- before the gate/up products
             uint32_t db = ddb[i];
             asm volatile("" : "+v"(db));
-            const float y = dot16_lev3(dq[i], hq1[hc], hq2[hc], hq3[hc], hsig[hc]) * f16_bits(db);
+            const int4 av = *reinterpret_cast<const int4 *>(ha + QK * hb);
+            const float y = lev3_sum(mfma_i8(av, dq[i])) * hsig[hb] * f16_bits(db);
             if (PP2) {
                 acc0 += (don[i] && !dsec[i]) ? y : 0.0f;
                 acc1 += (don[i] && dsec[i]) ? y : 0.0f;
@@ -653,8 +678,6 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
                 acc0 += don[i] ? y : 0.0f;
             }
         }
-        acc0 += xor1_dpp(acc0);
-        acc1 += xor1_dpp(acc1);
         if (hh == 0) {
             sh_pd[wave][cs] = acc0;
             sh_pd[DEC_WAVES + wave][cs] = acc1;
@@ -683,23 +706,25 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const uint64_t *pl[IPT];
         bool want[IPT];
         float *dst[IPT];
+        const float inv_krf = 1.0f / (float)(a.K * RF), inv_rf = 1.0f / (float)RF;
 #pragma unroll
         for (int s2 = 0; s2 < IPT; s2++) {
+            // item i: partial (x, k, q) of the group sums, or arrival word i - NP;
+            // both worked out and selected (no branch, no integer division:
+            // this runs right after the partials go out)
             const int i = tid + NT * s2;
-            if (i >= NP) {
-                pl[s2] = &a.arrive[min(i - NP, G - 1)];
-                want[s2] = i < NP + G;
-                dst[s2] = nullptr;
-            } else {
-                const int x = i / (a.K * RF);
-                const int r = i - x * a.K * RF;
-                const int k = r / RF;
-                const int q = r - k * RF;
-                const int xb0 = x * a.nbF / DEC_GROUPS, xb1 = (x + 1) * a.nbF / DEC_GROUPS;
-                pl[s2] = &a.part[((size_t)x * a.K + k) * a.H + min(q0 + q, a.H - 1)];
-                want[s2] = q < RFm && xb1 > xb0 && !((mrank >> k) & 1u);
-                dst[s2] = &pf[i];
-            }
+            const int ip = min(i, NP - 1);
+            const int x = div_small(ip, inv_krf);
+            const int r = ip - x * a.K * RF;
+            const int k = div_small(r, inv_rf);
+            const int q = r - k * RF;
+            const int xb0 = (x * a.nbF) >> 3, xb1 = ((x + 1) * a.nbF) >> 3;   // DEC_GROUPS = 8
+            const uint64_t *pp = &a.part[((size_t)x * a.K + k) * a.H + min(q0 + q, a.H - 1)];
+            const uint64_t *pa = &a.arrive[min(max(i - NP, 0), G - 1)];
+            const bool isp = i < NP;
+            pl[s2] = isp ? pp : pa;
+            want[s2] = isp ? (q < RFm && xb1 > xb0 && !((mrank >> k) & 1u)) : (i < NP + G);
+            dst[s2] = isp ? &pf[min(i, DEC_MAX_FIN - 1)] : nullptr;
         }
         ok = block_wait<NT, IPT>(tag, &sh_fail, pl, pl, want, dst);
     }

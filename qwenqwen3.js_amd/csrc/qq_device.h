@@ -339,9 +339,19 @@ __device__ __forceinline__ void decompose16(const float *v, Lev3 &o)
     o.l3 = make_int4((int)c[0], (int)c[1], (int)c[2], (int)c[3]);
 }
 
+// q . a over four int8 pairs, the accumulator starting at zero: the
+// three-operand form with an inline-constant zero (the compiler's choice, the
+// accumulating form, first needs a v_mov of zero into the destination).
+__device__ __forceinline__ int sdot4_first(int q, int a)
+{
+    int r;
+    asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(q), "v"(a));
+    return r;
+}
+
 __device__ __forceinline__ int sdot16(const int4 q, const int4 a)
 {
-    int s = __builtin_amdgcn_sdot4(q.x, a.x, 0, false);
+    int s = sdot4_first(q.x, a.x);
     s = __builtin_amdgcn_sdot4(q.y, a.y, s, false);
     s = __builtin_amdgcn_sdot4(q.z, a.z, s, false);
     return __builtin_amdgcn_sdot4(q.w, a.w, s, false);
