@@ -586,6 +586,16 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         }
     }
 
+    // The group's h values (zero for masked ranks and padding) and the
+    // partials (zero for groups without blocks and masked ranks) start
+    // cleared; the barrier after the gate/up products orders this before
+    // the waits that fill them.
+    {
+        const int HW = a.K * FRb * QK;
+        for (int i = tid; i < HW; i += DEC_THREADS) hl[i] = 0.0f;
+        for (int i = tid; i < DEC_MAX_FIN; i += DEC_THREADS) pf[i] = 0.0f;
+    }
+
     // ---- gate / up columns, SwiGLU (tensor.js:167-178), h out ----
     if (ok) {
         // block b of the wave: C = (x levels of b) x (b's bytes of the 32
@@ -629,12 +639,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         }
     }
 
-    // ---- the group's h values -> LDS (zero for masked ranks and padding) ----
-    const int HW = a.K * FRb * QK;
-    for (int i = tid; i < HW; i += DEC_THREADS) hl[i] = 0.0f;
-    // partials of groups without blocks and of masked ranks read as zero
-    for (int i = tid; i < DEC_MAX_FIN; i += DEC_THREADS) pf[i] = 0.0f;
-    lds_barrier();
+    // ---- the group's h values -> LDS (zero for masked ranks and padding,
+    // cleared above); waves 0..6 poll while wave 7 forms and publishes its h ----
     if (ok && NP2 > 0) {
         constexpr int IPT = (DEC_MAX_HW + PUB - 1) / PUB;
         const uint64_t *pl[IPT], *pd[IPT];
