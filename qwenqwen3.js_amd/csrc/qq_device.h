@@ -85,30 +85,27 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p)
 }
 
 // global_load_lds: each lane copies `size` bytes from its own address to
-// LDS (M0 + lane * size); M0 is set right before (one wait state after an
-// SALU write to M0).
+// LDS (M0 + lane * size); the compiler sets M0 (and its wait state) itself.
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
-                 :: "v"(g), "s"(lds) : "memory");
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                     (__attribute__((address_space(3))) void *)(uintptr_t)lds, 16, 0, 0);
 }
 
 __device__ __forceinline__ void dma4(const void *g, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off"
-                 :: "v"(g), "s"(lds) : "memory");
+    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
+                                     (__attribute__((address_space(3))) void *)(uintptr_t)lds, 4, 0, 0);
 }
-// The same with a wave-uniform base address (SGPR pair) and a 32-bit
-// per-lane byte offset: one VGPR per lane instead of two.
+// The same with a wave-uniform base address and a 32-bit per-lane byte
+// offset (the compiler takes the base from an SGPR pair: one VGPR per lane).
 __device__ __forceinline__ void dma16s(uint32_t off, const void *base, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-                 :: "v"(off), "s"(base), "s"(lds) : "memory");
+    dma16(static_cast<const char *>(base) + off, lds);
 }
 __device__ __forceinline__ void dma4s(uint32_t off, const void *base, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-                 :: "v"(off), "s"(base), "s"(lds) : "memory");
+    dma4(static_cast<const char *>(base) + off, lds);
 }
 
 // Value of lane ^ 1 (resp. lane ^ 2) by a DPP quad permutation: a VALU
