@@ -73,6 +73,21 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
 /* Same with host logits (n_vocab floats, or NULL); waits for the result. */
 int qq_lfm2_forward(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits);
 
+/* forward with the engine's expertMask and the whole onRouterUpdate payload
+ * of every MoE block (src/lfm2-engine.js:449-464):
+ *   mask   [n_experts] bytes, nonzero = the expert is skipped in every MoE
+ *          block (its weight is not renormalised away), or NULL;
+ *   idx    [n_layers][n_experts_used] int32  selected experts, rank order;
+ *   w      [n_layers][n_experts_used] binary64  p_k / (1e-6 + sum p);
+ *   probs  [n_layers][n_experts] fp32  sigmoid probabilities;
+ * each NULL or filled for the MoE blocks (rows of dense blocks are left as
+ * they are).  The _dev form takes device pointers (mask stays a host array)
+ * and is enqueued, not waited for; the host form waits. */
+int qq_lfm2_forward_routed_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits_dev,
+                               const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev);
+int qq_lfm2_forward_routed(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits,
+                           const uint8_t *mask, int32_t *idx, double *w, float *probs);
+
 void qq_lfm2_release(qq_ctx *ctx, qq_lfm2 *m);
 
 #ifdef __cplusplus

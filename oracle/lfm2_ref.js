@@ -173,7 +173,9 @@ function buildModel(kv, metas) {
     m.kCache = new Float32Array(ci * m.nHeadKV * m.maxCtx * m.headDim);
     m.vCache = new Float32Array(ci * m.nHeadKV * m.maxCtx * m.headDim);
     m.convState = m.layers.map(function (L) { return L.rec ? new Float32Array((m.lCache - 1) * H) : null; });
-    m.routes = null;
+    m.routes = null;       // selected experts of every MoE block, when an array
+    m.payloads = null;     // the whole onRouterUpdate payload of every MoE block, when an array
+    m.expertMask = null;   // Set of experts skipped in every MoE block (src/lfm2-engine.js:464)
     return m;
 }
 
@@ -251,9 +253,13 @@ function forward(m, token, pos, skipLogits, tm) {
         if (!L.moe) {
             denseFfn(m, L);
         } else {
+            const rec = m.routes || m.payloads;
             const eng = { nExperts: m.nExperts, nExpertsUsed: m.nExpertsUsed, bufNormed: m.normed,
-                          bufHidden: m.hidden, bufMoEOut: m.moeOut, expertMask: null,
-                          onRouterUpdate: m.routes ? function (r) { m.routes.push(r.selected); } : null };
+                          bufHidden: m.hidden, bufMoEOut: m.moeOut, expertMask: m.expertMask,
+                          onRouterUpdate: rec ? function (r) {
+                              if (m.routes) m.routes.push(r.selected);
+                              if (m.payloads) m.payloads.push(r);
+                          } : null };
             M.moEFFN(eng, li, L);
         }
         if (tm) tm.block(li, now() - ta);
@@ -281,11 +287,14 @@ function loadJob(path) {
 function run(path) {
     const o = loadJob(path), job = o.job, m = o.model;
     m.routes = [];
+    if (job.out_payloads) m.payloads = [];
+    if (job.mask) m.expertMask = new Set(job.mask);
     const V = m.nVocab, T = job.tokens.length;
     const logits = new Float32Array(T * V);
     for (let t = 0; t < T; t++) logits.set(forward(m, job.tokens[t], job.start + t, false), t * V);
     fs.writeFileSync(job.out_logits, Buffer.from(logits.buffer));
     fs.writeFileSync(job.out_routes, JSON.stringify(m.routes));
+    if (job.out_payloads) fs.writeFileSync(job.out_payloads, JSON.stringify(m.payloads));
 }
 
 // Times tokens through the model, per block and for the output head, so a

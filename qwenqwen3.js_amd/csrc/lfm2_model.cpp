@@ -65,6 +65,11 @@ struct qq_lfm2 {
           *ffn = nullptr, *logits = nullptr;
     double *freq = nullptr;
     double *attn_work = nullptr;       // per-chunk attention partials (long contexts)
+    // routing record staging of qq_lfm2_forward_routed: [n_layers][K] indices
+    // and weights, [n_layers][E] probabilities
+    int32_t *r_idx = nullptr;
+    double *r_w = nullptr;
+    float *r_probs = nullptr;
     std::vector<void *> dev;
     std::vector<qq_tensor *> tens;
     std::vector<qq_moe *> moes;
@@ -214,6 +219,10 @@ int bind(Binder &B)
     I.eps = B.num(p + "attention.layer_norm_rms_epsilon", 1e-5);
     I.n_experts = (int)B.num(p + "expert_count", 32);
     I.n_experts_used = (int)B.num(p + "expert_used_count", 4);
+    // the forward writes n_experts_used indices per MoE block into idx_dev
+    if (I.n_experts_used < 1 || I.n_experts_used > qq::MAX_K)
+        return set_error(B.ctx, "lfm2: %sexpert_used_count = %d, supported 1..%d", p.c_str(), I.n_experts_used,
+                         qq::MAX_K);
     I.n_dense_lead = (int)B.num(p + "leading_dense_block_count", 2);
     I.l_cache = (int)B.num(p + "shortconv.l_cache", 3);
     I.max_ctx = (int)std::min(B.num(p + "context_length", 4096), (double)kMaxCtx);
@@ -297,7 +306,10 @@ int bind(Binder &B)
             if (int rc = B.vec_f32(b + "attn_k_norm.weight", kHeadDim, &L.kn)) return rc;
         }
         if (L.moe) {
-            if (int rc = qq_gguf_moe_layer(B.ctx, B.g, i, 0, -1, &L.ffn_moe)) return rc;
+            // Lfm2Engine gates with sigmoid + bias and its own nExpertsUsed
+            // (src/lfm2-engine.js:417-447), whatever the architecture string
+            if (int rc = qq_gguf_moe_layer(B.ctx, B.g, i, I.n_experts_used, QQ_GATING_SIGMOID_BIAS, &L.ffn_moe))
+                return rc;
             m->moes.push_back(L.ffn_moe);
             if (!qq::decode_supported(B.ctx, L.ffn_moe, 1))
                 return set_error(B.ctx, "lfm2: MoE block %d is outside the batch-1 decode kernel's shapes", i);
@@ -338,6 +350,13 @@ int bind(Binder &B)
     }
     if (int rc = B.alloc(qq::lfm2_attn_work_bytes(I.n_heads), &v)) return rc;
     m->attn_work = static_cast<double *>(v);
+    const size_t nlk = (size_t)I.n_layers * I.n_experts_used;
+    if (int rc = B.alloc(nlk * 4, &v)) return rc;
+    m->r_idx = static_cast<int32_t *>(v);
+    if (int rc = B.alloc(nlk * 8, &v)) return rc;
+    m->r_w = static_cast<double *>(v);
+    if (int rc = B.alloc((size_t)I.n_layers * I.n_experts * 4, &v)) return rc;
+    m->r_probs = static_cast<float *>(v);
     // applyRoPE's frequencies 1 / base^(i / half) (src/tensor.js:135-137)
     double fr[kHeadDim / 2];
     for (int i = 0; i < kHeadDim / 2; i++) fr[i] = 1.0 / std::pow(I.rope_freq_base, (double)i / (kHeadDim / 2));
@@ -407,8 +426,8 @@ int qq_lfm2_reset(qq_ctx *ctx, qq_lfm2 *m)
     return qq::launch_lfm2_zero(ctx, m->vc, (size_t)m->info.n_attn_layers * m->kv_floats);
 }
 
-int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits_dev,
-                        int32_t *idx_dev)
+static int lfm2_forward(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits_dev, const uint8_t *mask,
+                 int32_t *idx_dev, double *w_dev, float *probs_dev)
 {
     if (!ctx) return QQ_E_ARG;
     if (!m) return set_error(ctx, "lfm2_forward: NULL model");
@@ -476,9 +495,10 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
         }
         // FFN block: ffn_norm, then dense SwiGLU or MoE, residual
         if (L.moe) {
-            if (int rc = qq_moe_forward_norm_dev(ctx, L.ffn_moe, m->hidden, L.ffn_norm, I.eps, 1, nullptr,
-                                                 idx_dev ? idx_dev + (size_t)i * I.n_experts_used : nullptr,
-                                                 nullptr, nullptr))
+            const size_t rk = (size_t)i * I.n_experts_used, re = (size_t)i * I.n_experts;
+            if (int rc = qq_moe_forward_norm_dev(ctx, L.ffn_moe, m->hidden, L.ffn_norm, I.eps, 1, mask,
+                                                 idx_dev ? idx_dev + rk : nullptr, w_dev ? w_dev + rk : nullptr,
+                                                 probs_dev ? probs_dev + re : nullptr))
                 return rc;
         } else {
             qq::LmLaunch s;
@@ -511,15 +531,46 @@ int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
     return QQ_OK;
 }
 
-int qq_lfm2_forward(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits)
+int qq_lfm2_forward_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits_dev,
+                        int32_t *idx_dev)
+{
+    return lfm2_forward(ctx, m, token, position, logits_dev, nullptr, idx_dev, nullptr, nullptr);
+}
+
+int qq_lfm2_forward_routed_dev(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits_dev,
+                               const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev)
+{
+    return lfm2_forward(ctx, m, token, position, logits_dev, mask, idx_dev, w_dev, probs_dev);
+}
+
+int qq_lfm2_forward_routed(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits,
+                           const uint8_t *mask, int32_t *idx, double *w, float *probs)
 {
     if (!ctx) return QQ_E_ARG;
     if (int rc = qq::no_capture(ctx, "qq_lfm2_forward")) return rc;
-    if (int rc = qq_lfm2_forward_dev(ctx, m, token, position, logits ? m->logits : nullptr, nullptr)) return rc;
+    if (!m) return set_error(ctx, "lfm2_forward: NULL model");
+    if (int rc = lfm2_forward(ctx, m, token, position, logits ? m->logits : nullptr, mask, idx ? m->r_idx : nullptr,
+                              w ? m->r_w : nullptr, probs ? m->r_probs : nullptr))
+        return rc;
+    const qq_lfm2_info &I = m->info;
     if (logits)
-        QQ_HIP(ctx, hipMemcpyAsync(logits, m->logits, (size_t)m->info.n_vocab * 4, hipMemcpyDeviceToHost,
+        QQ_HIP(ctx, hipMemcpyAsync(logits, m->logits, (size_t)I.n_vocab * 4, hipMemcpyDeviceToHost, ctx->stream));
+    // the MoE blocks' rows (blocks n_dense_lead .. n_layers - 1); dense rows stay as they are
+    const size_t l0 = (size_t)I.n_dense_lead, nm = (size_t)(I.n_layers - I.n_dense_lead);
+    const size_t K = (size_t)I.n_experts_used, E = (size_t)I.n_experts;
+    if (idx && nm)
+        QQ_HIP(ctx, hipMemcpyAsync(idx + l0 * K, m->r_idx + l0 * K, nm * K * 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (w && nm)
+        QQ_HIP(ctx, hipMemcpyAsync(w + l0 * K, m->r_w + l0 * K, nm * K * 8, hipMemcpyDeviceToHost, ctx->stream));
+    if (probs && nm)
+        QQ_HIP(ctx, hipMemcpyAsync(probs + l0 * E, m->r_probs + l0 * E, nm * E * 4, hipMemcpyDeviceToHost,
                                    ctx->stream));
     return qq::check_device_error(ctx);
+}
+
+int qq_lfm2_forward(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float *logits)
+{
+    return qq_lfm2_forward_routed(ctx, m, token, position, logits, nullptr, nullptr, nullptr, nullptr);
 }
 
 }  // extern "C"

@@ -15,7 +15,9 @@
 //                             the engine's ArrayBuffers
 //   device.attachLfm2Forward(engine)   Lfm2Engine.forward / resetState
 //                             (src/lfm2-engine.js:216-280) of one engine run the
-//                             whole token on the device from the attached file
+//                             whole token on the device from the attached file,
+//                             honouring engine.expertMask and calling
+//                             engine.onRouterUpdate for every MoE block
 //
 // There is no CPU fallback: when the addon or the device is missing, the
 // constructor and install() throw.  Written for Node 12 (no `?.`, no `??`).
@@ -69,7 +71,7 @@ class MoEDevice {
         this._tensors = new WeakMap();   // ArrayBuffer -> Map(key -> device tensor)
         this.fallbackMatmul = null;
         this._gguf = null;
-        this._lfm2 = null;
+        this._lfm2 = [];                 // {engine, model}: one device model per engine
     }
 
     // Bind MoE blocks from a GGUF file: the layer of block l is read from the
@@ -93,14 +95,45 @@ class MoEDevice {
     attachLfm2Forward(engine) {
         if (!this._gguf) throw new Error('attachLfm2Forward: attachGGUF(path) first');
         const model = this.native.lfm2Create(this.ctx, this._gguf);
-        if (this._lfm2) this.native.release(this._lfm2);
-        this._lfm2 = model;
+        // one model per engine: attaching an engine again releases only its own model
+        for (let i = 0; i < this._lfm2.length; i++) {
+            if (this._lfm2[i].engine === engine) {
+                this.native.release(this._lfm2[i].model);
+                this._lfm2.splice(i, 1);
+                break;
+            }
+        }
+        this._lfm2.push({ engine: engine, model: model });
         const info = this.native.lfm2Info(model);
         const dev = this;
+        const nl = info.nLayers, K = info.nExpertsUsed, E = info.nExperts;
+        const routes = { idx: new Int32Array(nl * K), w: new Float64Array(nl * K), probs: new Float32Array(nl * E) };
+        const mask = new Uint8Array(E);
         if (!(engine.bufLogits instanceof Float32Array) || engine.bufLogits.length !== info.nVocab)
             engine.bufLogits = new Float32Array(info.nVocab);
         engine.forward = function (tokenId, position, skipLogits) {
-            dev.native.lfm2Forward(dev.ctx, model, tokenId | 0, position | 0, skipLogits ? null : this.bufLogits);
+            // expertMask (src/lfm2-engine.js:464): experts skipped in every MoE block
+            let m = null;
+            if (this.expertMask && this.expertMask.size) {
+                mask.fill(0);
+                this.expertMask.forEach(function (e) { if (e >= 0 && e < E) mask[e] = 1; });
+                m = mask;
+            }
+            const want = !!this.onRouterUpdate;
+            dev.native.lfm2Forward(dev.ctx, model, tokenId | 0, position | 0, skipLogits ? null : this.bufLogits,
+                                   m, want ? routes : null);
+            if (want) {
+                // onRouterUpdate of every MoE block (src/lfm2-engine.js:449-456), with the
+                // reference's payload; delivered once the token has run
+                for (let l = info.nDenseLead; l < nl; l++) {
+                    this.onRouterUpdate({
+                        layer: l,
+                        probs: Array.from(routes.probs.subarray(l * E, (l + 1) * E)),
+                        selected: Array.from(routes.idx.subarray(l * K, (l + 1) * K)),
+                        weights: Array.from(routes.w.subarray(l * K, (l + 1) * K)),
+                    });
+                }
+            }
             return skipLogits ? null : this.bufLogits;
         };
         engine.resetState = function () { dev.native.lfm2Reset(dev.ctx, model); };
@@ -224,10 +257,8 @@ class MoEDevice {
     }
 
     release() {
-        if (this._lfm2) {
-            this.native.release(this._lfm2);
-            this._lfm2 = null;
-        }
+        for (const e of this._lfm2) this.native.release(e.model);
+        this._lfm2 = [];
         if (this._gguf) {
             this.native.release(this._gguf);
             this._gguf = null;

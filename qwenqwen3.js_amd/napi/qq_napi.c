@@ -27,8 +27,12 @@
  *   lfm2Create(ctx, gguf) -> lfm2      whole LFM2 model on the device (include/qq_lfm2.h)
  *   lfm2Info(lfm2) -> {nLayers, nEmbd, nHeads, nHeadKV, headDim, nVocab, nFF, nExperts,
  *                      nExpertsUsed, nDenseLead, lCache, maxCtx, nAttnLayers, eps, ropeFreqBase}
- *   lfm2Forward(ctx, lfm2, token, position, logits: Float32Array|null)
- *       one token through the model; logits (nVocab floats) or null (skipLogits)
+ *   lfm2Forward(ctx, lfm2, token, position, logits: Float32Array|null
+ *               [, mask: Uint8Array(nExperts)|null, routes: {idx, w, probs}|null])
+ *       one token through the model; logits (nVocab floats) or null (skipLogits);
+ *       mask: nonzero = expert skipped in every MoE block (expertMask);
+ *       routes: Int32Array(nLayers*K), Float64Array(nLayers*K), Float32Array(nLayers*E)
+ *       receive every MoE block's onRouterUpdate payload (dense rows untouched)
  *   lfm2Reset(ctx, lfm2)               zero the KV cache and conv states
  *   release(handle)    frees a tensor / moe / ctx / gguf now instead of at GC
  */
@@ -614,14 +618,21 @@ static napi_value js_lfm2_info(napi_env env, napi_callback_info info)
 
 static napi_value js_lfm2_forward(napi_env env, napi_callback_info info)
 {
-    ARGS(5);
+    // five arguments, and two optional ones (missing ones read as undefined)
+    size_t argc = 7;
+    napi_value argv[7];
+    CHECK_NAPI(env, napi_get_cb_info(env, info, &argc, argv, NULL, NULL));
+    if (argc < 5) {
+        napi_throw_type_error(env, NULL, "qq_napi: lfm2Forward expects at least 5 arguments");
+        return NULL;
+    }
     handle *ch = get_handle(env, argv[0], H_CTX);
     if (!ch) return NULL;
     handle *mh = get_handle(env, argv[1], H_LFM2);
     if (!mh) return NULL;
     int32_t token, pos;
     if (get_i32(env, argv[2], &token) || get_i32(env, argv[3], &pos)) {
-        napi_throw_type_error(env, NULL, "lfm2Forward(ctx, lfm2, token, position, logits | null)");
+        napi_throw_type_error(env, NULL, "lfm2Forward(ctx, lfm2, token, position, logits | null[, mask, routes])");
         return NULL;
     }
     float *logits = NULL;
@@ -632,8 +643,40 @@ static napi_value js_lfm2_forward(napi_env env, napi_callback_info info)
             return NULL;
         }
     }
+    qq_lfm2_info I;
+    if (qq_lfm2_get_info((qq_lfm2 *)mh->ptr, &I)) {
+        napi_throw_error(env, NULL, "lfm2Forward: model info");
+        return NULL;
+    }
+    uint8_t *mask = NULL;
+    if (argc > 5 && !is_nullish(env, argv[5])) {
+        size_t n;
+        if (get_typed(env, argv[5], napi_uint8_array, (void **)&mask, &n) || n < (size_t)I.n_experts) {
+            napi_throw_type_error(env, NULL, "lfm2Forward: mask must be a Uint8Array of nExperts bytes or null");
+            return NULL;
+        }
+    }
+    int32_t *idx = NULL;
+    double *w = NULL;
+    float *probs = NULL;
+    if (argc > 6 && !is_nullish(env, argv[6])) {
+        napi_value vi, vw, vp;
+        size_t ni = 0, nw = 0, np = 0;
+        const size_t nk = (size_t)I.n_layers * I.n_experts_used, ne = (size_t)I.n_layers * I.n_experts;
+        if (napi_get_named_property(env, argv[6], "idx", &vi) != napi_ok ||
+            napi_get_named_property(env, argv[6], "w", &vw) != napi_ok ||
+            napi_get_named_property(env, argv[6], "probs", &vp) != napi_ok ||
+            get_typed(env, vi, napi_int32_array, (void **)&idx, &ni) || ni < nk ||
+            get_typed(env, vw, napi_float64_array, (void **)&w, &nw) || nw < nk ||
+            get_typed(env, vp, napi_float32_array, (void **)&probs, &np) || np < ne) {
+            napi_throw_type_error(env, NULL,
+                                  "lfm2Forward: routes must be {idx: Int32Array(nLayers*K), w: Float64Array(nLayers*K), "
+                                  "probs: Float32Array(nLayers*nExperts)}");
+            return NULL;
+        }
+    }
     qq_ctx *ctx = (qq_ctx *)ch->ptr;
-    int rc = qq_lfm2_forward(ctx, (qq_lfm2 *)mh->ptr, token, pos, logits);
+    int rc = qq_lfm2_forward_routed(ctx, (qq_lfm2 *)mh->ptr, token, pos, logits, mask, idx, w, probs);
     if (rc) return throw_qq(env, "qq_lfm2_forward", rc, ctx);
     return NULL;
 }

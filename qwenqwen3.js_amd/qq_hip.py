@@ -46,6 +46,7 @@ GGUF_EXPORTS = (
 # ... and include/qq_lfm2.h
 LFM2_EXPORTS = (
     "qq_lfm2_create", "qq_lfm2_get_info", "qq_lfm2_reset", "qq_lfm2_forward_dev", "qq_lfm2_forward",
+    "qq_lfm2_forward_routed_dev", "qq_lfm2_forward_routed",
     "qq_lfm2_release",
 )
 
@@ -141,6 +142,8 @@ def load():
         "qq_lfm2_get_info": (I, [P, ctypes.POINTER(Lfm2Info)]),
         "qq_lfm2_reset": (I, [P, P]),
         "qq_lfm2_forward_dev": (I, [P, P, I, I, P, P]),
+        "qq_lfm2_forward_routed_dev": (I, [P, P, I, I, P, P, P, P, P]),
+        "qq_lfm2_forward_routed": (I, [P, P, I, I, P, P, P, P, P]),
         "qq_lfm2_forward": (I, [P, P, I, I, P]),
         "qq_lfm2_release": (None, [P, P]),
     }
@@ -384,6 +387,25 @@ class Lfm2Model:
     def forward_dev(self, token, position, logits_ptr=None, idx_ptr=None):
         self.ctx.check(self.L.qq_lfm2_forward_dev(self.ctx.h, self.h, token, position, logits_ptr, idx_ptr),
                        "qq_lfm2_forward_dev")
+
+    def forward_routed(self, token, position, mask=None, logits=True):
+        """(logits, idx, w, probs) on the host (qq_lfm2_forward_routed): the
+        onRouterUpdate payload of every MoE block, with the experts in `mask`
+        skipped; rows of dense blocks are -1 / NaN."""
+        I = self.info
+        nl, K, E = I["n_layers"], I["n_experts_used"], I["n_experts"]
+        out = np.empty(I["n_vocab"], np.float32) if logits else None
+        idx = np.full((nl, K), -1, np.int32)
+        w = np.full((nl, K), np.nan, np.float64)
+        probs = np.full((nl, E), np.nan, np.float32)
+        m = None
+        if mask is not None:
+            m = np.zeros(E, np.uint8)
+            for e in mask:
+                m[e] = 1
+        self.ctx.check(self.L.qq_lfm2_forward_routed(self.ctx.h, self.h, token, position, _ptr(out), _ptr(m),
+                                                     _ptr(idx), _ptr(w), _ptr(probs)), "qq_lfm2_forward_routed")
+        return out, idx, w, probs
 
     def release(self):
         if self.h:

@@ -40,12 +40,18 @@ def write_model(tmp, seed, cfg, **kw):
     return path, offs, tensors
 
 
-def js_forward(tmp, path, offs, tensors, cfg, tokens, start=0):
-    """Logits [T, vocab] and per-MoE-layer routes of lfm2_ref.js."""
+def js_forward(tmp, path, offs, tensors, cfg, tokens, start=0, mask=None, payloads=False):
+    """Logits [T, vocab] and per-MoE-layer routes of lfm2_ref.js (with the
+    experts in `mask` skipped); with payloads=True also the onRouterUpdate
+    payload of every MoE block ({layer, probs, selected, weights}, T x blocks)."""
     job = {"gguf": path, "kv": kv_dict(cfg), "tokens": [int(t) for t in tokens], "start": start,
            "tensors": {n: {"offset": offs[n], "shape": s, "type": t} for n, s, t, _ in tensors},
            "out_logits": os.path.join(str(tmp), "logits.f32"),
            "out_routes": os.path.join(str(tmp), "routes.json")}
+    if mask is not None:
+        job["mask"] = sorted(int(e) for e in mask)
+    if payloads:
+        job["out_payloads"] = os.path.join(str(tmp), "payloads.json")
     jp = os.path.join(str(tmp), "lfm2_job.json")
     with open(jp, "w") as f:
         json.dump(job, f)
@@ -54,7 +60,10 @@ def js_forward(tmp, path, offs, tensors, cfg, tokens, start=0):
     logits = np.fromfile(job["out_logits"], np.float32).reshape(len(tokens), -1)
     with open(job["out_routes"]) as f:
         routes = json.load(f)
-    return logits, routes
+    if not payloads:
+        return logits, routes
+    with open(job["out_payloads"]) as f:
+        return logits, routes, json.load(f)
 
 
 # ---------------------------------------------------------------- float64 forward

@@ -66,6 +66,53 @@ def test_forward_matches_oracle(tmp_path, seed, kw):
     m.release()
 
 
+def test_forward_full_width(tmp_path):
+    """LFM2-8B-A1B widths on three blocks: a dense FFN of 7168 (the residual
+    matvec's multi-chunk loop over 7168 inputs), one attention block with 32
+    query / 8 KV heads (GQA ratio 4), one MoE block (8 experts of 1792, top-4,
+    through the batch-1 decode kernel) and the 65536-row output head."""
+    _say("lfm2 full width")
+    cfg = dict(synth.LFM2_8B_A1B, n_layers=3, attn_layers=(1,), n_dense=1, E=8, ctx=64)
+    m, _ = _check_tokens(tmp_path, 12, cfg=cfg, tokens=TOKENS[:4])
+    m.release()
+
+
+def test_forward_routed_mask_and_payload(tmp_path):
+    """qq_lfm2_forward_routed: with an expert mask (skipped in every MoE block,
+    src/lfm2-engine.js:464) the logits follow the oracle run with the same
+    mask, and every MoE block's onRouterUpdate payload (src/lfm2-engine.js:
+    449-456) matches the oracle's: the selected experts equal, their weights
+    and the E probabilities within 1e-5 relative (past the first block the
+    hidden state differs from the oracle's in the last bits, and with it the
+    later routers' logits)."""
+    _say("lfm2 routed forward, mask and payload")
+    cfg = synth.LFM2_TINY
+    m, path, offs, tensors = _model(tmp_path, 6, cfg)
+    try:
+        tokens = TOKENS[:5]
+        _, routes0 = _lfm2.js_forward(tmp_path, path, offs, tensors, cfg, tokens[:1], 0)
+        mask = {routes0[0][0], routes0[1][1]}          # experts the unmasked run selects
+        ref, _, pay = _lfm2.js_forward(tmp_path, path, offs, tensors, cfg, tokens, 0, mask=mask, payloads=True)
+        nl = m.info["n_layers"]
+        moe = [l for l in range(nl) if l >= cfg["n_dense"]]
+        assert len(pay) == len(tokens) * len(moe)
+        for t, tok in enumerate(tokens):
+            logits, idx, w, probs = m.forward_routed(tok, t, mask=mask)
+            err = rel_l2(logits, ref[t])
+            _say("token", t, "rel_l2", err)
+            assert err < TOL, (t, err)
+            for j, l in enumerate(moe):
+                p = pay[t * len(moe) + j]
+                assert p["layer"] == l
+                assert idx[l].tolist() == p["selected"]
+                assert rel_l2(w[l], p["weights"]) < 1e-5, (t, l)
+                assert rel_l2(probs[l], p["probs"]) < 1e-5, (t, l)
+            for l in range(cfg["n_dense"]):          # dense rows are left as they are
+                assert (idx[l] == -1).all() and np.isnan(w[l]).all()
+    finally:
+        m.release()
+
+
 @pytest.mark.parametrize("start", [253, 700])
 def test_forward_long_context(tmp_path, start):
     """Positions past 256 take the chunked attention (chunks of 256 positions and a
