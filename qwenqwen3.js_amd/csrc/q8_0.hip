@@ -54,7 +54,7 @@ int launch_repack_q8_0(qq_ctx *ctx, const uint8_t *gguf_dev, qq_tensor *t)
 }
 
 // ---------------------------------------------------------------------------
-// Matvec.  A workgroup (4 waves) owns 32 output rows; lane l of every wave
+// Matvec over R input vectors.  A workgroup (4 waves) owns 32 output rows; lane l of every wave
 // takes row l/2 and half l%2 of a block, wave w takes block columns
 // w, w+4, ...  The R input vectors sit in LDS (a window of up to MV_WIN
 // blocks at a time) together with the sum of every 16-value half block.
@@ -139,13 +139,143 @@ __global__ __launch_bounds__(256) void q8_0_matvec_kernel(
     }
 }
 
+// Single input vector.  A workgroup owns RPW output rows and all of their
+// block columns; lane l of a wave takes half h = l & 1 of a block, row
+// (l >> 1) % RPW and block slot l / (2 RPW), so one 16-byte load per lane
+// covers RPW rows x 64 / (2 RPW) block columns (each a contiguous run of
+// 32 RPW bytes); scales come from the row-major copy, so the RPW rows' scales
+// are whole lines no other workgroup reads.  Every lane issues the weight and scale loads of its first
+// NBW blocks before the input row is staged in LDS, so at 1024 -> 3072 the
+// whole matrix is requested at once by 384 workgroups; a kernel that only
+// loads the same weights takes as long.  Each lane forms its own half-block
+// sums; rows are summed over the lanes of a wave and then over the waves in
+// wave order.  RAG: in_dim is not a multiple of 32 (the missing activations
+// of the last block read as zero).
+constexpr int MV1_MAX_NB = 384;   // 48 KiB of activations in LDS
+
+template <int RPW, int NWV, int NBW, bool RAG>
+__global__ __launch_bounds__(NWV * WAVE) void q8_0_matvec1_kernel(const int8_t *__restrict__ qs,
+                                                                  const __half *__restrict__ dcm, int mat,
+                                                                  int rows, int nb, int nbp, int in_dim,
+                                                                  const float *__restrict__ x,
+                                                                  float *__restrict__ y)
+{
+    constexpr int SPW = WAVE / (2 * RPW);   // block slots per wave
+    constexpr int BPR = NWV * SPW;          // block columns per round of the workgroup
+    constexpr int NT = NWV * WAVE;
+    extern __shared__ __align__(16) float mv_x[];   // nb * 32 activations
+    __shared__ float red[NWV][RPW];
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int h = lane & 1, r = (lane >> 1) & (RPW - 1), s = lane / (2 * RPW);
+    const int row = blockIdx.x * RPW + r;
+    const bool row_ok = row < rows;
+    const int rc = min(row, rows - 1);
+    const int first = wave * SPW + s;
+    int4 q[NBW];
+    float dd[NBW];
+    // branch-free: clamped block, zero scale past the last one
+    auto load = [&](int c0) {
+#pragma unroll
+        for (int u = 0; u < NBW; u++) {
+            const int bc = min(c0 + first + BPR * u, nb - 1);
+            const size_t o = bm_index(mat, nb, bc, rows, rc);
+            q[u] = *reinterpret_cast<const int4 *>(qs + o * QK + 16 * h);
+            dd[u] = __half2float(dcm[((size_t)mat * rows + rc) * nbp + bc]);
+        }
+#pragma unroll
+        for (int u = 0; u < NBW; u++) dd[u] = (row_ok && c0 + first + BPR * u < nb) ? dd[u] : 0.0f;
+    };
+    load(0);
+    const int kp = nb * QK;
+    for (int k = 4 * threadIdx.x; k < kp; k += 4 * NT) {
+        float4 v;
+        if (!RAG || k + 4 <= in_dim) {
+            v = *reinterpret_cast<const float4 *>(x + k);
+        } else {
+            v.x = k < in_dim ? x[k] : 0.0f;
+            v.y = k + 1 < in_dim ? x[k + 1] : 0.0f;
+            v.z = k + 2 < in_dim ? x[k + 2] : 0.0f;
+            v.w = k + 3 < in_dim ? x[k + 3] : 0.0f;
+        }
+        *reinterpret_cast<float4 *>(&mv_x[k]) = v;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    for (int c0 = 0;;) {
+#pragma unroll
+        for (int u = 0; u < NBW; u++) {
+            const int bc = min(c0 + first + BPR * u, nb - 1);
+            float xr[16];
+            const float4 *p = reinterpret_cast<const float4 *>(&mv_x[bc * QK + 16 * h]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 v = p[i];
+                xr[4 * i] = v.x;
+                xr[4 * i + 1] = v.y;
+                xr[4 * i + 2] = v.z;
+                xr[4 * i + 3] = v.w;
+            }
+            float xs = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 16; j++) xs += xr[j];
+            acc = fmaf(dot16_q8(q[u], xr, xs), dd[u], acc);
+        }
+        c0 += NBW * BPR;
+        if (c0 >= nb) break;
+        load(c0);
+    }
+    acc += __shfl_xor(acc, 1, WAVE);
+#pragma unroll
+    for (int o = 2 * RPW; o < WAVE; o <<= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (lane < 2 * RPW && h == 0) red[wave][r] = acc;
+    __syncthreads();
+    if (threadIdx.x < RPW) {
+        const int orow = blockIdx.x * RPW + threadIdx.x;
+        if (orow < rows) {
+            float v = red[0][threadIdx.x];
+#pragma unroll
+            for (int w = 1; w < NWV; w++) v += red[w][threadIdx.x];
+            y[orow] = v;
+        }
+    }
+}
+
+template <bool RAG>
+static void launch_matvec1(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, float *y)
+{
+    // launch shapes measured at 1024 -> 3072, 2048 -> 2048, 7168 -> 2048 and
+    // 2048 -> 7168: 8 rows per workgroup, 4 waves up to 32 block columns,
+    // else 8; up to 2 blocks in flight per lane for 64 block columns, else 4
+    constexpr int RPW = 8;
+    const dim3 grid((t->out_dim + RPW - 1) / RPW);
+    const size_t shm = (size_t)t->nb * QK * sizeof(float);
+    if (t->nb <= 16)
+        QQ_LAUNCH(ctx, (q8_0_matvec1_kernel<RPW, 4, 1, RAG>), grid, dim3(4 * WAVE), shm, t->qs, t->dcm, mat,
+                  t->out_dim, t->nb, t->nbp, t->in_dim, x, y);
+    else if (t->nb <= 32)
+        QQ_LAUNCH(ctx, (q8_0_matvec1_kernel<RPW, 4, 2, RAG>), grid, dim3(4 * WAVE), shm, t->qs, t->dcm, mat,
+                  t->out_dim, t->nb, t->nbp, t->in_dim, x, y);
+    else if (t->nb <= 64)
+        QQ_LAUNCH(ctx, (q8_0_matvec1_kernel<RPW, 8, 2, RAG>), grid, dim3(8 * WAVE), shm, t->qs, t->dcm, mat,
+                  t->out_dim, t->nb, t->nbp, t->in_dim, x, y);
+    else
+        QQ_LAUNCH(ctx, (q8_0_matvec1_kernel<RPW, 8, 4, RAG>), grid, dim3(8 * WAVE), shm, t->qs, t->dcm, mat,
+                  t->out_dim, t->nb, t->nbp, t->in_dim, x, y);
+}
+
 int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, int ldx,
                        float *y, int ldy, int rows)
 {
     if (rows <= 0) return QQ_OK;
     const unsigned gx = (unsigned)((t->out_dim + 31) / 32);
     prof_begin(ctx, K_MATVEC);
-    if (rows >= 4)
+    // one vector whose activations fit in LDS (in_dim <= 12288)
+    if (rows == 1 && ((uintptr_t)x & 15) == 0 && t->nb <= MV1_MAX_NB) {
+        if (t->in_dim % QK)
+            launch_matvec1<true>(ctx, t, mat, x, y);
+        else
+            launch_matvec1<false>(ctx, t, mat, x, y);
+    } else if (rows >= 4)
         QQ_LAUNCH(ctx, (q8_0_matvec_kernel<4>), dim3(gx, (rows + 3) / 4), dim3(256), 0, t->qs, t->d, mat, t->out_dim, t->nb, t->in_dim, x, ldx, y,
                            ldy, rows);
     else if (rows >= 2)

@@ -48,6 +48,9 @@ def _say(*a):
     (2080, 130, 2),      # three 1 KiB chunks
     (5000, 40, 1),       # long-row kernel
     (32, 1, 1),          # single block, single column
+    (7168, 2048, 1),     # LFM2 dense ffn_down: 224 block columns, two rounds of loads
+    (500, 33, 1),        # 16 block columns, partial last block
+    (12800, 48, 1),      # 400 block columns: more activations than the one-vector kernel stages
 ])
 def test_q8_0_matvec(in_dim, out_dim, rows):
     _say("matvec", in_dim, out_dim, rows)
