@@ -159,6 +159,37 @@ int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev,
                             const float *norm_w_dev, double eps, int T, const uint8_t *mask,
                             int32_t *idx_dev, double *w_dev, float *probs_dev);
 
+/* ---- The WebGPU engines' device-resident MoE block ------------------------
+ * Lfm2GPUEngine and Qwen3GPUEngine keep the residual stream in device
+ * buffers and run the block with no host round trip, leaving each MoE
+ * layer's routing in a buffer that is read back in one batch after the token
+ * (src/webgpu.js:1882-1945, :878-990).
+ *
+ * Device buffers, standing for GPUDevice.createBuffer / uploadBuffer,
+ * queue.writeBuffer and readF32 (src/webgpu.js:349-430): alloc returns
+ * zeroed device memory; write copies host bytes in and returns once they
+ * are copied; read waits for the work enqueued before it, then copies out.
+ * Not allowed while a capture is open. */
+int qq_buffer_alloc(qq_ctx *ctx, size_t nbytes, void **dev);
+int qq_buffer_free(qq_ctx *ctx, void *dev);
+int qq_buffer_write(qq_ctx *ctx, void *dev, const void *host, size_t nbytes);
+int qq_buffer_read(qq_ctx *ctx, const void *dev, void *host, size_t nbytes);
+
+/* _moEFFNGPU (src/webgpu.js:1882-1917 for LFM2, :878-915 for Qwen3):
+ * hidden += MoE(x) for T rows on device pointers, enqueued, and per row the
+ * routing record the engines' top-K shaders write for the batched readback
+ * (src/webgpu.js:1236-1240, :1175-1178):
+ *   record_dev[t*(2K+E) + k]        selected expert of rank k, as a float
+ *   record_dev[t*(2K+E) + K + k]    its weight, the w of qq_moe_forward
+ *                                   rounded to fp32
+ *   record_dev[t*(2K+E) + 2K + e]   probability of expert e
+ * (record_dev NULL: no record).  mask as in qq_moe_forward_dev (the WebGPU
+ * engines have none; NULL matches them).  The values are the CPU engine's
+ * (binary64 routing math, as qq_moe_forward), not the shaders' fp32
+ * arithmetic: the selection equals the CPU engine's. */
+int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev,
+                              int T, const uint8_t *mask, float *record_dev);
+
 /* Token batches (T > 1) of at least `tokens` rows per chunk run their expert
  * products as fp16 MFMA grouped GEMMs (fp16 activations and dequantised
  * weights, fp32 accumulation: ~1e-3 relative L2 on the layer output);

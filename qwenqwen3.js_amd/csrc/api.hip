@@ -648,6 +648,86 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     return check_device_error(ctx);
 }
 
+// ---- device buffers and the routing record ---------------------------------
+
+int qq_buffer_alloc(qq_ctx *ctx, size_t nbytes, void **dev)
+{
+    if (!ctx || !dev) return QQ_E_ARG;
+    *dev = nullptr;
+    if (int rc = no_capture(ctx, "qq_buffer_alloc")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    const size_t n = nbytes ? nbytes : 1;
+    void *p = nullptr;
+    QQ_HIP(ctx, hipMalloc(&p, n));
+    hipError_t e = hipMemsetAsync(p, 0, n, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return check_hip(ctx, e, "buffer_alloc: clear");
+    }
+    *dev = p;
+    return QQ_OK;
+}
+
+int qq_buffer_free(qq_ctx *ctx, void *dev)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!dev) return QQ_OK;
+    if (int rc = no_capture(ctx, "qq_buffer_free")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    QQ_HIP(ctx, hipFree(dev));
+    return QQ_OK;
+}
+
+int qq_buffer_write(qq_ctx *ctx, void *dev, const void *host, size_t nbytes)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (nbytes == 0) return QQ_OK;
+    if (!dev || !host) return set_error(ctx, "buffer_write: NULL pointer");
+    if (int rc = no_capture(ctx, "qq_buffer_write")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipMemcpyAsync(dev, host, nbytes, hipMemcpyHostToDevice, ctx->stream));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return check_device_error(ctx);
+}
+
+int qq_buffer_read(qq_ctx *ctx, const void *dev, void *host, size_t nbytes)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (nbytes == 0) return QQ_OK;
+    if (!dev || !host) return set_error(ctx, "buffer_read: NULL pointer");
+    if (int rc = no_capture(ctx, "qq_buffer_read")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return check_device_error(ctx);
+}
+
+int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev, int T,
+                              const uint8_t *mask, float *record_dev)
+{
+    int rc = forward_check(ctx, m, T);
+    if (rc || T == 0) return rc;
+    if (!x_dev || !hidden_dev) return set_error(ctx, "moe_forward_record: NULL buffer");
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
+    if (decode_supported(ctx, m, T))   // the decode kernel writes the record itself
+        return launch_moe_decode(ctx, m, x_dev, hidden_dev, mb, nullptr, nullptr, nullptr, nullptr, record_dev);
+    if (!record_dev) return forward_impl(ctx, m, x_dev, hidden_dev, T, mb, nullptr, nullptr, nullptr, 0);
+    // idx | w | probs ahead of the forward's scratch, then the record from them
+    const size_t ib = align256((size_t)T * m->K * 4), wb = align256((size_t)T * m->K * 8);
+    const size_t pb = align256((size_t)T * m->E * 4);
+    if ((rc = ensure_scratch(ctx, ib + wb + pb + forward_scratch(ctx, m, T)))) return rc;
+    char *s = static_cast<char *>(ctx->scratch);
+    int32_t *idx = reinterpret_cast<int32_t *>(s);
+    double *w = reinterpret_cast<double *>(s + ib);
+    float *probs = reinterpret_cast<float *>(s + ib + wb);
+    if ((rc = forward_impl(ctx, m, x_dev, hidden_dev, T, mb, idx, w, probs, ib + wb + pb))) return rc;
+    return launch_route_record(ctx, idx, w, probs, T, m->K, m->E, record_dev);
+}
+
 int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens)
 {
     if (!ctx) return QQ_E_ARG;

@@ -97,6 +97,7 @@ struct DecodeArgs {
     int32_t *out_idx;     // optional outputs
     double *out_w;
     float *out_probs;
+    float *out_rec;       // [K idx as float | K w rounded to fp32 | E probs]
     uint32_t *err;
 };
 
@@ -583,6 +584,15 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
                 for (int t = 0; t < EPL; t++)
                     if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
             }
+            if (a.out_rec) {
+                if (lane < a.K) {
+                    a.out_rec[lane] = (float)sh_idx[lane];
+                    a.out_rec[a.K + lane] = (float)wl;
+                }
+#pragma unroll
+                for (int t = 0; t < EPL; t++)
+                    if (lane + WAVE * t < a.E) a.out_rec[2 * a.K + lane + WAVE * t] = pr[t];
+            }
         }
     }
 
@@ -810,7 +820,7 @@ static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re, bool 
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      const NormArgs *norm)
+                      const NormArgs *norm, float *out_rec)
 {
     DecodeArgs a;
     a.x = x;
@@ -848,6 +858,7 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.out_idx = out_idx;
     a.out_w = out_w;
     a.out_probs = out_probs;
+    a.out_rec = out_rec;
     a.err = ctx->sync_err;
 
     const int G = decode_grid(ctx);

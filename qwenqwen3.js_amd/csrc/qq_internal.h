@@ -209,7 +209,11 @@ struct NormArgs {
 
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      const NormArgs *norm = nullptr);
+                      const NormArgs *norm = nullptr, float *out_rec = nullptr);
+// The routing record of T rows, rec[t * (2K + E) + ...] = [K idx as float |
+// K w rounded to fp32 | E probs], from the router's outputs.
+int launch_route_record(qq_ctx *ctx, const int32_t *idx, const double *w, const float *probs, int T,
+                        int K, int E, float *rec);
 size_t grouped_work_bytes(const qq_moe *m, int T);
 
 // LFM2 single-token forward (lfm2.hip).  Matvec modes: y = W x; hidden +=

@@ -259,4 +259,38 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
     return QQ_OK;
 }
 
+// The routing record of the WebGPU engines' top-K shaders
+// (src/webgpu.js:1236-1240): per row, K selected experts as floats, their K
+// weights rounded to fp32, the E probabilities.  One thread per record word.
+__global__ __launch_bounds__(256) void route_record_kernel(const int32_t *__restrict__ idx,
+                                                           const double *__restrict__ w,
+                                                           const float *__restrict__ probs, int T, int K,
+                                                           int E, float *__restrict__ rec)
+{
+    const int L = 2 * K + E;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (size_t)T * L) return;
+    const int t = (int)(i / L), j = (int)(i - (size_t)t * L);
+    float v;
+    if (j < K)
+        v = (float)idx[(size_t)t * K + j];
+    else if (j < 2 * K)
+        v = (float)w[(size_t)t * K + j - K];
+    else
+        v = probs[(size_t)t * E + j - 2 * K];
+    rec[i] = v;
+}
+
+int launch_route_record(qq_ctx *ctx, const int32_t *idx, const double *w, const float *probs, int T,
+                        int K, int E, float *rec)
+{
+    const size_t n = (size_t)T * (2 * K + E);
+    prof_begin(ctx, K_ROUTER_TOPK);
+    QQ_LAUNCH(ctx, route_record_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, idx, w, probs, T, K, E,
+              rec);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
 }  // namespace qq

@@ -18,6 +18,14 @@
 //                             whole token on the device from the attached file,
 //                             honouring engine.expertMask and calling
 //                             engine.onRouterUpdate for every MoE block
+// and, for hosts that keep activations in device memory as the WebGPU engines
+// do (src/webgpu.js):
+//   device.createBuffer / uploadBuffer / writeBuffer / readF32   GPUDevice's buffer
+//                             calls (src/webgpu.js:369-430) on DeviceBuffers
+//   Lfm2GPUEngine.prototype._moEFFNGPU, Qwen3GPUEngine.prototype._moEFFNGPU and
+//   their _readbackRoutingData (src/webgpu.js:1882-1945, :878-990), for engines
+//                             whose buffers are this device's
+//   device.moeForwardDev / matvecDev / rmsnormDev   the *_dev entry points
 //
 // There is no CPU fallback: when the addon or the device is missing, the
 // constructor and install() throw.  Written for Node 12 (no `?.`, no `??`).
@@ -64,6 +72,37 @@ function asFloat32(a) {
     return (a instanceof Float32Array) ? a : Float32Array.from(a);
 }
 
+// Device memory standing for a WebGPU GPUBuffer (src/webgpu.js:369-392), or a
+// byte range of one: views share their root's allocation, which release()
+// (or garbage collection) frees.
+class DeviceBuffer {
+    constructor(device, handle, byteOffset, size, root) {
+        this.device = device;
+        this.handle = handle;
+        this.byteOffset = byteOffset;
+        this.size = size;
+        this.root = root || null;
+    }
+
+    view(byteOffset, size) {
+        if (byteOffset < 0 || size < 0 || byteOffset + size > this.size || (byteOffset & 3))
+            throw new RangeError('DeviceBuffer.view: [' + byteOffset + ', +' + size + ') outside ' + this.size + ' bytes');
+        return new DeviceBuffer(this.device, this.handle, this.byteOffset + byteOffset, size, this.root || this);
+    }
+
+    release() {
+        if (!this.root && this.handle) this.device.native.release(this.handle);
+        this.handle = null;
+    }
+}
+
+function engineDims(eng) {
+    // Lfm2GPUEngine keeps the CPU engine's configuration in _cpu
+    // (src/webgpu.js:1470-1500); Qwen3GPUEngine holds it itself (:498-530)
+    const c = eng._cpu && eng._cpu.nExperts ? eng._cpu : eng;
+    return { E: c.nExperts, K: c.nExpertsUsed };
+}
+
 class MoEDevice {
     constructor(device) {
         this.native = native();
@@ -72,6 +111,162 @@ class MoEDevice {
         this.fallbackMatmul = null;
         this._gguf = null;
         this._lfm2 = [];                 // {engine, model}: one device model per engine
+        // GPUDevice.device.queue.writeBuffer (src/webgpu.js:1966), for engines
+        // whose _gpu is this device
+        const dev = this;
+        this.device = { queue: { writeBuffer: function (buf, off, data) { dev.writeBuffer(buf, off, data); } } };
+    }
+
+    // ---- device buffers: GPUDevice.createBuffer / uploadBuffer / readF32 ----
+    // (src/webgpu.js:369-430): sizes round up to 4 bytes, memory starts zeroed.
+    createBuffer(size) {
+        const n = Math.ceil(size / 4) * 4;
+        return new DeviceBuffer(this, this.native.bufAlloc(this.ctx, n), 0, n, null);
+    }
+
+    uploadBuffer(data) {
+        const bytes = data instanceof ArrayBuffer ? new Uint8Array(data)
+                    : new Uint8Array(data.buffer, data.byteOffset, data.byteLength);
+        const buf = this.createBuffer(bytes.length);
+        this.writeBuffer(buf, 0, bytes);
+        return buf;
+    }
+
+    writeBuffer(buf, byteOffset, data) {
+        this._own(buf, 'writeBuffer');
+        this.native.bufWrite(this.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), data);
+    }
+
+    // The values once the work enqueued before the call has run.
+    readF32Sync(buf, nElems, byteOffset) {
+        this._own(buf, 'readF32');
+        const out = new Float32Array(nElems);
+        this.native.bufRead(this.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), out);
+        return out;
+    }
+
+    readF32(buf, nElems) {
+        const dev = this;
+        return new Promise(function (resolve) { resolve(dev.readF32Sync(buf, nElems)); });
+    }
+
+    synchronize() { this.native.synchronize(this.ctx); }
+
+    _own(buf, what) {
+        if (!(buf instanceof DeviceBuffer) || buf.device !== this || !buf.handle)
+            throw new TypeError(what + ': expected a live DeviceBuffer of this device');
+    }
+
+    // ---- device-pointer calls (include/qq_moe.h *_dev), enqueued ----
+    // hidden += MoE(x) for T rows of device buffers; opts as moeForward plus
+    // record: a DeviceBuffer receiving the routing record of every row
+    // ([K experts | K weights | E probs] as floats, qq_moe_forward_record_dev).
+    moeForwardDev(layer, xBuf, hiddenBuf, T, opts) {
+        const o = opts || {};
+        const K = o.K !== undefined ? o.K : 4;
+        const E = layer.ffnGateExps.shape[2];
+        const h = this.layerHandle(layer, E, K, o.gating, o.block);
+        let mask = null;
+        if (o.mask && o.mask.size) {
+            mask = new Uint8Array(h.E);
+            o.mask.forEach(function (e) { if (e >= 0 && e < h.E) mask[e] = 1; });
+        }
+        this._own(xBuf, 'moeForwardDev');
+        this._own(hiddenBuf, 'moeForwardDev');
+        const rec = o.record || null;
+        if (rec) this._own(rec, 'moeForwardDev');
+        this.native.moeForwardDev(this.ctx, h.moe, xBuf.handle, xBuf.byteOffset, hiddenBuf.handle,
+                                  hiddenBuf.byteOffset, T | 0, mask, rec ? rec.handle : null, rec ? rec.byteOffset : 0);
+    }
+
+    // y = W x for `rows` vectors of device buffers (matmulQ80xF32 on device memory)
+    matvecDev(meta, xBuf, yBuf, rows) {
+        if (meta.type !== 8) throw new Error('matvecDev: tensor type ' + meta.type + ' is not Q8_0');
+        const t = this.tensorFor(meta, meta.shape[0], meta.shape[1], 1);
+        this._own(xBuf, 'matvecDev');
+        this._own(yBuf, 'matvecDev');
+        this.native.matvecDev(this.ctx, t, 0, xBuf.handle, xBuf.byteOffset, yBuf.handle, yBuf.byteOffset,
+                              rows === undefined ? 1 : rows | 0);
+    }
+
+    // rmsnorm (src/tensor.js:103-114) of T rows of H floats; wBuf null = unit weight
+    rmsnormDev(xBuf, wBuf, outBuf, T, H, eps) {
+        this._own(xBuf, 'rmsnormDev');
+        this._own(outBuf, 'rmsnormDev');
+        if (wBuf) this._own(wBuf, 'rmsnormDev');
+        this.native.rmsnormDev(this.ctx, xBuf.handle, xBuf.byteOffset, wBuf ? wBuf.handle : null,
+                               wBuf ? wBuf.byteOffset : 0, outBuf.handle, outBuf.byteOffset, T | 0, H | 0, +eps);
+    }
+
+    // ---- the WebGPU engines' MoE block ----
+    // True when `eng` keeps its activations in this device's buffers (its
+    // _buf.normed is a DeviceBuffer of this device).
+    ownsEngine(eng) {
+        return !!(eng && eng._buf && eng._buf.normed instanceof DeviceBuffer && eng._buf.normed.device === this);
+    }
+
+    // Lfm2GPUEngine._moEFFNGPU / Qwen3GPUEngine._moEFFNGPU (src/webgpu.js:
+    // 1882-1917, :878-915) on `eng`: _buf.hidden += MoE(_buf.normed), and the
+    // routing record of MoE layer gl._moeIdx into eng._gpuRoutingBufs[moeIdx]
+    // (a DeviceBuffer of 2K + E floats, made here when missing).  Enqueued: no
+    // host round trip, as in the reference.  expertMask is honoured when set
+    // (the WebGPU engines keep it null).
+    moEFFNGPU(eng, layerIdx, gl, cl, gating) {
+        const d = engineDims(eng);
+        const moeIdx = gl && gl._moeIdx !== undefined ? gl._moeIdx : layerIdx;
+        if (!eng._gpuRoutingBufs) eng._gpuRoutingBufs = [];
+        let rec = eng._gpuRoutingBufs[moeIdx];
+        const recBytes = (2 * d.K + d.E) * 4;
+        if (!(rec instanceof DeviceBuffer) || rec.device !== this || rec.size < recBytes) {
+            rec = this.createBuffer(recBytes);
+            eng._gpuRoutingBufs[moeIdx] = rec;
+        }
+        this.moeForwardDev(cl, eng._buf.normed, eng._buf.hidden, 1,
+                           { K: d.K, gating: gating, mask: eng.expertMask, block: layerIdx, record: rec });
+    }
+
+    // _readbackRoutingData (src/webgpu.js:1922-1945, :969-990): every MoE
+    // layer's routing record read back once the token's work has run (records
+    // that are views of one allocation in a single read), then onRouterUpdate
+    // per layer with {layer, probs, selected, weights}.
+    readbackRoutingData(eng) {
+        if (!eng.onRouterUpdate) return Promise.resolve();
+        const d = engineDims(eng), K = d.K, E = d.E, L = 2 * K + E;
+        const bufs = eng._gpuRoutingBufs || [];
+        const roots = new Map();   // root allocation -> its floats, read once
+        for (const b of bufs) {
+            this._own(b, 'readbackRoutingData');
+            const r = b.root || b;
+            if (!roots.has(r)) roots.set(r, this.readF32Sync(r, r.size / 4));
+        }
+        for (let m = 0; m < bufs.length; m++) {
+            const b = bufs[m], r = b.root || b;
+            const off = (b.byteOffset - r.byteOffset) / 4;
+            const res = roots.get(r).subarray(off, off + L);
+            const selected = [], weights = [];
+            for (let k = 0; k < K; k++) {
+                selected.push(Math.round(res[k]));
+                weights.push(res[K + k]);
+            }
+            eng.onRouterUpdate({
+                layer: eng._moeAbsLayerIndices ? eng._moeAbsLayerIndices[m] : m,
+                probs: Array.from(res.subarray(2 * K, 2 * K + E)),
+                selected: selected,
+                weights: weights,
+            });
+        }
+        return Promise.resolve();
+    }
+
+    // Routing records of `nMoE` MoE layers as views of one allocation, so the
+    // batched readback is a single copy; sets eng._gpuRoutingBufs.
+    routingBuffers(eng, nMoE) {
+        const d = engineDims(eng), recBytes = (2 * d.K + d.E) * 4;
+        const root = this.createBuffer(recBytes * nMoE);
+        const views = [];
+        for (let m = 0; m < nMoE; m++) views.push(root.view(m * recBytes, recBytes));
+        eng._gpuRoutingBufs = views;
+        return views;
     }
 
     // Bind MoE blocks from a GGUF file: the layer of block l is read from the
@@ -291,9 +486,27 @@ function install(scope, opts) {
             return dev.moEFFNQwen3(this, layerIdx, layer);
         };
     }
+    // The WebGPU engines: an engine whose buffers are this device's
+    // DeviceBuffers (its _gpu is the returned device) runs _moEFFNGPU and
+    // _readbackRoutingData here; any other engine keeps its own methods.
+    [['Lfm2GPUEngine', GATING_SIGMOID_BIAS], ['Qwen3GPUEngine', GATING_SOFTMAX]].forEach(function (c) {
+        const cls = scope[c[0]];
+        if (!cls || !cls.prototype) return;
+        const P = cls.prototype, block = P._moEFFNGPU, readback = P._readbackRoutingData;
+        P._moEFFNGPU = function (layerIdx, gl, cl) {
+            if (dev.ownsEngine(this)) return dev.moEFFNGPU(this, layerIdx, gl, cl, c[1]);
+            if (block) return block.call(this, layerIdx, gl, cl);
+            throw new Error(c[0] + '._moEFFNGPU: the engine\'s buffers are not on this device');
+        };
+        P._readbackRoutingData = function () {
+            if (dev.ownsEngine(this)) return dev.readbackRoutingData(this);
+            if (readback) return readback.call(this);
+            return Promise.resolve();
+        };
+    });
     return dev;
 }
 
-module.exports = { MoEDevice: MoEDevice, install: install, readWeightF32: readWeightF32,
+module.exports = { MoEDevice: MoEDevice, DeviceBuffer: DeviceBuffer, install: install, readWeightF32: readWeightF32,
                    halfToNumber: halfToNumber, ADDON_PATH: ADDON_PATH,
                    GATING_SIGMOID_BIAS: GATING_SIGMOID_BIAS, GATING_SOFTMAX: GATING_SOFTMAX };

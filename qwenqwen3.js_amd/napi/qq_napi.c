@@ -34,7 +34,19 @@
  *       routes: Int32Array(nLayers*K), Float64Array(nLayers*K), Float32Array(nLayers*E)
  *       receive every MoE block's onRouterUpdate payload (dense rows untouched)
  *   lfm2Reset(ctx, lfm2)               zero the KV cache and conv states
- *   release(handle)    frees a tensor / moe / ctx / gguf now instead of at GC
+ * Device buffers and the device-pointer calls (byte offsets range-checked
+ * against the buffer, multiples of 4):
+ *   bufAlloc(ctx, nbytes) -> buf       zeroed device memory
+ *   bufWrite(ctx, buf, byteOffset, data: ArrayBuffer | typed array)
+ *   bufRead(ctx, buf, byteOffset, out: typed array) -> out   waits for enqueued work
+ *   synchronize(ctx)
+ *   moeForwardDev(ctx, moe, xBuf, xOff, hiddenBuf, hiddenOff, T, mask | null,
+ *                 recordBuf | null, recordOff)
+ *       hidden += MoE(x), and per row the routing record [K idx | K w | E probs]
+ *       as floats (qq_moe_forward_record_dev); enqueued
+ *   matvecDev(ctx, tensor, mat, xBuf, xOff, yBuf, yOff, rows)      enqueued
+ *   rmsnormDev(ctx, xBuf, xOff, wBuf | null, wOff, outBuf, outOff, T, H, eps)   enqueued
+ *   release(handle)    frees a tensor / moe / ctx / gguf / buffer now instead of at GC
  */
 #include <node_api.h>
 #include <stdint.h>
@@ -46,17 +58,18 @@
 #include "../../include/qq_lfm2.h"
 #include "../../include/qq_moe.h"
 
-enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3, H_GGUF = 4, H_LFM2 = 5 };
+enum { H_CTX = 1, H_TENSOR = 2, H_MOE = 3, H_GGUF = 4, H_LFM2 = 5, H_BUF = 6 };
 
 typedef struct handle {
     int kind;
-    void *ptr;           /* qq_ctx*, qq_tensor*, qq_moe*, qq_gguf* or qq_lfm2* (NULL once released) */
+    void *ptr;           /* qq_ctx*, qq_tensor*, qq_moe*, qq_gguf*, qq_lfm2* or a device buffer (NULL once released) */
     struct handle *ctx;  /* owning context handle (tensor, moe) */
     napi_ref ctx_ref;    /* keeps the context alive while this handle lives */
     napi_ref keep[3];    /* moe: keeps gate/up/down tensors alive */
     int in_dim, out_dim, n_mats;
     int H, E, K;
     int vocab;           /* lfm2 */
+    size_t size;         /* buffer: bytes */
 } handle;
 
 #define CHECK_NAPI(env, call)                                                        \
@@ -85,6 +98,7 @@ static void release_handle(napi_env env, handle *h)
     case H_CTX: qq_destroy((qq_ctx *)h->ptr); break;
     case H_GGUF: qq_gguf_close((qq_gguf *)h->ptr); break;
     case H_LFM2: qq_lfm2_release(ctx, (qq_lfm2 *)h->ptr); break;
+    case H_BUF: qq_buffer_free(ctx, h->ptr); break;
     }
     h->ptr = NULL;
     for (int i = 0; i < 3; i++)
@@ -695,6 +709,200 @@ static napi_value js_lfm2_reset(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* ---- device buffers ---- */
+
+static int get_i64(napi_env env, napi_value v, int64_t *out)
+{
+    return napi_get_value_int64(env, v, out) == napi_ok ? 0 : -1;
+}
+
+/* Device address of bytes [off, off + need) of buffer `v`, range-checked;
+ * off must be a multiple of 4 (the buffers hold floats).  NULL with a thrown
+ * error when out of range. */
+static void *buf_span(napi_env env, napi_value v, napi_value offv, size_t need, const char *what)
+{
+    handle *h = get_handle(env, v, H_BUF);
+    if (!h) return NULL;
+    int64_t off;
+    if (get_i64(env, offv, &off) || off < 0 || (off & 3) || (uint64_t)off > h->size || need > h->size - (size_t)off) {
+        char msg[200];
+        snprintf(msg, sizeof msg, "%s: byte range [%lld, +%zu) outside the %zu-byte buffer or unaligned", what,
+                 (long long)off, need, h->size);
+        napi_throw_range_error(env, NULL, msg);
+        return NULL;
+    }
+    return (char *)h->ptr + off;
+}
+
+static napi_value js_buf_alloc(napi_env env, napi_callback_info info)
+{
+    ARGS(2);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    int64_t n;
+    if (get_i64(env, argv[1], &n) || n < 0) {
+        napi_throw_type_error(env, NULL, "bufAlloc(ctx, nbytes)");
+        return NULL;
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    void *p = NULL;
+    int rc = qq_buffer_alloc(ctx, (size_t)n, &p);
+    if (rc) return throw_qq(env, "qq_buffer_alloc", rc, ctx);
+    handle *h = child_of(env, argv[0], ch, H_BUF);
+    if (!h) {
+        qq_buffer_free(ctx, p);
+        napi_throw_error(env, NULL, "qq_napi: out of memory");
+        return NULL;
+    }
+    h->ptr = p;
+    h->size = (size_t)n;
+    return new_handle(env, h);
+}
+
+/* bufWrite(ctx, buf, byteOffset, data: ArrayBuffer | typed array) */
+static napi_value js_buf_write(napi_env env, napi_callback_info info)
+{
+    ARGS(4);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    uint8_t *data;
+    size_t len;
+    if (get_bytes(env, argv[3], &data, &len)) {
+        napi_throw_type_error(env, NULL, "bufWrite(ctx, buf, byteOffset, data)");
+        return NULL;
+    }
+    void *dst = buf_span(env, argv[1], argv[2], len, "bufWrite");
+    if (!dst) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_buffer_write(ctx, dst, data, len);
+    if (rc) return throw_qq(env, "qq_buffer_write", rc, ctx);
+    return NULL;
+}
+
+/* bufRead(ctx, buf, byteOffset, out: typed array) -> out (its whole view is filled) */
+static napi_value js_buf_read(napi_env env, napi_callback_info info)
+{
+    ARGS(4);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    uint8_t *data;
+    size_t len;
+    bool is_ta = false;
+    napi_is_typedarray(env, argv[3], &is_ta);
+    if (!is_ta || get_bytes(env, argv[3], &data, &len)) {
+        napi_throw_type_error(env, NULL, "bufRead(ctx, buf, byteOffset, out: typed array)");
+        return NULL;
+    }
+    const void *src = buf_span(env, argv[1], argv[2], len, "bufRead");
+    if (!src) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_buffer_read(ctx, src, data, len);
+    if (rc) return throw_qq(env, "qq_buffer_read", rc, ctx);
+    return argv[3];
+}
+
+static napi_value js_synchronize(napi_env env, napi_callback_info info)
+{
+    ARGS(1);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_synchronize(ctx);
+    if (rc) return throw_qq(env, "qq_synchronize", rc, ctx);
+    return NULL;
+}
+
+/* moeForwardDev(ctx, moe, xBuf, xOff, hiddenBuf, hiddenOff, T, mask | null,
+ *               recordBuf | null, recordOff): qq_moe_forward_record_dev, enqueued */
+static napi_value js_moe_forward_dev(napi_env env, napi_callback_info info)
+{
+    ARGS(10);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *mh = get_handle(env, argv[1], H_MOE);
+    if (!mh) return NULL;
+    int32_t T;
+    if (get_i32(env, argv[6], &T) || T < 0) {
+        napi_throw_type_error(env, NULL,
+                              "moeForwardDev(ctx, moe, xBuf, xOff, hiddenBuf, hiddenOff, T, mask, recordBuf, recordOff)");
+        return NULL;
+    }
+    const size_t rowb = (size_t)T * mh->H * 4;
+    const float *x = (const float *)buf_span(env, argv[2], argv[3], rowb, "moeForwardDev x");
+    if (!x) return NULL;
+    float *hid = (float *)buf_span(env, argv[4], argv[5], rowb, "moeForwardDev hidden");
+    if (!hid) return NULL;
+    uint8_t *mask = NULL;
+    if (!is_nullish(env, argv[7])) {
+        size_t n;
+        if (get_typed(env, argv[7], napi_uint8_array, (void **)&mask, &n) || n < (size_t)mh->E) {
+            napi_throw_type_error(env, NULL, "moeForwardDev: mask must be a Uint8Array of E bytes or null");
+            return NULL;
+        }
+    }
+    float *rec = NULL;
+    if (!is_nullish(env, argv[8])) {
+        rec = (float *)buf_span(env, argv[8], argv[9], (size_t)T * (2 * mh->K + mh->E) * 4, "moeForwardDev record");
+        if (!rec) return NULL;
+    }
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_moe_forward_record_dev(ctx, (qq_moe *)mh->ptr, x, hid, T, mask, rec);
+    if (rc) return throw_qq(env, "qq_moe_forward_record_dev", rc, ctx);
+    return NULL;
+}
+
+/* matvecDev(ctx, tensor, mat, xBuf, xOff, yBuf, yOff, rows): qq_q8_0_matvec_dev, enqueued */
+static napi_value js_matvec_dev(napi_env env, napi_callback_info info)
+{
+    ARGS(8);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    handle *th = get_handle(env, argv[1], H_TENSOR);
+    if (!th) return NULL;
+    int32_t mat, rows;
+    if (get_i32(env, argv[2], &mat) || get_i32(env, argv[7], &rows) || rows < 0) {
+        napi_throw_type_error(env, NULL, "matvecDev(ctx, tensor, mat, xBuf, xOff, yBuf, yOff, rows)");
+        return NULL;
+    }
+    const float *x = (const float *)buf_span(env, argv[3], argv[4], (size_t)rows * th->in_dim * 4, "matvecDev x");
+    if (!x) return NULL;
+    float *y = (float *)buf_span(env, argv[5], argv[6], (size_t)rows * th->out_dim * 4, "matvecDev y");
+    if (!y) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_q8_0_matvec_dev(ctx, (qq_tensor *)th->ptr, mat, x, y, rows);
+    if (rc) return throw_qq(env, "qq_q8_0_matvec_dev", rc, ctx);
+    return NULL;
+}
+
+/* rmsnormDev(ctx, xBuf, xOff, wBuf | null, wOff, outBuf, outOff, T, H, eps): qq_rmsnorm_dev, enqueued */
+static napi_value js_rmsnorm_dev(napi_env env, napi_callback_info info)
+{
+    ARGS(10);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    int32_t T, H;
+    double eps;
+    if (get_i32(env, argv[7], &T) || get_i32(env, argv[8], &H) || T < 0 || H < 0 ||
+        napi_get_value_double(env, argv[9], &eps) != napi_ok) {
+        napi_throw_type_error(env, NULL, "rmsnormDev(ctx, xBuf, xOff, wBuf, wOff, outBuf, outOff, T, H, eps)");
+        return NULL;
+    }
+    const size_t rowb = (size_t)T * H * 4;
+    const float *x = (const float *)buf_span(env, argv[1], argv[2], rowb, "rmsnormDev x");
+    if (!x) return NULL;
+    const float *w = NULL;
+    if (!is_nullish(env, argv[3])) {
+        w = (const float *)buf_span(env, argv[3], argv[4], (size_t)H * 4, "rmsnormDev weight");
+        if (!w) return NULL;
+    }
+    float *out = (float *)buf_span(env, argv[5], argv[6], rowb, "rmsnormDev out");
+    if (!out) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int rc = qq_rmsnorm_dev(ctx, x, w, out, T, H, eps);
+    if (rc) return throw_qq(env, "qq_rmsnorm_dev", rc, ctx);
+    return NULL;
+}
+
 static napi_value js_release(napi_env env, napi_callback_info info)
 {
     ARGS(1);
@@ -727,6 +935,13 @@ static napi_value module_init(napi_env env, napi_value exports)
         {"lfm2Info", NULL, js_lfm2_info, NULL, NULL, NULL, napi_enumerable, NULL},
         {"lfm2Forward", NULL, js_lfm2_forward, NULL, NULL, NULL, napi_enumerable, NULL},
         {"lfm2Reset", NULL, js_lfm2_reset, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"bufAlloc", NULL, js_buf_alloc, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"bufWrite", NULL, js_buf_write, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"bufRead", NULL, js_buf_read, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"moeForwardDev", NULL, js_moe_forward_dev, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"matvecDev", NULL, js_matvec_dev, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"rmsnormDev", NULL, js_rmsnorm_dev, NULL, NULL, NULL, napi_enumerable, NULL},
         {"release", NULL, js_release, NULL, NULL, NULL, napi_enumerable, NULL},
     };
     if (napi_define_properties(env, exports, sizeof props / sizeof props[0], props) != napi_ok) return NULL;

@@ -33,6 +33,7 @@ EXPORTS = (
     "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
+    "qq_buffer_alloc", "qq_buffer_free", "qq_buffer_write", "qq_buffer_read", "qq_moe_forward_record_dev",
 )
 # ... and include/qq_gguf.h
 GGUF_EXPORTS = (
@@ -119,6 +120,11 @@ def load():
         "qq_capture_end": (I, [P, PP]),
         "qq_graph_launch": (I, [P, P]),
         "qq_graph_release": (I, [P, P]),
+        "qq_buffer_alloc": (I, [P, S, PP]),
+        "qq_buffer_free": (I, [P, P]),
+        "qq_buffer_write": (I, [P, P, P, S]),
+        "qq_buffer_read": (I, [P, P, P, S]),
+        "qq_moe_forward_record_dev": (I, [P, P, P, P, I, P, P]),
         "qq_gguf_open": (I, [ctypes.c_char_p, PP]),
         "qq_gguf_open_memory": (I, [P, S, PP]),
         "qq_gguf_close": (None, [P]),
@@ -222,6 +228,25 @@ class Context:
         """out = rmsnorm(x) * weight (weight_ptr None: unit weight), device pointers."""
         self.check(self.L.qq_rmsnorm_dev(self.h, x_ptr, weight_ptr, out_ptr, int(T), int(H),
                                          float(eps)), "qq_rmsnorm_dev")
+
+    def buffer_alloc(self, nbytes):
+        """Zeroed device memory (qq_buffer_alloc); returns the device address."""
+        p = ctypes.c_void_p()
+        self.check(self.L.qq_buffer_alloc(self.h, int(nbytes), ctypes.byref(p)), "qq_buffer_alloc")
+        return p.value
+
+    def buffer_free(self, ptr):
+        self.check(self.L.qq_buffer_free(self.h, ctypes.c_void_p(ptr)), "qq_buffer_free")
+
+    def buffer_write(self, ptr, arr):
+        a = np.ascontiguousarray(arr)
+        self.check(self.L.qq_buffer_write(self.h, ctypes.c_void_p(ptr), _ptr(a), a.nbytes), "qq_buffer_write")
+
+    def buffer_read(self, ptr, out):
+        """Fill the contiguous array `out` from device address `ptr` once enqueued work has run."""
+        assert out.flags["C_CONTIGUOUS"]
+        self.check(self.L.qq_buffer_read(self.h, ctypes.c_void_p(ptr), _ptr(out), out.nbytes), "qq_buffer_read")
+        return out
 
     def set_mfma_min_tokens(self, tokens):
         """Token batches of >= tokens rows use the fp16 MFMA path (0: never)."""
@@ -475,6 +500,19 @@ class MoeLayer:
         self.ctx.check(self.ctx.L.qq_moe_forward_dev(self.ctx.h, self.h, ctypes.c_void_p(x_ptr),
                                                      ctypes.c_void_p(hidden_ptr), T, _ptr(m), vp(idx_ptr),
                                                      vp(w_ptr), vp(probs_ptr)), "qq_moe_forward_dev")
+
+    def forward_record_dev(self, x_ptr, hidden_ptr, T, mask=None, record_ptr=None):
+        """hidden += MoE(x) and the per-row routing record [K idx | K w | E probs] as
+        floats (qq_moe_forward_record_dev), device pointers, enqueued."""
+        m = None
+        if mask is not None:
+            m = np.zeros(self.E, np.uint8)
+            for e in mask:
+                m[e] = 1
+        vp = lambda p: None if p is None else ctypes.c_void_p(p)
+        self.ctx.check(self.ctx.L.qq_moe_forward_record_dev(self.ctx.h, self.h, ctypes.c_void_p(x_ptr),
+                                                            ctypes.c_void_p(hidden_ptr), T, _ptr(m),
+                                                            vp(record_ptr)), "qq_moe_forward_record_dev")
 
     def forward_noalloc_dev(self, x_ptr, hidden_ptr, T, mask=None, idx_ptr=None, w_ptr=None, probs_ptr=None):
         """forward_dev with the fixed per-GPU scratch array (qq_moe_forward_noalloc_dev)."""

@@ -48,6 +48,21 @@ def test_js_attach_gguf(tmp_path, arch):
     assert res["max_rel_l2"] < 1e-4
 
 
+@pytest.mark.parametrize("gating", ["sigmoid", "softmax"])
+def test_js_gpu_engine(gating):
+    """Lfm2GPUEngine / Qwen3GPUEngine._moEFFNGPU and _readbackRoutingData rebound by
+    install() for an engine whose buffers are the device's (src/webgpu.js:1882-1945,
+    :878-990), against the CPU engine's restatement."""
+    print("js gpu engine", gating, flush=True)
+    p = subprocess.run([NODE, os.path.join(ROOT, "tests", "js", "gpu_engine_check.js"),
+                        "256", "96", "16", "4", "3", gating], capture_output=True, text=True, timeout=240)
+    assert p.stdout.strip(), p.stderr
+    res = json.loads(p.stdout.strip().splitlines()[-1])
+    bad = [c for c in res["checks"] if not c["ok"]]
+    assert res["ok"] and not bad, (bad, p.stderr[-2000:])
+    assert res["max_rel_l2"] < 1e-4
+
+
 def test_js_lfm2_forward(tmp_path):
     """MoEDevice.attachLfm2Forward: Lfm2Engine.forward / resetKVCache run the whole
     token on the device from the attached file, against oracle/lfm2_ref.js."""
