@@ -109,7 +109,8 @@ def test_js_matvec_matches_c_oracle(tmp_path):
 
 ADDON_EXPORTS = ["init", "lastError", "uploadQ80", "matvec", "moeCreate", "moeSetGating", "moeForward",
                  "ggufOpen", "ggufTensors", "ggufMoeParams", "ggufMoeLayer", "lfm2Create", "lfm2Info",
-                 "lfm2Forward", "lfm2Reset", "release"]
+                 "lfm2Forward", "lfm2Reset", "bufAlloc", "bufWrite", "bufRead", "synchronize",
+                 "moeForwardDev", "matvecDev", "rmsnormDev", "release"]
 
 
 def test_addon_exports():
