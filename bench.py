@@ -398,6 +398,41 @@ def _time_steps(torch, ctx, stream, run, steps, warmup):
     return ev0.elapsed_time(ev1)
 
 
+def host_call_leg(ctx, layers, X, HID, steps, warmup):
+    """The host-pointer drop-in, qq_moe_forward: the call the JS _moEFFN makes
+    through the Node-API addon for every token (src/lfm2-engine.js:257).  x and
+    hidden go in over PCIe, hidden and the routing come out, and the call
+    synchronises.  Wall clock per call on the host, the same layer rotation as
+    the device-resident steps; without and with the router payload (the
+    probabilities onRouterUpdate carries)."""
+    import ctypes
+    L = ctx.L
+    x = np.ascontiguousarray(X.cpu().numpy())
+    h = np.ascontiguousarray(HID.cpu().numpy())
+    S, T, H = x.shape
+    K, E = layers[0].K, layers[0].E
+    idx = np.empty((T, K), np.int32)
+    w = np.empty((T, K), np.float64)
+    probs = np.empty((T, E), np.float32)
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    px = [vp(x[s]) for s in range(S)]
+    ph = [vp(h[s]) for s in range(S)]
+    pi, pw, pp = vp(idx), vp(w), vp(probs)
+    out = {}
+    for key, want in (("us_per_call", None), ("with_router_payload_us_per_call", pp)):
+        for i in range(-warmup, steps):
+            if i == 0:
+                t0 = time.perf_counter()
+            lay = layers[i % len(layers)]
+            rc = L.qq_moe_forward(ctx.h, lay.h, px[i % S], ph[i % S], T, None, pi, pw, want)
+            if rc:
+                raise RuntimeError("qq_moe_forward: %s" % L.qq_last_error(ctx.h).decode())
+        out[key] = round((time.perf_counter() - t0) * 1e6 / steps, 2)
+    out["tokens_per_s"] = round(T * 1e6 / out["us_per_call"], 1)
+    out["calls"] = steps
+    return out
+
+
 def timed(torch, ctx, stream, step, period, steps, warmup, launches_per_step):
     """step(i) enqueues step i and depends only on i % period.
 
@@ -573,6 +608,9 @@ def main():
         extra["tflops_layer"] = round(6.0 * n_pairs * H * F * calls / (ms_per_step * 1e9), 2)
         if stack and T == 1:
             extra["us_per_token"] = round(ms_per_step * 1000.0, 2)
+        if not stack and T == 1:
+            # beside `value`: the same layer through the host-pointer call (PCIe included)
+            extra["host_call"] = host_call_leg(ctx, keep, X, HID, min(args.steps, 400), min(args.warmup, 40))
 
     result = {
         "metric": LFM2_METRIC if kind == "lfm2" else METRIC,

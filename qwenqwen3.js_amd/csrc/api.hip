@@ -2,6 +2,7 @@
 #include "qq_internal.h"
 
 #include <cstdlib>
+#include <cstring>
 #include <new>
 
 // Scratch of qq_moe_forward_noalloc_dev: one array per GPU, held until the
@@ -49,14 +50,52 @@ int ensure_scratch(qq_ctx *ctx, size_t bytes)
 
 int ensure_pinned(qq_ctx *ctx, size_t bytes)
 {
+    bytes += PIN_HDR;
     if (bytes <= ctx->pinned_bytes) return QQ_OK;
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     if (ctx->pinned) (void)hipHostFree(ctx->pinned);
     ctx->pinned = nullptr;
     ctx->pinned_bytes = 0;
+    ctx->pinned_dev = nullptr;
     const size_t sz = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);
-    QQ_HIP(ctx, hipHostMalloc(&ctx->pinned, sz, hipHostMallocDefault));
+    // coherent: the staging kernels read and write it across calls, so no GPU
+    // cache may keep an old copy of a line
+    QQ_HIP(ctx, hipHostMalloc(&ctx->pinned, sz, hipHostMallocMapped | hipHostMallocCoherent));
+    void *d = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&d, ctx->pinned, 0);
+    if (e != hipSuccess) {
+        (void)hipHostFree(ctx->pinned);
+        ctx->pinned = nullptr;
+        return check_hip(ctx, e, "hipHostGetDevicePointer");
+    }
+    ctx->pinned_dev = static_cast<char *>(d);
     ctx->pinned_bytes = sz;
+    return QQ_OK;
+}
+
+// Small host <-> device transfers (the 8-16 KB rows of a decode call) as one
+// copy kernel over the mapped pinned buffer: the GPU reads or writes host
+// memory over PCIe directly instead of a DMA-engine transfer.
+// The device error word rides along to the pinned header, so the host learns
+// of a timed-out device wait from the same synchronisation.
+__global__ __launch_bounds__(256) void stage_copy_kernel(const uint4 *__restrict__ src, uint4 *__restrict__ dst,
+                                                         size_t n, const uint32_t *__restrict__ err,
+                                                         uint32_t *__restrict__ err_dst)
+{
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) dst[i] = src[i];
+    if (blockIdx.x == 0 && threadIdx.x == 0) *err_dst = *err;
+}
+
+int launch_stage_copy(qq_ctx *ctx, const void *src, void *dst, size_t bytes)
+{
+    if (bytes % 16) return set_error(ctx, "stage_copy: %zu bytes is not a multiple of 16", bytes);
+    if (!ctx->pinned_dev) return set_error(ctx, "stage_copy: no pinned staging buffer");
+    const size_t n = bytes / 16;
+    const unsigned g = (unsigned)std::max<size_t>(std::min<size_t>((n + 255) / 256, 256), 1);
+    QQ_LAUNCH(ctx, stage_copy_kernel, dim3(g), dim3(256), 0, static_cast<const uint4 *>(src),
+              static_cast<uint4 *>(dst), n, static_cast<const uint32_t *>(ctx->sync_err),
+              reinterpret_cast<uint32_t *>(ctx->pinned_dev));
+    QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
 }
 
@@ -78,12 +117,18 @@ static const char *const kKernelNames[K_COUNT] = {
 
 // Read and clear the device error word; non-zero means a bounded device-side
 // wait expired (the results of that call are not valid).
-int check_device_error(qq_ctx *ctx)
+int check_device_error(qq_ctx *ctx, bool staged)
 {
-    uint32_t e = 0;
-    QQ_HIP(ctx, hipMemcpyAsync(&e, ctx->sync_err, 4, hipMemcpyDeviceToHost, ctx->stream));
+    if (!staged) {   // the error word alone, behind the enqueued work
+        int rc = ensure_pinned(ctx, 0);
+        if (!rc) rc = launch_stage_copy(ctx, nullptr, nullptr, 0);
+        if (rc) return rc;
+    }
     QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    volatile uint32_t *word = static_cast<volatile uint32_t *>(ctx->pinned);
+    const uint32_t e = *word;
     if (e) {
+        *word = 0;
         QQ_HIP(ctx, hipMemsetAsync(ctx->sync_err, 0, 4, ctx->stream));
         QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
         snprintf(ctx->err, sizeof ctx->err, "device-side wait for the router timed out (code %u)", e);
@@ -285,7 +330,6 @@ int qq_synchronize(qq_ctx *ctx)
     if (!ctx) return QQ_E_ARG;
     if (int rc = no_capture(ctx, "qq_synchronize")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
-    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return check_device_error(ctx);
 }
 
@@ -392,12 +436,17 @@ int qq_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x, flo
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     const size_t xb = (size_t)rows * t->in_dim * 4, yb = (size_t)rows * t->out_dim * 4;
     if ((rc = ensure_scratch(ctx, align256(xb) + yb))) return rc;
+    if ((rc = ensure_pinned(ctx, align256(xb) + yb))) return rc;   // staging: x in, y out
+    char *ph = static_cast<char *>(ctx->pinned) + PIN_HDR;
+    char *pd = ctx->pinned_dev + PIN_HDR;
     float *dx = static_cast<float *>(ctx->scratch);
     float *dy = reinterpret_cast<float *>(static_cast<char *>(ctx->scratch) + align256(xb));
-    QQ_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
+    memcpy(ph, x, xb);
+    if ((rc = launch_stage_copy(ctx, pd, dx, align256(xb)))) return rc;
     if ((rc = launch_q8_0_matvec(ctx, t, mat, dx, t->in_dim, dy, t->out_dim, rows))) return rc;
-    QQ_HIP(ctx, hipMemcpyAsync(y, dy, yb, hipMemcpyDeviceToHost, ctx->stream));
-    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if ((rc = launch_stage_copy(ctx, dy, pd + align256(xb), (yb + 15) & ~(size_t)15))) return rc;
+    if ((rc = check_device_error(ctx, true))) return rc;
+    memcpy(y, ph + align256(xb), yb);
     return QQ_OK;
 }
 
@@ -626,26 +675,37 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     MaskBits mb;
     if ((rc = mask_from_bytes(ctx, mask, m->E, &mb))) return rc;
-    // device copies: x | hidden | idx | w | probs, then the forward's scratch
+    // device copies: x | hidden | idx | w | probs, then the forward's scratch.
+    // The same span is staged in the context's pinned host buffer, so each
+    // direction is one DMA copy: x | hidden in, hidden .. probs out.
     const size_t xb = (size_t)T * m->H * 4;
     const size_t ib = (size_t)T * m->K * 4, wb = (size_t)T * m->K * 8, pb = (size_t)T * m->E * 4;
-    const size_t io = 2 * align256(xb) + align256(ib) + align256(wb) + align256(pb);
+    const size_t xa = align256(xb), ia = align256(ib), wa = align256(wb);
+    const size_t io = 2 * xa + ia + wa + align256(pb);
     if ((rc = ensure_scratch(ctx, io + forward_scratch(ctx, m, T)))) return rc;
+    if ((rc = ensure_pinned(ctx, io))) return rc;
     char *s = static_cast<char *>(ctx->scratch);
+    char *ph = static_cast<char *>(ctx->pinned) + PIN_HDR;
+    char *pd = ctx->pinned_dev + PIN_HDR;
     float *dx = reinterpret_cast<float *>(s);
-    float *dh = reinterpret_cast<float *>(s + align256(xb));
-    int32_t *didx = reinterpret_cast<int32_t *>(s + 2 * align256(xb));
-    double *dw = reinterpret_cast<double *>(reinterpret_cast<char *>(didx) + align256(ib));
-    float *dp = reinterpret_cast<float *>(reinterpret_cast<char *>(dw) + align256(wb));
-    QQ_HIP(ctx, hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream));
-    QQ_HIP(ctx, hipMemcpyAsync(dh, hidden, xb, hipMemcpyHostToDevice, ctx->stream));
+    float *dh = reinterpret_cast<float *>(s + xa);
+    int32_t *didx = reinterpret_cast<int32_t *>(s + 2 * xa);
+    double *dw = reinterpret_cast<double *>(s + 2 * xa + ia);
+    float *dp = reinterpret_cast<float *>(s + 2 * xa + ia + wa);
+    memcpy(ph, x, xb);
+    memcpy(ph + xa, hidden, xb);
+    if ((rc = launch_stage_copy(ctx, pd, dx, 2 * xa))) return rc;
     if ((rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, probs ? dp : nullptr, io))) return rc;
-    QQ_HIP(ctx, hipMemcpyAsync(hidden, dh, xb, hipMemcpyDeviceToHost, ctx->stream));
-    if (idx) QQ_HIP(ctx, hipMemcpyAsync(idx, didx, ib, hipMemcpyDeviceToHost, ctx->stream));
-    if (w) QQ_HIP(ctx, hipMemcpyAsync(w, dw, wb, hipMemcpyDeviceToHost, ctx->stream));
-    if (probs) QQ_HIP(ctx, hipMemcpyAsync(probs, dp, pb, hipMemcpyDeviceToHost, ctx->stream));
-    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return check_device_error(ctx);
+    // hidden .. the last routing output wanted, in whole 16-byte words (the
+    // regions are 256-byte aligned, so the rounding stays inside them)
+    const size_t out_span = (xa + ia + (probs ? wa + pb : (w ? wb : 0)) + 15) & ~(size_t)15;
+    if ((rc = launch_stage_copy(ctx, dh, pd + xa, out_span))) return rc;
+    if ((rc = check_device_error(ctx, true))) return rc;
+    memcpy(hidden, ph + xa, xb);
+    if (idx) memcpy(idx, ph + 2 * xa, ib);
+    if (w) memcpy(w, ph + 2 * xa + ia, wb);
+    if (probs) memcpy(probs, ph + 2 * xa + ia + wa, pb);
+    return QQ_OK;
 }
 
 // ---- device buffers and the routing record ---------------------------------
@@ -688,7 +748,6 @@ int qq_buffer_write(qq_ctx *ctx, void *dev, const void *host, size_t nbytes)
     if (int rc = no_capture(ctx, "qq_buffer_write")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipMemcpyAsync(dev, host, nbytes, hipMemcpyHostToDevice, ctx->stream));
-    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return check_device_error(ctx);
 }
 
@@ -700,7 +759,6 @@ int qq_buffer_read(qq_ctx *ctx, const void *dev, void *host, size_t nbytes)
     if (int rc = no_capture(ctx, "qq_buffer_read")) return rc;
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     QQ_HIP(ctx, hipMemcpyAsync(host, dev, nbytes, hipMemcpyDeviceToHost, ctx->stream));
-    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return check_device_error(ctx);
 }
 

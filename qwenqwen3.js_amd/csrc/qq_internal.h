@@ -102,8 +102,10 @@ struct qq_ctx {
     // this device's fixed scratch array (qq_moe_forward_noalloc_dev), from
     // hipGetSymbolAddress at qq_init
     char *noalloc_scratch;
-    // pinned host staging for the host-pointer entry points
+    // pinned host staging for the host-pointer entry points, and its address
+    // in the device's address space (the staging copies are kernels)
     void *pinned;
+    char *pinned_dev;
     size_t pinned_bytes;
     // timing events of the bench entry points
     hipEvent_t ev0, ev1;
@@ -174,13 +176,22 @@ void prof_slot(qq_ctx *ctx, hipEvent_t *start, hipEvent_t *stop);
 
 int set_error(qq_ctx *ctx, const char *fmt, ...);
 int check_hip(qq_ctx *ctx, hipError_t e, const char *what);
-// Waits for the stream, then reads and clears the device error word (set by a
-// bounded device-side wait that expired).
-int check_device_error(qq_ctx *ctx);
+// Wait for the context stream and report a device-side wait that timed out
+// (the decode kernel's error word), in one synchronisation: the word is
+// copied to the pinned header by a small kernel behind the enqueued work, or
+// already was by the caller's last staging copy (`staged`).
+int check_device_error(qq_ctx *ctx, bool staged = false);
 // QQ_E_ARG while a graph capture is open on the context's stream.
 int no_capture(qq_ctx *ctx, const char *what);
 int ensure_scratch(qq_ctx *ctx, size_t bytes);
+// The pinned staging buffer: a PIN_HDR-byte header (word 0: the device error
+// word as of the last staging copy), then `bytes` of staging from PIN_HDR on.
+constexpr size_t PIN_HDR = 256;
 int ensure_pinned(qq_ctx *ctx, size_t bytes);
+// Copy `bytes` (a multiple of 16) between the pinned staging buffer and
+// device memory with one small kernel on the context stream (device
+// addresses: ctx->pinned_dev + offset on the host side).
+int launch_stage_copy(qq_ctx *ctx, const void *src, void *dst, size_t bytes);
 
 #define QQ_HIP(ctx, call)                                          \
     do {                                                           \
