@@ -28,6 +28,12 @@ qq_capture_begin/end).  The per-kernel roofline figure comes from a third
 pass over the same steps in which every launch carries its own start/stop
 events (hipExtLaunchKernelGGL, qq_profile_*).
 
+Beside `value`, the batch-1 decode lines carry `host_call`: the same layer
+through the host-pointer call the JS drop-in makes (x and hidden in over
+PCIe, results out, a synchronise per call), timed on the host.  The default
+line also carries `prefill_2048`: a shortened 2048-token prefill chunk with
+the MFMA roofline of its grouped GEMMs (skip with --no-prefill-leg).
+
 Prints one JSON line.
 """
 import argparse
@@ -433,6 +439,49 @@ def host_call_leg(ctx, layers, X, HID, steps, warmup):
     return out
 
 
+def prefill_leg(torch, ctx, stream, steps, warmup, n_layers=4):
+    """One MoE layer over a 2048-token prefill chunk with Zipf-skewed routing
+    (the prefill_2048 workload, shortened): the expert products on the fp16
+    MFMA grouped GEMMs, so the prefill GEMM's MFMA roofline is reported beside
+    the decode line.  n_layers fresh layer instances (1.5 GB > the 256 MB
+    Infinity Cache) rotated; per-launch events on the library stream."""
+    T = 2048
+    layers = [make_layer(torch, ctx, 3000 + i, "zipf") for i in range(n_layers)]
+    gx = torch.Generator(device="cuda")
+    gx.manual_seed(3)
+    X = torch.randn((2, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    HID = torch.randn((2, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    idx = torch.empty((2, T, K), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+    def step(i):
+        layers[i % n_layers].forward_dev(X[i % 2].data_ptr(), HID[i % 2].data_ptr(), T,
+                                         idx_ptr=idx[i % 2].data_ptr())
+
+    total_ms = _time_steps(torch, ctx, stream, step, steps, warmup)
+    ctx.profile_enable(steps * 10)
+    for i in range(steps):
+        step(i)
+    prof = ctx.profile_read()
+    ctx.profile_enable(0)
+    ctx.synchronize()
+    n_exp = float(len(np.unique(idx.cpu().numpy())))
+    kernels = kernel_table(prof, T, n_exp, T * K)
+    for lay in layers:
+        for t in getattr(lay, "_keep", ()):
+            t.release()
+        lay.release()
+    ms = total_ms / steps
+    out = {"workload": "moe_layer_prefill_2048_zipf", "T": T, "layer_instances": n_layers, "steps": steps,
+           "ms_per_step": round(ms, 4), "tokens_per_s": round(T / (ms / 1000.0), 1)}
+    for name in MFMA_KERNELS:
+        if name in kernels:
+            k = kernels[name]
+            out[name] = {"avg_us": k["avg_us"], "tflops": k["tflops"], "peak_tflops": MFMA_PEAK_TFLOPS,
+                         "frac": round(k["tflops"] / MFMA_PEAK_TFLOPS, 4)}
+    return out
+
+
 def timed(torch, ctx, stream, step, period, steps, warmup, launches_per_step):
     """step(i) enqueues step i and depends only on i % period.
 
@@ -501,6 +550,8 @@ def main():
     ap.add_argument("--layers", type=int, default=16, help="distinct layer instances rotated over")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill-leg", action="store_true",
+                    help="decode_b1: skip the 2048-token prefill GEMM leg reported beside the line")
     ap.add_argument("--position0", type=int, default=0,
                     help="lfm2_decode: first position of the timed sequence (step i runs at "
                          "position0 + i %% 512)")
@@ -611,6 +662,10 @@ def main():
         if not stack and T == 1:
             # beside `value`: the same layer through the host-pointer call (PCIe included)
             extra["host_call"] = host_call_leg(ctx, keep, X, HID, min(args.steps, 400), min(args.warmup, 40))
+        if args.workload == "decode_b1" and not args.no_prefill_leg:
+            # beside `value`: the prefill GEMM's MFMA roofline on a 2048-token chunk
+            extra["prefill_2048"] = prefill_leg(torch, ctx, stream, max(min(args.steps, 20), 5),
+                                                max(min(args.warmup, 3), 1))
 
     result = {
         "metric": LFM2_METRIC if kind == "lfm2" else METRIC,

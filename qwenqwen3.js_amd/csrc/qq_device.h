@@ -85,27 +85,43 @@ __device__ __forceinline__ uint32_t lds_u32(const void *p)
 }
 
 // global_load_lds: each lane copies `size` bytes from its own address to
-// LDS (M0 + lane * size); the compiler sets M0 (and its wait state) itself.
+// LDS (M0 + lane * size).  Issued from inline assembly: the compiler then
+// adds no waits of its own for these copies (with the builtin it cannot
+// tell the ring stages of one LDS array apart and drains every copy in flight
+// before each LDS read), so callers wait for them explicitly (s_waitcnt
+// vmcnt) before reading what they fill.  M0 is read when the copy issues; it
+// is saved and restored around the copy (one wait state after an SALU write
+// to M0), so any value the compiler keeps in M0 survives.
 __device__ __forceinline__ void dma16(const void *g, uint32_t lds)
 {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
-                                     (__attribute__((address_space(3))) void *)(uintptr_t)lds, 16, 0, 0);
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save) : "v"(g), "s"(lds) : "memory");
 }
 
 __device__ __forceinline__ void dma4(const void *g, uint32_t lds)
 {
-    __builtin_amdgcn_global_load_lds((const __attribute__((address_space(1))) void *)g,
-                                     (__attribute__((address_space(3))) void *)(uintptr_t)lds, 4, 0, 0);
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save) : "v"(g), "s"(lds) : "memory");
 }
-// The same with a wave-uniform base address and a 32-bit per-lane byte
-// offset (the compiler takes the base from an SGPR pair: one VGPR per lane).
+// The same with a wave-uniform base address (SGPR pair) and a 32-bit
+// per-lane byte offset: one VGPR per lane instead of two.
 __device__ __forceinline__ void dma16s(uint32_t off, const void *base, uint32_t lds)
 {
-    dma16(static_cast<const char *>(base) + off, lds);
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save) : "v"(off), "s"(base), "s"(lds) : "memory");
 }
 __device__ __forceinline__ void dma4s(uint32_t off, const void *base, uint32_t lds)
 {
-    dma4(static_cast<const char *>(base) + off, lds);
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save) : "v"(off), "s"(base), "s"(lds) : "memory");
 }
 
 // Value of lane ^ 1 (resp. lane ^ 2) by a DPP quad permutation: a VALU
