@@ -543,19 +543,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Every wave's gate/up requests go out before any down request: a CU's
-    // requests are served about in issue order, so the workgroup receives
-    // its gate/up bytes first (its h is ready early) and the down bytes
-    // arrive while the h values are exchanged.  (Loads also complete in
-    // issue order within a wave, so the gate/up products never wait for the
-    // down rows.)
     lds_barrier();
-    {
-#pragma unroll
-        for (int i = 0; i < DEC_DCH; i++)
-            dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
-        __builtin_amdgcn_sched_barrier(0);
-    }
     // ---- the weights, by wave 0 while the weight bytes stream in ----
     if (ok && wave == 0) {
         float pk[MAX_K];
@@ -623,6 +611,15 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             ga = fmaf(fg, bok ? sx * gs.get(i) : 0.0f, ga);
             ua = fmaf(fu, bok ? sx * us.get(i) : 0.0f, ua);
         }
+        // The down rows are requested only once this wave's gate/up bytes
+        // have arrived: every workgroup's gate/up requests then reach HBM
+        // ahead of any down request, so the h values are ready early, and
+        // the down bytes stream in while the h values are exchanged.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < DEC_DCH; i++)
+            dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
+        __builtin_amdgcn_sched_barrier(0);
         if (hh == 0) {
             redg[wave][cs] = ga;
             redu[wave][cs] = ua;
