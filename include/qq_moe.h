@@ -190,6 +190,18 @@ int qq_buffer_read(qq_ctx *ctx, const void *dev, void *host, size_t nbytes);
 int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev,
                               int T, const uint8_t *mask, float *record_dev);
 
+/* No reference counterpart.  The workgroups of the batch-1 decode kernel
+ * wait on each other through memory (the routing, the h values, the partial
+ * sums); every such wait gives up after `microseconds` (default
+ * QQ_WAIT_LIMIT_US_DEFAULT, 50 ms), the kernel then finishes with what it
+ * has, and the call's error surfaces at the next synchronising call as
+ * QQ_E_HIP ("a device-side wait of the decode kernel timed out") rather
+ * than the kernel waiting on.  0: a wait gives up at its first poll that
+ * misses a word (for tests of that path).  Calls after a failed one draw a
+ * fresh tag and are unaffected by it. */
+#define QQ_WAIT_LIMIT_US_DEFAULT 50000
+int qq_set_wait_limit(qq_ctx *ctx, int microseconds);
+
 /* Token batches (T > 1) of at least `tokens` rows per chunk run their expert
  * products as fp16 MFMA grouped GEMMs (fp16 activations and dequantised
  * weights, fp32 accumulation: ~1e-3 relative L2 on the layer output);

@@ -131,7 +131,7 @@ int check_device_error(qq_ctx *ctx, bool staged)
         *word = 0;
         QQ_HIP(ctx, hipMemsetAsync(ctx->sync_err, 0, 4, ctx->stream));
         QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        snprintf(ctx->err, sizeof ctx->err, "device-side wait for the router timed out (code %u)", e);
+        snprintf(ctx->err, sizeof ctx->err, "a device-side wait of the decode kernel timed out (code %u)", e);
         return QQ_E_HIP;
     }
     return QQ_OK;
@@ -254,6 +254,7 @@ int qq_init(int device, qq_ctx **out)
     ctx->own_stream = 1;
     ctx->prof_kind = -1;
     ctx->mfma_min_tokens = QQ_MFMA_MIN_TOKENS_DEFAULT;
+    ctx->dec_wait_ticks = (uint64_t)QQ_WAIT_LIMIT_US_DEFAULT * 100;
     if ((e = hipEventCreate(&ctx->ev0)) != hipSuccess || (e = hipEventCreate(&ctx->ev1)) != hipSuccess) {
         (void)hipStreamDestroy(ctx->stream);
         delete ctx;
@@ -784,6 +785,14 @@ int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, 
     float *probs = reinterpret_cast<float *>(s + ib + wb);
     if ((rc = forward_impl(ctx, m, x_dev, hidden_dev, T, mb, idx, w, probs, ib + wb + pb))) return rc;
     return launch_route_record(ctx, idx, w, probs, T, m->K, m->E, record_dev);
+}
+
+int qq_set_wait_limit(qq_ctx *ctx, int microseconds)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (microseconds < 0) return set_error(ctx, "set_wait_limit: %d us < 0", microseconds);
+    ctx->dec_wait_ticks = (uint64_t)microseconds * 100;   // the 100 MHz wall clock
+    return QQ_OK;
 }
 
 int qq_set_mfma_min_tokens(qq_ctx *ctx, int tokens)

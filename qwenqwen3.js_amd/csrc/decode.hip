@@ -58,7 +58,6 @@ constexpr int DEC_WAVES = 8;
 constexpr int DEC_THREADS = DEC_WAVES * WAVE;
 constexpr int DEC_GROUPS = 8;                  // one per XCD
 static_assert(DEC_GROUPS == 8, "group blocks are found with shifts by 3");
-constexpr uint64_t DEC_WAIT_TICKS = 5000000;   // 50 ms at the 100 MHz wall clock
 constexpr uint64_t DEC_LOCAL_TICKS = 1000;     // 10 us on the group's own table, then the copy
 constexpr int DEC_CCH = 32;                    // gate/up columns per chunk (two lanes each)
 constexpr int DEC_DCH = 8;                     // down loads per lane
@@ -99,6 +98,7 @@ struct DecodeArgs {
     float *out_probs;
     float *out_rec;       // [K idx as float | K w rounded to fp32 | E probs]
     uint32_t *err;
+    uint64_t wait_ticks;  // bound on every device-side wait (100 MHz wall clock)
 };
 
 __device__ __forceinline__ uint64_t tag_word(uint32_t tag, float v)
@@ -131,7 +131,7 @@ __device__ __forceinline__ void store_dev(uint64_t *p, uint64_t v)
 template <int NT, int IPT>
 __device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uint64_t *(&pl)[IPT],
                                            const uint64_t *(&pd)[IPT], bool (&want)[IPT],
-                                           float *(&dst)[IPT])
+                                           float *(&dst)[IPT], uint64_t wait_ticks)
 {
     bool fail = false;
     if ((int)threadIdx.x < NT) {
@@ -157,7 +157,7 @@ __device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uin
             if (__all(mine)) break;
             const uint64_t dt = wall_clock64() - t0;
             if (dt > DEC_LOCAL_TICKS) loc = false;
-            if (dt > DEC_WAIT_TICKS) {
+            if (dt >= wait_ticks) {
                 fail = true;
                 break;
             }
@@ -402,7 +402,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const uint64_t *pd[1] = {&a.rdev[(size_t)(j % SYNC_REPLICAS) * SYNC_REPLICA_WORDS + min(tid, a.E - 1)]};
         bool want[1] = {tid < a.E};
         float *dst[1] = {&sh_lg[min(tid, EPL * WAVE - 1)]};
-        ok = block_wait<4 * WAVE, 1>(tag, &sh_fail, pl, pd, want, dst);
+        ok = block_wait<4 * WAVE, 1>(tag, &sh_fail, pl, pd, want, dst, a.wait_ticks);
     }
 
     // ---- this workgroup's share (independent of the routing) ----
@@ -663,7 +663,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             want[s2] = tid + PUB * s2 < NC && !((mrank >> k) & 1u);
             dst[s2] = &hl[k * FRb * QK + (i - k * FR)];
         }
-        ok = block_wait<PUB, IPT>(tag, &sh_fail, pl, pd, want, dst);
+        ok = block_wait<PUB, IPT>(tag, &sh_fail, pl, pd, want, dst, a.wait_ticks);
     }
     if (ok && NP2 > 0) {
         decompose32<DEC_MAX_HW + 8 * QK>(hl, a.K * FRb, &hlev[0][0], hsig);
@@ -739,7 +739,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             want[s2] = isp ? (q < RFm && xb1 > xb0 && !((mrank >> k) & 1u)) : (i < NP + G);
             dst[s2] = isp ? &pf[min(i, DEC_MAX_FIN - 1)] : nullptr;
         }
-        ok = block_wait<NT, IPT>(tag, &sh_fail, pl, pl, want, dst);
+        ok = block_wait<NT, IPT>(tag, &sh_fail, pl, pl, want, dst, a.wait_ticks);
     }
     if (ok && tid < RFm) {
         float acc = 0.0f;
@@ -857,6 +857,7 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.out_probs = out_probs;
     a.out_rec = out_rec;
     a.err = ctx->sync_err;
+    a.wait_ticks = ctx->dec_wait_ticks;
 
     const int G = decode_grid(ctx);
     const int re = (m->E + G / DEC_GROUPS - 1) / (G / DEC_GROUPS);

@@ -118,6 +118,8 @@ struct qq_ctx {
     uint64_t *sync_slots;
     uint64_t *sync_local;
     uint32_t *sync_err;
+    // bound on the decode kernel's device-side waits, in 100 MHz wall-clock ticks
+    uint64_t dec_wait_ticks;
     uint32_t *sync_epoch;
     uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive;
     // a graph capture on `stream` is open (qq_capture_begin)

@@ -22,6 +22,7 @@ TYPE_F32 = 0
 TYPE_Q8_0 = 8
 GATING_SIGMOID_BIAS = 0   # LFM2-MoE
 GATING_SOFTMAX = 1        # Qwen3-MoE
+QQ_WAIT_LIMIT_US_DEFAULT = 50000
 
 # Every symbol include/qq_moe.h declares (tests/test_abi.py keeps them in sync).
 EXPORTS = (
@@ -30,7 +31,7 @@ EXPORTS = (
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
     "qq_moe_forward_norm_dev", "qq_moe_forward_noalloc_dev", "qq_moe_set_gating",
-    "qq_set_mfma_min_tokens", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
+    "qq_set_mfma_min_tokens", "qq_set_wait_limit", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
     "qq_buffer_alloc", "qq_buffer_free", "qq_buffer_write", "qq_buffer_read", "qq_moe_forward_record_dev",
@@ -109,6 +110,7 @@ def load():
         "qq_moe_forward_norm_dev": (I, [P, P, P, P, ctypes.c_double, I, P, P, P, P]),
         "qq_moe_set_gating": (I, [P, P, I]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
+        "qq_set_wait_limit": (I, [P, I]),
         "qq_rmsnorm_dev": (I, [P, P, P, P, I, I, ctypes.c_double]),
         "qq_timer_start": (I, [P]),
         "qq_timer_stop": (I, [P, ctypes.POINTER(ctypes.c_float)]),
@@ -247,6 +249,10 @@ class Context:
         assert out.flags["C_CONTIGUOUS"]
         self.check(self.L.qq_buffer_read(self.h, ctypes.c_void_p(ptr), _ptr(out), out.nbytes), "qq_buffer_read")
         return out
+
+    def set_wait_limit(self, microseconds):
+        """Bound on the decode kernel's device-side waits (qq_set_wait_limit)."""
+        self.check(self.L.qq_set_wait_limit(self.h, int(microseconds)), "qq_set_wait_limit")
 
     def set_mfma_min_tokens(self, tokens):
         """Token batches of >= tokens rows use the fp16 MFMA path (0: never)."""

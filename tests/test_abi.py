@@ -47,6 +47,7 @@ def test_header_constants_match_binding():
     assert int(consts["QQ_OK"]) == qq_hip.QQ_OK
     assert int(consts["QQ_TYPE_F32"]) == qq_hip.TYPE_F32
     assert int(consts["QQ_TYPE_Q8_0"]) == qq_hip.TYPE_Q8_0
+    assert int(consts["QQ_WAIT_LIMIT_US_DEFAULT"]) == qq_hip.QQ_WAIT_LIMIT_US_DEFAULT
 
 
 @pytest.mark.skipif(HAS_GPU, reason="checks the no-device error path")

@@ -1,0 +1,68 @@
+"""Failure path of the batch-1 decode kernel's device-side waits, forced from
+the host (qq_set_wait_limit): with a zero bound every wait gives up at its
+first poll that misses a word, the kernel still runs to its end, and the call
+either reports the timeout or -- when every wait happened to find its words
+on the first poll -- returns the correct result; never a wrong result without
+an error.  The calls after it, with the default bound, are correct: a failed
+call leaves nothing behind that a later call reads (each call's words carry
+its own tag)."""
+import numpy as np
+import pytest
+
+import oracle
+import qq_hip
+from _util import full_layer, gpu_context, moe_delta, rel_l2, upload_layer
+
+pytestmark = pytest.mark.gpu
+
+
+def test_zero_wait_bound_fails_loudly_and_recovers():
+    import torch
+    import synth
+    print("decode wait bound 0, then default", flush=True)
+    ctx = gpu_context()
+    L = full_layer(11)
+    m = upload_layer(ctx, L)
+    try:
+        x, h0 = synth.activations(31, 4, L["H"])
+        ref_h, ref_idx, _, _ = oracle.moe_ffn(L, x, h0)
+        dx = torch.from_numpy(x).cuda()
+        dh = torch.from_numpy(h0).cuda()
+        idx = torch.full((4, L["K"]), -1, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        failed = 0
+        ctx.set_wait_limit(0)
+        try:
+            for t in range(3):
+                m.forward_dev(dx[t].data_ptr(), dh[t].data_ptr(), 1, idx_ptr=idx[t].data_ptr())
+                try:
+                    ctx.synchronize()
+                except qq_hip.QQError as e:
+                    assert "timed out" in str(e), e
+                    failed += 1
+                    continue
+                # no error reported: the result must be the right one
+                got = dh[t].cpu().numpy()
+                assert np.array_equal(idx[t].cpu().numpy(), ref_idx[t])
+                assert rel_l2(moe_delta(got, h0[t]), moe_delta(ref_h[t], h0[t])) < 1e-4
+        finally:
+            ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
+        print("calls that timed out:", failed, "of 3", flush=True)
+        # recovery: fresh rows through the default bound, exact routing and 1e-4
+        for t in range(3, 4):
+            m.forward_dev(dx[t].data_ptr(), dh[t].data_ptr(), 1, idx_ptr=idx[t].data_ptr())
+        ctx.synchronize()
+        assert np.array_equal(idx[3].cpu().numpy(), ref_idx[3])
+        assert rel_l2(moe_delta(dh[3].cpu().numpy(), h0[3]), moe_delta(ref_h[3], h0[3])) < 1e-4
+        # and the host-pointer call
+        out, oidx, _, _ = m.forward(x[:1], h0[:1])
+        assert np.array_equal(oidx, ref_idx[:1])
+        assert rel_l2(moe_delta(out, h0[:1]), moe_delta(ref_h[:1], h0[:1])) < 1e-4
+    finally:
+        m.release()
+
+
+def test_wait_limit_rejects_negative():
+    ctx = gpu_context()
+    with pytest.raises(qq_hip.QQError):
+        ctx.set_wait_limit(-1)
