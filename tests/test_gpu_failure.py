@@ -48,6 +48,10 @@ def test_zero_wait_bound_fails_loudly_and_recovers():
         finally:
             ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
         print("calls that timed out:", failed, "of 3", flush=True)
+        # the workgroups start up to ~0.5 us apart and poll the routing table
+        # right after publishing their own logits, so the first poll of some
+        # workgroup misses a later member's word in every call
+        assert failed >= 1
         # recovery: fresh rows through the default bound, exact routing and 1e-4
         for t in range(3, 4):
             m.forward_dev(dx[t].data_ptr(), dh[t].data_ptr(), 1, idx_ptr=idx[t].data_ptr())
