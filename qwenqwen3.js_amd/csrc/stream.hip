@@ -5,8 +5,9 @@
 // by very few rows, so the layer is bound by streaming the experts' Q8_0
 // weights from HBM once.  A workgroup owns one expert, one tile of 16*MF
 // slots and a group of 128 weight columns; its 4 waves split the reduction
-// dimension block by block (each streaming its blocks through a private LDS
-// ring, below) and their partial sums are added in wave order through LDS.
+// dimension block by block (each streaming its blocks straight into
+// registers, a few blocks ahead, below) and their partial sums are added in
+// wave order through LDS.
 //
 // Accuracy (the fp32 path's 1e-4 relative L2): activations are split into
 // two fp16 halves, a = a_hi + a_lo (22 significant bits); the int8 weights
@@ -78,89 +79,76 @@ __device__ __forceinline__ h8_t int8_to_f16x8(const uint2 q)
 }
 
 // ---------------------------------------------------------------------------
-// Operand stream.  Each wave keeps a ring of ST_D stages in LDS; a stage holds
-// one 32-value block of the reduction for the workgroup: the 16*MF activation
-// rows (128 B each) and the 128 weight columns (two halves of 64 columns,
-// 32 int8 each) with their 128 fp16 scales.  Stages are filled by
-// global_load_lds copies straight from memory (no registers held while in
-// flight), issued from inline assembly so that the compiler's wait-counter
-// pass leaves them alone; a stage is only ever read by the wave that filled
-// it, so the wave's own vector-memory counter is the only synchronisation:
-//   S0 S1 | S2 [wait S0] use 0 | S3 [wait S1] use 1 | ...
-// When block i is used exactly two stages (2 * ST_NDMA copies) were issued
-// after S_i, so "vmcnt <= 2 * ST_NDMA" means S_i has landed.  No other vector
-// memory instruction is issued inside the loop.
-// Activation rows are stored with their 16-byte chunks permuted, chunk c of
-// row r at position c ^ ((r >> 1) & 7), so that the 16 rows of a fragment
-// read fall in 16 different bank groups.
+// Operand stream.  Wave w reduces blocks w, w+4, w+8, ... of the reduction
+// dimension.  Every operand of a block goes straight to registers: the
+// lane's 8 activations of each of its MF rows (two float4), its 8 weight
+// bytes of each of the ST_NF fragment columns (uint2) and those columns'
+// fp16 scales.  Each wave keeps ST_PF blocks in flight: block i + ST_PF is
+// requested as soon as block i's products are done.  (Staged through LDS the
+// stream is held to ~100 KB in flight per CU by the LDS size.)
+// Fragment j: column 16*(j%4) + lane%16 of half j/4; lane l holds row l%16
+// of A and column l%16 of B at k = 8*(l/16) .. 8*(l/16) + 7 of the block.
 // ---------------------------------------------------------------------------
-constexpr int ST_D = 3;                          // stages per wave
-constexpr int ST_HALF = 64 * QK;                 // 64 columns x 32 int8
+template <int MF>
+struct StBlock {
+    float4 a[MF][2];     // rows 16m + lane%16, k = 8*(lane/16) .. +7
+    uint2 q[ST_NF];      // fragment j's 8 weight bytes
+    h2_t d[ST_NF / 2];   // fragment j's column scale: d[j / 2][j % 2]
+};
 
 template <int MF>
-struct StLayout {
-    static constexpr int A = 0;                          // 16*MF rows x 128 B
-    static constexpr int B = 16 * MF * 128;              // two halves of ST_HALF
-    static constexpr int S = B + 2 * ST_HALF;            // 2 x 64 fp16 scales
-    static constexpr int STAGE = S + 256;
-    static constexpr int NDMA = 2 * MF + 4 + 1;          // copies per stage
-};
+constexpr int st_pf() { return MF == 1 ? 3 : 2; }   // blocks in flight per wave
 
 template <int MF>
 struct StSrc {
     const char *abase;          // activation rows (bytes)
-    uint32_t aoff[MF * 2];      // copy instruction i: lane's 16 bytes of row 8i + lane/8
+    uint32_t arow[MF];          // lane's row 16m + lane%16: byte offset + its k chunk
     const int8_t *qb[2];        // weights of column halves 0 / 1 at the expert's block 0
     const uint16_t *db[2];      // their scales
-    uint32_t qoff[4];           // weight copy instruction i: lane's 16 bytes (half i/2)
-    uint32_t doff;              // scale copy: lane's 2 scales (half lane/32), in halves
-    uint32_t qstep, dstep;      // one block: rows * 32 bytes, rows halves
-    bool ok[ST_NF];             // fragment j's column in range (else its scale is zero)
+    int cb[2];                  // column half h: the lane's column c0[h] + lane%16 (fragment j adds 16*(j%4))
+    int cmax;                   // last column (loads clamp to it)
+    uint32_t qk;                // the lane's byte offset within a column's 32 bytes
+    uint32_t qstep, dstep;      // one block: rows * 32 bytes, rows scales
+    uint32_t okm;               // bit j: fragment j's column in range (else its scale is zero)
 };
 
-// Copy block kb into the stage at LDS address `st` (ST_NDMA instructions).
+// 32-bit offsets from workgroup-uniform bases (one VGPR per address).
 template <int MF>
-__device__ __forceinline__ void st_stage(const StSrc<MF> &s, uint32_t st, int kb)
+__device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int kb)
 {
-    using L = StLayout<MF>;
-    const int lane = threadIdx.x & (WAVE - 1);
-    const char *ab = s.abase + (size_t)kb * QK * 4;
+    const uint32_t ak = (uint32_t)kb * (QK * 4), qk = (uint32_t)kb * s.qstep, dk = (uint32_t)kb * s.dstep;
 #pragma unroll
-    for (int i = 0; i < 2 * MF; i++) dma16(ab + s.aoff[i], st + L::A + i * 1024);
+    for (int m = 0; m < MF; m++) {
+        b.a[m][0] = *reinterpret_cast<const float4 *>(s.abase + (size_t)(s.arow[m] + ak));
+        b.a[m][1] = *reinterpret_cast<const float4 *>(s.abase + (size_t)(s.arow[m] + ak + 16));
+    }
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        dma16(s.qb[i >> 1] + (size_t)kb * s.qstep + s.qoff[i], st + L::B + i * 1024);
-    dma4(s.db[lane >> 5] + (size_t)kb * s.dstep + s.doff, st + L::S);
+    for (int j = 0; j < ST_NF; j++) {
+        const uint32_t c = (uint32_t)min(s.cb[j >> 2] + 16 * (j & 3), s.cmax);
+        b.q[j] = *reinterpret_cast<const uint2 *>(s.qb[j >> 2] + (size_t)(qk + c * QK + s.qk));
+    }
+#pragma unroll
+    for (int j = 0; j < ST_NF; j++) {
+        const uint32_t c = (uint32_t)min(s.cb[j >> 2] + 16 * (j & 3), s.cmax);
+        b.d[j >> 1][j & 1] = *reinterpret_cast<const _Float16 *>(reinterpret_cast<const char *>(s.db[j >> 2]) +
+                                                                 (size_t)(2u * (dk + c)));
+    }
 }
 
-// Fragment j: column 16*(j%4) + lane%16 of half j/4, k = 8*(lane/16) .. +7.
 // The block's int8 weights enter the MFMA exactly (as fp16 integers); the
 // block's scale is applied to the block's fp32 partial sum:
 //   acc += d * (a_hi * q + a_lo * q).
 // A lane's four outputs of a fragment share one column, hence one scale.
 template <int MF>
-__device__ __forceinline__ void st_compute(const char *st, const StSrc<MF> &s,
-                                           f4_t (&acc)[MF][ST_NF])
+__device__ __forceinline__ void st_block(const StBlock<MF> &b, const StSrc<MF> &s, f4_t (&acc)[MF][ST_NF])
 {
-    using L = StLayout<MF>;
-    const int lane = threadIdx.x & (WAVE - 1);
     h8_t ah[MF], al[MF];
 #pragma unroll
-    for (int m = 0; m < MF; m++) {
-        const int r = 16 * m + (lane & 15);
-        const int sw = (r >> 1) & 7, c = 2 * (lane >> 4);
-        const float4 a0 = *reinterpret_cast<const float4 *>(st + L::A + r * 128 + 16 * (c ^ sw));
-        const float4 a1 = *reinterpret_cast<const float4 *>(st + L::A + r * 128 + 16 * ((c + 1) ^ sw));
-        split8(a0, a1, ah[m], al[m]);
-    }
+    for (int m = 0; m < MF; m++) split8(b.a[m][0], b.a[m][1], ah[m], al[m]);
 #pragma unroll
     for (int j = 0; j < ST_NF; j++) {
-        const int c = 16 * (j & 3) + (lane & 15);
-        const uint2 q = *reinterpret_cast<const uint2 *>(st + L::B + (j >> 2) * ST_HALF + c * QK +
-                                                         8 * (lane >> 4));
-        const uint16_t sb = *reinterpret_cast<const uint16_t *>(st + L::S + (j >> 2) * 128 + 2 * c);
-        const float d = s.ok[j] ? (float)__builtin_bit_cast(_Float16, sb) : 0.0f;
-        const h8_t qh = int8_to_f16x8(q);
+        const float d = ((s.okm >> j) & 1u) ? (float)b.d[j >> 1][j & 1] : 0.0f;
+        const h8_t qh = int8_to_f16x8(b.q[j]);
 #pragma unroll
         for (int m = 0; m < MF; m++) {
             f4_t p = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[m], qh, f4_t{0.0f, 0.0f, 0.0f, 0.0f}, 0, 0, 0);
@@ -171,31 +159,32 @@ __device__ __forceinline__ void st_compute(const char *st, const StSrc<MF> &s,
     }
 }
 
-// Wave w reduces blocks w, w+4, w+8, ... of nb in its ring `ring` (ST_D
-// stages).  Copies past the wave's last block reload that block (clamped,
-// never read) so that every step issues the same instructions.  On return
-// every copy of this wave has landed.
+// Wave w reduces blocks w, w+4, w+8, ... of nb with st_pf blocks in flight.
 template <int MF>
-__device__ __forceinline__ void st_mainloop(const StSrc<MF> &s, char *ring, int nb, int wave,
-                                            f4_t (&acc)[MF][ST_NF])
+__device__ __forceinline__ void st_mainloop(const StSrc<MF> &s, int nb, int wave, f4_t (&acc)[MF][ST_NF])
 {
-    using L = StLayout<MF>;
+    constexpr int PF = st_pf<MF>();
     const int nblk = (nb - wave + 3) / 4;
-    if (nblk > 0) {
-        const int lastb = wave + 4 * (nblk - 1);
-        const uint32_t r0 = __builtin_amdgcn_readfirstlane(lds_u32(ring));
-        st_stage<MF>(s, r0, min(wave, lastb));
-        st_stage<MF>(s, r0 + L::STAGE, min(wave + 4, lastb));
-        for (int i = 0; i < nblk; i++) {
-            st_stage<MF>(s, r0 + ((i + 2) % ST_D) * L::STAGE, min(wave + 4 * (i + 2), lastb));
-            wait_vm<2 * L::NDMA>();
-            st_compute<MF>(ring + (i % ST_D) * L::STAGE, s, acc);
+    StBlock<MF> r[PF];
+#pragma unroll
+    for (int u = 0; u < PF; u++)
+        if (u < nblk) st_load<MF>(r[u], s, wave + 4 * u);
+    for (int i = 0; i < nblk; i += PF) {
+#pragma unroll
+        for (int u = 0; u < PF; u++) {
+            if (i + u < nblk) {
+                st_block<MF>(r[u], s, acc);
+                // the refill goes out only after the products, so the
+                // compiler waits for this block alone, not the ones behind it
+                __builtin_amdgcn_sched_barrier(0);
+                if (i + u + PF < nblk) st_load<MF>(r[u], s, wave + 4 * (i + u + PF));
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
-    wait_vm<0>();
 }
 
-// Copy offsets: activation row r of the tile has byte offset rowoff(r);
+// Load offsets: activation row r of the tile has byte offset rowoff(r);
 // weight halves start at columns c0[0], c0[1] of a matrix with `rows`
 // columns per block (clamped into range).
 template <int MF, typename RowOff>
@@ -203,19 +192,14 @@ __device__ __forceinline__ void st_offsets(StSrc<MF> &s, RowOff rowoff, const in
                                            int rows, int lane)
 {
 #pragma unroll
-    for (int i = 0; i < 2 * MF; i++) {
-        const int r = 8 * i + (lane >> 3);
-        const int chunk = (lane & 7) ^ ((r >> 1) & 7);   // lands at position lane & 7
-        s.aoff[i] = rowoff(r) + 16 * chunk;
-    }
+    for (int m = 0; m < MF; m++) s.arow[m] = rowoff(16 * m + (lane & 15)) + 32 * (lane >> 4);
+    s.qk = 8 * (lane >> 4);
+    s.cb[0] = c0[0] + (lane & 15);
+    s.cb[1] = c0[1] + (lane & 15);
+    s.cmax = rows - 1;
+    s.okm = 0;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int c = min(c0[i >> 1] + 32 * (i & 1) + (lane >> 1), rows - 1);
-        s.qoff[i] = (uint32_t)c * QK + 16 * (lane & 1);
-    }
-    s.doff = (uint32_t)min(c0[lane >> 5] + 2 * (lane & 31), rows - 2);
-#pragma unroll
-    for (int j = 0; j < ST_NF; j++) s.ok[j] = c0[j >> 2] + 16 * (j & 3) + (lane & 15) < rows;
+    for (int j = 0; j < ST_NF; j++) s.okm |= (c0[j >> 2] + 16 * (j & 3) + (lane & 15) < rows ? 1u : 0u) << j;
 }
 
 // Cross-wave sums of fragment row block m: each wave writes its fragments of
@@ -237,12 +221,8 @@ __device__ __forceinline__ float wave_order_sum(const float (*red)[16][65], int 
     return ((red[0][row][c] + red[1][row][c]) + red[2][row][c]) + red[3][row][c];
 }
 
-template <int MF>
-constexpr int st_lds_bytes()
-{
-    return 4 * ST_D * StLayout<MF>::STAGE;
-}
-static_assert(2 * 4 * 16 * 65 * 4 <= st_lds_bytes<1>(), "reduction tiles must fit the rings");
+// LDS: the cross-wave reduction tiles only
+constexpr int ST_LDS = 2 * 4 * 16 * 65 * 4;
 
 // ---------------------------------------------------------------------------
 // gate/up: column half 0 = gate features f0 .. f0+63, half 1 = the same up
@@ -251,7 +231,7 @@ static_assert(2 * 4 * 16 * 65 * 4 <= st_lds_bytes<1>(), "reduction tiles must fi
 template <int MF>
 __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(StreamArgs a)
 {
-    __shared__ __align__(16) char lds[st_lds_bytes<MF>()];
+    __shared__ __align__(16) char lds[ST_LDS];
     const int ncg = (a.F + 63) / 64;
     const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
     if (tile >= *a.n_tiles) return;
@@ -281,7 +261,7 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 #pragma unroll
         for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(src, lds + wave * ST_D * StLayout<MF>::STAGE, a.nbH, wave, acc);
+    st_mainloop<MF>(src, a.nbH, wave, acc);
     float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
     float (*red1)[16][65] = red0 + 4;
 #pragma unroll
@@ -308,7 +288,7 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 template <int MF>
 __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamArgs a)
 {
-    __shared__ __align__(16) char lds[st_lds_bytes<MF>()];
+    __shared__ __align__(16) char lds[ST_LDS];
     const int ncg = (a.H + 127) / 128;
     const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
     if (tile >= *a.n_tiles) return;
@@ -335,7 +315,7 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
 #pragma unroll
         for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(src, lds + wave * ST_D * StLayout<MF>::STAGE, a.nbF, wave, acc);
+    st_mainloop<MF>(src, a.nbF, wave, acc);
     float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
     float (*red1)[16][65] = red0 + 4;
 #pragma unroll
