@@ -39,8 +39,8 @@ constexpr int LM_ATTN_THREADS = 256;
 
 struct LmMat {
     const int8_t *qs;
-    const __half *d;
-    int rows;
+    const __half *dcm;   // scales row by row: dcm[r * nbp + b]
+    int rows, nbp;
 };
 
 struct LmArgs {
@@ -135,23 +135,27 @@ __device__ __forceinline__ float lm_dot(const uint32_t (&w)[BPL / 4], const floa
     return fmaf(-128.0f, xsum, acc);
 }
 
-// G row groups of RPW rows, WPG waves each.  In a wave, 64 / RPW lanes share
-// a row and each takes BPL = 32 * RPW / 64 bytes of a block; a wave keeps up to
-// NBW blocks of its rows in flight (blocks wg, wg + WPG, ... of a chunk of
-// WPG * NBW).  Fewer rows per wave spread a matrix over more workgroups
-// (CUs): one CU pulls only a few tens of GB/s.
+// G row groups of RPW rows, WPG waves each.  A wave's lanes take a row,
+// a 16-byte half of a block and a block slot: lane l holds half l & 1, row
+// (l >> 1) % RPW and slot l / (2 RPW), so one 16-byte load per lane covers
+// the group's RPW rows x SPW = 64 / (2 RPW) block columns (each a contiguous
+// run of 32 RPW bytes).  A wave keeps NBW such loads in flight per lane
+// (blocks of a chunk of WPG * SPW * NBW); the row sums are added over the
+// lanes of a wave by shuffles, then over the group's waves in wave order.
+// Fewer rows per group spread a matrix over more workgroups (CUs): one CU
+// pulls only a few tens of GB/s.
 template <int MODE, int G, int WPG, int NBW, int RPW>
 __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
 {
     constexpr int NT = G * WPG * WAVE;
     constexpr int NW = G * WPG;
-    constexpr int LPR = WAVE / RPW;       // lanes per row
-    constexpr int BPL = QK / LPR;         // bytes (weights) per lane per block
-    static_assert(LPR * BPL == QK && BPL % 4 == 0, "lane layout");
+    constexpr int SPW = WAVE / (2 * RPW);   // block slots per wave
+    constexpr int BPR = WPG * SPW;          // block columns per round of a row group
+    static_assert(SPW * 2 * RPW == WAVE, "lane layout");
     static_assert(MODE != LM_QKV || LM_HEAD % (G * RPW) == 0, "a workgroup within one head");
     extern __shared__ __align__(16) float lm_lds[];
     float *xl = lm_lds;                  // nb * 32 activations (zero padded)
-    float *xs = lm_lds + a.nb * QK;      // sums of every BPL-value chunk
+    float *xs = lm_lds + a.nb * QK;      // sums of every 16-value half block
     __shared__ float red[G][WPG][RPW];
     __shared__ double redd[NW];
     const int tid = threadIdx.x;
@@ -159,41 +163,31 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     const int wave = tid / WAVE;
     const int kp = a.nb * QK;
 
-    // ---- row groups: lane l takes row l / LPR, bytes BPL * (l % LPR) of a block ----
+    // ---- row groups: lane l takes row (l >> 1) % RPW, half l & 1 of slot l / (2 RPW) ----
     const int g = wave / WPG, wg = wave % WPG;
     int mat;
     const int row0 = lm_row<MODE, G, RPW>(a, g, mat);
     const LmMat M = a.m[mat];
-    const int row = row0 + lane / LPR, part = lane % LPR;
+    const int h = lane & 1, rr = (lane >> 1) & (RPW - 1), sl = lane / (2 * RPW);
+    const int row = row0 + rr;
     const bool row_ok = row < M.rows;
     const int rc = min(row, M.rows - 1);
-    uint32_t q[NBW][BPL / 4];
+    const int first = wg * SPW + sl;     // this lane's first block of a chunk
+    uint4 q[NBW];
     float dd[NBW];
-    // NBW blocks from block bb on (stride WPG); clamped addresses, zero scale
-    // out of range
-    auto load = [&](int bb) {
+    // NBW blocks from chunk c0 on (stride BPR); clamped addresses, zero scale
+    // out of range; scales from the row-major copy (a group's rows' scales
+    // are lines no other workgroup reads)
+    auto load = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < NBW; u++) {
-            const int b = min(bb + WPG * u, a.nb - 1);
+            const int b = min(c0 + first + BPR * u, a.nb - 1);
             const size_t o = bm_index(0, a.nb, b, M.rows, rc);
-            const int8_t *src = M.qs + o * QK + BPL * part;
-            if (BPL == 16) {
-                const int4 v = *reinterpret_cast<const int4 *>(src);
-                q[u][0] = v.x;
-                q[u][BPL / 4 > 1 ? 1 : 0] = v.y;
-                q[u][BPL / 4 > 2 ? 2 : 0] = v.z;
-                q[u][BPL / 4 > 3 ? 3 : 0] = v.w;
-            } else if (BPL == 8) {
-                const int2 v = *reinterpret_cast<const int2 *>(src);
-                q[u][0] = v.x;
-                q[u][BPL / 4 > 1 ? 1 : 0] = v.y;
-            } else {
-                q[u][0] = *reinterpret_cast<const uint32_t *>(src);
-            }
-            dd[u] = __half2float(M.d[o]);
+            q[u] = *reinterpret_cast<const uint4 *>(M.qs + o * QK + 16 * h);
+            dd[u] = __half2float(M.dcm[(size_t)rc * M.nbp + b]);
         }
 #pragma unroll
-        for (int u = 0; u < NBW; u++) dd[u] = (row_ok && bb + WPG * u < a.nb) ? dd[u] : 0.0f;
+        for (int u = 0; u < NBW; u++) dd[u] = (row_ok && c0 + first + BPR * u < a.nb) ? dd[u] : 0.0f;
     };
     // ---- input row -> LDS, normalised when asked (src/tensor.js:103-114) ----
     double inv = 1.0;
@@ -212,30 +206,31 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         xl[k] = v;
     }
     __syncthreads();
-    for (int i = tid; i < kp / BPL; i += NT) {
+    for (int i = tid; i < kp / 16; i += NT) {
         float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < BPL; j++) s += xl[BPL * i + j];
+        for (int j = 0; j < 16; j++) s += xl[16 * i + j];
         xs[i] = s;
     }
     __syncthreads();
 
     float acc = 0.0f;
-    for (int bb = wg; bb < a.nb; bb += NBW * WPG) {
-        load(bb);
+    for (int c0 = 0; c0 < a.nb; c0 += NBW * BPR) {
+        load(c0);
         __builtin_amdgcn_sched_barrier(0);   // every load of the chunk before its arithmetic
 #pragma unroll
         for (int u = 0; u < NBW; u++) {
-            const int b = bb + WPG * u;
+            const int b = c0 + first + BPR * u;
             if (b < a.nb) {
-                const int c = (b * QK + BPL * part) / BPL;
-                acc = fmaf(lm_dot<BPL>(q[u], &xl[b * QK + BPL * part], xs[c]), dd[u], acc);
+                const uint32_t w4[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+                acc = fmaf(lm_dot<16>(w4, &xl[b * QK + 16 * h], xs[2 * b + h]), dd[u], acc);
             }
         }
     }
+    acc += __shfl_xor(acc, 1, WAVE);
 #pragma unroll
-    for (int o = 1; o < LPR; o <<= 1) acc += __shfl_xor(acc, o, WAVE);
-    if (part == 0) red[g][wg][lane / LPR] = acc;
+    for (int o = 2 * RPW; o < WAVE; o <<= 1) acc += __shfl_xor(acc, o, WAVE);
+    if (lane < 2 * RPW && h == 0) red[g][wg][rr] = acc;
     __syncthreads();
 
     // ---- epilogues ----
@@ -589,7 +584,7 @@ __global__ __launch_bounds__(256) void lfm2_zero_kernel(float *__restrict__ p, s
 
 // ---------------------------------------------------------------------------
 
-static LmMat lm_mat(const qq_tensor *t) { return LmMat{t->qs, t->d, t->out_dim}; }
+static LmMat lm_mat(const qq_tensor *t) { return LmMat{t->qs, t->dcm, t->out_dim, t->nbp}; }
 
 int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
 {
@@ -619,26 +614,30 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     a.max_ctx = l.max_ctx;
     a.freq = l.freq;
     if (a.in_dim > LM_MAX_IN) return set_error(ctx, "lfm2: input row of %d > %d", a.in_dim, LM_MAX_IN);
-    // LDS: the activations and the chunk sums (BPL >= 4: at most nb * 8 of them)
-    const size_t shm = (size_t)a.nb * QK * 4 + (size_t)a.nb * 8 * 4;
+    // LDS: the activations and the sums of their 16-value halves
+    const size_t shm = (size_t)a.nb * QK * 4 + (size_t)a.nb * 2 * 4;
     prof_begin(ctx, K_LFM2_MV);
-    // rows per wave and waves per row panel chosen so that a 2048-row matrix
-    // spreads over 256 workgroups with every block of a row in flight
+    // rows per group and waves per row group chosen so that a 2048-row matrix
+    // spreads over 256 workgroups with every block of a row in flight (a
+    // 2048-value input row is 64 blocks: one chunk of WPG * SPW * NBW)
     switch (mode) {
     case LM_PLAIN:   // the output head: 65536 rows
         QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_PLAIN, 1, 16, 4, 32>), dim3((a.m[0].rows + 31) / 32), dim3(16 * WAVE), shm, a);
         break;
-    case LM_RESID:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 4, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
+    case LM_RESID:   // 2048 inputs (64 blocks), or the dense FFN's 7168 (224)
+        if (a.nb <= 64)
+            QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 1, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
+        else
+            QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 4, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
         break;
     case LM_SWIGLU:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2, 8, 8, 16>), dim3((a.m[0].rows + 15) / 16), dim3(16 * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2, 8, 4, 16>), dim3((a.m[0].rows + 15) / 16), dim3(16 * WAVE), shm, a);
         break;
     case LM_CONV:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3, 5, 13, 8>), dim3((a.H + 7) / 8), dim3(15 * WAVE), shm, a);
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3, 5, 4, 8>), dim3((a.H + 7) / 8), dim3(15 * WAVE), shm, a);
         break;
     default:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 1, 16, 4, 8>),
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 1, 16, 1, 8>),
                   dim3((a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 8), dim3(16 * WAVE), shm, a);
         break;
     }
