@@ -13,7 +13,7 @@
 //     reads it, from the residual row (binary64 sum of squares);
 //   * residual adds (addVec, src/tensor.js:181-185) are the epilogue of the
 //     matvec whose output is added (hidden = fp32(hidden + fp32(W x)));
-//   * short-conv: a workgroup owns 32 channels d and computes rows d, H + d
+//   * short-conv: a workgroup owns 8 channels d and computes rows d, H + d
 //     and 2H + d of in_proj (B, C, x), then bx = B * x, the depthwise causal
 //     conv over its channels' state, the state shift and y = C * conv;
 //   * attention: q, k and v are one matvec over their concatenated rows (v
@@ -65,11 +65,18 @@ struct LmArgs {
 };
 
 // Sum of one value per thread over a block of NW waves: waves by DPP, then
-// the wave sums in wave order.  Contains a __syncthreads.
+// the wave sums in wave order (the order of block_sum_f64).  Its barrier
+// orders LDS only, so global loads issued before it stay in flight.
 template <int NW>
 __device__ __forceinline__ double lm_block_sum(double v, double *red)
 {
-    return block_sum_f64<NW>(v, red);
+    v = wave_sum_dpp(v);
+    if ((threadIdx.x & (WAVE - 1)) == 0) red[threadIdx.x / WAVE] = v;
+    lds_barrier();
+    double s = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; w++) s = s + red[w];
+    return s;
 }
 
 template <int NW>
@@ -143,8 +150,9 @@ __device__ __forceinline__ float lm_dot(const uint32_t (&w)[BPL / 4], const floa
 // (blocks of a chunk of WPG * SPW * NBW); the row sums are added over the
 // lanes of a wave by shuffles, then over the group's waves in wave order.
 // Fewer rows per group spread a matrix over more workgroups (CUs): one CU
-// pulls only a few tens of GB/s.
-template <int MODE, int G, int WPG, int NBW, int RPW>
+// pulls only a few tens of GB/s.  Each thread loads XR values of the input
+// row (XR * threads >= nb * 32) before the weights.
+template <int MODE, int G, int WPG, int NBW, int RPW, int XR>
 __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
 {
     constexpr int NT = G * WPG * WAVE;
@@ -189,35 +197,75 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
 #pragma unroll
         for (int u = 0; u < NBW; u++) dd[u] = (row_ok && c0 + first + BPR * u < a.nb) ? dd[u] : 0.0f;
     };
+    // ---- loads first: this thread's share of the input row (and norm
+    // weights), then the first chunk of weight blocks, then the operands of
+    // the epilogue.  Loads complete in issue order and the barriers below
+    // order LDS only, so the row is normalised and staged while the weight
+    // bytes are still in flight. ----
+    // (unconditional loads at clamped indices, values selected once they
+    // arrive: a load under a branch is waited for where the branch joins)
+    float xr[XR], wr[XR];
+    const float *nw = a.norm_w ? a.norm_w : a.x;
+#pragma unroll
+    for (int i = 0; i < XR; i++) {
+        const int k = min(tid + NT * i, a.in_dim - 1);
+        xr[i] = a.x[k];
+        wr[i] = nw[k];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    load(0);
+    // epilogue operands: the residual value (RESID), the conv state and
+    // kernel taps of this thread's channel (CONV)
+    float yold = 0.0f;
+    float st[LM_MAX_L], kw[LM_MAX_L];
+    if (MODE == LM_RESID && tid < G * RPW) {
+        const int orow = G * RPW * blockIdx.x + tid;
+        if (orow < a.m[0].rows) yold = a.y[orow];
+    }
+    if (MODE == LM_CONV) {
+        const int d = RPW * blockIdx.x + tid;
+        const bool own = tid < RPW && d < a.H;
+#pragma unroll
+        for (int k = 0; k < LM_MAX_L; k++) {
+            st[k] = (own && k < a.L - 1) ? a.state[(size_t)k * a.H + d] : 0.0f;
+            kw[k] = (own && k < a.L) ? a.kern[(size_t)d * a.L + k] : 0.0f;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- input row -> LDS, normalised when asked (src/tensor.js:103-114) ----
     double inv = 1.0;
     if (a.norm) {
         double ss = 0.0;
-        for (int k = tid; k < a.in_dim; k += NT) {
-            const double v = (double)a.x[k];
-            ss = fma(v, v, ss);
-        }
+#pragma unroll
+        for (int i = 0; i < XR; i++)
+            if (tid + NT * i < a.in_dim) {
+                const double v = (double)xr[i];
+                ss = fma(v, v, ss);
+            }
         inv = rms_inv(lm_block_sum<NW>(ss, redd), a.in_dim, a.eps);
     }
-    for (int k = tid; k < kp; k += NT) {
-        float v = k < a.in_dim ? a.x[k] : 0.0f;
-        if (a.norm && k < a.in_dim)
-            v = (float)((double)(a.norm_w ? a.norm_w[k] : 1.0f) * (double)v * inv);
-        xl[k] = v;
+#pragma unroll
+    for (int i = 0; i < XR; i++) {
+        const int k = tid + NT * i;
+        if (k < kp) {
+            float v = k < a.in_dim ? xr[i] : 0.0f;
+            if (a.norm && k < a.in_dim)
+                v = (float)((double)(a.norm_w ? wr[i] : 1.0f) * (double)v * inv);
+            xl[k] = v;
+        }
     }
-    __syncthreads();
+    lds_barrier();
     for (int i = tid; i < kp / 16; i += NT) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < 16; j++) s += xl[16 * i + j];
         xs[i] = s;
     }
-    __syncthreads();
+    lds_barrier();
 
     float acc = 0.0f;
-    for (int c0 = 0; c0 < a.nb; c0 += NBW * BPR) {
-        load(c0);
-        __builtin_amdgcn_sched_barrier(0);   // every load of the chunk before its arithmetic
+    for (int c0 = 0;;) {
 #pragma unroll
         for (int u = 0; u < NBW; u++) {
             const int b = c0 + first + BPR * u;
@@ -226,6 +274,10 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
                 acc = fmaf(lm_dot<16>(w4, &xl[b * QK + 16 * h], xs[2 * b + h]), dd[u], acc);
             }
         }
+        c0 += NBW * BPR;
+        if (c0 >= a.nb) break;
+        load(c0);
+        __builtin_amdgcn_sched_barrier(0);   // every load of the chunk before its arithmetic
     }
     acc += __shfl_xor(acc, 1, WAVE);
 #pragma unroll
@@ -246,7 +298,7 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
             const int orow = G * RPW * blockIdx.x + RPW * gg + r;
             if (orow < a.m[0].rows) {
                 const float v = rowsum(gg, r);
-                a.y[orow] = MODE == LM_RESID ? a.y[orow] + v : v;
+                a.y[orow] = MODE == LM_RESID ? yold + v : v;
             }
         }
     } else if (MODE == LM_SWIGLU) {
@@ -265,14 +317,10 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
             const float B = rowsum(0, tid), C = rowsum(1, tid), X = rowsum(2, tid);
             const float bx = B * X;
             double s = 0.0;
-            float st[LM_MAX_L];
-#pragma unroll
-            for (int k = 0; k < LM_MAX_L - 1; k++)
-                if (k < a.L - 1) st[k] = a.state[(size_t)k * a.H + d];
 #pragma unroll
             for (int k = 0; k < LM_MAX_L; k++) {
                 if (k >= a.L) break;
-                const double w = (double)a.kern[(size_t)d * a.L + k];
+                const double w = (double)kw[k];
                 const double t = w * (double)(k < a.L - 1 ? st[k] : bx);
                 s = k == 0 ? t : s + t;
             }
@@ -586,6 +634,20 @@ __global__ __launch_bounds__(256) void lfm2_zero_kernel(float *__restrict__ p, s
 
 static LmMat lm_mat(const qq_tensor *t) { return LmMat{t->qs, t->dcm, t->out_dim, t->nbp}; }
 
+// One launch of lfm2_mv_kernel; XR, the input values each thread holds, is
+// the smaller of two instances (rows of up to 2048 values, or up to
+// LM_MAX_IN) whose threads cover the row's nb * 32 values.
+template <int MODE, int G, int WPG, int NBW, int RPW>
+static void mv_launch(qq_ctx *ctx, int grid, size_t shm, const LmArgs &a)
+{
+    constexpr int NT = G * WPG * WAVE;
+    constexpr int XS = (2048 + NT - 1) / NT, XL = (LM_MAX_IN + NT - 1) / NT;
+    if (a.nb * QK <= XS * NT)
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<MODE, G, WPG, NBW, RPW, XS>), dim3(grid), dim3(NT), shm, a);
+    else
+        QQ_LAUNCH(ctx, (lfm2_mv_kernel<MODE, G, WPG, NBW, RPW, XL>), dim3(grid), dim3(NT), shm, a);
+}
+
 int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
 {
     LmArgs a{};
@@ -622,23 +684,22 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     // 2048-value input row is 64 blocks: one chunk of WPG * SPW * NBW)
     switch (mode) {
     case LM_PLAIN:   // the output head: 65536 rows
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_PLAIN, 1, 16, 4, 32>), dim3((a.m[0].rows + 31) / 32), dim3(16 * WAVE), shm, a);
+        mv_launch<LM_PLAIN, 1, 16, 4, 32>(ctx, (a.m[0].rows + 31) / 32, shm, a);
         break;
     case LM_RESID:   // 2048 inputs (64 blocks), or the dense FFN's 7168 (224)
         if (a.nb <= 64)
-            QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 1, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
+            mv_launch<LM_RESID, 1, 16, 1, 8>(ctx, (a.m[0].rows + 7) / 8, shm, a);
         else
-            QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_RESID, 1, 16, 4, 8>), dim3((a.m[0].rows + 7) / 8), dim3(16 * WAVE), shm, a);
+            mv_launch<LM_RESID, 1, 16, 4, 8>(ctx, (a.m[0].rows + 7) / 8, shm, a);
         break;
     case LM_SWIGLU:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_SWIGLU, 2, 8, 4, 16>), dim3((a.m[0].rows + 15) / 16), dim3(16 * WAVE), shm, a);
+        mv_launch<LM_SWIGLU, 2, 8, 4, 16>(ctx, (a.m[0].rows + 15) / 16, shm, a);
         break;
     case LM_CONV:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_CONV, 3, 5, 4, 8>), dim3((a.H + 7) / 8), dim3(15 * WAVE), shm, a);
+        mv_launch<LM_CONV, 3, 5, 4, 8>(ctx, (a.H + 7) / 8, shm, a);
         break;
     default:
-        QQ_LAUNCH(ctx, (lfm2_mv_kernel<LM_QKV, 1, 16, 1, 8>),
-                  dim3((a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 8), dim3(16 * WAVE), shm, a);
+        mv_launch<LM_QKV, 1, 16, 1, 8>(ctx, (a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 8, shm, a);
         break;
     }
     prof_end(ctx);
