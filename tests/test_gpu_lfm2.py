@@ -68,12 +68,26 @@ def test_forward_matches_oracle(tmp_path, seed, kw):
 
 def test_forward_full_width(tmp_path):
     """LFM2-8B-A1B widths on three blocks: a dense FFN of 7168 (the residual
-    matvec's multi-chunk loop over 7168 inputs), one attention block with 32
-    query / 8 KV heads (GQA ratio 4), one MoE block (8 experts of 1792, top-4,
-    through the batch-1 decode kernel) and the 65536-row output head."""
+    matvec over 7168 inputs, 8 input values per thread), one attention block
+    with 32 query / 8 KV heads (GQA ratio 4), one MoE block (8 experts of
+    1792, top-4, through the batch-1 decode kernel) and the 65536-row output
+    head."""
     _say("lfm2 full width")
     cfg = dict(synth.LFM2_8B_A1B, n_layers=3, attn_layers=(1,), n_dense=1, E=8, ctx=64)
     m, _ = _check_tokens(tmp_path, 12, cfg=cfg, tokens=TOKENS[:4])
+    m.release()
+
+
+def test_forward_rows_past_one_chunk(tmp_path):
+    """H = 3072 (96 blocks per input row), dense FFNs only (the batch-1 MoE
+    kernel takes H <= 2048): the output head, q/k/v, short-conv in_proj and
+    dense gate/up matvecs cover a row's blocks in two chunks (64 or 80 blocks
+    in flight per row group), and every matvec holds 8 or 9 input values per
+    thread; 48 query / 12 KV heads."""
+    _say("lfm2 H=3072")
+    cfg = dict(synth.LFM2_TINY, H=3072, n_heads=48, n_head_kv=12, n_layers=4, attn_layers=(1,), n_dense=4,
+               n_ff=1024, vocab=500)
+    m, _ = _check_tokens(tmp_path, 21, cfg=cfg, tokens=TOKENS[:3])
     m.release()
 
 
