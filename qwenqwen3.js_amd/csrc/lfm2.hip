@@ -680,15 +680,17 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     const size_t shm = (size_t)a.nb * QK * 4 + (size_t)a.nb * 2 * 4;
     prof_begin(ctx, K_LFM2_MV);
     // rows per group and waves per row group chosen so that a 2048-row matrix
-    // spreads over 256 workgroups with every block of a row in flight (a
-    // 2048-value input row is 64 blocks: one chunk of WPG * SPW * NBW)
+    // spreads over 256 to 512 workgroups with every block of a row in flight
+    // (a 2048-value input row is 64 blocks: one chunk of WPG * SPW * NBW);
+    // measured on the LFM2-8B-A1B token against 2 to 32 rows per group and 1
+    // to 16 waves
     switch (mode) {
     case LM_PLAIN:   // the output head: 65536 rows
         mv_launch<LM_PLAIN, 1, 16, 4, 32>(ctx, (a.m[0].rows + 31) / 32, shm, a);
         break;
     case LM_RESID:   // 2048 inputs (64 blocks), or the dense FFN's 7168 (224)
         if (a.nb <= 64)
-            mv_launch<LM_RESID, 1, 16, 1, 8>(ctx, (a.m[0].rows + 7) / 8, shm, a);
+            mv_launch<LM_RESID, 1, 8, 1, 4>(ctx, (a.m[0].rows + 3) / 4, shm, a);
         else
             mv_launch<LM_RESID, 1, 16, 4, 8>(ctx, (a.m[0].rows + 7) / 8, shm, a);
         break;
@@ -699,7 +701,7 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
         mv_launch<LM_CONV, 3, 5, 4, 8>(ctx, (a.H + 7) / 8, shm, a);
         break;
     default:
-        mv_launch<LM_QKV, 1, 16, 1, 8>(ctx, (a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 8, shm, a);
+        mv_launch<LM_QKV, 1, 8, 1, 4>(ctx, (a.n_heads + 2 * a.n_kv_heads) * LM_HEAD / 4, shm, a);
         break;
     }
     prof_end(ctx);
