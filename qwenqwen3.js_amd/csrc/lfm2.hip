@@ -396,6 +396,28 @@ __device__ __forceinline__ bool lm_first_of_group(int hq, int g, int n_heads, in
     return hq == 0 || (int)(((long long)(hq - 1) * n_kv_heads) / n_heads) != g;
 }
 
+// blockIdx.x -> (query head hq, chunk c) of the attention kernels.  The
+// dispatcher deals workgroups to the 8 XCDs round robin, so the GQ =
+// n_heads / n_kv_heads query heads of one (chunk, KV head) unit get block
+// indices 8 apart: they run on one XCD and read that KV head's rows into one
+// L2 (head hq of KV head hq / GQ, as (h * n_kv_heads / n_heads) | 0 with
+// n_heads a multiple of n_kv_heads).  False for the padding blocks.
+__device__ __forceinline__ bool lm_attn_unit(int n_heads, int n_kv_heads, int nch, int &hq, int &c)
+{
+    const int GQ = n_heads / n_kv_heads;
+    const int x = blockIdx.x & 7, r = blockIdx.x >> 3;
+    const int u = (r / GQ) * 8 + x;   // unit c * n_kv_heads + KV head
+    if (u >= n_kv_heads * nch) return false;
+    c = u / n_kv_heads;
+    hq = (u - c * n_kv_heads) * GQ + r % GQ;
+    return true;
+}
+
+static unsigned lm_attn_grid(int n_heads, int n_kv_heads, int nch)
+{
+    return 8u * (unsigned)((n_kv_heads * nch + 7) / 8) * (unsigned)(n_heads / n_kv_heads);
+}
+
 // GQA attention of one token (src/lfm2-engine.js:354-388), one workgroup
 // per query head h over kv head (h * n_kv_heads / n_heads) | 0 and positions
 // 0..n-1:
@@ -420,7 +442,8 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in,
     __shared__ double redd[NW];
     __shared__ float part[NW][LM_HEAD];
     const int tid = threadIdx.x;
-    const int hq = blockIdx.x;
+    int hq, c;
+    if (!lm_attn_unit(n_heads, n_kv_heads, 1, hq, c)) return;
     const int g = (int)(((long long)hq * n_kv_heads) / n_heads);
     const float *K = kc + (size_t)g * max_ctx * LM_HEAD;
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
@@ -512,7 +535,7 @@ constexpr int LM_PART = LM_HEAD + 2;   // doubles per (head, chunk): o[64], m, l
 
 __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_chunk_kernel(
     LmAttnIn in, float *__restrict__ kc, const float *__restrict__ vc, int n_heads,
-    int n_kv_heads, int max_ctx, int n, double scale, double *__restrict__ part)
+    int n_kv_heads, int max_ctx, int n, int nch, double scale, double *__restrict__ part)
 {
     constexpr int NW = LM_ATTN_THREADS / WAVE;
     constexpr int VPT = LM_CHUNK / NW;   // V values per thread
@@ -524,7 +547,8 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_chunk_kernel(
     __shared__ double redd[NW];
     __shared__ double po[NW][LM_HEAD];
     const int tid = threadIdx.x;
-    const int hq = blockIdx.x, c = blockIdx.y;
+    int hq, c;
+    if (!lm_attn_unit(n_heads, n_kv_heads, nch, hq, c)) return;
     const int g = (int)(((long long)hq * n_kv_heads) / n_heads);
     const float *K = kc + (size_t)g * max_ctx * LM_HEAD;
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
@@ -719,12 +743,12 @@ int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kraw, const float
     const LmAttnIn in{q, kraw, qn, kn, freq, eps};
     prof_begin(ctx, K_LFM2_ATTN);
     if (n <= LM_CHUNK) {
-        QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(n_heads), dim3(LM_ATTN_THREADS), 0, in, kc, vc, n_heads,
-                  n_kv_heads, max_ctx, n, scale, out);
+        QQ_LAUNCH(ctx, lfm2_attn_kernel, dim3(lm_attn_grid(n_heads, n_kv_heads, 1)), dim3(LM_ATTN_THREADS), 0,
+                  in, kc, vc, n_heads, n_kv_heads, max_ctx, n, scale, out);
     } else {
         const int nch = (n + LM_CHUNK - 1) / LM_CHUNK;
-        QQ_LAUNCH(ctx, lfm2_attn_chunk_kernel, dim3(n_heads, nch), dim3(LM_ATTN_THREADS), 0, in, kc, vc,
-                  n_heads, n_kv_heads, max_ctx, n, scale, work);
+        QQ_LAUNCH(ctx, lfm2_attn_chunk_kernel, dim3(lm_attn_grid(n_heads, n_kv_heads, nch)),
+                  dim3(LM_ATTN_THREADS), 0, in, kc, vc, n_heads, n_kv_heads, max_ctx, n, nch, scale, work);
         QQ_LAUNCH(ctx, lfm2_attn_join_kernel, dim3(n_heads), dim3(LM_HEAD), 0, work, nch, out);
     }
     prof_end(ctx);
