@@ -36,6 +36,7 @@ constexpr int LM_MAX_L = 4;      // short-conv kernel length (l_cache) supported
 constexpr int LM_HEAD = 64;      // head_dim supported by the QKV epilogue and attention
 constexpr int LM_MAX_CTX = 4096; // the reference caps the context at 4096 (lfm2-engine.js:33)
 constexpr int LM_ATTN_THREADS = 256;
+constexpr int LM_CHUNK = 256;    // positions of the one-workgroup attention, and of a long-context chunk
 
 struct LmMat {
     const int8_t *qs;
@@ -449,9 +450,10 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in,
     const float *V = vc + (size_t)g * max_ctx * LM_HEAD;
     const int d = tid % LM_HEAD, cls = tid / LM_HEAD;
     // loads that depend on nothing are issued first: this thread's first K
-    // row (cached positions only: position n - 1 is this call's), the first
-    // LM_VPRE values of its V column
-    constexpr int LM_VPRE = 8;
+    // row (cached positions only: position n - 1 is this call's) and every
+    // value of its V column it sums (positions cls, cls + NW, ...)
+    constexpr int VPT = LM_CHUNK / NW;   // V values per thread
+    static_assert(LM_ATTN_THREADS == LM_CHUNK, "up to LM_CHUNK positions");
     float4 kr[LM_HEAD / 4];
     auto load_k = [&](int p) {
         if (p >= n - 1) return;
@@ -462,9 +464,9 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in,
 #pragma unroll
     for (int i = 0; i < LM_HEAD / 4; i++) kr[i] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     load_k(tid);
-    float vpre[LM_VPRE];
+    float vv[VPT];
 #pragma unroll
-    for (int u = 0; u < LM_VPRE; u++) vpre[u] = V[(size_t)min(cls + NW * u, n - 1) * LM_HEAD + d];
+    for (int u = 0; u < VPT; u++) vv[u] = V[(size_t)min(cls + NW * u, n - 1) * LM_HEAD + d];
     // this query head (wave 0) and the new k row (wave 1), normed and rotated
     if (tid / WAVE == 0) lm_head_prep(in.q + (size_t)hq * LM_HEAD, in.qn, in.eps, n - 1, in.freq, qh);
     else if (tid / WAVE == 1) lm_head_prep(in.kraw + (size_t)g * LM_HEAD, in.kn, in.eps, n - 1, in.freq, kpos);
@@ -499,18 +501,12 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in,
     for (int p = tid; p < n; p += LM_ATTN_THREADS) sc[p] = (float)((double)sc[p] * inv);
     __syncthreads();
     float acc = 0.0f;
-    int u = 0;
-    for (int p = cls; p < n; p += NW, u++) {
-        const float w = sc[p];
-        float v;
-        if (u < LM_VPRE) {
-            v = vpre[0];
 #pragma unroll
-            for (int k = 1; k < LM_VPRE; k++) v = u == k ? vpre[k] : v;
-        } else {
-            v = V[(size_t)p * LM_HEAD + d];
-        }
-        if (w != 0.0f) acc = (float)fma((double)v, (double)w, (double)acc);
+    for (int u = 0; u < VPT; u++) {
+        const int p = cls + NW * u;
+        if (p >= n) break;
+        const float w = sc[p];
+        if (w != 0.0f) acc = (float)fma((double)vv[u], (double)w, (double)acc);
     }
     part[cls][d] = acc;
     __syncthreads();
@@ -529,7 +525,6 @@ __global__ __launch_bounds__(LM_ATTN_THREADS) void lfm2_attn_kernel(LmAttnIn in,
 // (binary64); lfm2_attn_join_kernel then forms
 // out[d] = fp32(sum_c o_c[d] e^(m_c - M) / sum_c l_c e^(m_c - M)), M = max m_c,
 // over the chunks in order.  Equal to the one-workgroup form to rounding.
-constexpr int LM_CHUNK = 256;
 constexpr int LM_MAX_CHUNKS = LM_MAX_CTX / LM_CHUNK;
 constexpr int LM_PART = LM_HEAD + 2;   // doubles per (head, chunk): o[64], m, l
 
