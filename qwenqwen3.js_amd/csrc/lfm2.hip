@@ -632,16 +632,17 @@ __global__ __launch_bounds__(LM_HEAD) void lfm2_attn_join_kernel(const double *_
 }
 
 // embeddingLookupQ80 (src/tensor.js:56-77) of column `token` of the repacked
-// [H, vocab] table: hidden[i] = q * d (exact in fp32).
+// [H, vocab] table: hidden[i] = q * d (exact in fp32).  One value per thread,
+// so the row costs one round trip to memory.
 __global__ __launch_bounds__(256) void lfm2_embed_kernel(const int8_t *__restrict__ qs,
                                                         const __half *__restrict__ d, int nb,
                                                         int vocab, int token, int H,
                                                         float *__restrict__ out)
 {
-    for (int i = threadIdx.x; i < H; i += 256) {
-        const size_t o = bm_index(0, nb, i / QK, vocab, token);
-        out[i] = (float)qs[o * QK + i % QK] * __half2float(d[o]);
-    }
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= H) return;
+    const size_t o = bm_index(0, nb, i / QK, vocab, token);
+    out[i] = (float)qs[o * QK + i % QK] * __half2float(d[o]);
 }
 
 __global__ __launch_bounds__(256) void lfm2_zero_kernel(float *__restrict__ p, size_t n)
@@ -754,8 +755,8 @@ int launch_lfm2_attn(qq_ctx *ctx, const float *q, const float *kraw, const float
 int launch_lfm2_embed(qq_ctx *ctx, const qq_tensor *t, int token, float *out)
 {
     prof_begin(ctx, K_LFM2_EMBED);
-    QQ_LAUNCH(ctx, lfm2_embed_kernel, dim3(1), dim3(256), 0, t->qs, t->d, t->nb, t->out_dim, token,
-              t->in_dim, out);
+    QQ_LAUNCH(ctx, lfm2_embed_kernel, dim3((t->in_dim + 255) / 256), dim3(256), 0, t->qs, t->d, t->nb,
+              t->out_dim, token, t->in_dim, out);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
