@@ -82,8 +82,10 @@ __device__ __forceinline__ h8_t int8_to_f16x8(const uint2 q)
 // Operand stream.  Wave w reduces blocks w, w+4, w+8, ... of the reduction
 // dimension.  Every operand of a block goes straight to registers: the
 // lane's 8 activations of each of its MF rows (two float4), its 8 weight
-// bytes of each of the ST_NF fragment columns (uint2) and those columns'
-// fp16 scales.  Each wave keeps ST_PF blocks in flight: block i + ST_PF is
+// bytes of each of the ST_NF fragment columns (uint2) and one fp16 scale per
+// column half: lane l loads column c0[h] + l's, and a fragment's scale is
+// taken from the lane that loaded it (lanes 16t .. 16t+15 hold the columns
+// of fragment t of each half).  Each wave keeps ST_PF blocks in flight: block i + ST_PF is
 // requested as soon as block i's products are done.  (Staged through LDS the
 // stream is held to ~100 KB in flight per CU by the LDS size.)
 // Fragment j: column 16*(j%4) + lane%16 of half j/4; lane l holds row l%16
@@ -93,7 +95,7 @@ template <int MF>
 struct StBlock {
     float4 a[MF][2];     // rows 16m + lane%16, k = 8*(lane/16) .. +7
     uint2 q[ST_NF];      // fragment j's 8 weight bytes
-    h2_t d[ST_NF / 2];   // fragment j's column scale: d[j / 2][j % 2]
+    uint32_t ds[2];      // scale bits of column c0[h] + lane of half h
 };
 
 template <int MF>
@@ -107,6 +109,7 @@ struct StSrc {
     const uint16_t *db[2];      // their scales
     int cb[2];                  // column half h: the lane's column c0[h] + lane%16 (fragment j adds 16*(j%4))
     int cmax;                   // last column (loads clamp to it)
+    uint32_t sc[2];             // column of this lane's scale load in half h (clamped)
     uint32_t qk;                // the lane's byte offset within a column's 32 bytes
     uint32_t qstep, dstep;      // one block: rows * 32 bytes, rows scales
     uint32_t okm;               // bit j: fragment j's column in range (else its scale is zero)
@@ -128,11 +131,9 @@ __device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int 
         b.q[j] = *reinterpret_cast<const uint2 *>(s.qb[j >> 2] + (size_t)(qk + c * QK + s.qk));
     }
 #pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const uint32_t c = (uint32_t)min(s.cb[j >> 2] + 16 * (j & 3), s.cmax);
-        b.d[j >> 1][j & 1] = *reinterpret_cast<const _Float16 *>(reinterpret_cast<const char *>(s.db[j >> 2]) +
-                                                                 (size_t)(2u * (dk + c)));
-    }
+    for (int h = 0; h < 2; h++)
+        b.ds[h] = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(s.db[h]) +
+                                                      (size_t)(2u * (dk + s.sc[h])));
 }
 
 // The block's int8 weights enter the MFMA exactly (as fp16 integers); the
@@ -145,9 +146,11 @@ __device__ __forceinline__ void st_block(const StBlock<MF> &b, const StSrc<MF> &
     h8_t ah[MF], al[MF];
 #pragma unroll
     for (int m = 0; m < MF; m++) split8(b.a[m][0], b.a[m][1], ah[m], al[m]);
+    const int l16 = threadIdx.x & 15;
 #pragma unroll
     for (int j = 0; j < ST_NF; j++) {
-        const float d = ((s.okm >> j) & 1u) ? (float)b.d[j >> 1][j & 1] : 0.0f;
+        const uint32_t bits = (uint32_t)__shfl((int)b.ds[j >> 2], 16 * (j & 3) + l16, WAVE);
+        const float d = ((s.okm >> j) & 1u) ? (float)__builtin_bit_cast(_Float16, (uint16_t)bits) : 0.0f;
         const h8_t qh = int8_to_f16x8(b.q[j]);
 #pragma unroll
         for (int m = 0; m < MF; m++) {
@@ -197,6 +200,8 @@ __device__ __forceinline__ void st_offsets(StSrc<MF> &s, RowOff rowoff, const in
     s.cb[0] = c0[0] + (lane & 15);
     s.cb[1] = c0[1] + (lane & 15);
     s.cmax = rows - 1;
+    s.sc[0] = (uint32_t)min(c0[0] + lane, rows - 1);
+    s.sc[1] = (uint32_t)min(c0[1] + lane, rows - 1);
     s.okm = 0;
 #pragma unroll
     for (int j = 0; j < ST_NF; j++) s.okm |= (c0[j >> 2] + 16 * (j & 3) + (lane & 15) < rows ? 1u : 0u) << j;
