@@ -156,23 +156,24 @@ __global__ __launch_bounds__(256) void router_logits_kernel(const float *__restr
 
 // One wavefront per token: logit = fp32(sum of the KS partial sums in order),
 // then the layer's gating (sigmoid + bias, or softmax), stable top-K and
-// renormalisation.
+// renormalisation.  EPL = experts per lane (E <= 64 EPL).
+template <int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const double *__restrict__ part, int KS, int T, int E, int K, const float *__restrict__ bias,
     int softmax, int32_t *__restrict__ idx, double *__restrict__ w, float *__restrict__ probs)
 {
-    constexpr int EPL = MAX_E / WAVE;
     const int lane = threadIdx.x & (WAVE - 1);
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
     if (t >= T) return;
-    // every partial sum of this lane in flight at once, then added in slice order
+    // every partial sum of this lane in flight at once (loaded at clamped
+    // slices, unconditionally), then added in slice order
     double pv[EPL][ROUTER_MAX_SPLIT];
 #pragma unroll
     for (int i = 0; i < EPL; i++) {
         const int e = min(lane + WAVE * i, E - 1);
 #pragma unroll
         for (int ks = 0; ks < ROUTER_MAX_SPLIT; ks++)
-            pv[i][ks] = ks < KS ? part[((size_t)ks * T + t) * E + e] : 0.0;
+            pv[i][ks] = part[((size_t)min(ks, KS - 1) * T + t) * E + e];
     }
     float lg[EPL];
 #pragma unroll
@@ -252,8 +253,16 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_ROUTER_TOPK);
-    QQ_LAUNCH(ctx, router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, part, KS, T, m->E, m->K,
-              m->bias, m->gating == QQ_GATING_SOFTMAX ? 1 : 0, idx, w, probs);
+    const int sm = m->gating == QQ_GATING_SOFTMAX ? 1 : 0;
+    if (m->E <= WAVE)
+        QQ_LAUNCH(ctx, router_topk_kernel<1>, dim3((T + 3) / 4), dim3(256), 0, part, KS, T, m->E, m->K,
+                  m->bias, sm, idx, w, probs);
+    else if (m->E <= 2 * WAVE)
+        QQ_LAUNCH(ctx, router_topk_kernel<2>, dim3((T + 3) / 4), dim3(256), 0, part, KS, T, m->E, m->K,
+                  m->bias, sm, idx, w, probs);
+    else
+        QQ_LAUNCH(ctx, (router_topk_kernel<MAX_E / WAVE>), dim3((T + 3) / 4), dim3(256), 0, part, KS, T,
+                  m->E, m->K, m->bias, sm, idx, w, probs);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
