@@ -184,9 +184,13 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     const int first = wg * SPW + sl;     // this lane's first block of a chunk
     uint4 q[NBW];
     float dd[NBW];
-    // NBW blocks from chunk c0 on (stride BPR); clamped addresses, zero scale
-    // out of range; scales from the row-major copy (a group's rows' scales
-    // are lines no other workgroup reads)
+    // NBW blocks from chunk c0 on (stride BPR), at clamped addresses and
+    // without a condition on the loaded values (a value selected against a
+    // condition lets the compiler move its load under a branch, whose join
+    // then waits for every load in flight).  Blocks past nb are skipped in
+    // the products; a row past the matrix reads row rows - 1 and is never
+    // stored.  Scales come from the row-major copy (a group's rows' scales
+    // are lines no other workgroup reads).
     auto load = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < NBW; u++) {
@@ -195,8 +199,6 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
             q[u] = *reinterpret_cast<const uint4 *>(M.qs + o * QK + 16 * h);
             dd[u] = __half2float(M.dcm[(size_t)rc * M.nbp + b]);
         }
-#pragma unroll
-        for (int u = 0; u < NBW; u++) dd[u] = (row_ok && c0 + first + BPR * u < a.nb) ? dd[u] : 0.0f;
     };
     // ---- loads first: this thread's share of the input row (and norm
     // weights), then the first chunk of weight blocks, then the operands of
@@ -223,13 +225,12 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         const int orow = G * RPW * blockIdx.x + tid;
         if (orow < a.m[0].rows) yold = a.y[orow];
     }
-    if (MODE == LM_CONV) {
-        const int d = RPW * blockIdx.x + tid;
-        const bool own = tid < RPW && d < a.H;
+    if (MODE == LM_CONV) {   // clamped, unconditional (used only where in range)
+        const int d = min(RPW * (int)blockIdx.x + tid, a.H - 1);
 #pragma unroll
         for (int k = 0; k < LM_MAX_L; k++) {
-            st[k] = (own && k < a.L - 1) ? a.state[(size_t)k * a.H + d] : 0.0f;
-            kw[k] = (own && k < a.L) ? a.kern[(size_t)d * a.L + k] : 0.0f;
+            st[k] = a.state[(size_t)min(k, a.L - 2) * a.H + d];
+            kw[k] = a.kern[(size_t)d * a.L + min(k, a.L - 1)];
         }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -696,6 +697,7 @@ int launch_lfm2_mv(qq_ctx *ctx, int mode, const LmLaunch &l)
     a.max_ctx = l.max_ctx;
     a.freq = l.freq;
     if (a.in_dim > LM_MAX_IN) return set_error(ctx, "lfm2: input row of %d > %d", a.in_dim, LM_MAX_IN);
+    if (mode == LM_CONV && (a.L < 2 || a.L > LM_MAX_L)) return set_error(ctx, "lfm2: short-conv length %d", a.L);
     // LDS: the activations and the sums of their 16-value halves
     const size_t shm = (size_t)a.nb * QK * 4 + (size_t)a.nb * 2 * 4;
     prof_begin(ctx, K_LFM2_MV);
