@@ -410,11 +410,16 @@ __global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict_
         sv[k] = k < K ? inv[t * K + k] : -1;
         wv[k] = k < K ? w[t * K + k] : 0.0;
     }
+    // the hidden values and every rank's row in flight at once: rows are
+    // loaded at clamped slots (slot 0 for a masked rank) and pinned before
+    // the sum, whose conditions would otherwise pull each load under a
+    // branch, waited for where the branch joins -- one round trip per rank
+    float4 *hp = reinterpret_cast<float4 *>(hidden + (size_t)t * H + j);
+    float4 hv = *hp;
     float v[KM][4];
 #pragma unroll
     for (int k = 0; k < KM; k++) {
-        const int s = sv[k];
-        if (s < 0) continue;
+        const int s = max(sv[k], 0);
         if constexpr (sizeof(YT) == 4) {
             const float4 q = *reinterpret_cast<const float4 *>(y + (size_t)s * H + j);
             v[k][0] = q.x; v[k][1] = q.y; v[k][2] = q.z; v[k][3] = q.w;
@@ -425,6 +430,10 @@ __global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict_
             for (int i = 0; i < 4; i++) v[k][i] = (float)h[i];
         }
     }
+#pragma unroll
+    for (int k = 0; k < KM; k++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) asm volatile("" : "+v"(v[k][i]));
     float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int k = 0; k < KM; k++) {
@@ -432,8 +441,6 @@ __global__ __launch_bounds__(256) void moe_combine4_kernel(const YT *__restrict_
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[i] = (float)((double)acc[i] + wv[k] * (double)v[k][i]);
     }
-    float4 *hp = reinterpret_cast<float4 *>(hidden + (size_t)t * H + j);
-    float4 hv = *hp;
     hv.x = hv.x + acc[0];
     hv.y = hv.y + acc[1];
     hv.z = hv.z + acc[2];
