@@ -77,19 +77,57 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
     const int ka = ks * kchunk, kb = min(W.H, ka + kchunk);
 
     d4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll 2
-    for (int k = ka + 16 * wave; k < kb; k += 64) {
-        const int kk = k + 4 * kq;
-        const float4 xv = *reinterpret_cast<const float4 *>(xr + kk);
-        double wa[4], wb[4];
-        W.at4(e0 + r16, kk, Q8, wa);
-        W.at4(e0 + 16 + r16, kk, Q8, wb);
+    auto step = [&](const float4 xv, const double (&wa)[4], const double (&wb)[4]) {
         const double xd[4] = {(double)xv.x * tz, (double)xv.y * tz, (double)xv.z * tz,
                               (double)xv.w * tz};
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wa[j], acc0, 0, 0, 0);
             acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wb[j], acc1, 0, 0, 0);
+        }
+    };
+    int k = ka + 16 * wave;
+    if constexpr (!Q8) {
+        // F32 router: the raw rows of RB steps are loaded before any of them
+        // is used (one round trip per RB steps, not per step); steps past
+        // the slice load clamped addresses and are skipped
+        constexpr int RB = 4;
+        const int ea = min(e0 + r16, W.E - 1), eb = min(e0 + 16 + r16, W.E - 1);
+        const double za = e0 + r16 < W.E ? 1.0 : 0.0, zb = e0 + 16 + r16 < W.E ? 1.0 : 0.0;
+        for (; k < kb; k += 64 * RB) {
+            float4 xv[RB], va[RB], vb[RB];
+#pragma unroll
+            for (int u = 0; u < RB; u++) {
+                const int kk = min(k + 64 * u, kb - 16) + 4 * kq;
+                xv[u] = *reinterpret_cast<const float4 *>(xr + kk);
+                va[u] = *reinterpret_cast<const float4 *>(W.f32 + (size_t)ea * W.H + kk);
+                vb[u] = *reinterpret_cast<const float4 *>(W.f32 + (size_t)eb * W.H + kk);
+            }
+            // keeps the loads above the skip test below (otherwise each is
+            // sunk into its step's branch and waited for there)
+#pragma unroll
+            for (int u = 0; u < RB; u++)
+                asm volatile("" : "+v"(xv[u].x), "+v"(xv[u].y), "+v"(xv[u].z), "+v"(xv[u].w),
+                                  "+v"(va[u].x), "+v"(va[u].y), "+v"(va[u].z), "+v"(va[u].w),
+                                  "+v"(vb[u].x), "+v"(vb[u].y), "+v"(vb[u].z), "+v"(vb[u].w));
+#pragma unroll
+            for (int u = 0; u < RB; u++) {
+                if (k + 64 * u >= kb) break;
+                const double wa[4] = {(double)va[u].x * za, (double)va[u].y * za, (double)va[u].z * za,
+                                      (double)va[u].w * za};
+                const double wb[4] = {(double)vb[u].x * zb, (double)vb[u].y * zb, (double)vb[u].z * zb,
+                                      (double)vb[u].w * zb};
+                step(xv[u], wa, wb);
+            }
+        }
+    } else {
+        for (; k < kb; k += 64) {
+            const int kk = k + 4 * kq;
+            const float4 xv = *reinterpret_cast<const float4 *>(xr + kk);
+            double wa[4], wb[4];
+            W.at4(e0 + r16, kk, Q8, wa);
+            W.at4(e0 + 16 + r16, kk, Q8, wb);
+            step(xv, wa, wb);
         }
     }
 #pragma unroll
