@@ -125,10 +125,20 @@ __device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int 
         b.a[m][0] = *reinterpret_cast<const float4 *>(s.abase + (size_t)(s.arow[m] + ak));
         b.a[m][1] = *reinterpret_cast<const float4 *>(s.abase + (size_t)(s.arow[m] + ak + 16));
     }
+    // one row tile per expert (MF == 1: at most 16 rows on average) reads
+    // every weight byte once, so those loads are non-temporal; with more
+    // rows the expert's other row tiles read the same bytes through the L2
 #pragma unroll
     for (int j = 0; j < ST_NF; j++) {
         const uint32_t c = (uint32_t)min(s.cb[j >> 2] + 16 * (j & 3), s.cmax);
-        b.q[j] = *reinterpret_cast<const uint2 *>(s.qb[j >> 2] + (size_t)(qk + c * QK + s.qk));
+        const uint2 *src = reinterpret_cast<const uint2 *>(s.qb[j >> 2] + (size_t)(qk + c * QK + s.qk));
+        if constexpr (MF == 1) {
+            typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+            const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(src));
+            b.q[j] = make_uint2(v.x, v.y);
+        } else {
+            b.q[j] = *src;
+        }
     }
 #pragma unroll
     for (int h = 0; h < 2; h++)
