@@ -94,6 +94,16 @@ __device__ __forceinline__ float lm_block_max(float v, float *red)
 }
 
 // First row of matrix `mat` owned by row group g (RPW rows) of this workgroup.
+// 16 weight bytes read once per token: a non-temporal load, so the weight
+// stream does not evict the activations, caches and state other launches
+// read again
+__device__ __forceinline__ uint4 load_nt16(const int8_t *p)
+{
+    typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+    const v4u v = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 template <int MODE, int G, int RPW>
 __device__ __forceinline__ int lm_row(const LmArgs &a, int g, int &mat)
 {
@@ -196,7 +206,7 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
         for (int u = 0; u < NBW; u++) {
             const int b = min(c0 + first + BPR * u, a.nb - 1);
             const size_t o = bm_index(0, a.nb, b, M.rows, rc);
-            q[u] = *reinterpret_cast<const uint4 *>(M.qs + o * QK + 16 * h);
+            q[u] = load_nt16(M.qs + o * QK + 16 * h);
             dd[u] = __half2float(M.dcm[(size_t)rc * M.nbp + b]);
         }
     };
