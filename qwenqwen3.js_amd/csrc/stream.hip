@@ -239,6 +239,23 @@ __device__ __forceinline__ float wave_order_sum(const float (*red)[16][65], int 
 // LDS: the cross-wave reduction tiles only
 constexpr int ST_LDS = 2 * 4 * 16 * 65 * 4;
 
+// blockIdx -> (row tile, column group): the dispatcher deals workgroups to
+// the 8 XCDs round robin (XCD x runs blocks x, x+8, ...), and each XCD takes
+// a contiguous run of the real items, row-tile major, so the column groups
+// of a row tile read its activation rows through one L2.  False once past
+// the real items.
+__device__ __forceinline__ bool st_item(int n_tiles, int ncg, int &tile, int &cg)
+{
+    const int R = n_tiles * ncg;
+    const int per = (R + 7) >> 3;
+    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
+    const int w = x * per + i;
+    if (i >= per || w >= R) return false;
+    tile = w / ncg;
+    cg = w - tile * ncg;
+    return true;
+}
+
 // ---------------------------------------------------------------------------
 // gate/up: column half 0 = gate features f0 .. f0+63, half 1 = the same up
 // features.
@@ -248,8 +265,8 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 {
     __shared__ __align__(16) char lds[ST_LDS];
     const int ncg = (a.F + 63) / 64;
-    const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
-    if (tile >= *a.n_tiles) return;
+    int tile, cg;
+    if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
     const int n = min(16 * MF, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
@@ -305,8 +322,8 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
 {
     __shared__ __align__(16) char lds[ST_LDS];
     const int ncg = (a.H + 127) / 128;
-    const int tile = blockIdx.x / ncg, cg = blockIdx.x - tile * ncg;
-    if (tile >= *a.n_tiles) return;
+    int tile, cg;
+    if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
     const int n = min(16 * MF, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
@@ -410,8 +427,9 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.nbH = m->H / QK;
     a.nbF = m->F / QK;
 
-    const unsigned g1 = (unsigned)cap * ((m->F + 63) / 64);
-    const unsigned g2 = (unsigned)cap * ((m->H + 127) / 128);
+    // XCD-aware grids (st_item): 8 * ceil(items / 8) workgroups at most
+    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 63) / 64) + 7) / 8);
+    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8);
     prof_begin(ctx, K_STREAM_GATEUP);
     if (MF == 1)
         QQ_LAUNCH(ctx, moe_stream_gateup_kernel<1>, dim3(g1), dim3(ST_THREADS), 0, a);
