@@ -586,9 +586,13 @@ static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         float *cp = probs ? probs + (size_t)t0 * m->E : nullptr;
         const float *cx = x + (size_t)t0 * m->H;
         float *ch = hidden + (size_t)t0 * m->H;
-        if ((rc = launch_router_topk(ctx, m, cx, tn, part, ci, cw, cp))) return rc;
-        switch (chunk_path(ctx, m, tn, cx)) {
-        case PATH_MFMA: rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
+        const Path path = chunk_path(ctx, m, tn, cx);
+        // on the MFMA path the router launch also writes the fp16 rows
+        void *xh = path == PATH_MFMA ? mfma_xh(m, tn, work) : nullptr;
+        bool xh_done = false;
+        if ((rc = launch_router_topk(ctx, m, cx, tn, part, ci, cw, cp, xh, &xh_done))) return rc;
+        switch (path) {
+        case PATH_MFMA: rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work, xh_done); break;
         case PATH_STREAM: rc = launch_moe_stream(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
         default: rc = launch_moe_grouped(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
         }

@@ -404,8 +404,17 @@ size_t mfma_work_bytes(const qq_moe *m, int T)
            al256(P * m->H * 2);
 }
 
+void *mfma_xh(const qq_moe *m, int T, char *work)
+{
+    const size_t P = (size_t)T * m->K;
+    const size_t cap = (size_t)tile_cap(m, T);
+    return work + al256((size_t)m->E * 4) + al256((size_t)(m->E + 1) * 4) + 2 * al256(P * 4) +
+           2 * al256(cap * 4) + 256;
+}
+
 int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                    const MaskBits &mask, const int32_t *idx, const double *w, char *work)
+                    const MaskBits &mask, const int32_t *idx, const double *w, char *work,
+                    bool x_cast)
 {
     const size_t P = (size_t)T * m->K;
     const int cap = tile_cap(m, T);
@@ -427,12 +436,15 @@ int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
     int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, tiles);
     if (rc) return rc;
 
-    const size_t n4 = (size_t)T * m->H / 4;
-    prof_begin(ctx, K_CAST_F16);
-    QQ_LAUNCH(ctx, cast_f16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
-              reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(xh), n4);
-    prof_end(ctx);
-    QQ_HIP(ctx, hipGetLastError());
+    if (static_cast<void *>(xh) != mfma_xh(m, T, work)) return set_error(ctx, "mfma: scratch layout");
+    if (!x_cast) {   // else the router launch stored the fp16 rows
+        const size_t n4 = (size_t)T * m->H / 4;
+        prof_begin(ctx, K_CAST_F16);
+        QQ_LAUNCH(ctx, cast_f16_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                  reinterpret_cast<const float4 *>(x), reinterpret_cast<uint2 *>(xh), n4);
+        prof_end(ctx);
+        QQ_HIP(ctx, hipGetLastError());
+    }
 
     MfmaArgs a;
     a.xh = xh;

@@ -209,8 +209,11 @@ int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x,
 // scratch at `part`), then top-K.
 constexpr int ROUTER_MAX_SPLIT = 8;
 size_t router_work_bytes(const qq_moe *m, int T);
+// With xh (T x H fp16) the F32 matrix-core router also stores x rounded to
+// fp16 there and sets *xh_done.
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
-                       int32_t *idx, double *w, float *probs);
+                       int32_t *idx, double *w, float *probs, void *xh = nullptr,
+                       bool *xh_done = nullptr);
 // Batch-1 decode in one launch (decode.hip); its exchange tables live in the
 // context's sync area, so it needs no scratch.
 bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T);
@@ -282,7 +285,11 @@ int launch_combine(qq_ctx *ctx, const qq_moe *m, int T, const void *y, bool y_f1
 bool mfma_supported(const qq_moe *m);
 size_t mfma_work_bytes(const qq_moe *m, int T);
 int launch_moe_mfma(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                    const MaskBits &mask, const int32_t *idx, const double *w, char *work);
+                    const MaskBits &mask, const int32_t *idx, const double *w, char *work,
+                    bool x_cast = false);
+// Where launch_moe_mfma keeps the fp16 activations in `work` (x_cast: the
+// router launch filled them).
+void *mfma_xh(const qq_moe *m, int T, char *work);
 // Split-fp16 MFMA kernels with weights streamed into registers, for decode
 // batches at fp32 accuracy (stream.hip); same shape needs as the MFMA path.
 size_t stream_work_bytes(const qq_moe *m, int T);

@@ -16,6 +16,7 @@
 namespace qq {
 
 typedef double d4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 
 // Router weight of expert e (F32: column e of [H, E] = E rows of H floats;
 // Q8_0: block-major panel, exactly dequantised).
@@ -65,7 +66,8 @@ struct RouterW {
 template <bool Q8>
 __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int T,
                                                           RouterW W, int kchunk,
-                                                          double *__restrict__ part)
+                                                          double *__restrict__ part,
+                                                          _Float16 *__restrict__ xh)
 {
     __shared__ double red[4][16][33];
     const int t0 = blockIdx.x * 16, ks = blockIdx.y, e0 = blockIdx.z * 32;
@@ -118,6 +120,14 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
                 const double wb[4] = {(double)vb[u].x * zb, (double)vb[u].y * zb, (double)vb[u].z * zb,
                                       (double)vb[u].w * zb};
                 step(xv[u], wa, wb);
+                // the fp16 copy of x for the prefill GEMMs (xh != nullptr):
+                // every (token, k) of the slice once, rounded to nearest even
+                if (xh && t < T && blockIdx.z == 0) {
+                    const h2_t lo = {(_Float16)xv[u].x, (_Float16)xv[u].y};
+                    const h2_t hi = {(_Float16)xv[u].z, (_Float16)xv[u].w};
+                    *reinterpret_cast<uint2 *>(xh + (size_t)t * W.H + k + 64 * u + 4 * kq) =
+                        make_uint2(__builtin_bit_cast(uint32_t, lo), __builtin_bit_cast(uint32_t, hi));
+                }
             }
         }
     } else {
@@ -260,8 +270,9 @@ size_t router_work_bytes(const qq_moe *m, int T)
 }
 
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
-                       int32_t *idx, double *w, float *probs)
+                       int32_t *idx, double *w, float *probs, void *xh, bool *xh_done)
 {
+    if (xh_done) *xh_done = false;
     if (T <= 0) return QQ_OK;
     const bool q8 = m->router_type == QQ_TYPE_Q8_0;
     RouterW W;
@@ -277,10 +288,13 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
     if (m->H % 16 == 0 && ((uintptr_t)x & 15) == 0) {
         const int kchunk = ((m->H + KS * 64 - 1) / (KS * 64)) * 64;
         const dim3 g((T + 15) / 16, KS, (m->E + 31) / 32);
-        if (q8)
-            QQ_LAUNCH(ctx, router_mfma_kernel<true>, g, dim3(256), 0, x, T, W, kchunk, part);
-        else
-            QQ_LAUNCH(ctx, router_mfma_kernel<false>, g, dim3(256), 0, x, T, W, kchunk, part);
+        if (q8) {
+            QQ_LAUNCH(ctx, router_mfma_kernel<true>, g, dim3(256), 0, x, T, W, kchunk, part, nullptr);
+        } else {
+            QQ_LAUNCH(ctx, router_mfma_kernel<false>, g, dim3(256), 0, x, T, W, kchunk, part,
+                      static_cast<_Float16 *>(xh));
+            if (xh && xh_done) *xh_done = true;
+        }
     } else {
         const dim3 g((T + 3) / 4, (m->E + 7) / 8);
         if (q8)
