@@ -57,7 +57,10 @@ typedef struct qq_lfm2_info {
 int qq_lfm2_create(qq_ctx *ctx, const qq_gguf *g, qq_lfm2 **out);
 int qq_lfm2_get_info(const qq_lfm2 *m, qq_lfm2_info *out);
 
-/* resetState (src/lfm2-engine.js:216-222): zero the KV cache and conv states. */
+/* resetState (src/lfm2-engine.js:216-222): zero the KV cache and conv states.
+ * Also required after a device-side wait on the context timed out (the
+ * forward calls fail with QQ_E_STATE until then: that call may have left the
+ * hidden row, conv states and KV cache half written). */
 int qq_lfm2_reset(qq_ctx *ctx, qq_lfm2 *m);
 
 /* forward(tokenId, position, skipLogits) (src/lfm2-engine.js:228-280) on

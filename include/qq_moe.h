@@ -34,6 +34,7 @@ extern "C" {
 #define QQ_E_HIP        -2   /* HIP runtime error                      */
 #define QQ_E_NODEV      -3   /* no usable gfx950 device                */
 #define QQ_E_NOMEM      -4   /* device or pinned allocation failed     */
+#define QQ_E_STATE      -5   /* device-resident state invalid: reset it */
 
 /* GGUF tensor type codes (src/gguf.js TENSOR_TYPES) accepted on this path. */
 #define QQ_TYPE_F32      0
@@ -197,10 +198,24 @@ int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, 
  * has, and the call's error surfaces at the next synchronising call as
  * QQ_E_HIP ("a device-side wait of the decode kernel timed out") rather
  * than the kernel waiting on.  0: a wait gives up at its first poll that
- * misses a word (for tests of that path).  Calls after a failed one draw a
- * fresh tag and are unaffected by it. */
+ * misses a word (for tests of that path).
+ * What a failed call leaves: each row of hidden holds either its value
+ * before the call or its correct new value (a workgroup writes its rows only
+ * when all of its waits succeeded); idx/w/probs are not valid.  When the
+ * error is read, the host moves the device epoch past every tag the failed
+ * launch can have written, so later calls are unaffected by it.  Device-
+ * resident state built across calls is invalid after such a call: an LFM2
+ * model's forward then fails with QQ_E_STATE until qq_lfm2_reset. */
 #define QQ_WAIT_LIMIT_US_DEFAULT 50000
 int qq_set_wait_limit(qq_ctx *ctx, int microseconds);
+
+/* Test hooks, no reference counterpart (they wait for the stream; not
+ * allowed while a capture is open): the device epoch that tags the decode
+ * kernel's exchange words (a call uses the tags after it and advances it),
+ * and a fill of every exchange table of the context with words carrying
+ * `tag`, standing for what a workgroup of a failed call may have left. */
+int qq_debug_epoch(qq_ctx *ctx, uint32_t *epoch);
+int qq_debug_plant_words(qq_ctx *ctx, uint32_t tag);
 
 /* Token batches (T > 1) of at least `tokens` rows per chunk run their expert
  * products as fp16 MFMA grouped GEMMs (fp16 activations and dequantised

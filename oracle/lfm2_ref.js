@@ -219,7 +219,7 @@ function attention(m, L, pos) {
             for (let d = 0; d < hd; d++) dot += q[h * hd + d] * m.kCache[lay + (g * C + p) * hd + d];
             sc[h * n + p] = dot * scale;
         }
-        M.softmaxInPlace(sc, h * n, (h + 1) * n);
+        M.softmaxF32(sc, h * n, (h + 1) * n);
         for (let p = 0; p < n; p++) {
             const w = sc[h * n + p];
             if (w === 0) continue;

@@ -13,7 +13,7 @@
 //   siluInPlace / mulInPlace / addVec   src/tensor.js:167-185
 //   _expertSlice    src/lfm2-engine.js:489-505
 //   _moEFFN         src/lfm2-engine.js:413-487 (sigmoid + expert bias gating)
-//   softmaxInPlace  src/tensor.js:150-164
+//   softmaxF32      src/tensor.js:150-164 (softmaxInPlace)
 //   Qwen3 _moEFFN   src/qwen3-engine.js:304-363 (softmax gating, no bias)
 // Node 12 has no DataView.getFloat16, so binary16 is decoded in closed form.
 //
@@ -167,16 +167,22 @@ function moEFFN(eng, layerIdx, layer) {
     addVec(eng.bufHidden, eng.bufMoEOut);
 }
 
-function softmaxInPlace(arr, start, end) {
-    let maxVal = arr[start];
-    for (let i = start + 1; i < end; i++) if (arr[i] > maxVal) maxVal = arr[i];
-    let sumExp = 0;
-    for (let i = start; i < end; i++) {
-        arr[i] = Math.exp(arr[i] - maxVal);
-        sumExp += arr[i];
+// Normalised exponentials of the fp32 row[lo, hi), in place, with the float
+// operations of src/tensor.js:150-164 in the same order: the shift is the
+// first largest entry (a strict compare); each exponential is taken in
+// binary64 of (entry - shift), stored back to fp32, and the stored values
+// are summed in binary64 in index order; one binary64 reciprocal of the
+// sum; every entry times it, stored to fp32.
+function softmaxF32(row, lo, hi) {
+    let peak = row[lo];
+    for (let j = lo + 1; j < hi; j++) peak = row[j] > peak ? row[j] : peak;
+    let total = 0;
+    for (let j = lo; j < hi; j++) {
+        row[j] = Math.exp(row[j] - peak);   // the store rounds to fp32 ...
+        total += row[j];                    // ... and the sum takes the stored value
     }
-    const invSum = 1.0 / sumExp;
-    for (let i = start; i < end; i++) arr[i] *= invSum;
+    const scale = 1.0 / total;
+    for (let j = lo; j < hi; j++) row[j] = row[j] * scale;
 }
 
 // The Qwen3-MoE block: softmax over the router logits, top-K by probability,
@@ -185,7 +191,7 @@ function softmaxInPlace(arr, start, end) {
 function moEFFNSoftmax(eng, layerIdx, layer) {
     const K = layer.nExpertsUsed;
     const probs = matmulGeneric(layer.routerWeight, eng.bufNormed);
-    softmaxInPlace(probs, 0, probs.length);
+    softmaxF32(probs, 0, probs.length);
     const order = Array.from(probs).map(function (v, i) { return [v, i]; });
     order.sort(function (a, b) { return b[0] - a[0]; });
     const chosen = [], chosenP = [];
@@ -362,7 +368,7 @@ function benchMatvec(seconds) {
 }
 
 module.exports = { halfToNumber, matmulQ80xF32, matmulF32xF32, matmulGeneric, readWeightF32,
-                   siluInPlace, mulInPlace, addVec, expertSlice, moEFFN, softmaxInPlace,
+                   siluInPlace, mulInPlace, addVec, expertSlice, moEFFN, softmaxF32,
                    moEFFNSoftmax };
 
 if (require.main === module) {

@@ -14,6 +14,14 @@ namespace qq {
 
 static thread_local char g_init_err[512] = "";
 
+// 64-bit exchange words of a context's sync area, ahead of the error word
+// and the epoch.
+static size_t sync_table_words()
+{
+    return (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS +
+           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS;
+}
+
 int set_error(qq_ctx *ctx, const char *fmt, ...)
 {
     char *dst = ctx ? ctx->err : g_init_err;
@@ -115,6 +123,24 @@ static const char *const kKernelNames[K_COUNT] = {
     "rmsnorm", "lfm2_embed", "lfm2_matvec", "lfm2_attention",
 };
 
+// After a timed-out call: clear the error word and move the epoch on by
+// SYNC_EPOCH_SKIP, so no exchange word that call left behind carries a tag a
+// later call accepts.  (A workgroup of the failed launch that started after
+// workgroup 0 advanced the epoch used the next call's tags.)  The stream has
+// drained, so no workgroup of that launch still runs.
+__global__ void sync_recover_kernel(uint32_t *err, uint32_t *epoch)
+{
+    *err = 0;
+    *epoch = *epoch + SYNC_EPOCH_SKIP;
+}
+
+// Every exchange word of the context (test hook qq_debug_plant_words).
+__global__ void sync_plant_kernel(uint64_t *w, size_t n, uint64_t word)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        w[i] = word;
+}
+
 // Read and clear the device error word; non-zero means a bounded device-side
 // wait expired (the results of that call are not valid).
 int check_device_error(qq_ctx *ctx, bool staged)
@@ -129,7 +155,9 @@ int check_device_error(qq_ctx *ctx, bool staged)
     const uint32_t e = *word;
     if (e) {
         *word = 0;
-        QQ_HIP(ctx, hipMemsetAsync(ctx->sync_err, 0, 4, ctx->stream));
+        ctx->timeouts++;
+        hipLaunchKernelGGL(sync_recover_kernel, dim3(1), dim3(1), 0, ctx->stream, ctx->sync_err, ctx->sync_epoch);
+        QQ_HIP(ctx, hipGetLastError());
         QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
         snprintf(ctx->err, sizeof ctx->err, "a device-side wait of the decode kernel timed out (code %u)", e);
         return QQ_E_HIP;
@@ -261,10 +289,7 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "hipEventCreate");
     }
     void *sync = nullptr;
-    const size_t sync_words = (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS +
-                              (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS + 2 * (size_t)SYNC_H_WORDS +
-                              SYNC_P_WORDS + SYNC_ARRIVE_WORDS;
-    const size_t sync_bytes = sync_words * sizeof(uint64_t) + 512;
+    const size_t sync_bytes = sync_table_words() * sizeof(uint64_t) + 512;
     if ((e = hipMalloc(&sync, sync_bytes)) != hipSuccess || (e = hipMemset(sync, 0, sync_bytes)) != hipSuccess) {
         if (sync) (void)hipFree(sync);
         (void)hipEventDestroy(ctx->ev0);
@@ -796,6 +821,30 @@ int qq_set_wait_limit(qq_ctx *ctx, int microseconds)
     if (!ctx) return QQ_E_ARG;
     if (microseconds < 0) return set_error(ctx, "set_wait_limit: %d us < 0", microseconds);
     ctx->dec_wait_ticks = (uint64_t)microseconds * 100;   // the 100 MHz wall clock
+    return QQ_OK;
+}
+
+int qq_debug_epoch(qq_ctx *ctx, uint32_t *epoch)
+{
+    if (!ctx || !epoch) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_debug_epoch")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    QQ_HIP(ctx, hipMemcpy(epoch, ctx->sync_epoch, 4, hipMemcpyDeviceToHost));
+    return QQ_OK;
+}
+
+int qq_debug_plant_words(qq_ctx *ctx, uint32_t tag)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (int rc = no_capture(ctx, "qq_debug_plant_words")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    // 1e30f: a logit, h value, partial or row that a call accepted would show
+    const uint64_t word = ((uint64_t)tag << 32) | 0x7149f2cau;
+    const size_t n = sync_table_words();
+    hipLaunchKernelGGL(sync_plant_kernel, dim3(256), dim3(256), 0, ctx->stream, ctx->sync_slots, n, word);
+    QQ_HIP(ctx, hipGetLastError());
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
     return QQ_OK;
 }
 

@@ -73,6 +73,9 @@ struct qq_lfm2 {
     std::vector<void *> dev;
     std::vector<qq_tensor *> tens;
     std::vector<qq_moe *> moes;
+    // the context's timeout count when the conv states and KV cache were
+    // last cleared: a later timed-out call may have left them half written
+    uint64_t timeouts_at_reset = 0;
 };
 
 namespace {
@@ -419,6 +422,7 @@ int qq_lfm2_reset(qq_ctx *ctx, qq_lfm2 *m)
     if (!ctx) return QQ_E_ARG;
     if (!m) return set_error(ctx, "lfm2_reset: NULL model");
     QQ_HIP(ctx, hipSetDevice(ctx->device));
+    m->timeouts_at_reset = ctx->timeouts;
     int n_conv = 0;
     for (const LmLayer &L : m->layers) n_conv += L.rec ? 1 : 0;
     if (int rc = qq::launch_lfm2_zero(ctx, m->conv_state, (size_t)n_conv * m->conv_floats)) return rc;
@@ -436,6 +440,12 @@ static int lfm2_forward(qq_ctx *ctx, qq_lfm2 *m, int token, int position, float 
         return set_error(ctx, "lfm2_forward: token %d outside [0, %d)", token, I.n_vocab);
     if (position < 0 || position >= I.max_ctx)
         return set_error(ctx, "lfm2_forward: position %d outside [0, %d)", position, I.max_ctx);
+    if (ctx->timeouts != m->timeouts_at_reset) {
+        set_error(ctx, "lfm2_forward: a device-side wait on this context timed out since the model's "
+                       "last reset, so its hidden row, conv states and KV cache are not valid: call "
+                       "qq_lfm2_reset first");
+        return QQ_E_STATE;
+    }
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     const int H = I.n_embd;
     if (int rc = qq::launch_lfm2_embed(ctx, m->embd, token, m->hidden)) return rc;

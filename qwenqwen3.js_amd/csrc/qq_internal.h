@@ -36,6 +36,11 @@ static_assert(SYNC_REPLICA_WORDS >= 2 * MAX_E, "slot table");
 constexpr int SYNC_H_WORDS = MAX_K * 4096;
 constexpr int SYNC_P_WORDS = 8 * MAX_K * 2048;
 constexpr int SYNC_ARRIVE_WORDS = 256;
+// After a timed-out call the host moves the epoch on by this much: a
+// workgroup of that call that started after workgroup 0 advanced the epoch
+// wrote words tagged with the next call's tags (up to twice the call's layer
+// count past the old epoch), which the next call must not accept.
+constexpr uint32_t SYNC_EPOCH_SKIP = 1024;
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
 struct MaskBits {
@@ -122,6 +127,10 @@ struct qq_ctx {
     uint64_t dec_wait_ticks;
     uint32_t *sync_epoch;
     uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive;
+    // device-side waits that timed out on this context so far (counted when
+    // the error word is read); device-resident state built across calls (an
+    // LFM2 model's conv states and KV cache) is invalid after one
+    uint64_t timeouts;
     // a graph capture on `stream` is open (qq_capture_begin)
     int capturing;
     // token batches of at least this many rows take the fp16 MFMA path (0: never)

@@ -115,6 +115,19 @@ class MoEDevice {
         // whose _gpu is this device
         const dev = this;
         this.device = { queue: { writeBuffer: function (buf, off, data) { dev.writeBuffer(buf, off, data); } } };
+        // device-side waits reported as timed out by this device's synchronising
+        // calls: an engine whose residual stream lives here is invalid after one
+        this.timeouts = 0;
+    }
+
+    // A synchronising native call; counts a reported device-side timeout.
+    _sync(f) {
+        try {
+            return f();
+        } catch (e) {
+            if (/timed out/.test(String(e && e.message))) this.timeouts++;
+            throw e;
+        }
     }
 
     // ---- device buffers: GPUDevice.createBuffer / uploadBuffer / readF32 ----
@@ -134,14 +147,16 @@ class MoEDevice {
 
     writeBuffer(buf, byteOffset, data) {
         this._own(buf, 'writeBuffer');
-        this.native.bufWrite(this.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), data);
+        const dev = this;
+        this._sync(function () { dev.native.bufWrite(dev.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), data); });
     }
 
     // The values once the work enqueued before the call has run.
     readF32Sync(buf, nElems, byteOffset) {
         this._own(buf, 'readF32');
         const out = new Float32Array(nElems);
-        this.native.bufRead(this.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), out);
+        const dev = this;
+        this._sync(function () { dev.native.bufRead(dev.ctx, buf.handle, buf.byteOffset + (byteOffset | 0), out); });
         return out;
     }
 
@@ -150,7 +165,10 @@ class MoEDevice {
         return new Promise(function (resolve) { resolve(dev.readF32Sync(buf, nElems)); });
     }
 
-    synchronize() { this.native.synchronize(this.ctx); }
+    synchronize() {
+        const dev = this;
+        this._sync(function () { dev.native.synchronize(dev.ctx); });
+    }
 
     _own(buf, what) {
         if (!(buf instanceof DeviceBuffer) || buf.device !== this || !buf.handle)
@@ -212,6 +230,13 @@ class MoEDevice {
     // host round trip, as in the reference.  expertMask is honoured when set
     // (the WebGPU engines keep it null).
     moEFFNGPU(eng, layerIdx, gl, cl, gating) {
+        // A timed-out call leaves each row of _buf.hidden old or new, and the
+        // engine's other state past that point: refuse until the engine's
+        // state is reset (_resetGPUState / resetKVCache, src/webgpu.js:2119)
+        if (eng._qqTimeouts === undefined) eng._qqTimeouts = this.timeouts;
+        if (eng._qqTimeouts !== this.timeouts)
+            throw new Error('_moEFFNGPU: a device-side wait timed out since the engine\'s state was last ' +
+                            'reset, so its residual stream is not valid: call resetKVCache() first');
         const d = engineDims(eng);
         const moeIdx = gl && gl._moeIdx !== undefined ? gl._moeIdx : layerIdx;
         if (!eng._gpuRoutingBufs) eng._gpuRoutingBufs = [];
@@ -493,6 +518,14 @@ function install(scope, opts) {
         const cls = scope[c[0]];
         if (!cls || !cls.prototype) return;
         const P = cls.prototype, block = P._moEFFNGPU, readback = P._readbackRoutingData;
+        const reset = P._resetGPUState;
+        if (reset) {
+            P._resetGPUState = function () {
+                const r = reset.apply(this, arguments);
+                if (dev.ownsEngine(this)) this._qqTimeouts = dev.timeouts;
+                return r;
+            };
+        }
         P._moEFFNGPU = function (layerIdx, gl, cl) {
             if (dev.ownsEngine(this)) return dev.moEFFNGPU(this, layerIdx, gl, cl, c[1]);
             if (block) return block.call(this, layerIdx, gl, cl);

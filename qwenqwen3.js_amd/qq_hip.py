@@ -31,7 +31,7 @@ EXPORTS = (
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
     "qq_moe_forward_norm_dev", "qq_moe_forward_noalloc_dev", "qq_moe_set_gating",
-    "qq_set_mfma_min_tokens", "qq_set_wait_limit", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
+    "qq_set_mfma_min_tokens", "qq_set_wait_limit", "qq_debug_epoch", "qq_debug_plant_words", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
     "qq_buffer_alloc", "qq_buffer_free", "qq_buffer_write", "qq_buffer_read", "qq_moe_forward_record_dev",
@@ -111,6 +111,8 @@ def load():
         "qq_moe_set_gating": (I, [P, P, I]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
         "qq_set_wait_limit": (I, [P, I]),
+        "qq_debug_epoch": (I, [P, ctypes.POINTER(ctypes.c_uint32)]),
+        "qq_debug_plant_words": (I, [P, ctypes.c_uint32]),
         "qq_rmsnorm_dev": (I, [P, P, P, P, I, I, ctypes.c_double]),
         "qq_timer_start": (I, [P]),
         "qq_timer_stop": (I, [P, ctypes.POINTER(ctypes.c_float)]),
@@ -253,6 +255,16 @@ class Context:
     def set_wait_limit(self, microseconds):
         """Bound on the decode kernel's device-side waits (qq_set_wait_limit)."""
         self.check(self.L.qq_set_wait_limit(self.h, int(microseconds)), "qq_set_wait_limit")
+
+    def debug_epoch(self):
+        """The device epoch of the decode exchange tags (qq_debug_epoch)."""
+        v = ctypes.c_uint32()
+        self.check(self.L.qq_debug_epoch(self.h, ctypes.byref(v)), "qq_debug_epoch")
+        return v.value
+
+    def debug_plant_words(self, tag):
+        """Fill every exchange table with words tagged `tag` (qq_debug_plant_words)."""
+        self.check(self.L.qq_debug_plant_words(self.h, int(tag) & 0xffffffff), "qq_debug_plant_words")
 
     def set_mfma_min_tokens(self, tokens):
         """Token batches of >= tokens rows use the fp16 MFMA path (0: never)."""
