@@ -620,12 +620,13 @@ def main():
         torch.cuda.synchronize()
 
         if stack:
+            moe_stack = ctx.moe_stack(keep)
+
             def step(i):
                 # one token (or chunk) through every layer: hidden += MoE(rmsnorm(hidden))
+                # (qq_moe_stack_forward_dev: one launch for a single token)
                 s = i % S
-                for li, layer in enumerate(keep):
-                    layer.forward_norm_dev(HID[s].data_ptr(), T, eps=1e-5,
-                                           idx_ptr=idx[s, li].data_ptr())
+                moe_stack.forward_dev(HID[s].data_ptr(), T, eps=1e-5, idx_ptr=idx[s].data_ptr())
         else:
             def step(i):
                 s = i % S
@@ -652,6 +653,9 @@ def main():
                   "layer_instances": n_layers, "distinct_experts_per_layer_call": round(n_exp, 2)}
         if stack:
             config["per_layer"] = "rmsnorm(hidden) -> MoE -> hidden +="
+            config["call"] = "qq_moe_stack_forward_dev (%s)" % (
+                "one launch for the 22 layers" if T == 1 else "layer after layer")
+            moe_stack.release()
         dtype = "f16" if dom in MFMA_KERNELS else "f32"
         lb = layer_bytes(T, n_exp) * calls
         extra["hbm_gbps_layer"] = round(lb / (ms_per_step * 1e6), 1)

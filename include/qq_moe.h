@@ -44,6 +44,7 @@ typedef struct qq_ctx qq_ctx;
 typedef struct qq_tensor qq_tensor;
 typedef struct qq_moe qq_moe;
 typedef struct qq_graph qq_graph;
+typedef struct qq_moe_stack qq_moe_stack;
 
 /* ---- context --------------------------------------------------------- */
 
@@ -159,6 +160,28 @@ int qq_moe_forward_noalloc_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev,
 int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev,
                             const float *norm_w_dev, double eps, int T, const uint8_t *mask,
                             int32_t *idx_dev, double *w_dev, float *probs_dev);
+
+/* ---- MoE stacks: a token through many layers in one launch ----------------
+ * Lfm2Engine.forward runs, per block, the FFN sub-block `x = rmsnorm(hidden)
+ * * ffn_norm; hidden += _moEFFN(x)` (src/lfm2-engine.js:232-258, :250-257),
+ * and the WebGPU engine records a token's blocks into one command encoder
+ * (src/webgpu.js:1954-2034).  A stack binds n MoE layers of equal shape,
+ * gating and router type (borrowed; they must outlive the stack), with their
+ * ffn_norm weights (norm_w_dev: n device pointers of H floats, entries or
+ * the whole array NULL for unit weights), 1 <= n <= 256. */
+int qq_moe_stack_create(qq_ctx *ctx, const qq_moe *const *layers, const float *const *norm_w_dev, int n,
+                        qq_moe_stack **out);
+int qq_moe_stack_release(qq_ctx *ctx, qq_moe_stack *s);
+/* For l = 0 .. n-1, on T rows: x = rmsnorm(hidden) * norm_w[l];
+ * hidden += MoE_l(x) -- qq_moe_forward_norm_dev layer after layer, with the
+ * same results.  Routing outputs of layer l at idx_dev + l*T*K,
+ * w_dev + l*T*K, probs_dev + l*T*E (each NULL or device memory).  A single
+ * row (T = 1) runs the whole stack in one launch of the decode kernel: the
+ * residual row passes from layer to layer inside the launch, and each
+ * layer's router rows are read while the previous layer's down weights
+ * stream in.  Device pointers; enqueued, not waited for. */
+int qq_moe_stack_forward_dev(qq_ctx *ctx, const qq_moe_stack *s, float *hidden_dev, double eps, int T,
+                             const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev);
 
 /* ---- The WebGPU engines' device-resident MoE block ------------------------
  * Lfm2GPUEngine and Qwen3GPUEngine keep the residual stream in device

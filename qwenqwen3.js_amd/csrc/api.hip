@@ -4,6 +4,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <new>
+#include <vector>
 
 // Scratch of qq_moe_forward_noalloc_dev: one array per GPU, held until the
 // process ends.  Host code reaches it only through the address that
@@ -19,7 +20,7 @@ static thread_local char g_init_err[512] = "";
 static size_t sync_table_words()
 {
     return (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS +
-           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS;
+           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 2 * (size_t)SYNC_X_WORDS;
 }
 
 int set_error(qq_ctx *ctx, const char *fmt, ...)
@@ -304,8 +305,9 @@ int qq_init(int device, qq_ctx **out)
     ctx->sync_hdev = ctx->sync_hloc + SYNC_H_WORDS;
     ctx->sync_part = ctx->sync_hdev + SYNC_H_WORDS;
     ctx->sync_arrive = ctx->sync_part + SYNC_P_WORDS;
+    ctx->sync_hx = ctx->sync_arrive + SYNC_ARRIVE_WORDS;
     // error word and epoch each on a 128-byte line of their own
-    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_arrive + SYNC_ARRIVE_WORDS);
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_hx + 2 * SYNC_X_WORDS);
     ctx->sync_epoch = ctx->sync_err + 32;
     ctx->capturing = 0;
     *out = ctx;
@@ -693,6 +695,82 @@ int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev, con
     float *x = static_cast<float *>(ctx->scratch);
     if ((rc = launch_rmsnorm(ctx, hidden_dev, norm_w_dev, x, T, m->H, eps))) return rc;
     return forward_impl(ctx, m, x, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, xb);
+}
+
+// ---- MoE stacks ------------------------------------------------------------
+
+int qq_moe_stack_create(qq_ctx *ctx, const qq_moe *const *layers, const float *const *norm_w_dev, int n,
+                        qq_moe_stack **out)
+{
+    if (!ctx || !out) return QQ_E_ARG;
+    *out = nullptr;
+    if (int rc = no_capture(ctx, "qq_moe_stack_create")) return rc;
+    if (!layers || n < 1 || n > STACK_MAX_LAYERS)
+        return set_error(ctx, "moe_stack_create: %d layers (1 .. %d)", n, STACK_MAX_LAYERS);
+    const qq_moe *m0 = layers[0];
+    for (int l = 0; l < n; l++) {
+        const qq_moe *m = layers[l];
+        if (!m) return set_error(ctx, "moe_stack_create: layer %d is NULL", l);
+        if (m->H != m0->H || m->F != m0->F || m->E != m0->E || m->K != m0->K || m->gating != m0->gating ||
+            m->router_type != m0->router_type)
+            return set_error(ctx, "moe_stack_create: layer %d differs from layer 0 in shape, gating or router type", l);
+    }
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    qq_moe_stack *st = new (std::nothrow) qq_moe_stack();
+    if (!st) return set_error(ctx, "host allocation failed");
+    st->n = n;
+    st->layers.assign(layers, layers + n);
+    st->norm_w.assign((size_t)n, nullptr);
+    if (norm_w_dev) st->norm_w.assign(norm_w_dev, norm_w_dev + n);
+    std::vector<DecodeLayer> table((size_t)n);
+    for (int l = 0; l < n; l++) table[l] = decode_layer_of(layers[l], st->norm_w[l]);
+    hipError_t e = hipMalloc(&st->table, sizeof(DecodeLayer) * n);
+    if (e == hipSuccess) e = hipMemcpy(st->table, table.data(), sizeof(DecodeLayer) * n, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (st->table) (void)hipFree(st->table);
+        delete st;
+        return check_hip(ctx, e, "moe_stack_create: layer table");
+    }
+    *out = st;
+    return QQ_OK;
+}
+
+int qq_moe_stack_release(qq_ctx *ctx, qq_moe_stack *st)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!st) return QQ_OK;
+    if (int rc = no_capture(ctx, "qq_moe_stack_release")) return rc;
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (st->table) (void)hipFree(st->table);
+    delete st;
+    return QQ_OK;
+}
+
+int qq_moe_stack_forward_dev(qq_ctx *ctx, const qq_moe_stack *st, float *hidden_dev, double eps, int T,
+                             const uint8_t *mask, int32_t *idx_dev, double *w_dev, float *probs_dev)
+{
+    if (!ctx) return QQ_E_ARG;
+    if (!st) return set_error(ctx, "moe_stack_forward: NULL stack");
+    if (T < 0) return set_error(ctx, "moe_stack_forward: T=%d", T);
+    if (T == 0) return QQ_OK;
+    if (!hidden_dev) return set_error(ctx, "moe_stack_forward: NULL buffer");
+    if (!(eps >= 0.0)) return set_error(ctx, "moe_stack_forward: eps %g", eps);
+    const qq_moe *m0 = st->layers[0];
+    QQ_HIP(ctx, hipSetDevice(ctx->device));
+    MaskBits mb;
+    if (int rc = mask_from_bytes(ctx, mask, m0->E, &mb)) return rc;
+    if (decode_supported(ctx, m0, T))   // one launch for the whole stack
+        return launch_moe_stack_decode(ctx, m0, st->table, st->n, hidden_dev, eps, mb, idx_dev, w_dev, probs_dev);
+    // layer by layer (routing outputs of layer l at l T K resp. l T E)
+    const size_t TK = (size_t)T * m0->K, TE = (size_t)T * m0->E;
+    for (int l = 0; l < st->n; l++) {
+        if (int rc = qq_moe_forward_norm_dev(ctx, st->layers[l], hidden_dev, st->norm_w[l], eps, T, mask,
+                                             idx_dev ? idx_dev + l * TK : nullptr, w_dev ? w_dev + l * TK : nullptr,
+                                             probs_dev ? probs_dev + l * TE : nullptr))
+            return rc;
+    }
+    return QQ_OK;
 }
 
 int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,

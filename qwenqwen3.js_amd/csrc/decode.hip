@@ -66,24 +66,16 @@ static_assert(DEC_THREADS == NORM_THREADS, "the decode kernel normalises like rm
 struct DecodeArgs {
     const float *x;       // the MoE input, or the residual row when norm
     int norm;             // x = rmsnorm(x) * norm_w is formed in every workgroup
-    const float *norm_w;  // NULL: unit weight
     double eps;
     float *hidden;
     int H, F, E, K;
     int nbH, nbF;
-    const float *rf32;    // F32 router [E][H], or
-    const int8_t *rq;     // Q8_0 router (block-major)
-    const __half *rd;
     int router_q8;
     int softmax;          // Qwen3-MoE gating
-    const float *bias;
-    const int8_t *gq;
-    const __half *gdcm;   // gate/up scales row by row (qq_tensor.dcm), nbpH per row
-    const int8_t *uq;
-    const __half *udcm;
     int nbpH;
-    const int8_t *dq;
-    const __half *dd;     // down scales, block-major
+    int L;                // layers of a stack launch (1 otherwise)
+    DecodeLayer one;      // the layer of a single-layer launch
+    const DecodeLayer *layers;   // [L]: the layers of a stack launch
     MaskBits mask;
     uint32_t *epoch_word;
     // exchange tables (tag << 32 | bits):
@@ -93,13 +85,31 @@ struct DecodeArgs {
     uint64_t *hdev;       // device-coherent copy
     uint64_t *part;       // partial down sums [8][K][H], device-coherent
     uint64_t *arrive;     // [G]
-    int32_t *out_idx;     // optional outputs
+    uint64_t *hx;         // stack: the residual row after layer l in table l % 2 [2][SYNC_X_WORDS]
+    int32_t *out_idx;     // optional outputs (a stack's: layer l at l K, l K, l E)
     double *out_w;
     float *out_probs;
     float *out_rec;       // [K idx as float | K w rounded to fp32 | E probs]
     uint32_t *err;
     uint64_t wait_ticks;  // bound on every device-side wait (100 MHz wall clock)
 };
+
+// A pointer read from memory (a stack's layer table) has no known address
+// space: loads through it compile to flat loads, which also count in lgkmcnt,
+// so every LDS barrier would wait for the whole weight stream.  Typed as a
+// global-memory pointer at the table, loads through it are global loads.
+#if defined(__HIP_DEVICE_COMPILE__)
+template <typename T>
+using gptr = T __attribute__((address_space(1))) *;
+#else
+template <typename T>
+using gptr = T *;
+#endif
+template <typename T>
+__device__ __forceinline__ gptr<T> as_global(T *p)
+{
+    return (gptr<T>)p;
+}
 
 __device__ __forceinline__ uint64_t tag_word(uint32_t tag, float v)
 {
@@ -117,7 +127,7 @@ __device__ __forceinline__ void store_dev(uint64_t *p, uint64_t v)
 }
 
 // Bounded wait of the first NT threads for their words: thread t polls the
-// words of its items s < IPT with want[s] (loads issued together, each wave
+// words of its items s < IPT with want[s] for tag[s] (loads issued together, each wave
 // on its own with wave votes), at pl[s] -- its group's table -- and after
 // DEC_LOCAL_TICKS at pd[s], the device-coherent copy (pd[s] = pl[s] when
 // there is none).  Once a word carries `tag` its low half goes to *dst[s]
@@ -127,11 +137,13 @@ __device__ __forceinline__ void store_dev(uint64_t *p, uint64_t v)
 // counter as loads here, so a wave that has just written device-scope words
 // would wait for their acknowledgement before every poll: the waves that
 // publish are kept out of the waits that follow.)  Returns false (in every
-// thread) when some wave's wait expired.
+// thread) when some wave's wait expired, or -- once a wait has run past
+// DEC_LOCAL_TICKS -- when the error word says another workgroup gave up (its
+// words will not come, so the failure spreads in ~10 us instead of a bound).
 template <int NT, int IPT>
-__device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uint64_t *(&pl)[IPT],
+__device__ __forceinline__ bool block_wait(const uint32_t (&tag)[IPT], int *sh_fail, const uint64_t *(&pl)[IPT],
                                            const uint64_t *(&pd)[IPT], bool (&want)[IPT],
-                                           float *(&dst)[IPT], uint64_t wait_ticks)
+                                           float *(&dst)[IPT], uint64_t wait_ticks, const uint32_t *err)
 {
     bool fail = false;
     if ((int)threadIdx.x < NT) {
@@ -147,7 +159,7 @@ __device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uin
 #pragma unroll
             for (int s = 0; s < IPT; s++) {
                 if (!want[s]) continue;
-                if ((uint32_t)(v[s] >> 32) == tag) {
+                if ((uint32_t)(v[s] >> 32) == tag[s]) {
                     want[s] = false;
                     if (dst[s]) *dst[s] = __uint_as_float((uint32_t)v[s]);
                 } else {
@@ -156,11 +168,12 @@ __device__ __forceinline__ bool block_wait(uint32_t tag, int *sh_fail, const uin
             }
             if (__all(mine)) break;
             const uint64_t dt = wall_clock64() - t0;
-            if (dt > DEC_LOCAL_TICKS) loc = false;
-            if (dt >= wait_ticks) {
+            if (dt >= wait_ticks ||
+                (dt > DEC_LOCAL_TICKS && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
                 fail = true;
                 break;
             }
+            if (dt > DEC_LOCAL_TICKS) loc = false;
             __builtin_amdgcn_s_sleep(1);
         }
     }
@@ -214,10 +227,10 @@ __device__ __forceinline__ float lev3_sum(const mf_v16i c)
 
 // 16 weight bytes read once per call: a non-temporal load, so the stream of
 // expert weights does not push the exchange tables and activations out of L2.
-__device__ __forceinline__ int4 load_stream16(const int8_t *p)
+__device__ __forceinline__ int4 load_stream16(gptr<const int8_t> p)
 {
     typedef int v4i __attribute__((ext_vector_type(4)));
-    const v4i v = __builtin_nontemporal_load(reinterpret_cast<const v4i *>(p));
+    const v4i v = __builtin_nontemporal_load((gptr<const v4i>)p);
     return make_int4(v.x, v.y, v.z, v.w);
 }
 
@@ -233,18 +246,18 @@ __device__ __forceinline__ int div_small(int q, float inv_d) { return (int)(((fl
 template <int NBW>
 struct ScaleRun {
     uint32_t s[(NBW + 1) / 2];
-    __device__ __forceinline__ void load(const __half *p)
+    __device__ __forceinline__ void load(gptr<const __half> p)
     {
         if constexpr (NBW == 8) {
-            const uint4 v = *reinterpret_cast<const uint4 *>(p);
+            const uint4 v = *(gptr<const uint4>)p;
             s[0] = v.x; s[1] = v.y; s[2] = v.z; s[3] = v.w;
         } else if constexpr (NBW == 4) {
-            const uint2 v = *reinterpret_cast<const uint2 *>(p);
+            const uint2 v = *(gptr<const uint2>)p;
             s[0] = v.x; s[1] = v.y;
         } else if constexpr (NBW == 2) {
-            s[0] = *reinterpret_cast<const uint32_t *>(p);
+            s[0] = *(gptr<const uint32_t>)p;
         } else {
-            s[0] = *reinterpret_cast<const uint16_t *>(p);
+            s[0] = *(gptr<const uint16_t>)p;
         }
     }
     __device__ __forceinline__ float get(int i) const { return f16_bits(s[i / 2] >> (16 * (i % 2))); }
@@ -256,8 +269,23 @@ constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read b
 
 // NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
 // experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64));
-// PP2: a wave takes two (rank, row half) pairs of down rows (K x halves > 8).
-template <int NBW, int RE, int EPL, bool PP2>
+// PP2: a wave takes two (rank, row half) pairs of down rows (K x halves > 8);
+// STACK: the launch runs a.L layers (ffn_norm folded in) on one residual row.
+//
+// Stack launches.  Layer l uses tag epoch + 1 + l.  After the combine of
+// layer l a workgroup publishes its rows of the new residual as tagged words
+// in table l % 2 of a.hx (device-coherent) instead of writing hidden, and
+// layer l + 1 starts with every workgroup waiting for all H of them; only the
+// last layer writes hidden.  Every exchange table can be reused layer after
+// layer: a workgroup can only publish layer l + 1 words once it holds the
+// whole residual after layer l, that is once every workgroup has finished
+// layer l and with it every wait on a layer-l word.  (The two hx tables keep
+// a layer-l + 1 row from overwriting a layer-l row some workgroup still
+// waits for.)  The arrival words are published at layer 0 and waited for
+// before the final write of hidden, which is the launch's input row.  The
+// next layer's router rows, bias and norm weights are loaded while the
+// current layer's down rows stream in.
+template <int NBW, int RE, int EPL, bool PP2, bool STACK>
 __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 {
     constexpr int XN = NBW * DEC_WAVES * QK;    // activations, zero padded
@@ -294,7 +322,12 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int gx = j % DEC_GROUPS;   // group (XCD)
     const int mi = j / DEC_GROUPS;   // member
     const int M = G / DEC_GROUPS;
-    const uint16_t *dd16 = reinterpret_cast<const uint16_t *>(a.dd);
+    const int NL = STACK ? a.L : 1;
+
+    // a field of layer i (each read where it is used, so no layer's pointers
+    // are held in scalar registers across the layer)
+#define LAYER(i, f) as_global(STACK ? as_global(A.layers)[i].f : A.one.f)
+#define LAYER0(f) as_global(STACK ? as_global(a.layers)[0].f : a.one.f)
 
     // ---- every load of the routing phase, unconditional (clamped addresses) ----
     const uint32_t epoch = __hip_atomic_load(a.epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -302,14 +335,16 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int RF = (a.H + G - 1) / G;
     const int q0 = j * RF;
     const int RFm = max(min(RF, a.H - q0), 0);
-    const float hin = a.hidden[min(q0 + tid, a.H - 1)];
+    float hin = a.hidden[min(q0 + tid, a.H - 1)];
     float xv[XPT], wv[XPT];
-    const float *nw = a.norm_w ? a.norm_w : a.x;
+    {
+        const gptr<const float> nw = LAYER0(norm_w) ? LAYER0(norm_w) : as_global(a.x);
 #pragma unroll
-    for (int s = 0; s < XPT; s++) {
-        const int k = min(tid + DEC_THREADS * s, a.H - 1);
-        xv[s] = a.x[k];
-        wv[s] = nw[k];
+        for (int s = 0; s < XPT; s++) {
+            const int k = min(tid + DEC_THREADS * s, a.H - 1);
+            xv[s] = a.x[k];
+            wv[s] = nw[k];
+        }
     }
     // router rows of this member's experts e = mi + M t (F32 router)
     float rw[RE][XPT];
@@ -319,26 +354,72 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const int e = min(mi + M * t, a.E - 1);
 #pragma unroll
             for (int s = 0; s < XPT; s++)
-                rw[t][s] = a.rf32[(size_t)e * a.H + min(tid + DEC_THREADS * s, a.H - 1)];
+                rw[t][s] = LAYER0(rf32)[(size_t)e * a.H + min(tid + DEC_THREADS * s, a.H - 1)];
         }
     }
     // selection bias of experts lane, lane + 64, ...
     float bias_l[EPL];
 #pragma unroll
-    for (int t = 0; t < EPL; t++) bias_l[t] = a.bias[min(lane + WAVE * t, a.E - 1)];
+    for (int t = 0; t < EPL; t++) bias_l[t] = LAYER0(bias)[min(lane + WAVE * t, a.E - 1)];
 #pragma unroll
     for (int s = 0; s < XPT; s++) {
         const bool in = tid + DEC_THREADS * s < a.H;
         xv[s] = in ? xv[s] : 0.0f;
-        wv[s] = (in && a.norm_w) ? wv[s] : 1.0f;
+        wv[s] = (in && LAYER0(norm_w)) ? wv[s] : 1.0f;
+    }
+    if (tid == 0) {
+        sh_tag = epoch + 1u;
+        sh_fail = 0;
+    }
+    lds_barrier();
+    const uint32_t tag0 = sh_tag;
+    bool ok = true;
+    constexpr int PUB = (DEC_WAVES - 1) * WAVE;
+
+#define A a
+    for (int l = 0; l < NL; l++) {
+    // The index work of a layer is the same for every layer; computed from
+    // opaque copies of the ids it stays inside the loop instead of being
+    // hoisted out of it and held, spilled, across all the layers.
+    int tid = threadIdx.x, j = blockIdx.x;
+    asm volatile("" : "+v"(tid), "+s"(j));
+    const int lane = tid & (WAVE - 1);
+    const int wave = tid / WAVE;
+    const int gx = j % DEC_GROUPS;
+    const int mi = j / DEC_GROUPS;
+    const uint32_t tag = tag0 + (uint32_t)l;
+    const bool last = l == NL - 1;
+    if (STACK && l > 0) {
+        // ---- the residual row after layer l - 1, from every workgroup ----
+        const uint64_t *pl[XPT];
+        bool want[XPT];
+        float *dst[XPT];
+        const uint64_t *hxp = A.hx + (size_t)((l - 1) & 1) * SYNC_X_WORDS;
+#pragma unroll
+        for (int s = 0; s < XPT; s++) {
+            const int k = tid + DEC_THREADS * s;
+            pl[s] = hxp + min(k, A.H - 1);
+            want[s] = k < A.H;
+            dst[s] = &xl[min(k, XN - 1)];
+        }
+        uint32_t tg[XPT];
+#pragma unroll
+        for (int s = 0; s < XPT; s++) tg[s] = tag - 1u;
+        ok = block_wait<DEC_THREADS, XPT>(tg, &sh_fail, pl, pl, want, dst, A.wait_ticks, A.err);
+        if (!ok) break;
+#pragma unroll
+        for (int s = 0; s < XPT; s++) {
+            const int k = tid + DEC_THREADS * s;
+            xv[s] = (k < A.H) ? xl[k] : 0.0f;
+        }
     }
 
     // ---- x -> LDS (ffn_norm first when asked: lfm2-engine.js:251-252) ----
-    if (a.norm) {
+    if (A.norm) {
         double ss = 0.0;   // padding adds exact zeros
 #pragma unroll
         for (int s = 0; s < XPT; s++) ss = fma((double)xv[s], (double)xv[s], ss);
-        const double inv = rms_inv(block_sum_f64<DEC_WAVES>(ss, nsum), a.H, a.eps);
+        const double inv = rms_inv(block_sum_f64<DEC_WAVES>(ss, nsum), A.H, A.eps);
 #pragma unroll
         for (int s = 0; s < XPT; s++) xv[s] = (float)((double)wv[s] * (double)xv[s] * inv);
     }
@@ -348,17 +429,17 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         if (k < XN) xl[k] = xv[s];
     }
     // ---- router dots (lfm2-engine.js:418, tensor.js:469-482): exact products, binary64 sums ----
-    const int re = (a.E > mi) ? (a.E - mi + M - 1) / M : 0;
+    const int re = (A.E > mi) ? (A.E - mi + M - 1) / M : 0;
 #pragma unroll
     for (int t = 0; t < RE; t++) {
         double acc = 0.0;
-        if (a.router_q8) {
-            const int e = min(mi + M * t, a.E - 1);
+        if (A.router_q8) {
+            const int e = min(mi + M * t, A.E - 1);
 #pragma unroll
             for (int s = 0; s < XPT; s++) {
-                const int k = min(tid + DEC_THREADS * s, a.H - 1);
-                const size_t o = bm_index(0, a.nbH, k >> 5, a.E, e);
-                acc = fma((double)xv[s], (double)a.rq[o * QK + (k & 31)] * (double)__half2float(a.rd[o]), acc);
+                const int k = min(tid + DEC_THREADS * s, A.H - 1);
+                const size_t o = bm_index(0, A.nbH, k >> 5, A.E, e);
+                acc = fma((double)xv[s], (double)LAYER(l, rq)[o * QK + (k & 31)] * (double)__half2float(LAYER(l, rd)[o]), acc);
             }
         } else {
 #pragma unroll
@@ -367,16 +448,12 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         acc = wave_sum_dpp(acc);
         if (lane == 0) rsum[t][wave] = acc;
     }
-    if (tid == 0) {
-        sh_tag = epoch + 1u;
-        sh_fail = 0;
-    }
+    // (the residual rows have arrived before the arrival word goes out)
+    asm volatile("" : "+v"(hin));
     lds_barrier();
-    const uint32_t tag = sh_tag;
-    // the last wave publishes (arrival: x and hidden have been read; the
-    // router logits); waves 0..3 poll
-    constexpr int PUB = (DEC_WAVES - 1) * WAVE;
-    if (tid == PUB) store_dev(&a.arrive[j], (uint64_t)tag << 32);
+    // the last wave publishes (arrival, at the first layer: x and hidden
+    // have been read; the router logits); waves 0..3 poll
+    if (l == 0 && tid == PUB) store_dev(&A.arrive[j], (uint64_t)tag << 32);
     if (tid >= PUB && tid - PUB < re) {
         const int t = tid - PUB;
         const int e = mi + M * t;
@@ -384,43 +461,45 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 #pragma unroll
         for (int w = 1; w < DEC_WAVES; w++) s = s + rsum[t][w];
         const uint64_t word = tag_word(tag, (float)s);
-        store_local(&a.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
+        store_local(&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
         if (gx == 0) {
 #pragma unroll
-            for (int c = 0; c < SYNC_REPLICAS; c++) store_dev(&a.rdev[(size_t)c * SYNC_REPLICA_WORDS + e], word);
+            for (int c = 0; c < SYNC_REPLICAS; c++) store_dev(&A.rdev[(size_t)c * SYNC_REPLICA_WORDS + e], word);
         }
     }
     // x -> three int8 levels for the MFMA products; the rows of zeros
     decompose32<XN>(xl, XN / QK, &xlev[0][0], xsig);
-    for (int i = tid; i < XN / 16; i += DEC_THREADS) reinterpret_cast<int4 *>(xlev[3])[i] = make_int4(0, 0, 0, 0);
-    for (int i = tid; i < (DEC_MAX_HW + 8 * QK) / 16; i += DEC_THREADS)
-        reinterpret_cast<int4 *>(hlev[3])[i] = make_int4(0, 0, 0, 0);
+    if (l == 0) {
+        for (int i = tid; i < XN / 16; i += DEC_THREADS) reinterpret_cast<int4 *>(xlev[3])[i] = make_int4(0, 0, 0, 0);
+        for (int i = tid; i < (DEC_MAX_HW + 8 * QK) / 16; i += DEC_THREADS)
+            reinterpret_cast<int4 *>(hlev[3])[i] = make_int4(0, 0, 0, 0);
+    }
 
-    bool ok;
     {
-        const uint64_t *pl[1] = {&a.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, a.E - 1)]};
-        const uint64_t *pd[1] = {&a.rdev[(size_t)(j % SYNC_REPLICAS) * SYNC_REPLICA_WORDS + min(tid, a.E - 1)]};
-        bool want[1] = {tid < a.E};
+        const uint64_t *pl[1] = {&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, A.E - 1)]};
+        const uint64_t *pd[1] = {&A.rdev[(size_t)(j % SYNC_REPLICAS) * SYNC_REPLICA_WORDS + min(tid, A.E - 1)]};
+        bool want[1] = {tid < A.E};
         float *dst[1] = {&sh_lg[min(tid, EPL * WAVE - 1)]};
-        ok = block_wait<4 * WAVE, 1>(tag, &sh_fail, pl, pd, want, dst, a.wait_ticks);
+        const uint32_t tg[1] = {tag};
+        ok = block_wait<4 * WAVE, 1>(tg, &sh_fail, pl, pd, want, dst, A.wait_ticks, A.err);
     }
 
     // ---- this workgroup's share (independent of the routing) ----
-    const int fb0 = gx * a.nbF / DEC_GROUPS, fb1 = (gx + 1) * a.nbF / DEC_GROUPS;
+    const int fb0 = gx * A.nbF / DEC_GROUPS, fb1 = (gx + 1) * A.nbF / DEC_GROUPS;
     const int FRb = fb1 - fb0;                        // F blocks of the group (<= 8)
     const int f0 = fb0 * QK;
-    const int FR = max(min(fb1 * QK, a.F) - f0, 0);   // features of the group
+    const int FR = max(min(fb1 * QK, A.F) - f0, 0);   // features of the group
     const float inv_fr = 1.0f / (float)max(FR, 1);
     const float inv_frb = 1.0f / (float)max(FRb, 1);
-    const int NC = a.K * FR;                          // its (rank, feature) columns
+    const int NC = A.K * FR;                          // its (rank, feature) columns
     const int CPM = (NC + M - 1) / M;
     const int c0 = mi * CPM;
     const int nc = max(min(CPM, NC - c0), 0);         // this member's columns (<= 32)
-    const int RM = (a.H + M - 1) / M;                 // down rows per member (<= 64)
+    const int RM = (A.H + M - 1) / M;                 // down rows per member (<= 64)
     const int r0 = mi * RM;
-    const int RMm = max(min(RM, a.H - r0), 0);
+    const int RMm = max(min(RM, A.H - r0), 0);
     const int NRH = RM > 32 ? 2 : 1;                  // 32-row halves of the member's rows
-    const int NP2 = (FRb > 0 && RMm > 0) ? a.K * NRH : 0;   // (rank, row half) pairs
+    const int NP2 = (FRb > 0 && RMm > 0) ? A.K * NRH : 0;   // (rank, row half) pairs
     const int PPW = (NP2 + DEC_WAVES - 1) / DEC_WAVES;      // pairs per wave
     const int NUW = PPW * FRb;                               // down units per lane (<= 8)
     const int hh = lane >> 5;
@@ -433,14 +512,14 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int cf = (nc > 0) ? f0 + cl - ck * FR : 0;        // feature
     uint32_t goff[NBW];
 #pragma unroll
-    for (int i = 0; i < NBW; i++) goff[i] = (uint32_t)(min(NBW * wave + i, a.nbH - 1) * a.F + cf);
+    for (int i = 0; i < NBW; i++) goff[i] = (uint32_t)(min(NBW * wave + i, A.nbH - 1) * A.F + cf);
     // down: wave w takes the (rank, row half) pairs w, w + 8 over the group's
     // blocks, lane r + 32h row r of the half; row offsets within an expert
     int pk2[2];   // ranks of this wave's two pairs
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
-        pk2[t] = min((NRH == 2) ? (p >> 1) : p, a.K - 1);
+        pk2[t] = min((NRH == 2) ? (p >> 1) : p, A.K - 1);
     }
     uint32_t doff[DEC_DCH];
     bool dsec[DEC_DCH];   // unit of the second pair
@@ -453,7 +532,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const int p = min(wave + DEC_WAVES * t, max(NP2 - 1, 0));
         const int rh = (NRH == 2) ? (p & 1) : 0;
         const int rl = min(rh * 32 + cs, max(RMm - 1, 0));
-        doff[i] = (uint32_t)(min(fb0 + bl, a.nbF - 1) * a.H + min(r0 + rl, a.H - 1));
+        doff[i] = (uint32_t)(min(fb0 + bl, A.nbF - 1) * A.H + min(r0 + rl, A.H - 1));
         dsec[i] = t != 0;
         don[i] = i < NUW && wave + DEC_WAVES * t < NP2 && rh * 32 + cs < RMm;
         // one pair: the units' blocks are consecutive (immediate LDS offsets)
@@ -472,9 +551,9 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     if (ok && wave == 0) {
         float lg[EPL];
 #pragma unroll
-        for (int t = 0; t < EPL; t++) lg[t] = sh_lg[min(lane + WAVE * t, a.E - 1)];
-        if (a.softmax) {
-            softmax_probs<EPL>(lg, a.E, pr);
+        for (int t = 0; t < EPL; t++) lg[t] = sh_lg[min(lane + WAVE * t, A.E - 1)];
+        if (A.softmax) {
+            softmax_probs<EPL>(lg, A.E, pr);
         } else {
 #pragma unroll
             for (int t = 0; t < EPL; t++) pr[t] = (float)(1.0 / (1.0 + exp(-(double)lg[t])));
@@ -483,10 +562,10 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 #pragma unroll
         for (int t = 0; t < EPL; t++) {
             const int e = lane + WAVE * t;
-            const float sc = (a.softmax ? pr[t] : pr[t] + bias_l[t]) + 0.0f;   // -0 -> +0
+            const float sc = (A.softmax ? pr[t] : pr[t] + bias_l[t]) + 0.0f;   // -0 -> +0
             const uint32_t u = __float_as_uint(sc);
             const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-            key[t] = (e < a.E) ? (((uint64_t)ord << 32) | (uint32_t)~e) : 0;
+            key[t] = (e < A.E) ? (((uint64_t)ord << 32) | (uint32_t)~e) : 0;
             if (e < SLOTS) sh_key[e] = key[t];
         }
         // (a wave's LDS accesses are done in order, so its lanes read what
@@ -503,13 +582,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 #pragma unroll
         for (int t = 0; t < EPL; t++) {
             const int e = lane + WAVE * t;
-            if (e < a.E && rank[t] < a.K) {
+            if (e < A.E && rank[t] < A.K) {
                 sh_idx[rank[t]] = e;
                 sh_pr[rank[t]] = pr[t];
             }
         }
         // bit k: the rank-k expert is masked (lfm2-engine.js:464)
-        const uint64_t mb = __ballot(lane < a.K && mask_has(a.mask, sh_idx[min(lane, MAX_K - 1)]));
+        const uint64_t mb = __ballot(lane < A.K && mask_has(A.mask, sh_idx[min(lane, MAX_K - 1)]));
         if (lane == 0) sh_mrank = (uint32_t)mb;
     }
     lds_barrier();
@@ -524,18 +603,19 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     bool cok = false;
     const int eg = ok ? sh_idx[ck] : 0;
     const int ed0 = ok ? sh_idx[pk2[0]] : 0, ed1 = ok ? sh_idx[pk2[1]] : 0;
-    const size_t dst0 = (size_t)ed0 * a.nbF * a.H, dst1 = (size_t)ed1 * a.nbF * a.H;
+    const size_t dst0 = (size_t)ed0 * A.nbF * A.H, dst1 = (size_t)ed1 * A.nbF * A.H;
+    const gptr<const uint16_t> dd16 = (gptr<const uint16_t>)LAYER(l, dd);
     {
         // The scales go out first: small requests to pages the weight rows do
         // not touch are otherwise served after the whole stream.
-        const size_t grow = (size_t)eg * a.F + cf;
-        gs.load(a.gdcm + grow * a.nbpH + NBW * wave);
-        us.load(a.udcm + grow * a.nbpH + NBW * wave);
+        const size_t grow = (size_t)eg * A.F + cf;
+        gs.load(LAYER(l, gdcm) + grow * A.nbpH + NBW * wave);
+        us.load(LAYER(l, udcm) + grow * A.nbpH + NBW * wave);
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++) ddb[i] = dd16[(dsec[i] ? dst1 : dst0) + doff[i]];
         cok = ok && cs < nc && !((mrank >> ck) & 1u);
-        const int8_t *gbase = a.gq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
-        const int8_t *ubase = a.uq + (size_t)eg * a.nbH * a.F * QK + 16 * hh;
+        const gptr<const int8_t> gbase = LAYER(l, gq) + (size_t)eg * A.nbH * A.F * QK + 16 * hh;
+        const gptr<const int8_t> ubase = LAYER(l, uq) + (size_t)eg * A.nbH * A.F * QK + 16 * hh;
 #pragma unroll
         for (int i = 0; i < NBW; i++) {
             gq[i] = load_stream16(gbase + (size_t)goff[i] * QK);
@@ -555,31 +635,31 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             pk[4 * u + 2] = v.z;
             pk[4 * u + 3] = v.w;
         }
-        double sumW = a.softmax ? 0.0 : 1e-6;
+        double sumW = A.softmax ? 0.0 : 1e-6;
 #pragma unroll
         for (int k = 0; k < MAX_K; k++)
-            if (k < a.K) sumW = sumW + (double)pk[k];
-        const double inv = a.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
+            if (k < A.K) sumW = sumW + (double)pk[k];
+        const double inv = A.softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
         const double wl = (double)sh_pr[min(lane, MAX_K - 1)] * inv;   // w of rank `lane`
-        if (lane < a.K) sh_w[lane] = wl;
+        if (lane < A.K) sh_w[lane] = wl;
         if (j == 0) {
-            if (lane < a.K) {
-                if (a.out_idx) a.out_idx[lane] = sh_idx[lane];
-                if (a.out_w) a.out_w[lane] = wl;
+            if (lane < A.K) {
+                if (A.out_idx) A.out_idx[l * A.K + lane] = sh_idx[lane];
+                if (A.out_w) A.out_w[l * A.K + lane] = wl;
             }
-            if (a.out_probs) {
+            if (A.out_probs) {
 #pragma unroll
                 for (int t = 0; t < EPL; t++)
-                    if (lane + WAVE * t < a.E) a.out_probs[lane + WAVE * t] = pr[t];
+                    if (lane + WAVE * t < A.E) A.out_probs[l * A.E + lane + WAVE * t] = pr[t];
             }
-            if (a.out_rec) {
-                if (lane < a.K) {
-                    a.out_rec[lane] = (float)sh_idx[lane];
-                    a.out_rec[a.K + lane] = (float)wl;
+            if (A.out_rec) {
+                if (lane < A.K) {
+                    A.out_rec[lane] = (float)sh_idx[lane];
+                    A.out_rec[A.K + lane] = (float)wl;
                 }
 #pragma unroll
                 for (int t = 0; t < EPL; t++)
-                    if (lane + WAVE * t < a.E) a.out_rec[2 * a.K + lane + WAVE * t] = pr[t];
+                    if (lane + WAVE * t < A.E) A.out_rec[2 * A.K + lane + WAVE * t] = pr[t];
             }
         }
     }
@@ -589,10 +669,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     // cleared; the barrier after the gate/up products orders this before
     // the waits that fill them.
     {
-        const int HW = a.K * FRb * QK;
+        const int HW = A.K * FRb * QK;
         for (int i = tid; i < HW; i += DEC_THREADS) hl[i] = 0.0f;
         for (int i = tid; i < DEC_MAX_FIN; i += DEC_THREADS) pf[i] = 0.0f;
     }
+
+    // the next layer's router rows, bias and norm weights (stack launches)
+    float rwn[RE][XPT] = {}, wvn[XPT] = {}, bsn[EPL] = {};
 
     // ---- gate / up columns, SwiGLU (tensor.js:167-178), h out ----
     if (ok) {
@@ -606,7 +689,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const int4 av = *reinterpret_cast<const int4 *>(xa + QK * b);
             const float fg = lev3_sum(mfma_i8(av, gq[i]));
             const float fu = lev3_sum(mfma_i8(av, uq[i]));
-            const bool bok = cok && b < a.nbH;
+            const bool bok = cok && b < A.nbH;
             const float sx = xsig[b];
             ga = fmaf(fg, bok ? sx * gs.get(i) : 0.0f, ga);
             ua = fmaf(fu, bok ? sx * us.get(i) : 0.0f, ua);
@@ -618,7 +701,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < DEC_DCH; i++)
-            dq[i] = load_stream16(a.dq + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
+            dq[i] = load_stream16(LAYER(l, dq) + ((dsec[i] ? dst1 : dst0) + doff[i]) * QK + 16 * hh);
         __builtin_amdgcn_sched_barrier(0);
         if (hh == 0) {
             redg[wave][cs] = ga;
@@ -640,8 +723,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
                 const double g64 = (double)G;
                 const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
                 const uint64_t word = tag_word(tag, sg * U);
-                store_local(&a.hloc[(size_t)k * a.F + f], word);
-                store_dev(&a.hdev[(size_t)k * a.F + f], word);
+                store_local(&A.hloc[(size_t)k * A.F + f], word);
+                store_dev(&A.hdev[(size_t)k * A.F + f], word);
             }
         }
     }
@@ -653,20 +736,22 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const uint64_t *pl[IPT], *pd[IPT];
         bool want[IPT];
         float *dst[IPT];
+        uint32_t tg[IPT];
 #pragma unroll
         for (int s2 = 0; s2 < IPT; s2++) {
+            tg[s2] = tag;
             const int i = min(tid + PUB * s2, NC - 1);
             const int k = div_small(i, inv_fr);
             const int f = f0 + i - k * FR;
-            pl[s2] = &a.hloc[(size_t)k * a.F + f];
-            pd[s2] = &a.hdev[(size_t)k * a.F + f];
+            pl[s2] = &A.hloc[(size_t)k * A.F + f];
+            pd[s2] = &A.hdev[(size_t)k * A.F + f];
             want[s2] = tid + PUB * s2 < NC && !((mrank >> k) & 1u);
             dst[s2] = &hl[k * FRb * QK + (i - k * FR)];
         }
-        ok = block_wait<PUB, IPT>(tag, &sh_fail, pl, pd, want, dst, a.wait_ticks);
+        ok = block_wait<PUB, IPT>(tg, &sh_fail, pl, pd, want, dst, A.wait_ticks, A.err);
     }
     if (ok && NP2 > 0) {
-        decompose32<DEC_MAX_HW + 8 * QK>(hl, a.K * FRb, &hlev[0][0], hsig);
+        decompose32<DEC_MAX_HW + 8 * QK>(hl, A.K * FRb, &hlev[0][0], hsig);
         lds_barrier();
         // ---- partial down products: lane r of wave w adds up the products
         // of its row r of pairs w and w + 8 over the group's blocks (in block
@@ -696,6 +781,27 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             sh_pd[DEC_WAVES + wave][cs] = acc1;
         }
     }
+    // the next layer's router rows, bias and norm weights: requested once the
+    // down products are done (the weight registers are free), they arrive
+    // while the partials and the residual row are exchanged
+    if (STACK && ok && !last) {
+        if (!A.router_q8) {
+#pragma unroll
+            for (int t = 0; t < RE; t++) {
+                const int e = min(mi + M * t, A.E - 1);
+#pragma unroll
+                for (int s = 0; s < XPT; s++)
+                    rwn[t][s] = LAYER(l + 1, rf32)[(size_t)e * A.H + min(tid + DEC_THREADS * s, A.H - 1)];
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < EPL; t++) bsn[t] = LAYER(l + 1, bias)[min(lane + WAVE * t, A.E - 1)];
+#pragma unroll
+        for (int s = 0; s < XPT; s++) {
+            const int k = tid + DEC_THREADS * s;
+            wvn[s] = (LAYER(l + 1, norm_w) && k < A.H) ? LAYER(l + 1, norm_w)[k] : 1.0f;
+        }
+    }
     lds_barrier();
     // waves 4..7 publish the pairs' sums (the polling waves 0..3 then hold no
     // device stores to wait for)
@@ -706,20 +812,22 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const int k = (NRH == 2) ? (p >> 1) : p;
             const int rl = ((NRH == 2) ? (p & 1) : 0) * 32 + r;
             if (rl < RMm && !((mrank >> k) & 1u))
-                store_dev(&a.part[((size_t)gx * a.K + k) * a.H + r0 + rl], tag_word(tag, sh_pd[p][r]));
+                store_dev(&A.part[((size_t)gx * A.K + k) * A.H + r0 + rl], tag_word(tag, sh_pd[p][r]));
         }
     }
 
     // ---- combine (lfm2-engine.js:459-486): y_k = sum of the groups' partials,
-    // acc = fp32(acc + w_k y_k) in rank order, hidden += acc ----
-    const int NP = DEC_GROUPS * a.K * RF;
+    // acc = fp32(acc + w_k y_k) in rank order, hidden += acc.  The arrival
+    // words (of the first layer) are waited for before hidden is written ----
+    const int NP = DEC_GROUPS * A.K * RF;
     if (ok) {
         constexpr int NT = DEC_THREADS / 2;
         constexpr int IPT = DEC_MAX_FIN / NT;
         const uint64_t *pl[IPT];
         bool want[IPT];
         float *dst[IPT];
-        const float inv_krf = 1.0f / (float)(a.K * RF), inv_rf = 1.0f / (float)RF;
+        uint32_t tg[IPT];   // arrival words carry the first layer's tag
+        const float inv_krf = 1.0f / (float)(A.K * RF), inv_rf = 1.0f / (float)RF;
 #pragma unroll
         for (int s2 = 0; s2 < IPT; s2++) {
             // item i: partial (x, k, q) of the group sums, or arrival word i - NP;
@@ -728,29 +836,30 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const int i = tid + NT * s2;
             const int ip = min(i, NP - 1);
             const int x = div_small(ip, inv_krf);
-            const int r = ip - x * a.K * RF;
+            const int r = ip - x * A.K * RF;
             const int k = div_small(r, inv_rf);
             const int q = r - k * RF;
-            const int xb0 = (x * a.nbF) >> 3, xb1 = ((x + 1) * a.nbF) >> 3;   // DEC_GROUPS = 8
-            const uint64_t *pp = &a.part[((size_t)x * a.K + k) * a.H + min(q0 + q, a.H - 1)];
-            const uint64_t *pa = &a.arrive[min(max(i - NP, 0), G - 1)];
+            const int xb0 = (x * A.nbF) >> 3, xb1 = ((x + 1) * A.nbF) >> 3;   // DEC_GROUPS = 8
+            const uint64_t *pp = &A.part[((size_t)x * A.K + k) * A.H + min(q0 + q, A.H - 1)];
+            const uint64_t *pa = &A.arrive[min(max(i - NP, 0), G - 1)];
             const bool isp = i < NP;
             pl[s2] = isp ? pp : pa;
-            want[s2] = isp ? (q < RFm && xb1 > xb0 && !((mrank >> k) & 1u)) : (i < NP + G);
+            want[s2] = isp ? (q < RFm && xb1 > xb0 && !((mrank >> k) & 1u)) : (last && i < NP + G);
             dst[s2] = isp ? &pf[min(i, DEC_MAX_FIN - 1)] : nullptr;
+            tg[s2] = isp ? tag : tag0;
         }
-        ok = block_wait<NT, IPT>(tag, &sh_fail, pl, pl, want, dst, a.wait_ticks);
+        ok = block_wait<NT, IPT>(tg, &sh_fail, pl, pl, want, dst, A.wait_ticks, A.err);
     }
     if (ok && tid < RFm) {
         float acc = 0.0f;
-        for (int k0 = 0; k0 < a.K; k0 += 4) {   // four ranks' reads issued together
+        for (int k0 = 0; k0 < A.K; k0 += 4) {   // four ranks' reads issued together
             float v[4][DEC_GROUPS];
             double w4[4];
 #pragma unroll
             for (int kk = 0; kk < 4; kk++) {
-                const int k = min(k0 + kk, a.K - 1);
+                const int k = min(k0 + kk, A.K - 1);
 #pragma unroll
-                for (int x = 0; x < DEC_GROUPS; x++) v[kk][x] = pf[(x * a.K + k) * RF + tid];
+                for (int x = 0; x < DEC_GROUPS; x++) v[kk][x] = pf[(x * A.K + k) * RF + tid];
                 w4[kk] = sh_w[k];
             }
 #pragma unroll
@@ -759,18 +868,37 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 #pragma unroll
                 for (int x = 0; x < DEC_GROUPS; x++) y += v[kk][x];
                 const int k = k0 + kk;
-                if (k < a.K && !((mrank >> k) & 1u)) acc = (float)((double)acc + w4[kk] * (double)y);
+                if (k < A.K && !((mrank >> k) & 1u)) acc = (float)((double)acc + w4[kk] * (double)y);
             }
         }
-        a.hidden[q0 + tid] = hin + acc;
+        const float hn = hin + acc;
+        if (!STACK || last) A.hidden[q0 + tid] = hn;
+        else store_dev(&A.hx[(size_t)(l & 1) * SYNC_X_WORDS + q0 + tid], tag_word(tag, hn));
+        hin = hn;
     }
+    if constexpr (STACK) {
+        if (!ok) break;
+#pragma unroll
+        for (int t = 0; t < RE; t++)
+#pragma unroll
+            for (int s = 0; s < XPT; s++) rw[t][s] = rwn[t][s];
+#pragma unroll
+        for (int s = 0; s < XPT; s++) wv[s] = wvn[s];
+#pragma unroll
+        for (int t = 0; t < EPL; t++) bias_l[t] = bsn[t];
+    }
+    }   // layers
+
     if (tid == 0) {
         if (!ok) atomicOr(a.err, 1u);
-        // workgroup 0 has seen every arrival word carry this tag (or gave up
-        // waiting), so every workgroup has read the epoch: the next call draws
-        // the next tag
-        if (j == 0) __hip_atomic_store(a.epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // workgroup 0 has seen every arrival word carry the first tag (or gave
+        // up waiting), so every workgroup has read the epoch: the next call
+        // draws the tags after this call's
+        if (j == 0) __hip_atomic_store(a.epoch_word, tag0 + (uint32_t)NL - 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+#undef LAYER
+#undef LAYER0
+#undef A
 }
 
 static int decode_grid(const qq_ctx *ctx)
@@ -797,34 +925,44 @@ bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T)
            (size_t)m->K * m->F <= SYNC_H_WORDS && (size_t)m->K * m->H * DEC_GROUPS <= SYNC_P_WORDS;
 }
 
-template <int NBW, int RE, int EPL>
+template <int NBW, int RE, int EPL, bool STACK>
 static void launch_t(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, bool pp2)
 {
-    if (pp2) QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, true>), grid, dim3(DEC_THREADS), 0, a);
-    else QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, false>), grid, dim3(DEC_THREADS), 0, a);
+    if (pp2) QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, true, STACK>), grid, dim3(DEC_THREADS), 0, a);
+    else QQ_LAUNCH(ctx, (moe_decode_kernel<NBW, RE, EPL, false, STACK>), grid, dim3(DEC_THREADS), 0, a);
 }
 
 // (RE, EPL) pairs: with M <= 32 members per group, ceil(E / M) <= RE implies
 // ceil(E / 64) <= EPL for these four
-template <int NBW>
+template <int NBW, bool STACK>
 static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re, bool pp2)
 {
-    if (re <= 1) launch_t<NBW, 1, 1>(ctx, a, grid, pp2);
-    else if (re <= 2) launch_t<NBW, 2, 1>(ctx, a, grid, pp2);
-    else if (re <= 4) launch_t<NBW, 4, 2>(ctx, a, grid, pp2);
-    else launch_t<NBW, 8, 4>(ctx, a, grid, pp2);
+    if (re <= 1) launch_t<NBW, 1, 1, STACK>(ctx, a, grid, pp2);
+    else if (re <= 2) launch_t<NBW, 2, 1, STACK>(ctx, a, grid, pp2);
+    else if (re <= 4) launch_t<NBW, 4, 2, STACK>(ctx, a, grid, pp2);
+    else launch_t<NBW, 8, 4, STACK>(ctx, a, grid, pp2);
 }
 
-int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
-                      const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
-                      const NormArgs *norm, float *out_rec)
+DecodeLayer decode_layer_of(const qq_moe *m, const float *norm_w)
 {
-    DecodeArgs a;
-    a.x = x;
-    a.norm = norm != nullptr;
-    a.norm_w = norm ? norm->w : nullptr;
-    a.eps = norm ? norm->eps : 0.0;
-    a.hidden = hidden;
+    DecodeLayer d;
+    const bool q8 = m->router_type == QQ_TYPE_Q8_0;
+    d.rf32 = m->router_f32;
+    d.rq = q8 ? m->router_q8->qs : nullptr;
+    d.rd = q8 ? m->router_q8->d : nullptr;
+    d.bias = m->bias;
+    d.gq = m->gate->qs;
+    d.gdcm = m->gate->dcm;
+    d.uq = m->up->qs;
+    d.udcm = m->up->dcm;
+    d.dq = m->down->qs;
+    d.dd = m->down->d;
+    d.norm_w = norm_w;
+    return d;
+}
+
+static void decode_common(qq_ctx *ctx, const qq_moe *m, DecodeArgs &a)
+{
     a.H = m->H;
     a.F = m->F;
     a.E = m->E;
@@ -832,19 +970,8 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.nbH = (m->H + QK - 1) / QK;
     a.nbF = (m->F + QK - 1) / QK;
     a.router_q8 = m->router_type == QQ_TYPE_Q8_0;
-    a.rf32 = m->router_f32;
-    a.rq = a.router_q8 ? m->router_q8->qs : nullptr;
-    a.rd = a.router_q8 ? m->router_q8->d : nullptr;
     a.softmax = m->gating == QQ_GATING_SOFTMAX;
-    a.bias = m->bias;
-    a.gq = m->gate->qs;
-    a.gdcm = m->gate->dcm;
-    a.uq = m->up->qs;
-    a.udcm = m->up->dcm;
     a.nbpH = m->gate->nbp;
-    a.dq = m->down->qs;
-    a.dd = m->down->d;
-    a.mask = mask;
     a.epoch_word = ctx->sync_epoch;
     a.rloc = ctx->sync_local;
     a.rdev = ctx->sync_slots;
@@ -852,13 +979,14 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.hdev = ctx->sync_hdev;
     a.part = ctx->sync_part;
     a.arrive = ctx->sync_arrive;
-    a.out_idx = out_idx;
-    a.out_w = out_w;
-    a.out_probs = out_probs;
-    a.out_rec = out_rec;
+    a.hx = ctx->sync_hx;
     a.err = ctx->sync_err;
     a.wait_ticks = ctx->dec_wait_ticks;
+}
 
+template <bool STACK>
+static int decode_launch(qq_ctx *ctx, const qq_moe *m, const DecodeArgs &a)
+{
     const int G = decode_grid(ctx);
     const int re = (m->E + G / DEC_GROUPS - 1) / (G / DEC_GROUPS);
     const int nbw = (a.nbH + DEC_WAVES - 1) / DEC_WAVES;
@@ -866,13 +994,54 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     const bool pp2 = m->K * (RM > 32 ? 2 : 1) > DEC_WAVES;
     const dim3 grid(G);
     prof_begin(ctx, K_DECODE);
-    if (nbw <= 1) launch_re<1>(ctx, a, grid, re, pp2);
-    else if (nbw <= 2) launch_re<2>(ctx, a, grid, re, pp2);
-    else if (nbw <= 4) launch_re<4>(ctx, a, grid, re, pp2);
-    else launch_re<8>(ctx, a, grid, re, pp2);
+    if (nbw <= 1) launch_re<1, STACK>(ctx, a, grid, re, pp2);
+    else if (nbw <= 2) launch_re<2, STACK>(ctx, a, grid, re, pp2);
+    else if (nbw <= 4) launch_re<4, STACK>(ctx, a, grid, re, pp2);
+    else launch_re<8, STACK>(ctx, a, grid, re, pp2);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;
+}
+
+int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
+                      const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
+                      const NormArgs *norm, float *out_rec)
+{
+    DecodeArgs a;
+    decode_common(ctx, m, a);
+    a.x = x;
+    a.norm = norm != nullptr;
+    a.eps = norm ? norm->eps : 0.0;
+    a.hidden = hidden;
+    a.L = 1;
+    a.one = decode_layer_of(m, norm ? norm->w : nullptr);
+    a.layers = nullptr;
+    a.mask = mask;
+    a.out_idx = out_idx;
+    a.out_w = out_w;
+    a.out_probs = out_probs;
+    a.out_rec = out_rec;
+    return decode_launch<false>(ctx, m, a);
+}
+
+int launch_moe_stack_decode(qq_ctx *ctx, const qq_moe *m0, const DecodeLayer *layers_dev, int L, float *hidden,
+                            double eps, const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs)
+{
+    DecodeArgs a;
+    decode_common(ctx, m0, a);
+    a.x = hidden;
+    a.norm = 1;
+    a.eps = eps;
+    a.hidden = hidden;
+    a.L = L;
+    a.one = decode_layer_of(m0, nullptr);
+    a.layers = layers_dev;
+    a.mask = mask;
+    a.out_idx = out_idx;
+    a.out_w = out_w;
+    a.out_probs = out_probs;
+    a.out_rec = nullptr;
+    return decode_launch<true>(ctx, m0, a);
 }
 
 }  // namespace qq

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdarg>
 #include <cstring>
+#include <vector>
 
 #include "../../include/qq_moe.h"
 
@@ -36,11 +37,16 @@ static_assert(SYNC_REPLICA_WORDS >= 2 * MAX_E, "slot table");
 constexpr int SYNC_H_WORDS = MAX_K * 4096;
 constexpr int SYNC_P_WORDS = 8 * MAX_K * 2048;
 constexpr int SYNC_ARRIVE_WORDS = 256;
+// Stack decode (several layers in one launch): the residual row after each
+// layer, in two alternating tables of up to SYNC_X_WORDS words.
+constexpr int SYNC_X_WORDS = 2048;
+constexpr int STACK_MAX_LAYERS = 256;
 // After a timed-out call the host moves the epoch on by this much: a
 // workgroup of that call that started after workgroup 0 advanced the epoch
 // wrote words tagged with the next call's tags (up to twice the call's layer
 // count past the old epoch), which the next call must not accept.
 constexpr uint32_t SYNC_EPOCH_SKIP = 1024;
+static_assert(SYNC_EPOCH_SKIP >= 2 * STACK_MAX_LAYERS + 2, "epoch skip");
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
 struct MaskBits {
@@ -95,6 +101,17 @@ struct qq_moe {
     qq_tensor *owned[3];                 // ... unless the layer owns them (GGUF loader)
 };
 
+namespace qq { struct DecodeLayer; }
+
+// Layers of one MoE stack (qq_moe_stack_create): borrowed layer handles, their
+// ffn_norm weights, and the decode kernel's device table of their pointers.
+struct qq_moe_stack {
+    int n = 0;
+    std::vector<const qq_moe *> layers;
+    std::vector<const float *> norm_w;
+    qq::DecodeLayer *table = nullptr;
+};
+
 struct qq_ctx {
     int device;
     int num_cus;
@@ -126,7 +143,7 @@ struct qq_ctx {
     // bound on the decode kernel's device-side waits, in 100 MHz wall-clock ticks
     uint64_t dec_wait_ticks;
     uint32_t *sync_epoch;
-    uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive;
+    uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive, *sync_hx;
     // device-side waits that timed out on this context so far (counted when
     // the error word is read); device-resident state built across calls (an
     // LFM2 model's conv states and KV cache) is invalid after one
@@ -232,6 +249,27 @@ struct NormArgs {
     double eps;
 };
 
+// The weights of one layer of the batch-1 decode kernel (a stack launch
+// reads them from a device table of these).
+struct DecodeLayer {
+    const float *rf32;    // F32 router [E][H], or
+    const int8_t *rq;     // Q8_0 router (block-major)
+    const __half *rd;
+    const float *bias;
+    const int8_t *gq;
+    const __half *gdcm;   // gate/up scales row by row (qq_tensor.dcm), nbpH per row
+    const int8_t *uq;
+    const __half *udcm;
+    const int8_t *dq;
+    const __half *dd;     // down scales, block-major
+    const float *norm_w;  // ffn_norm weight; NULL: unit weight
+};
+DecodeLayer decode_layer_of(const qq_moe *m, const float *norm_w);
+// L layers of equal shape and gating on one residual row in one launch:
+// hidden = hidden + MoE_l(rmsnorm(hidden) * norm_w_l) for l = 0 .. L-1
+// (layers_dev: a device table of L entries); routing outputs at l K / l E.
+int launch_moe_stack_decode(qq_ctx *ctx, const qq_moe *m0, const DecodeLayer *layers_dev, int L, float *hidden,
+                            double eps, const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs);
 int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden,
                       const MaskBits &mask, int32_t *out_idx, double *out_w, float *out_probs,
                       const NormArgs *norm = nullptr, float *out_rec = nullptr);

@@ -31,6 +31,7 @@ EXPORTS = (
     "qq_q8_0_matvec", "qq_q8_0_matvec_dev",
     "qq_moe_create", "qq_moe_release", "qq_moe_forward", "qq_moe_forward_dev",
     "qq_moe_forward_norm_dev", "qq_moe_forward_noalloc_dev", "qq_moe_set_gating",
+    "qq_moe_stack_create", "qq_moe_stack_release", "qq_moe_stack_forward_dev",
     "qq_set_mfma_min_tokens", "qq_set_wait_limit", "qq_debug_epoch", "qq_debug_plant_words", "qq_rmsnorm_dev", "qq_timer_start", "qq_timer_stop",
     "qq_profile_enable", "qq_profile_read", "qq_profile_name", "qq_profile_kernel_count",
     "qq_capture_begin", "qq_capture_end", "qq_graph_launch", "qq_graph_release",
@@ -109,6 +110,9 @@ def load():
         "qq_moe_forward_noalloc_dev": (I, [P, P, P, P, I, P, P, P, P]),
         "qq_moe_forward_norm_dev": (I, [P, P, P, P, ctypes.c_double, I, P, P, P, P]),
         "qq_moe_set_gating": (I, [P, P, I]),
+        "qq_moe_stack_create": (I, [P, P, P, I, PP]),
+        "qq_moe_stack_release": (I, [P, P]),
+        "qq_moe_stack_forward_dev": (I, [P, P, P, ctypes.c_double, I, P, P, P, P]),
         "qq_set_mfma_min_tokens": (I, [P, I]),
         "qq_set_wait_limit": (I, [P, I]),
         "qq_debug_epoch": (I, [P, ctypes.POINTER(ctypes.c_uint32)]),
@@ -312,6 +316,18 @@ class Context:
                                         H, F, E, K, ctypes.byref(h)), "qq_moe_create")
         return MoeLayer(self, h, H, F, E, K, (gate, up, down))
 
+    def moe_stack(self, layers, norm_w_ptrs=None):
+        """A stack of MoE layers of one shape (qq_moe_stack_create); norm_w_ptrs:
+        one device pointer (or None) per layer, or None for unit weights."""
+        n = len(layers)
+        arr = (ctypes.c_void_p * n)(*[l.h for l in layers])
+        nw = None
+        if norm_w_ptrs is not None:
+            nw = (ctypes.c_void_p * n)(*[None if p is None else ctypes.c_void_p(p) for p in norm_w_ptrs])
+        h = ctypes.c_void_p()
+        self.check(self.L.qq_moe_stack_create(self.h, arr, nw, n, ctypes.byref(h)), "qq_moe_stack_create")
+        return MoeStack(self, h, list(layers))
+
 
 class Gguf:
     """Native GGUF reader (include/qq_gguf.h) over a file (memory-mapped) or
@@ -477,6 +493,32 @@ class Tensor:
     def release(self):
         if self.h:
             self.ctx.L.qq_tensor_release(self.ctx.h, self.h)
+            self.h = None
+
+
+class MoeStack:
+    """n MoE layers applied in order to residual rows (qq_moe_stack_*)."""
+
+    def __init__(self, ctx, h, layers):
+        self.ctx, self.h, self.layers = ctx, h, layers
+        self.n = len(layers)
+
+    def forward_dev(self, hidden_ptr, T, eps=1e-5, mask=None, idx_ptr=None, w_ptr=None, probs_ptr=None):
+        """For each layer: hidden += MoE_l(rmsnorm(hidden) * norm_w_l), device
+        pointers; routing of layer l at l*T*K / l*T*E."""
+        m = None
+        if mask is not None:
+            m = np.zeros(self.layers[0].E, np.uint8)
+            for e in mask:
+                m[e] = 1
+        vp = lambda p: None if p is None else ctypes.c_void_p(p)
+        self.ctx.check(self.ctx.L.qq_moe_stack_forward_dev(
+            self.ctx.h, self.h, ctypes.c_void_p(hidden_ptr), float(eps), T, _ptr(m), vp(idx_ptr), vp(w_ptr),
+            vp(probs_ptr)), "qq_moe_stack_forward_dev")
+
+    def release(self):
+        if self.h:
+            self.ctx.check(self.ctx.L.qq_moe_stack_release(self.ctx.h, self.h), "qq_moe_stack_release")
             self.h = None
 
 

@@ -169,3 +169,60 @@ def test_lfm2_forward_refuses_after_a_timeout(tmp_path):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
     finally:
         m.release()
+
+
+def test_stack_zero_wait_bound_fails_loudly_and_recovers():
+    """The one-launch stack under a zero wait bound: the call reports the
+    timeout (or is exact), each element of hidden is its old value or the
+    stack's correct result, the epoch moves past every tag the launch can
+    have used (2 per layer), and the next call is exact."""
+    import torch
+    print("stack decode wait bound 0, then default", flush=True)
+    ctx = gpu_context()
+    n, H = 6, 256
+    Ls = [synth.moe_layer(900 + l, H=H, F=192, E=16, K=4) for l in range(n)]
+    layers = [upload_layer(ctx, L) for L in Ls]
+    stack = ctx.moe_stack(layers)
+    try:
+        _, h0 = synth.activations(33, 1, H)
+        good = torch.from_numpy(h0.copy()).cuda()
+        torch.cuda.synchronize()
+        stack.forward_dev(good.data_ptr(), 1)
+        ctx.synchronize()
+        good = good.cpu().numpy()
+        failed = 0
+        ctx.set_wait_limit(0)
+        try:
+            for _ in range(3):
+                dh = torch.from_numpy(h0.copy()).cuda()
+                torch.cuda.synchronize()
+                e0 = ctx.debug_epoch()
+                stack.forward_dev(dh.data_ptr(), 1)
+                try:
+                    ctx.synchronize()
+                except qq_hip.QQError as e:
+                    assert "timed out" in str(e), e
+                    failed += 1
+                    got = dh.cpu().numpy()
+                    ok = (got.view(np.uint32) == h0.view(np.uint32)) | (got.view(np.uint32) == good.view(np.uint32))
+                    assert ok.all()
+                    assert (ctx.debug_epoch() - e0) % (1 << 32) >= 2 * n + 2
+                    for d in range(1, 2 * n + 1):
+                        ctx.debug_plant_words(e0 + d)
+                    continue
+                assert np.array_equal(dh.cpu().numpy().view(np.uint32), good.view(np.uint32))
+                assert ctx.debug_epoch() == (e0 + n) % (1 << 32)
+        finally:
+            ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
+        assert failed >= 1
+        dh = torch.from_numpy(h0.copy()).cuda()
+        torch.cuda.synchronize()
+        stack.forward_dev(dh.data_ptr(), 1)
+        ctx.synchronize()
+        assert np.array_equal(dh.cpu().numpy().view(np.uint32), good.view(np.uint32))
+    finally:
+        stack.release()
+        for m in layers:
+            for t in m._keep:
+                t.release()
+            m.release()

@@ -7,6 +7,11 @@ then `hidden += _moEFFN(x)`; a prompt is T sequential calls, :550-555).
   (qq_moe_forward_norm_dev), against the oracle's chain
   (oracle.rmsnorm_unit + oracle.moe_ffn per layer): top-4 indices bit-exact
   at every layer, the stack's total contribution within 1e-4 relative L2.
+  The same tokens through the one-launch stack (qq_moe_stack_forward_dev):
+  bit-equal to the layer-by-layer chain, routing and residual.
+* Stacks of small layers (ffn_norm weights, expert masks, softmax gating,
+  token batches): the one-launch stack bit-equal to the chain of
+  qq_moe_forward_norm_dev calls, routing against the oracle.
 * Prefill: one full-shape layer at T = 4096 (the largest chunk) and T = 4100
   (a 4096-row chunk on the fp16 MFMA path and a 4-row chunk on the fp32
   path): routing bit-exact on every row against the oracle, every row's
@@ -66,14 +71,94 @@ def test_stack22_decode():
                 m.forward_norm_dev(HID[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX[t, l].data_ptr())
         ctx.synchronize()
         got_idx, got = IDX.cpu().numpy(), HID.cpu().numpy()
+        _say("one-launch stack")
+        stack = ctx.moe_stack(layers)
+        try:
+            HID2 = torch.from_numpy(hid.copy()).cuda()
+            IDX2 = torch.full((n_tok, N_LAYERS, 4), -1, dtype=torch.int32, device="cuda")
+            torch.cuda.synchronize()
+            for t in range(n_tok):
+                stack.forward_dev(HID2[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX2[t].data_ptr())
+            ctx.synchronize()
+            got2_idx, got2 = IDX2.cpu().numpy(), HID2.cpu().numpy()
+        finally:
+            stack.release()
     finally:
         for m in layers:
             _release(m)
     np.testing.assert_array_equal(got_idx, idx_ref)
+    np.testing.assert_array_equal(got2_idx, idx_ref)
+    assert np.array_equal(got2.view(np.uint32), got.view(np.uint32))
     for t in range(n_tok):
         err = rel_l2(got[t].astype(np.float64) - hid[t], h_ref[t].astype(np.float64) - hid[t])
         _say("token", t, "stack rel_l2", err)
         assert err < 1e-4, (t, err)
+
+
+@pytest.mark.parametrize("shape,n,T,masked,weighted", [
+    (dict(H=256, F=192, E=16, K=4), 5, 1, False, True),
+    (dict(H=256, F=192, E=16, K=4), 5, 1, True, True),
+    (dict(H=2048, F=768, E=128, K=8, bias=None, gating="softmax"), 3, 1, False, False),
+    (dict(H=512, F=256, E=32, K=4), 4, 3, True, True),
+    (dict(H=2048, F=1792, E=32, K=4), 3, 2, False, True),
+])
+def test_stack_matches_layer_chain(shape, n, T, masked, weighted):
+    """qq_moe_stack_forward_dev equals qq_moe_forward_norm_dev layer after
+    layer, bit for bit (T = 1: the one-launch stack; T > 1: the batch path per
+    layer); without weights and masks the routing equals the oracle's chain."""
+    import torch
+    _say("stack", shape, n, T, masked, weighted)
+    ctx = gpu_context()
+    H, E, K = shape["H"], shape["E"], shape["K"]
+    Ls = [synth.moe_layer(7000 + 13 * l, **shape) for l in range(n)]
+    layers = [upload_layer(ctx, L) for L in Ls]
+    rng = np.random.default_rng(n * 100 + T)
+    nw = [torch.from_numpy(rng.uniform(0.5, 1.5, H).astype(np.float32)).cuda() for _ in range(n)] \
+        if weighted else [None] * n
+    mask = [1, 5] if masked else None
+    _, hid = synth.activations(77 + n, T, H)
+    stack = ctx.moe_stack(layers, [None if w is None else w.data_ptr() for w in nw])
+    try:
+        A = torch.from_numpy(hid.copy()).cuda()
+        B = torch.from_numpy(hid.copy()).cuda()
+        IA = torch.full((n, T, K), -1, dtype=torch.int32, device="cuda")
+        IB = torch.full((n, T, K), -1, dtype=torch.int32, device="cuda")
+        WB = torch.zeros((n, T, K), dtype=torch.float64, device="cuda")
+        PB = torch.zeros((n, T, E), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        for l, m in enumerate(layers):
+            m.forward_norm_dev(A.data_ptr(), T, norm_w_ptr=None if nw[l] is None else nw[l].data_ptr(),
+                               eps=EPS, mask=mask, idx_ptr=IA[l].data_ptr())
+        stack.forward_dev(B.data_ptr(), T, eps=EPS, mask=mask, idx_ptr=IB.data_ptr(), w_ptr=WB.data_ptr(),
+                          probs_ptr=PB.data_ptr())
+        ctx.synchronize()
+        a, b = A.cpu().numpy(), B.cpu().numpy()
+        ia, ib = IA.cpu().numpy(), IB.cpu().numpy()
+    finally:
+        stack.release()
+        for m in layers:
+            _release(m)
+    np.testing.assert_array_equal(ib, ia)
+    assert np.array_equal(b.view(np.uint32), a.view(np.uint32))
+    if not weighted and not masked:
+        h = hid.copy()
+        for l, L in enumerate(Ls):
+            x = np.stack([oracle.rmsnorm_unit(r, EPS) for r in h])
+            r_idx, r_w, r_p = oracle.moe_route(L, x)
+            np.testing.assert_array_equal(ib[l], r_idx)
+            if l == 0:
+                np.testing.assert_array_equal(WB[l].cpu().numpy(), r_w)
+                np.testing.assert_array_equal(PB[l].cpu().numpy(), r_p)
+            else:
+                # later layers see the GPU's residual, which differs from the
+                # oracle chain's by ~1e-7 relative: the weights and
+                # probabilities follow it at fp32 level
+                np.testing.assert_allclose(WB[l].cpu().numpy(), r_w, rtol=1e-5)
+                np.testing.assert_allclose(PB[l].cpu().numpy(), r_p, rtol=1e-5, atol=1e-9)
+            h, _, _, _ = oracle.moe_ffn(L, x, h)
+        err = rel_l2(b.astype(np.float64) - hid, h.astype(np.float64) - hid)
+        _say("stack rel_l2 vs oracle", err)
+        assert err < 1e-4, err
 
 
 @pytest.mark.parametrize("T", [4096, 4100])
