@@ -20,7 +20,7 @@ static thread_local char g_init_err[512] = "";
 static size_t sync_table_words()
 {
     return (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS +
-           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 2 * (size_t)SYNC_X_WORDS;
+           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 4 * 8 * (size_t)SYNC_X_WORDS;
 }
 
 int set_error(qq_ctx *ctx, const char *fmt, ...)
@@ -307,7 +307,7 @@ int qq_init(int device, qq_ctx **out)
     ctx->sync_arrive = ctx->sync_part + SYNC_P_WORDS;
     ctx->sync_hx = ctx->sync_arrive + SYNC_ARRIVE_WORDS;
     // error word and epoch each on a 128-byte line of their own
-    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_hx + 2 * SYNC_X_WORDS);
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_hx + 4 * 8 * SYNC_X_WORDS);
     ctx->sync_epoch = ctx->sync_err + 32;
     ctx->capturing = 0;
     *out = ctx;
@@ -760,7 +760,7 @@ int qq_moe_stack_forward_dev(qq_ctx *ctx, const qq_moe_stack *st, float *hidden_
     QQ_HIP(ctx, hipSetDevice(ctx->device));
     MaskBits mb;
     if (int rc = mask_from_bytes(ctx, mask, m0->E, &mb)) return rc;
-    if (decode_supported(ctx, m0, T))   // one launch for the whole stack
+    if (T == 1 && stack_decode_supported(ctx, m0))   // one launch for the whole stack
         return launch_moe_stack_decode(ctx, m0, st->table, st->n, hidden_dev, eps, mb, idx_dev, w_dev, probs_dev);
     // layer by layer (routing outputs of layer l at l T K resp. l T E)
     const size_t TK = (size_t)T * m0->K, TE = (size_t)T * m0->E;

@@ -85,7 +85,8 @@ struct DecodeArgs {
     uint64_t *hdev;       // device-coherent copy
     uint64_t *part;       // partial down sums [8][K][H], device-coherent
     uint64_t *arrive;     // [G]
-    uint64_t *hx;         // stack: the residual row after layer l in table l % 2 [2][SYNC_X_WORDS]
+    uint64_t *hxl;        // stack: each group's residual row after layer l, table l % 2
+    uint64_t *hxd;        //   [2][8][SYNC_X_WORDS]: group-local and device-coherent copies
     int32_t *out_idx;     // optional outputs (a stack's: layer l at l K, l K, l E)
     double *out_w;
     float *out_probs;
@@ -266,25 +267,33 @@ struct ScaleRun {
 // Limits of one launch (checked by decode_supported on the host).
 constexpr int DEC_MAX_HW = 2048;               // h values of one group (K x F-range)
 constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read by one workgroup
+constexpr int DEC_MAX_FIN_STACK = 5 * DEC_THREADS;   // ... by one member of a stack launch
 
 // NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
 // experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64));
 // PP2: a wave takes two (rank, row half) pairs of down rows (K x halves > 8);
 // STACK: the launch runs a.L layers (ffn_norm folded in) on one residual row.
 //
-// Stack launches.  Layer l uses tag epoch + 1 + l.  After the combine of
-// layer l a workgroup publishes its rows of the new residual as tagged words
-// in table l % 2 of a.hx (device-coherent) instead of writing hidden, and
-// layer l + 1 starts with every workgroup waiting for all H of them; only the
-// last layer writes hidden.  Every exchange table can be reused layer after
-// layer: a workgroup can only publish layer l + 1 words once it holds the
-// whole residual after layer l, that is once every workgroup has finished
-// layer l and with it every wait on a layer-l word.  (The two hx tables keep
-// a layer-l + 1 row from overwriting a layer-l row some workgroup still
-// waits for.)  The arrival words are published at layer 0 and waited for
-// before the final write of hidden, which is the launch's input row.  The
-// next layer's router rows, bias and norm weights are loaded while the
-// current layer's down rows stream in.
+// Stack launches.  Layer l uses tag epoch + 1 + l.  The combine is done by
+// every group for all H rows: member i of each group waits for the 8 groups'
+// partials of its rows [i RM, (i + 1) RM), adds them up and publishes its rows
+// of the new residual in its group's table (group-local, with a device-
+// coherent copy); layer l + 1 starts with every member gathering its group's
+// H rows.  So the only device-wide exchange of a layer is the partials; the
+// residual row passes between layers inside each XCD.  Only group 0 writes
+// hidden, at the last layer, once the arrival words of the first layer (every
+// workgroup has read the input row) are in.
+// Groups are coupled only through the partials, so one group can run up to a
+// layer ahead of another: the partials and the device copies of the routing
+// logits (the tables other groups read) alternate between two halves by layer
+// parity.  A member publishes layer l + 2 words there only after its group
+// has gathered the layer l + 1 residual, which every member of every group
+// publishes only after it has read all of its layer-l words.  Group-local
+// tables are reused each layer (a member writes layer l + 1 words only after
+// every member of its group has published its layer-l residual rows, and so
+// has finished layer l); the residual tables alternate by parity as well.
+// The next layer's router rows, bias and norm weights are loaded while the
+// current layer's partials are exchanged.
 template <int NBW, int RE, int EPL, bool PP2, bool STACK>
 __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 {
@@ -310,7 +319,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     __shared__ __align__(16) int8_t hlev[4][DEC_MAX_HW + 8 * QK];
     __shared__ float hsig[DEC_MAX_HW / QK + 8];
     __shared__ float sh_pd[2 * DEC_WAVES][32];   // sums of the (rank, row half) pairs
-    __shared__ float pf[DEC_MAX_FIN];
+    __shared__ float pf[STACK ? DEC_MAX_FIN_STACK : DEC_MAX_FIN];
+    __shared__ float hraw[STACK ? XN : 1];       // the layer's input residual row
     __shared__ uint32_t sh_tag;
     __shared__ int sh_fail;
 
@@ -335,7 +345,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const int RF = (a.H + G - 1) / G;
     const int q0 = j * RF;
     const int RFm = max(min(RF, a.H - q0), 0);
-    float hin = a.hidden[min(q0 + tid, a.H - 1)];
+    float hin = STACK ? 0.0f : a.hidden[min(q0 + tid, a.H - 1)];   // (stack: hraw)
     float xv[XPT], wv[XPT];
     {
         const gptr<const float> nw = LAYER0(norm_w) ? LAYER0(norm_w) : as_global(a.x);
@@ -390,22 +400,23 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     const uint32_t tag = tag0 + (uint32_t)l;
     const bool last = l == NL - 1;
     if (STACK && l > 0) {
-        // ---- the residual row after layer l - 1, from every workgroup ----
-        const uint64_t *pl[XPT];
+        // ---- the residual row after layer l - 1, from the members of the group ----
+        const uint64_t *pl[XPT], *pd[XPT];
         bool want[XPT];
         float *dst[XPT];
-        const uint64_t *hxp = A.hx + (size_t)((l - 1) & 1) * SYNC_X_WORDS;
+        const size_t xo = ((size_t)((l - 1) & 1) * DEC_GROUPS + gx) * SYNC_X_WORDS;
 #pragma unroll
         for (int s = 0; s < XPT; s++) {
             const int k = tid + DEC_THREADS * s;
-            pl[s] = hxp + min(k, A.H - 1);
+            pl[s] = A.hxl + xo + min(k, A.H - 1);
+            pd[s] = A.hxd + xo + min(k, A.H - 1);
             want[s] = k < A.H;
             dst[s] = &xl[min(k, XN - 1)];
         }
         uint32_t tg[XPT];
 #pragma unroll
         for (int s = 0; s < XPT; s++) tg[s] = tag - 1u;
-        ok = block_wait<DEC_THREADS, XPT>(tg, &sh_fail, pl, pl, want, dst, A.wait_ticks, A.err);
+        ok = block_wait<DEC_THREADS, XPT>(tg, &sh_fail, pl, pd, want, dst, A.wait_ticks, A.err);
         if (!ok) break;
 #pragma unroll
         for (int s = 0; s < XPT; s++) {
@@ -414,6 +425,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         }
     }
 
+    if constexpr (STACK) {
+#pragma unroll
+        for (int s = 0; s < XPT; s++) {
+            const int k = tid + DEC_THREADS * s;
+            if (k < XN) hraw[k] = xv[s];
+        }
+    }
     // ---- x -> LDS (ffn_norm first when asked: lfm2-engine.js:251-252) ----
     if (A.norm) {
         double ss = 0.0;   // padding adds exact zeros
@@ -449,7 +467,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         if (lane == 0) rsum[t][wave] = acc;
     }
     // (the residual rows have arrived before the arrival word goes out)
-    asm volatile("" : "+v"(hin));
+    if constexpr (!STACK) asm volatile("" : "+v"(hin));
     lds_barrier();
     // the last wave publishes (arrival, at the first layer: x and hidden
     // have been read; the router logits); waves 0..3 poll
@@ -463,8 +481,11 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         const uint64_t word = tag_word(tag, (float)s);
         store_local(&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
         if (gx == 0) {
+            // (stack launches: replicas [0, 8) for even layers, [8, 16) for odd)
+            constexpr int NREP = STACK ? SYNC_REPLICAS / 2 : SYNC_REPLICAS;
+            const int c0 = STACK ? (l & 1) * NREP : 0;
 #pragma unroll
-            for (int c = 0; c < SYNC_REPLICAS; c++) store_dev(&A.rdev[(size_t)c * SYNC_REPLICA_WORDS + e], word);
+            for (int c = 0; c < NREP; c++) store_dev(&A.rdev[(size_t)(c0 + c) * SYNC_REPLICA_WORDS + e], word);
         }
     }
     // x -> three int8 levels for the MFMA products; the rows of zeros
@@ -477,7 +498,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 
     {
         const uint64_t *pl[1] = {&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, A.E - 1)]};
-        const uint64_t *pd[1] = {&A.rdev[(size_t)(j % SYNC_REPLICAS) * SYNC_REPLICA_WORDS + min(tid, A.E - 1)]};
+        const int rc = STACK ? (l & 1) * (SYNC_REPLICAS / 2) + j % (SYNC_REPLICAS / 2) : j % SYNC_REPLICAS;
+        const uint64_t *pd[1] = {&A.rdev[(size_t)rc * SYNC_REPLICA_WORDS + min(tid, A.E - 1)]};
         bool want[1] = {tid < A.E};
         float *dst[1] = {&sh_lg[min(tid, EPL * WAVE - 1)]};
         const uint32_t tg[1] = {tag};
@@ -671,7 +693,7 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     {
         const int HW = A.K * FRb * QK;
         for (int i = tid; i < HW; i += DEC_THREADS) hl[i] = 0.0f;
-        for (int i = tid; i < DEC_MAX_FIN; i += DEC_THREADS) pf[i] = 0.0f;
+        for (int i = tid; i < (STACK ? DEC_MAX_FIN_STACK : DEC_MAX_FIN); i += DEC_THREADS) pf[i] = 0.0f;
     }
 
     // the next layer's router rows, bias and norm weights (stack launches)
@@ -804,7 +826,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     }
     lds_barrier();
     // waves 4..7 publish the pairs' sums (the polling waves 0..3 then hold no
-    // device stores to wait for)
+    // device stores to wait for); stack launches alternate two halves
+    const size_t ppar = STACK ? (size_t)(l & 1) * DEC_GROUPS * A.K * A.H : 0;
     if (ok && NP2 > 0) {
         for (int t = tid - DEC_THREADS / 2; t >= 0 && t < NP2 * 32; t += DEC_THREADS / 2) {
             const int p = t >> 5;
@@ -812,13 +835,75 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             const int k = (NRH == 2) ? (p >> 1) : p;
             const int rl = ((NRH == 2) ? (p & 1) : 0) * 32 + r;
             if (rl < RMm && !((mrank >> k) & 1u))
-                store_dev(&A.part[((size_t)gx * A.K + k) * A.H + r0 + rl], tag_word(tag, sh_pd[p][r]));
+                store_dev(&A.part[ppar + ((size_t)gx * A.K + k) * A.H + r0 + rl], tag_word(tag, sh_pd[p][r]));
         }
     }
 
     // ---- combine (lfm2-engine.js:459-486): y_k = sum of the groups' partials,
     // acc = fp32(acc + w_k y_k) in rank order, hidden += acc.  The arrival
     // words (of the first layer) are waited for before hidden is written ----
+    if constexpr (STACK) {
+        // member mi of every group: the 8 groups' partials of rows
+        // [r0, r0 + RM) (and, at the last layer, the arrival words)
+        const int NPm = DEC_GROUPS * A.K * RM;
+        if (ok) {
+            constexpr int IPT = DEC_MAX_FIN_STACK / DEC_THREADS;
+            const uint64_t *pl[IPT];
+            bool want[IPT];
+            float *dst[IPT];
+            uint32_t tg[IPT];
+            const float inv_krm = 1.0f / (float)(A.K * RM), inv_rm = 1.0f / (float)RM;
+#pragma unroll
+            for (int s2 = 0; s2 < IPT; s2++) {
+                const int i = tid + DEC_THREADS * s2;
+                const int ip = min(i, NPm - 1);
+                const int x = div_small(ip, inv_krm);
+                const int r = ip - x * A.K * RM;
+                const int k = div_small(r, inv_rm);
+                const int q = r - k * RM;
+                const int xb0 = (x * A.nbF) >> 3, xb1 = ((x + 1) * A.nbF) >> 3;   // DEC_GROUPS = 8
+                const uint64_t *pp = &A.part[ppar + ((size_t)x * A.K + k) * A.H + min(r0 + q, A.H - 1)];
+                const uint64_t *pa = &A.arrive[min(max(i - NPm, 0), G - 1)];
+                const bool isp = i < NPm;
+                pl[s2] = isp ? pp : pa;
+                want[s2] = isp ? (q < RMm && xb1 > xb0 && !((mrank >> k) & 1u)) : (last && i < NPm + G);
+                dst[s2] = isp ? &pf[min(i, DEC_MAX_FIN_STACK - 1)] : nullptr;
+                tg[s2] = isp ? tag : tag0;
+            }
+            ok = block_wait<DEC_THREADS, IPT>(tg, &sh_fail, pl, pl, want, dst, A.wait_ticks, A.err);
+        }
+        if (ok && tid < RMm) {
+            float acc = 0.0f;
+            for (int k0 = 0; k0 < A.K; k0 += 4) {   // four ranks' reads issued together
+                float v[4][DEC_GROUPS];
+                double w4[4];
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    const int k = min(k0 + kk, A.K - 1);
+#pragma unroll
+                    for (int x = 0; x < DEC_GROUPS; x++) v[kk][x] = pf[(x * A.K + k) * RM + tid];
+                    w4[kk] = sh_w[k];
+                }
+#pragma unroll
+                for (int kk = 0; kk < 4; kk++) {
+                    float y = 0.0f;
+#pragma unroll
+                    for (int x = 0; x < DEC_GROUPS; x++) y += v[kk][x];
+                    const int k = k0 + kk;
+                    if (k < A.K && !((mrank >> k) & 1u)) acc = (float)((double)acc + w4[kk] * (double)y);
+                }
+            }
+            const float hn = hraw[r0 + tid] + acc;
+            if (last) {
+                if (gx == 0) A.hidden[r0 + tid] = hn;
+            } else {
+                const size_t xo = ((size_t)(l & 1) * DEC_GROUPS + gx) * SYNC_X_WORDS + r0 + tid;
+                const uint64_t word = tag_word(tag, hn);
+                store_local(&A.hxl[xo], word);
+                store_dev(&A.hxd[xo], word);
+            }
+        }
+    } else {
     const int NP = DEC_GROUPS * A.K * RF;
     if (ok) {
         constexpr int NT = DEC_THREADS / 2;
@@ -871,10 +956,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
                 if (k < A.K && !((mrank >> k) & 1u)) acc = (float)((double)acc + w4[kk] * (double)y);
             }
         }
-        const float hn = hin + acc;
-        if (!STACK || last) A.hidden[q0 + tid] = hn;
-        else store_dev(&A.hx[(size_t)(l & 1) * SYNC_X_WORDS + q0 + tid], tag_word(tag, hn));
-        hin = hn;
+        A.hidden[q0 + tid] = hin + acc;
+    }
     }
     if constexpr (STACK) {
         if (!ok) break;
@@ -934,6 +1017,15 @@ static void launch_t(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, bool pp2)
 
 // (RE, EPL) pairs: with M <= 32 members per group, ceil(E / M) <= RE implies
 // ceil(E / 64) <= EPL for these four
+bool stack_decode_supported(const qq_ctx *ctx, const qq_moe *m)
+{
+    if (!decode_supported(ctx, m, 1) || m->H > SYNC_X_WORDS) return false;
+    const int M = decode_grid(ctx) / DEC_GROUPS;
+    const int RM = (m->H + M - 1) / M;
+    return DEC_GROUPS * m->K * RM + decode_grid(ctx) <= DEC_MAX_FIN_STACK &&
+           2 * (size_t)DEC_GROUPS * m->K * m->H <= SYNC_P_WORDS;
+}
+
 template <int NBW, bool STACK>
 static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re, bool pp2)
 {
@@ -979,7 +1071,8 @@ static void decode_common(qq_ctx *ctx, const qq_moe *m, DecodeArgs &a)
     a.hdev = ctx->sync_hdev;
     a.part = ctx->sync_part;
     a.arrive = ctx->sync_arrive;
-    a.hx = ctx->sync_hx;
+    a.hxl = ctx->sync_hx;
+    a.hxd = ctx->sync_hx + 2 * DEC_GROUPS * SYNC_X_WORDS;
     a.err = ctx->sync_err;
     a.wait_ticks = ctx->dec_wait_ticks;
 }

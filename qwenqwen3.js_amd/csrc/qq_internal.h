@@ -37,8 +37,9 @@ static_assert(SYNC_REPLICA_WORDS >= 2 * MAX_E, "slot table");
 constexpr int SYNC_H_WORDS = MAX_K * 4096;
 constexpr int SYNC_P_WORDS = 8 * MAX_K * 2048;
 constexpr int SYNC_ARRIVE_WORDS = 256;
-// Stack decode (several layers in one launch): the residual row after each
-// layer, in two alternating tables of up to SYNC_X_WORDS words.
+// Stack decode (several layers in one launch): each XCD group's residual row
+// after each layer, in two alternating sets of 8 tables of up to SYNC_X_WORDS
+// words, group-local and device-coherent.
 constexpr int SYNC_X_WORDS = 2048;
 constexpr int STACK_MAX_LAYERS = 256;
 // After a timed-out call the host moves the epoch on by this much: a
@@ -243,6 +244,8 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
 // Batch-1 decode in one launch (decode.hip); its exchange tables live in the
 // context's sync area, so it needs no scratch.
 bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T);
+// ... and a whole stack of such layers in one launch
+bool stack_decode_supported(const qq_ctx *ctx, const qq_moe *m);
 // ffn_norm folded into a forward: x = rmsnorm(x) * w (w NULL: unit weight).
 struct NormArgs {
     const float *w;
