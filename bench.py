@@ -169,45 +169,91 @@ def make_matvec_weight(torch, ctx, seed):
     return ctx.upload_q8_0_dev(blocks.data_ptr(), blocks.numel(), MV_IN, MV_OUT, 1)
 
 
-def _node_bench(mode, seconds):
+CPU_RUNS = 5
+
+
+def _cpu_job(kind, shape, d):
+    """Raw input files for the Node baseline, from the oracle's seeded generator
+    (oracle/synth.py): Q8_0 int8 uniform in [-127, 127] with fp16 scales
+    |N(0,1)| * 0.002, the F32 router N(0, 0.02), the bias U(-0.01, 0.01), and
+    x and hidden rows N(0,1) -- the distributions of the GPU run's inputs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import synth
+
+    def raw(name, arr):
+        path = os.path.join(d, name)
+        np.ascontiguousarray(arr).tofile(path)
+        return path
+
+    if kind == "matvec":
+        w, _ = synth.matvec_case(31, MV_IN, MV_OUT)
+        x = np.random.default_rng(32).standard_normal((64, MV_IN)).astype(np.float32)
+        return {"kind": "matvec", "in_dim": MV_IN, "out_dim": MV_OUT, "weight": raw("w.bin", w),
+                "x": raw("x.bin", x)}
+    Hs, Fs, Es, Ks, gating = SHAPES[shape]
+    L = synth.moe_layer(41, H=Hs, F=Fs, E=Es, K=Ks, bias=None if gating == "softmax" else "uniform",
+                        gating=gating)
+    x, hid = synth.activations(42, 64, Hs)
+    job = {"kind": "moe", "H": Hs, "F": Fs, "E": Es, "K": Ks, "gating": gating,
+           "router": raw("router.bin", L["router"]), "router_type": L["router_type"],
+           "gate": raw("gate.bin", L["gate"]), "up": raw("up.bin", L["up"]), "down": raw("down.bin", L["down"]),
+           "x": raw("x.bin", x), "hidden": raw("hidden.bin", hid)}
+    if L.get("bias") is not None:
+        job["bias"] = raw("bias.bin", L["bias"])
+    return job
+
+
+def _node_job(kind, shape, seconds):
+    """Median rate of CPU_RUNS bounded runs of the Node baseline, or None
+    without node."""
     import shutil
+    import tempfile
     node = shutil.which("node")
     if not node:
         return None
-    p = subprocess.run([node, os.path.join(ROOT, "oracle", "moe_ref.js"), mode, str(seconds)],
-                       capture_output=True, text=True, timeout=seconds * 4 + 120, check=True)
+    base = "/dev/shm" if os.path.isdir("/dev/shm") else None
+    with tempfile.TemporaryDirectory(dir=base) as d:
+        job = _cpu_job(kind, shape, d)
+        jp = os.path.join(d, "job.json")
+        with open(jp, "w") as f:
+            json.dump(job, f)
+        per_run = max(seconds / CPU_RUNS, 0.5)
+        p = subprocess.run([node, os.path.join(ROOT, "oracle", "moe_ref.js"), "bench-job", jp,
+                            str(CPU_RUNS), str(per_run)],
+                           capture_output=True, text=True, timeout=seconds * 4 + 300, check=True)
     return json.loads(p.stdout.strip().splitlines()[-1])
 
 
 def cpu_baseline(seconds, kind, shape="lfm2"):
     """The reference's CPU path restated for Node 12 (oracle/moe_ref.js: same loop
     order and float64 arithmetic as src/tensor.js / src/lfm2-engine.js, checked bit
-    for bit against the C oracle by the tests), timed on one host thread on a
-    bounded sample.  Without node, the C oracle is timed instead."""
+    for bit against the C oracle by the tests), timed on one host thread: the
+    median of CPU_RUNS bounded runs of single-token calls on the oracle
+    generator's inputs.  Without node, the C oracle is timed instead."""
     ncores = os.cpu_count() or 0
-    if kind == "matvec":
-        r = _node_bench("bench-matvec", seconds)
-        if r:
-            return {"value": round(r["matvecs_per_s"], 3), "unit": "matvecs/s", "cores": 1,
-                    "kind": "port",
-                    "sample": "%d matmulQ80xF32 calls (1024 -> 3072 Q8_0) in %.1f s: the "
-                              "reference's JS CPU path restated for Node %s, 1 thread of %d host "
-                              "cores" % (r["matvecs"], r["seconds"], r["node"], ncores)}
     if kind == "lfm2":
         return lfm2_cpu_baseline(seconds)
+    r = _node_job("matvec" if kind == "matvec" else "moe", shape, seconds)
+    if r and kind == "matvec":
+        return {"value": round(r["median_per_s"], 3), "unit": "matvecs/s", "cores": 1, "kind": "port",
+                "sample": "median of %d runs of %.1f s (%s matvecs/s) of matmulQ80xF32 (1024 -> 3072 "
+                          "Q8_0, x ~ N(0,1)): the reference's JS CPU path restated for Node %s, 1 thread "
+                          "of %d host cores" % (len(r["runs"]), r["seconds_per_run"],
+                                                ", ".join("%.1f" % v for v in r["runs"]), r["node"], ncores)}
     per = STACK_LAYERS if kind == "stack" else 1
-    r = _node_bench("bench-qwen3" if shape == "qwen3" else "bench", seconds)
     if r:
         what = ("Qwen3-MoE layer calls (H=2048, F=768, E=128, K=8, softmax routing, Q8_0 experts; "
                 "Qwen3Engine._moEFFN)" if shape == "qwen3" else
-                "MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts)")
+                "MoE-layer calls (H=2048, F=1792, E=32, K=4, Q8_0 experts; Lfm2Engine._moEFFN)")
         return {
-            "value": round(r["tokens_per_s"] / per, 4), "unit": "tokens/s", "cores": 1,
+            "value": round(r["median_per_s"] / per, 4), "unit": "tokens/s", "cores": 1,
             "kind": "port",
-            "sample": "%d single-token %s "
-                      "in %.1f s: the reference's JS CPU path restated for Node %s, 1 thread of %d "
-                      "host cores; tokens are independent, so tokens/s is the rate at any batch%s"
-                      % (r["tokens"], what, r["seconds"], r["node"], ncores,
+            "sample": "median of %d runs of %.1f s (%s tokens/s) of single-token %s on the oracle "
+                      "generator's inputs (int8 uniform, fp16 scales |N(0,1)|*0.002, router N(0,0.02), "
+                      "x N(0,1)): the reference's JS CPU path restated for Node %s, 1 thread of %d host "
+                      "cores; tokens are independent, so tokens/s is the rate at any batch%s"
+                      % (len(r["runs"]), r["seconds_per_run"], ", ".join("%.2f" % v for v in r["runs"]),
+                         what, r["node"], ncores,
                          "; divided by %d layers for the stack" % per if per > 1 else ""),
         }
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -479,7 +525,124 @@ def prefill_leg(torch, ctx, stream, steps, warmup, n_layers=4):
             k = kernels[name]
             out[name] = {"avg_us": k["avg_us"], "tflops": k["tflops"], "peak_tflops": MFMA_PEAK_TFLOPS,
                          "frac": round(k["tflops"] / MFMA_PEAK_TFLOPS, 4)}
+    _, out["roofline"] = roofline_of(prof, kernels, "prefill_2048")
+    ideal, target_ms = LEG_TARGETS["moe_layer_prefill_2048_zipf"]
+    out["ideal"] = ideal
+    out["target_ms_per_step"] = target_ms
+    out["meets_target"] = ms <= target_ms
     return out
+
+
+# BASELINE.md's ceilings: (ideal time at the roofline, the north-star target)
+LEG_TARGETS = {
+    "q8_0_matvec_1024x3072": ("0.42 us per matvec at 8 TB/s (launch bound)", None),
+    "moe_layer_decode_batch64": ("47.0 us per step at 8 TB/s", 78.3e-3),
+    "moe_layer_prefill_2048_zipf": ("72.2 us per step at 2.5 PFLOP/s", 180e-3),
+    "moe_stack22_decode_batch1": ("129 us per token at 8 TB/s", 216e-3),
+    "moe_stack22_prefill_4096": ("3.17 ms per chunk at 2.5 PFLOP/s", 7.94),
+}
+
+
+def leg(torch, ctx, stream, name, step, steps, warmup, tokens, launches, T, n_exp_fn, layers_per_step=1,
+        value_unit="tokens/s", extra=None):
+    """One configuration timed beside the headline line: `steps` steps of
+    step(i) between two events on the library stream (after `warmup`), then
+    the same steps again with per-launch events for the dominant kernel's
+    roofline.  tokens: rows per step (matvecs for the matvec leg)."""
+    total_ms = _time_steps(torch, ctx, stream, step, steps, warmup)
+    ctx.profile_enable(steps * launches)
+    for i in range(steps):
+        step(i)
+    prof = ctx.profile_read()
+    ctx.profile_enable(0)
+    ctx.synchronize()
+    n_exp = n_exp_fn()
+    kernels = kernel_table(prof, T, n_exp, T * K, decode_layers=layers_per_step if T == 1 else 1)
+    _, roof = roofline_of(prof, kernels, LEG_WORKLOADS.get(name, name))
+    ms = total_ms / steps
+    out = {"workload": name, "steps": steps, "ms_per_step": round(ms, 5),
+           "value": round(tokens / (ms / 1000.0), 1), "unit": value_unit, "roofline": roof,
+           "kernels": {k: {kk: v[kk] for kk in ("avg_us", "launches", "gbps", "tflops") if kk in v}
+                       for k, v in kernels.items()}}
+    if layers_per_step > 1 and T == 1:
+        out["us_per_token"] = round(ms * 1000.0, 2)
+    ideal, target_ms = LEG_TARGETS.get(name, (None, None))
+    out["ideal"] = ideal
+    if target_ms is not None:
+        out["target_ms_per_step"] = target_ms
+        out["meets_target"] = ms <= target_ms
+    if extra:
+        out.update(extra)
+    return out
+
+
+# leg name -> the --workload whose profiles/traffic_<workload>.json holds its traffic
+LEG_WORKLOADS = {"q8_0_matvec_1024x3072": "matvec", "moe_layer_decode_batch64": "decode_b64",
+                 "moe_layer_prefill_2048_zipf": "prefill_2048", "moe_stack22_decode_batch1": "stack22_decode",
+                 "moe_stack22_prefill_4096": "stack22_prefill"}
+
+
+def config_legs(torch, ctx, stream, layers, warmup):
+    """Configs 1, 3, 5a and 5b of the benchmark timed beside the batch-1 line
+    (config 4 is prefill_leg): the 1024 -> 3072 matvec over 80 rotated
+    weights; a 64-token decode batch over 4 of the line's layers; the 22-layer
+    stack (the line's 16 layers and 6 more, 8.2 GB) for one token and for a
+    4096-token chunk."""
+    legs = {}
+    gx = torch.Generator(device="cuda")
+    gx.manual_seed(7)
+    # config 1
+    n_w = 80
+    ws = [make_matvec_weight(torch, ctx, 500 + i) for i in range(n_w)]
+    Xm = torch.randn((16, MV_IN), generator=gx, device="cuda", dtype=torch.float32)
+    Ym = torch.empty((16, MV_OUT), device="cuda", dtype=torch.float32)
+    torch.cuda.synchronize()
+    legs["matvec"] = leg(torch, ctx, stream, "q8_0_matvec_1024x3072",
+                         lambda i: ws[i % n_w].matvec_dev(Xm[i % 16].data_ptr(), Ym[i % 16].data_ptr(), 1),
+                         400, warmup, 1, 2, 1, lambda: 0, value_unit="matvecs/s",
+                         extra={"weight_instances": n_w})
+    for w in ws:
+        w.release()
+    del Xm, Ym
+    # config 3
+    T = 64
+    X = torch.randn((2, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    HID = torch.randn((2, T, H), generator=gx, device="cuda", dtype=torch.float32)
+    idx = torch.empty((2, T, K), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    lay4 = layers[:4]
+    legs["decode_b64"] = leg(
+        torch, ctx, stream, "moe_layer_decode_batch64",
+        lambda i: lay4[i % 4].forward_dev(X[i % 2].data_ptr(), HID[i % 2].data_ptr(), T, idx_ptr=idx[i % 2].data_ptr()),
+        100, warmup, T, 10, T, lambda: float(np.mean([len(np.unique(idx[s].cpu().numpy())) for s in range(2)])),
+        extra={"layer_instances": 4})
+    del X, HID
+    # configs 5a and 5b
+    stack_layers = list(layers[:STACK_LAYERS])
+    extra_layers = [make_layer(torch, ctx, 1000 + i, "uniform") for i in range(len(stack_layers), STACK_LAYERS)]
+    stack_layers += extra_layers
+    st = ctx.moe_stack(stack_layers)
+    for T, steps, name in ((1, 100, "moe_stack22_decode_batch1"), (4096, 4, "moe_stack22_prefill_4096")):
+        HID = torch.randn((2, T, H), generator=gx, device="cuda", dtype=torch.float32)
+        idx = torch.empty((2, STACK_LAYERS, T, K), dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        legs["stack22_decode" if T == 1 else "stack22_prefill"] = leg(
+            torch, ctx, stream, name,
+            lambda i: st.forward_dev(HID[i % 2].data_ptr(), T, eps=1e-5, idx_ptr=idx[i % 2].data_ptr()),
+            steps, min(warmup, 2) if T > 1 else warmup, T, 12 * STACK_LAYERS, T,
+            lambda: float(np.mean([len(np.unique(idx[s, l].cpu().numpy())) for s in range(2)
+                                   for l in range(STACK_LAYERS)])),
+            layers_per_step=STACK_LAYERS,
+            extra={"layers": STACK_LAYERS, "per_layer": "rmsnorm(hidden) -> MoE -> hidden +=",
+                   "call": "qq_moe_stack_forward_dev (%s)" % ("one launch for the 22 layers" if T == 1
+                                                               else "layer after layer")})
+        del HID, idx
+    st.release()
+    for lay in extra_layers:
+        for t in getattr(lay, "_keep", ()):
+            t.release()
+        lay.release()
+    return legs
 
 
 def timed(torch, ctx, stream, step, period, steps, warmup, launches_per_step):
@@ -508,10 +671,14 @@ def timed(torch, ctx, stream, step, period, steps, warmup, launches_per_step):
     return eager_ms, graph_ms, prof
 
 
-def kernel_table(prof, T, n_exp, n_pairs):
+def kernel_table(prof, T, n_exp, n_pairs, decode_layers=1):
+    """Per-kernel averages; decode_layers: layers one decode launch runs (a
+    stack launch runs them all, so its algorithmic bytes are that many layers')."""
     kernels = {}
     for name, (ms, cnt) in prof.items():
         b = kernel_bytes(name, T, n_exp)
+        if name == "moe_decode" and b is not None:
+            b *= decode_layers
         avg_us = 1000.0 * ms / cnt
         kernels[name] = {"avg_us": round(avg_us, 3), "launches": cnt,
                          "bytes": None if b is None else int(b),
@@ -552,6 +719,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill-leg", action="store_true",
                     help="decode_b1: skip the 2048-token prefill GEMM leg reported beside the line")
+    ap.add_argument("--no-legs", action="store_true",
+                    help="decode_b1: skip the legs of configs 1, 3, 5a and 5b reported beside the line")
     ap.add_argument("--position0", type=int, default=0,
                     help="lfm2_decode: first position of the timed sequence (step i runs at "
                          "position0 + i %% 512)")
@@ -644,7 +813,7 @@ def main():
         n_exp = float(np.mean([len(np.unique(used[s, l])) for s in range(ns)
                                for l in range(used.shape[1])]))
         n_pairs = T * K
-        kernels = kernel_table(prof, T, n_exp, n_pairs)
+        kernels = kernel_table(prof, T, n_exp, n_pairs, decode_layers=STACK_LAYERS if stack and T == 1 else 1)
         dom, roofline = roofline_of(prof, kernels, args.workload)
         value, unit = T * args.steps / (total_ms / 1000.0), "tokens/s"
         config = {"workload": wname, "H": H, "F": F, "E": E, "K": K, "T": T,
@@ -670,6 +839,11 @@ def main():
             # beside `value`: the prefill GEMM's MFMA roofline on a 2048-token chunk
             extra["prefill_2048"] = prefill_leg(torch, ctx, stream, max(min(args.steps, 20), 5),
                                                 max(min(args.warmup, 3), 1))
+        if args.workload == "decode_b1" and not args.no_legs:
+            # beside `value`: every other configuration of the benchmark
+            extra["legs"] = config_legs(torch, ctx, stream, keep, max(min(args.warmup, 5), 1))
+            if "prefill_2048" in extra:
+                extra["legs"]["prefill_2048"] = extra["prefill_2048"]
 
     result = {
         "metric": LFM2_METRIC if kind == "lfm2" else METRIC,

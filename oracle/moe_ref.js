@@ -23,6 +23,11 @@
 //   node moe_ref.js bench <seconds>    time single-token MoE-layer calls on a
 //                                      seeded LFM2-8B-A1B-shaped layer; prints JSON
 //   node moe_ref.js bench-matvec <s>   time matmulQ80xF32 on a 1024 -> 3072 weight
+//   node moe_ref.js bench-job <job.json> <runs> <s>
+//                                      time single-token calls of a job's layer
+//                                      (or matvec) over its input rows: the rate
+//                                      of each of <runs> runs of <s> seconds and
+//                                      their median (the CPU baseline)
 
 const fs = require('fs');
 
@@ -367,6 +372,69 @@ function benchMatvec(seconds) {
                                           threads: 1, node: process.version }) + '\n');
 }
 
+// The CPU baseline: single-token calls of a job's layer (or matvec) over its
+// input rows, in `runs` runs of `seconds` each after a warm-up call; prints
+// the rate of every run and their median.  Tokens are independent in the
+// reference (src/lfm2-engine.js:550-555), so the per-token rate is the rate
+// at any batch.
+function benchJob(jobPath, runs, seconds) {
+    const job = JSON.parse(fs.readFileSync(jobPath, 'utf8'));
+    let step;
+    if (job.kind === 'matvec') {
+        const meta = { buffer: readRaw(job.weight), offset: 0, shape: [job.in_dim, job.out_dim], type: 8 };
+        const X = new Float32Array(readRaw(job.x));
+        const n = X.length / job.in_dim;
+        step = function (i) {
+            const r = i % n;
+            matmulQ80xF32(meta, X.subarray(r * job.in_dim, (r + 1) * job.in_dim));
+        };
+    } else {
+        const H = job.H, F = job.F, E = job.E, K = job.K;
+        const tensor = function (path, shape, type) {
+            return { buffer: readRaw(path), offset: 0, shape: shape, type: type };
+        };
+        const layer = {
+            routerWeight: tensor(job.router, [H, E], job.router_type),
+            expProbsBias: job.bias ? tensor(job.bias, [E], 0) : null,
+            ffnGateExps: tensor(job.gate, [H, F, E], 8),
+            ffnUpExps: tensor(job.up, [H, F, E], 8),
+            ffnDownExps: tensor(job.down, [F, H, E], 8),
+            nExpertsUsed: K,
+        };
+        const X = new Float32Array(readRaw(job.x));
+        const hid = new Float32Array(readRaw(job.hidden));
+        const n = X.length / H;
+        const eng = { nExperts: E, nExpertsUsed: K, bufNormed: new Float32Array(H),
+                      bufHidden: new Float32Array(H), bufMoEOut: new Float32Array(H),
+                      expertMask: null, onRouterUpdate: null };
+        step = function (i) {
+            const r = i % n;
+            eng.bufNormed.set(X.subarray(r * H, (r + 1) * H));
+            eng.bufHidden.set(hid.subarray(r * H, (r + 1) * H));
+            if (job.gating === 'softmax') moEFFNSoftmax(eng, 0, layer);
+            else moEFFN(eng, 0, layer);
+        };
+    }
+    step(0);   // warm-up (JIT)
+    const rates = [];
+    let calls = 1;
+    for (let r = 0; r < runs; r++) {
+        let n = 0, el = 0;
+        const t0 = process.hrtime.bigint();
+        while (el < seconds) {
+            step(calls++);
+            n++;
+            el = Number(process.hrtime.bigint() - t0) / 1e9;
+        }
+        rates.push(n / el);
+    }
+    const sorted = rates.slice().sort(function (a, b) { return a - b; });
+    const med = sorted.length % 2 ? sorted[(sorted.length - 1) / 2]
+                                  : 0.5 * (sorted[sorted.length / 2 - 1] + sorted[sorted.length / 2]);
+    process.stdout.write(JSON.stringify({ runs: rates, median_per_s: med, calls: calls - 1,
+                                          seconds_per_run: seconds, threads: 1, node: process.version }) + '\n');
+}
+
 module.exports = { halfToNumber, matmulQ80xF32, matmulF32xF32, matmulGeneric, readWeightF32,
                    siluInPlace, mulInPlace, addVec, expertSlice, moEFFN, softmaxF32,
                    moEFFNSoftmax };
@@ -377,9 +445,10 @@ if (require.main === module) {
     else if (cmd === 'bench') bench(Number(process.argv[3] || 10), false);
     else if (cmd === 'bench-qwen3') bench(Number(process.argv[3] || 10), true);
     else if (cmd === 'bench-matvec') benchMatvec(Number(process.argv[3] || 10));
+    else if (cmd === 'bench-job') benchJob(process.argv[3], Number(process.argv[4] || 5), Number(process.argv[5] || 2));
     else {
         process.stderr.write('usage: node moe_ref.js run <job.json> | bench <seconds> | bench-qwen3 <seconds> | ' +
-                             'bench-matvec <seconds>\n');
+                             'bench-matvec <seconds> | bench-job <job.json> <runs> <seconds per run>\n');
         process.exit(2);
     }
 }
