@@ -137,6 +137,18 @@ def test_forward_long_context(tmp_path, start):
     m.release()
 
 
+@pytest.mark.parametrize("start", [1100, 3584])
+def test_forward_long_context_full_width(tmp_path, start):
+    """LFM2-8B-A1B attention widths (32 query / 8 KV heads of 64, H = 2048, a
+    dense FFN of 7168) past one 256-position chunk: positions 1100.. (5
+    chunks) and 3584.. (15 chunks of the 4096-position cache), each side's
+    cache zero below `start` (src/lfm2-engine.js:329-392)."""
+    _say("lfm2 full-width long context", start)
+    cfg = dict(synth.LFM2_8B_A1B, n_layers=2, attn_layers=(1,), n_dense=2, vocab=512, ctx=4096)
+    m, _ = _check_tokens(tmp_path, 14, cfg=cfg, tokens=TOKENS[:4], start=start)
+    m.release()
+
+
 def test_info_reset_and_host_entry_point(tmp_path):
     _say("lfm2 info/reset")
     cfg = synth.LFM2_TINY

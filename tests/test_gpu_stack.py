@@ -9,6 +9,11 @@ then `hidden += _moEFFN(x)`; a prompt is T sequential calls, :550-555).
   at every layer, the stack's total contribution within 1e-4 relative L2.
   The same tokens through the one-launch stack (qq_moe_stack_forward_dev):
   bit-equal to the layer-by-layer chain, routing and residual.
+* Prefill: the same 22 layers chained over one 4096-token chunk (the fp16
+  MFMA path, layer after layer through the stack entry point's batch path):
+  every row's routing at every layer bit-exact against the oracle's router fed
+  with the GPU's own input residual for that layer, and 16 sampled rows per
+  layer against oracle.moe_ffn on that same input within 1e-2.
 * Stacks of small layers (ffn_norm weights, expert masks, softmax gating,
   token batches): the one-launch stack bit-equal to the chain of
   qq_moe_forward_norm_dev calls, routing against the oracle.
@@ -44,48 +49,57 @@ def _release(m):
     m.release()
 
 
-def test_stack22_decode():
+@pytest.fixture(scope="module")
+def stack22():
+    """22 independently seeded full-shape layers: the oracle's dicts and the
+    device layers (8.2 GB resident), shared by the tests of this module."""
+    ctx = gpu_context()
+    Ls, layers = [], []
+    try:
+        for l in range(N_LAYERS):
+            Ls.append(synth.moe_layer(5000 + l))
+            layers.append(upload_layer(ctx, Ls[-1]))
+        _say("22 layers bound")
+        yield Ls, layers
+    finally:
+        for m in layers:
+            _release(m)
+
+
+def test_stack22_decode(stack22):
     import torch
     ctx = gpu_context()
+    Ls, layers = stack22
     n_tok = 2
     _, hid = synth.activations(501, n_tok, 2048)
     h_ref = hid.copy()
     idx_ref = np.empty((n_tok, N_LAYERS, 4), np.int32)
-    layers = []
+    for l, L in enumerate(Ls):
+        for t in range(n_tok):
+            x = oracle.rmsnorm_unit(h_ref[t], EPS)
+            out, idx, _, _ = oracle.moe_ffn(L, x[None], h_ref[t:t + 1])
+            h_ref[t] = out[0]
+            idx_ref[t, l] = idx[0]
+    HID = torch.from_numpy(hid.copy()).cuda()
+    IDX = torch.full((n_tok, N_LAYERS, 4), -1, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    for t in range(n_tok):
+        for l, m in enumerate(layers):
+            m.forward_norm_dev(HID[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX[t, l].data_ptr())
+    ctx.synchronize()
+    got_idx, got = IDX.cpu().numpy(), HID.cpu().numpy()
+    _say("one-launch stack")
+    stack = ctx.moe_stack(layers)
     try:
-        for l in range(N_LAYERS):
-            L = synth.moe_layer(5000 + l)
-            layers.append(upload_layer(ctx, L))
-            for t in range(n_tok):
-                x = oracle.rmsnorm_unit(h_ref[t], EPS)
-                out, idx, _, _ = oracle.moe_ffn(L, x[None], h_ref[t:t + 1])
-                h_ref[t] = out[0]
-                idx_ref[t, l] = idx[0]
-            del L
-            _say("layer", l, "bound")
-        HID = torch.from_numpy(hid.copy()).cuda()
-        IDX = torch.full((n_tok, N_LAYERS, 4), -1, dtype=torch.int32, device="cuda")
+        HID2 = torch.from_numpy(hid.copy()).cuda()
+        IDX2 = torch.full((n_tok, N_LAYERS, 4), -1, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
         for t in range(n_tok):
-            for l, m in enumerate(layers):
-                m.forward_norm_dev(HID[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX[t, l].data_ptr())
+            stack.forward_dev(HID2[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX2[t].data_ptr())
         ctx.synchronize()
-        got_idx, got = IDX.cpu().numpy(), HID.cpu().numpy()
-        _say("one-launch stack")
-        stack = ctx.moe_stack(layers)
-        try:
-            HID2 = torch.from_numpy(hid.copy()).cuda()
-            IDX2 = torch.full((n_tok, N_LAYERS, 4), -1, dtype=torch.int32, device="cuda")
-            torch.cuda.synchronize()
-            for t in range(n_tok):
-                stack.forward_dev(HID2[t].data_ptr(), 1, eps=EPS, idx_ptr=IDX2[t].data_ptr())
-            ctx.synchronize()
-            got2_idx, got2 = IDX2.cpu().numpy(), HID2.cpu().numpy()
-        finally:
-            stack.release()
+        got2_idx, got2 = IDX2.cpu().numpy(), HID2.cpu().numpy()
     finally:
-        for m in layers:
-            _release(m)
+        stack.release()
     np.testing.assert_array_equal(got_idx, idx_ref)
     np.testing.assert_array_equal(got2_idx, idx_ref)
     assert np.array_equal(got2.view(np.uint32), got.view(np.uint32))
@@ -93,6 +107,47 @@ def test_stack22_decode():
         err = rel_l2(got[t].astype(np.float64) - hid[t], h_ref[t].astype(np.float64) - hid[t])
         _say("token", t, "stack rel_l2", err)
         assert err < 1e-4, (t, err)
+
+
+def test_stack22_prefill_chain(stack22):
+    """The 22 layers over one 4096-token chunk (qq_moe_stack_forward_dev,
+    T = 4096: the fp16 MFMA path layer after layer).  The GPU's input residual
+    of each layer is read back and fed to the oracle: routing of all 4096 rows
+    bit-exact (idx, w, probs), and 16 sampled rows per layer within 1e-2 of
+    oracle.moe_ffn on the same input."""
+    import torch
+    ctx = gpu_context()
+    Ls, layers = stack22
+    T = 4096
+    _, hid = synth.activations(610, T, 2048)
+    rows = np.sort(np.random.default_rng(611).choice(T, 16, replace=False))
+    HID = torch.from_numpy(hid.copy()).cuda()
+    IDX = torch.empty((T, 4), dtype=torch.int32, device="cuda")
+    W = torch.empty((T, 4), dtype=torch.float64, device="cuda")
+    P = torch.empty((T, 32), dtype=torch.float32, device="cuda")
+    worst = 0.0
+    for l, (L, m) in enumerate(zip(Ls, layers)):
+        torch.cuda.synchronize()
+        h_in = HID.cpu().numpy()
+        stack = ctx.moe_stack([m])      # one layer: the same calls the 22-layer chunk makes
+        try:
+            stack.forward_dev(HID.data_ptr(), T, eps=EPS, idx_ptr=IDX.data_ptr(), w_ptr=W.data_ptr(),
+                              probs_ptr=P.data_ptr())
+            ctx.synchronize()
+        finally:
+            stack.release()
+        h_out = HID.cpu().numpy()
+        x = np.stack([oracle.rmsnorm_unit(r, EPS) for r in h_in])
+        r_idx, r_w, r_p = oracle.moe_route(L, x)
+        np.testing.assert_array_equal(IDX.cpu().numpy(), r_idx)
+        np.testing.assert_array_equal(W.cpu().numpy(), r_w)
+        np.testing.assert_array_equal(P.cpu().numpy(), r_p)
+        ref, _, _, _ = oracle.moe_ffn(L, x[rows], h_in[rows])
+        err = rel_l2(h_out[rows].astype(np.float64) - h_in[rows], ref.astype(np.float64) - h_in[rows])
+        worst = max(worst, err)
+        _say("layer", l, "sampled rows rel_l2", err)
+        assert err < 1e-2, (l, err)
+    _say("worst layer", worst)
 
 
 @pytest.mark.parametrize("shape,n,T,masked,weighted", [
