@@ -165,6 +165,9 @@ class MoEDevice {
         return new Promise(function (resolve) { resolve(dev.readF32Sync(buf, nElems)); });
     }
 
+    // Bound on the batch-1 decode kernel's device-side waits (qq_set_wait_limit).
+    setWaitLimit(microseconds) { this.native.setWaitLimit(this.ctx, microseconds | 0); }
+
     synchronize() {
         const dev = this;
         this._sync(function () { dev.native.synchronize(dev.ctx); });

@@ -812,6 +812,20 @@ static napi_value js_synchronize(napi_env env, napi_callback_info info)
     return NULL;
 }
 
+/* setWaitLimit(ctx, microseconds): qq_set_wait_limit */
+static napi_value js_set_wait_limit(napi_env env, napi_callback_info info)
+{
+    ARGS(2);
+    handle *ch = get_handle(env, argv[0], H_CTX);
+    if (!ch) return NULL;
+    qq_ctx *ctx = (qq_ctx *)ch->ptr;
+    int32_t us;
+    CHECK_NAPI(env, napi_get_value_int32(env, argv[1], &us));
+    int rc = qq_set_wait_limit(ctx, us);
+    if (rc) return throw_qq(env, "qq_set_wait_limit", rc, ctx);
+    return NULL;
+}
+
 /* moeForwardDev(ctx, moe, xBuf, xOff, hiddenBuf, hiddenOff, T, mask | null,
  *               recordBuf | null, recordOff): qq_moe_forward_record_dev, enqueued */
 static napi_value js_moe_forward_dev(napi_env env, napi_callback_info info)
@@ -939,6 +953,7 @@ static napi_value module_init(napi_env env, napi_value exports)
         {"bufWrite", NULL, js_buf_write, NULL, NULL, NULL, napi_enumerable, NULL},
         {"bufRead", NULL, js_buf_read, NULL, NULL, NULL, napi_enumerable, NULL},
         {"synchronize", NULL, js_synchronize, NULL, NULL, NULL, napi_enumerable, NULL},
+        {"setWaitLimit", NULL, js_set_wait_limit, NULL, NULL, NULL, napi_enumerable, NULL},
         {"moeForwardDev", NULL, js_moe_forward_dev, NULL, NULL, NULL, napi_enumerable, NULL},
         {"matvecDev", NULL, js_matvec_dev, NULL, NULL, NULL, napi_enumerable, NULL},
         {"rmsnormDev", NULL, js_rmsnorm_dev, NULL, NULL, NULL, napi_enumerable, NULL},

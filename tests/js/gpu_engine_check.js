@@ -70,9 +70,12 @@ const layers = ABS.map(makeLayer);
 // The WebGPU engine classes of the scope: their own methods stand for the
 // WGSL path and must run only for engines that are not on the device.
 let webgpuCalls = 0;
+let resets = 0;
 class Lfm2GPUEngine {
     _moEFFNGPU() { webgpuCalls++; }
     _readbackRoutingData() { webgpuCalls++; return Promise.resolve(); }
+    _resetGPUState() { resets++; }
+    resetKVCache() { this._resetGPUState(); }
 }
 class Qwen3GPUEngine extends Lfm2GPUEngine {}
 const scope = { matmulGeneric: ref.matmulGeneric, Lfm2GPUEngine: Lfm2GPUEngine, Qwen3GPUEngine: Qwen3GPUEngine };
@@ -219,6 +222,42 @@ check('WebGPU methods not called for device engines', webgpuCalls === 0, { calls
     try { dev.moeForwardDev(layers[0], xb, hb, T + 1, { K: K, gating: SOFTMAX ? qq.GATING_SOFTMAX : qq.GATING_SIGMOID_BIAS }); }
     catch (e) { range = e instanceof RangeError; }
     check('rows past the buffer are a RangeError', range);
+}
+
+// ---- 5. a timed-out device wait (forced from the host with a zero bound)
+// leaves the engine's residual stream half updated: _moEFFNGPU refuses until
+// resetKVCache(), then runs exactly again ----
+{
+    const eng = makeEngine(true);
+    const host = new HostEngine();
+    const hid = new Float32Array(H), x = new Float32Array(H);
+    for (let i = 0; i < H; i++) { hid[i] = gauss(); x[i] = gauss(); }
+    dev.setWaitLimit(0);
+    let timedOut = false;
+    for (let t = 0; t < 4 && !timedOut; t++) {
+        dev.writeBuffer(eng._buf.hidden, 0, hid);
+        dev.writeBuffer(eng._buf.normed, 0, x);
+        eng._moEFFNGPU(ABS[0], { _moeIdx: 0 }, layers[0]);
+        try { dev.readF32Sync(eng._buf.hidden, H); } catch (e) { timedOut = /timed out/.test(e.message); }
+    }
+    dev.setWaitLimit(50000);
+    check('zero wait bound times out', timedOut);
+    let refused = false;
+    try { eng._moEFFNGPU(ABS[0], { _moeIdx: 0 }, layers[0]); } catch (e) { refused = /resetKVCache/.test(e.message); }
+    check('engine refuses after a timeout', refused);
+    eng.resetKVCache();
+    check('resetKVCache reached the engine', resets === 1, { resets: resets });
+    dev.writeBuffer(eng._buf.hidden, 0, hid);
+    dev.writeBuffer(eng._buf.normed, 0, x);
+    eng._moEFFNGPU(ABS[0], { _moeIdx: 0 }, layers[0]);
+    const hd = dev.readF32Sync(eng._buf.hidden, H);
+    const hr = hostBlock(host, 0, x, hid);
+    const err = relL2(hd.map(function (v, i) { return v - hid[i]; }), hr.map(function (v, i) { return v - hid[i]; }));
+    check('exact again after resetKVCache', err < 1e-4, { rel_l2: err });
+    // an engine made after the timeout starts valid
+    let fresh = true;
+    try { makeEngine(true)._moEFFNGPU(ABS[0], { _moeIdx: 0 }, layers[0]); dev.synchronize(); } catch (e) { fresh = false; }
+    check('an engine made after the timeout runs', fresh);
 }
 
 dev.release();

@@ -109,7 +109,7 @@ def test_js_matvec_matches_c_oracle(tmp_path):
 
 ADDON_EXPORTS = ["init", "lastError", "uploadQ80", "matvec", "moeCreate", "moeSetGating", "moeForward",
                  "ggufOpen", "ggufTensors", "ggufMoeParams", "ggufMoeLayer", "lfm2Create", "lfm2Info",
-                 "lfm2Forward", "lfm2Reset", "bufAlloc", "bufWrite", "bufRead", "synchronize",
+                 "lfm2Forward", "lfm2Reset", "bufAlloc", "bufWrite", "bufRead", "synchronize", "setWaitLimit",
                  "moeForwardDev", "matvecDev", "rmsnormDev", "release"]
 
 
