@@ -222,6 +222,9 @@ int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, 
  * QQ_E_HIP ("a device-side wait of the decode kernel timed out") rather
  * than the kernel waiting on.  0: a wait gives up at its first poll that
  * misses a word (for tests of that path).
+ * qq_moe_forward (host pointers) recovers by itself: when the decode
+ * launch's wait times out, the call runs again through the multi-launch
+ * path, which needs no co-residency, and returns its result.
  * What a failed call leaves: each row of hidden holds either its value
  * before the call or its correct new value (a workgroup writes its rows only
  * when all of its waits succeeded); idx/w/probs are not valid.  When the

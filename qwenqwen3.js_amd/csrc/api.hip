@@ -572,6 +572,13 @@ constexpr int T_CHUNK = 4096;
 // takes (H or F not a multiple of 32, unaligned activations).
 enum Path { PATH_MFMA, PATH_STREAM, PATH_GROUPED };
 
+// The one-launch decode kernel for this call (the host-pointer forward turns
+// it off for its retry after a timed-out wait).
+static bool use_decode(const qq_ctx *ctx, const qq_moe *m, int T)
+{
+    return !ctx->batch_only && decode_supported(ctx, m, T);
+}
+
 static Path chunk_path(const qq_ctx *ctx, const qq_moe *m, int tn, const float *x)
 {
     if (!mfma_supported(m) || ((uintptr_t)x & 15) != 0) return PATH_GROUPED;
@@ -581,7 +588,7 @@ static Path chunk_path(const qq_ctx *ctx, const qq_moe *m, int tn, const float *
 
 static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
 {
-    if (decode_supported(ctx, m, T)) return 0;
+    if (use_decode(ctx, m, T)) return 0;
     const int Tc = T < T_CHUNK ? T : T_CHUNK;
     size_t work = grouped_work_bytes(m, Tc);
     if (mfma_supported(m)) {
@@ -600,7 +607,7 @@ static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
                        const MaskBits &mask, int32_t *idx, double *w, float *probs, char *s)
 {
     int rc = QQ_OK;
-    if (decode_supported(ctx, m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs);
+    if (use_decode(ctx, m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs);
     const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
     double *part = reinterpret_cast<double *>(s);
     int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(router_work_bytes(m, (int)Tc)));
@@ -790,25 +797,38 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     const size_t ib = (size_t)T * m->K * 4, wb = (size_t)T * m->K * 8, pb = (size_t)T * m->E * 4;
     const size_t xa = align256(xb), ia = align256(ib), wa = align256(wb);
     const size_t io = 2 * xa + ia + wa + align256(pb);
-    if ((rc = ensure_scratch(ctx, io + forward_scratch(ctx, m, T)))) return rc;
     if ((rc = ensure_pinned(ctx, io))) return rc;
-    char *s = static_cast<char *>(ctx->scratch);
     char *ph = static_cast<char *>(ctx->pinned) + PIN_HDR;
     char *pd = ctx->pinned_dev + PIN_HDR;
-    float *dx = reinterpret_cast<float *>(s);
-    float *dh = reinterpret_cast<float *>(s + xa);
-    int32_t *didx = reinterpret_cast<int32_t *>(s + 2 * xa);
-    double *dw = reinterpret_cast<double *>(s + 2 * xa + ia);
-    float *dp = reinterpret_cast<float *>(s + 2 * xa + ia + wa);
-    memcpy(ph, x, xb);
-    memcpy(ph + xa, hidden, xb);
-    if ((rc = launch_stage_copy(ctx, pd, dx, 2 * xa))) return rc;
-    if ((rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, probs ? dp : nullptr, io))) return rc;
     // hidden .. the last routing output wanted, in whole 16-byte words (the
     // regions are 256-byte aligned, so the rounding stays inside them)
     const size_t out_span = (xa + ia + (probs ? wa + pb : (w ? wb : 0)) + 15) & ~(size_t)15;
-    if ((rc = launch_stage_copy(ctx, dh, pd + xa, out_span))) return rc;
-    if ((rc = check_device_error(ctx, true))) return rc;
+    // A batch-1 call runs the one-launch decode kernel, whose workgroups must
+    // all be resident at once.  When one of its waits timed out (the CUs were
+    // held by other work), the call is run again through the multi-launch
+    // path, which needs no co-residency: the caller's rows are untouched
+    // until the results are copied back, so the retry starts from them.
+    for (int attempt = 0;; attempt++) {
+        ctx->batch_only = attempt > 0;
+        rc = ensure_scratch(ctx, io + forward_scratch(ctx, m, T));
+        char *s = static_cast<char *>(ctx->scratch);
+        float *dx = reinterpret_cast<float *>(s);
+        float *dh = reinterpret_cast<float *>(s + xa);
+        int32_t *didx = reinterpret_cast<int32_t *>(s + 2 * xa);
+        double *dw = reinterpret_cast<double *>(s + 2 * xa + ia);
+        float *dp = reinterpret_cast<float *>(s + 2 * xa + ia + wa);
+        memcpy(ph, x, xb);
+        memcpy(ph + xa, hidden, xb);
+        const uint64_t timeouts = ctx->timeouts;
+        if (!rc) rc = launch_stage_copy(ctx, pd, dx, 2 * xa);
+        if (!rc) rc = forward_impl(ctx, m, dx, dh, T, mb, didx, dw, probs ? dp : nullptr, io);
+        if (!rc) rc = launch_stage_copy(ctx, dh, pd + xa, out_span);
+        if (!rc) rc = check_device_error(ctx, true);
+        ctx->batch_only = 0;
+        if (rc && attempt == 0 && ctx->timeouts != timeouts) continue;
+        if (rc) return rc;
+        break;
+    }
     memcpy(hidden, ph + xa, xb);
     if (idx) memcpy(idx, ph + 2 * xa, ib);
     if (w) memcpy(w, ph + 2 * xa + ia, wb);

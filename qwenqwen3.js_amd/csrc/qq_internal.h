@@ -149,6 +149,9 @@ struct qq_ctx {
     // the error word is read); device-resident state built across calls (an
     // LFM2 model's conv states and KV cache) is invalid after one
     uint64_t timeouts;
+    // set while a call must take the multi-launch path (a host-pointer
+    // forward's retry after a timed-out decode launch)
+    int batch_only;
     // a graph capture on `stream` is open (qq_capture_begin)
     int capturing;
     // token batches of at least this many rows take the fp16 MFMA path (0: never)

@@ -23,6 +23,8 @@ TYPE_Q8_0 = 8
 GATING_SIGMOID_BIAS = 0   # LFM2-MoE
 GATING_SOFTMAX = 1        # Qwen3-MoE
 QQ_WAIT_LIMIT_US_DEFAULT = 50000
+# the device epoch moves on by this much when a timed-out decode wait is reported
+SYNC_EPOCH_SKIP = 1024
 
 # Every symbol include/qq_moe.h declares (tests/test_abi.py keeps them in sync).
 EXPORTS = (

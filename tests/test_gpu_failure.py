@@ -226,3 +226,30 @@ def test_stack_zero_wait_bound_fails_loudly_and_recovers():
             for t in m._keep:
                 t.release()
             m.release()
+
+
+def test_host_call_recovers_through_the_multi_launch_path():
+    """qq_moe_forward under a zero wait bound: a timed-out decode launch is
+    run again through the multi-launch path (no co-residency needed), so
+    every call returns the oracle's routing and a result within 1e-4."""
+    print("host-pointer decode under wait bound 0", flush=True)
+    ctx = gpu_context()
+    L = full_layer(13)
+    m = upload_layer(ctx, L)
+    try:
+        x, h0 = synth.activations(34, 3, L["H"])
+        ref_h, ref_idx, ref_w, _ = oracle.moe_ffn(L, x, h0)
+        t0 = ctx.debug_epoch()
+        ctx.set_wait_limit(0)
+        try:
+            for t in range(3):
+                out, idx, w, _ = m.forward(x[t:t + 1], h0[t:t + 1])
+                assert np.array_equal(idx, ref_idx[t:t + 1])
+                assert np.array_equal(w, ref_w[t:t + 1])
+                assert rel_l2(moe_delta(out, h0[t:t + 1]), moe_delta(ref_h[t:t + 1], h0[t:t + 1])) < 1e-4
+        finally:
+            ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
+        # the decode launches did time out (the epoch moved past their tags)
+        assert (ctx.debug_epoch() - t0) % (1 << 32) >= qq_hip.SYNC_EPOCH_SKIP
+    finally:
+        m.release()
