@@ -20,7 +20,8 @@ static thread_local char g_init_err[512] = "";
 static size_t sync_table_words()
 {
     return (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS +
-           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 4 * 8 * (size_t)SYNC_X_WORDS;
+           2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 4 * 8 * (size_t)SYNC_X_WORDS +
+           SYNC_RP_WORDS + SYNC_RI_WORDS;
 }
 
 int set_error(qq_ctx *ctx, const char *fmt, ...)
@@ -121,7 +122,7 @@ static const char *const kKernelNames[K_COUNT] = {
     "repack_q8_0",      "q8_0_matvec",    "router_logits",  "router_topk",   "moe_decode",
     "dispatch",       "grouped_gateup", "grouped_down",  "combine",
     "cast_f16",         "mfma_gateup",    "mfma_down",      "stream_gateup", "stream_down",
-    "rmsnorm", "lfm2_embed", "lfm2_matvec", "lfm2_attention",
+    "rmsnorm", "lfm2_embed", "lfm2_matvec", "lfm2_attention", "route_dispatch",
 };
 
 // After a timed-out call: clear the error word and move the epoch on by
@@ -160,7 +161,8 @@ int check_device_error(qq_ctx *ctx, bool staged)
         hipLaunchKernelGGL(sync_recover_kernel, dim3(1), dim3(1), 0, ctx->stream, ctx->sync_err, ctx->sync_epoch);
         QQ_HIP(ctx, hipGetLastError());
         QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        snprintf(ctx->err, sizeof ctx->err, "a device-side wait of the decode kernel timed out (code %u)", e);
+        snprintf(ctx->err, sizeof ctx->err,
+                 "a device-side wait of the decode or fused routing kernel timed out (code %u)", e);
         return QQ_E_HIP;
     }
     return QQ_OK;
@@ -306,8 +308,10 @@ int qq_init(int device, qq_ctx **out)
     ctx->sync_part = ctx->sync_hdev + SYNC_H_WORDS;
     ctx->sync_arrive = ctx->sync_part + SYNC_P_WORDS;
     ctx->sync_hx = ctx->sync_arrive + SYNC_ARRIVE_WORDS;
+    ctx->sync_rp = ctx->sync_hx + 4 * 8 * SYNC_X_WORDS;
+    ctx->sync_ri = ctx->sync_rp + SYNC_RP_WORDS;
     // error word and epoch each on a 128-byte line of their own
-    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_hx + 4 * 8 * SYNC_X_WORDS);
+    ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_ri + SYNC_RI_WORDS);
     ctx->sync_epoch = ctx->sync_err + 32;
     ctx->capturing = 0;
     *out = ctx;
@@ -579,6 +583,13 @@ static bool use_decode(const qq_ctx *ctx, const qq_moe *m, int T)
     return !ctx->batch_only && decode_supported(ctx, m, T);
 }
 
+// The one-launch router + top-K + dispatch for a stream-path chunk (off for
+// the host-pointer forward's retry, like the decode kernel).
+static bool use_route_fused(const qq_ctx *ctx, const qq_moe *m, int T, const float *x)
+{
+    return !ctx->batch_only && route_dispatch_supported(ctx, m, T, x);
+}
+
 static Path chunk_path(const qq_ctx *ctx, const qq_moe *m, int tn, const float *x)
 {
     if (!mfma_supported(m) || ((uintptr_t)x & 15) != 0) return PATH_GROUPED;
@@ -624,6 +635,14 @@ static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         // on the MFMA path the router launch also writes the fp16 rows
         void *xh = path == PATH_MFMA ? mfma_xh(m, tn, work) : nullptr;
         bool xh_done = false;
+        if (path == PATH_STREAM && use_route_fused(ctx, m, tn, cx)) {
+            const StreamDispatch d = stream_dispatch(m, tn, work);
+            if ((rc = launch_route_dispatch(ctx, m, cx, tn, mask, ci, cw, cp, d.counts, d.offsets, d.perm,
+                                            d.inv, d.tiles)))
+                return rc;
+            if ((rc = launch_moe_stream(ctx, m, cx, ch, tn, mask, ci, cw, work, true))) return rc;
+            continue;
+        }
         if ((rc = launch_router_topk(ctx, m, cx, tn, part, ci, cw, cp, xh, &xh_done))) return rc;
         switch (path) {
         case PATH_MFMA: rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work, xh_done); break;
@@ -803,10 +822,11 @@ int qq_moe_forward(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, 
     // hidden .. the last routing output wanted, in whole 16-byte words (the
     // regions are 256-byte aligned, so the rounding stays inside them)
     const size_t out_span = (xa + ia + (probs ? wa + pb : (w ? wb : 0)) + 15) & ~(size_t)15;
-    // A batch-1 call runs the one-launch decode kernel, whose workgroups must
-    // all be resident at once.  When one of its waits timed out (the CUs were
-    // held by other work), the call is run again through the multi-launch
-    // path, which needs no co-residency: the caller's rows are untouched
+    // A batch-1 call runs the one-launch decode kernel and a small batch the
+    // one-launch routing kernel, whose workgroups must all be resident at
+    // once.  When one of their waits timed out (the CUs were held by other
+    // work), the call is run again through the multi-launch path, which
+    // needs no co-residency: the caller's rows are untouched
     // until the results are copied back, so the retry starts from them.
     for (int attempt = 0;; attempt++) {
         ctx->batch_only = attempt > 0;

@@ -35,20 +35,6 @@ struct GrMT {
 // nothing depends on it: every slot row is computed on its own and the
 // combine reads slots through inv, so results are the same bit for bit.
 // ---------------------------------------------------------------------------
-// Exclusive scan over the 64 lanes; *total = sum of all lanes.
-__device__ __forceinline__ int wave_excl_scan(int v, int *total)
-{
-    const int lane = threadIdx.x & (WAVE - 1);
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const int u = __shfl_up(incl, o, WAVE);
-        if (lane >= o) incl += u;
-    }
-    *total = __shfl(incl, WAVE - 1, WAVE);
-    return incl - v;
-}
-
 constexpr int DISP_THREADS = 1024;
 constexpr int DISP_ROUND = 16;   // pair loads in flight per thread
 

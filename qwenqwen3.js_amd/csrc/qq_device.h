@@ -387,6 +387,20 @@ __device__ __forceinline__ size_t bm_index(int mat, int nb, int b, int rows, int
     return ((size_t)mat * nb + b) * rows + r;
 }
 
+// Exclusive scan over the 64 lanes; *total = sum of all lanes.
+__device__ __forceinline__ int wave_excl_scan(int v, int *total)
+{
+    const int lane = threadIdx.x & (WAVE - 1);
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < WAVE; o <<= 1) {
+        const int u = __shfl_up(incl, o, WAVE);
+        if (lane >= o) incl += u;
+    }
+    *total = __shfl(incl, WAVE - 1, WAVE);
+    return incl - v;
+}
+
 // Sigmoid routing for one token in one wavefront (lfm2-engine.js:420-447).
 // Lane e (+64*i) holds the fp32 logit of expert e.  Every lane returns the
 // same ranked selection: idx[k], unbiased probability p[k] and 1/S with

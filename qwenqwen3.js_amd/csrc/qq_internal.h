@@ -42,6 +42,10 @@ constexpr int SYNC_ARRIVE_WORDS = 256;
 // words, group-local and device-coherent.
 constexpr int SYNC_X_WORDS = 2048;
 constexpr int STACK_MAX_LAYERS = 256;
+// Fused routing and dispatch of a small token batch: the binary64 partial
+// logits [KS][T][E] as two tagged words each, and the expert ids [T][K].
+constexpr int SYNC_RP_WORDS = 2 * 8 * 128 * 128;
+constexpr int SYNC_RI_WORDS = 1024;
 // After a timed-out call the host moves the epoch on by this much: a
 // workgroup of that call that started after workgroup 0 advanced the epoch
 // wrote words tagged with the next call's tags (up to twice the call's layer
@@ -144,7 +148,7 @@ struct qq_ctx {
     // bound on the decode kernel's device-side waits, in 100 MHz wall-clock ticks
     uint64_t dec_wait_ticks;
     uint32_t *sync_epoch;
-    uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive, *sync_hx;
+    uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive, *sync_hx, *sync_rp, *sync_ri;
     // device-side waits that timed out on this context so far (counted when
     // the error word is read); device-resident state built across calls (an
     // LFM2 model's conv states and KV cache) is invalid after one
@@ -186,6 +190,7 @@ enum KernelId {
     K_LFM2_EMBED,
     K_LFM2_MV,
     K_LFM2_ATTN,
+    K_ROUTE_DISPATCH,
     K_COUNT
 };
 
@@ -244,6 +249,14 @@ size_t router_work_bytes(const qq_moe *m, int T);
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
                        int32_t *idx, double *w, float *probs, void *xh = nullptr,
                        bool *xh_done = nullptr);
+// Router, top-K and dispatch of a small batch in one launch (all workgroups
+// resident, tagged-word exchange through the context's sync area); writes
+// what launch_router_topk and launch_dispatch together write.
+bool route_dispatch_supported(const qq_ctx *ctx, const qq_moe *m, int T, const float *x);
+struct DispatchTiles;
+int launch_route_dispatch(qq_ctx *ctx, const qq_moe *m, const float *x, int T, const MaskBits &mask,
+                          int32_t *idx, double *w, float *probs, int32_t *counts, int32_t *offsets,
+                          int32_t *perm, int32_t *inv, const DispatchTiles &tiles);
 // Batch-1 decode in one launch (decode.hip); its exchange tables live in the
 // context's sync area, so it needs no scratch.
 bool decode_supported(const qq_ctx *ctx, const qq_moe *m, int T);
@@ -346,8 +359,16 @@ void *mfma_xh(const qq_moe *m, int T, char *work);
 // Split-fp16 MFMA kernels with weights streamed into registers, for decode
 // batches at fp32 accuracy (stream.hip); same shape needs as the MFMA path.
 size_t stream_work_bytes(const qq_moe *m, int T);
+// The stream path's dispatch outputs inside `work`.
+struct StreamDispatch {
+    int32_t *counts, *offsets, *perm, *inv;
+    DispatchTiles tiles;
+};
+StreamDispatch stream_dispatch(const qq_moe *m, int T, char *work);
+// dispatched: `work` already holds the dispatch of idx (stream_dispatch)
 int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                      const MaskBits &mask, const int32_t *idx, const double *w, char *work);
+                      const MaskBits &mask, const int32_t *idx, const double *w, char *work,
+                      bool dispatched = false);
 int launch_rmsnorm(qq_ctx *ctx, const float *x, const float *w, float *out, int T, int H,
                    double eps);
 int launch_moe_grouped(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,

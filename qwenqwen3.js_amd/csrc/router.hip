@@ -253,6 +253,311 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small token batches: router logits, top-K and the dispatch in one launch.
+// Grid (ceil(T/16), KS, ceil(E/32)) of 256 threads, every workgroup resident.
+//  1. Each workgroup forms the binary64 partial logits of its 16 tokens x 32
+//     experts x H slice on the matrix cores (as router_mfma_kernel) and
+//     publishes each as two tagged words (low and high half).
+//  2. The workgroups of expert tile 0 then take 16 / KS tokens each, one wave
+//     per token: the KS partials of every expert, added in slice order, the
+//     gating and stable top-K of router_topk_kernel (wave_route); the token's
+//     routing is stored and its expert ids published as tagged words.
+//  3. Workgroup 0 gathers the T K expert ids and does the dispatch of
+//     moe_dispatch_kernel: counts, exclusive offsets, row tiles, and slots
+//     handed out with LDS atomics (order within an expert unspecified).
+// Tags are the decode kernel's: the device epoch + 1, advanced by workgroup 0
+// at the end, after every workgroup has published (and so read the epoch).
+// Every wait is bounded; on expiry the error word is set and the workgroup
+// skips what is left.
+// ---------------------------------------------------------------------------
+struct FusedRouteArgs {
+    const float *x;
+    int T;
+    RouterW W;
+    int kchunk, KS;
+    const float *bias;
+    int softmax, K;
+    MaskBits mask;
+    int32_t *idx;          // [T][K]
+    double *w;             // [T][K]
+    float *probs;          // [T][E] or NULL
+    int32_t *counts, *offsets, *perm, *inv;
+    DispatchTiles tiles;
+    uint32_t *epoch_word;
+    uint64_t *pw;          // [KS][T][E][2] tagged halves of the partial logits
+    uint64_t *iw;          // [T][K] tagged expert ids
+    uint32_t *err;
+    uint64_t wait_ticks;
+};
+
+// Bounded wait of one wave for its N words per lane at p[i] (want[i]) to
+// carry `tag`; the low halves go to v[i].  Returns false when it gave up.
+template <int N>
+__device__ __forceinline__ bool wave_wait(const uint64_t *(&p)[N], const bool (&want)[N], uint32_t tag,
+                                          uint32_t (&v)[N], uint64_t wait_ticks, const uint32_t *err)
+{
+    bool need[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) need[i] = want[i];
+    const uint64_t t0 = wall_clock64();
+    while (true) {
+        uint64_t u[N];
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            u[i] = need[i] ? __hip_atomic_load(p[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        bool mine = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            if (!need[i]) continue;
+            if ((uint32_t)(u[i] >> 32) == tag) {
+                need[i] = false;
+                v[i] = (uint32_t)u[i];
+            } else {
+                mine = false;
+            }
+        }
+        if (__all(mine)) return true;
+        const uint64_t dt = wall_clock64() - t0;
+        if (dt >= wait_ticks ||
+            (dt > 1000 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)))
+            return false;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__device__ __forceinline__ void store_tagged(uint64_t *p, uint32_t tag, uint32_t bits)
+{
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int FR_MAX_KS = 8;
+constexpr int FR_MAX_P = 1024;      // T K pairs dispatched by one workgroup
+
+template <int EPL>
+__global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
+{
+    __shared__ double red[4][16][33];
+    __shared__ int cnt[MAX_E], cur[MAX_E], offs[MAX_E + 1];
+    __shared__ int pe[FR_MAX_P];
+    __shared__ uint32_t sh_tag;
+    __shared__ int sh_fail;
+    const int T = a.T, E = a.W.E, K = a.K, KS = a.KS;
+    const int t0 = blockIdx.x * 16, ks = blockIdx.y, e0 = blockIdx.z * 32;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const uint32_t epoch = __hip_atomic_load(a.epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
+        sh_tag = epoch + 1u;
+        sh_fail = 0;
+    }
+
+    // ---- 1. partial logits of 16 tokens x 32 experts over slice ks ----
+    {
+        const int r16 = lane & 15, kq = lane >> 4;
+        const int t = t0 + r16;
+        const double tz = t < T ? 1.0 : 0.0;
+        const float *xr = a.x + (size_t)min(t, T - 1) * a.W.H;
+        const int ka = ks * a.kchunk, kb = min(a.W.H, ka + a.kchunk);
+        d4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
+        constexpr int RB = 4;
+        const int ea = min(e0 + r16, E - 1), eb = min(e0 + 16 + r16, E - 1);
+        const double za = e0 + r16 < E ? 1.0 : 0.0, zb = e0 + 16 + r16 < E ? 1.0 : 0.0;
+        for (int k = ka + 16 * wave; k < kb; k += 64 * RB) {
+            float4 xv[RB], va[RB], vb[RB];
+#pragma unroll
+            for (int u = 0; u < RB; u++) {
+                const int kk = min(k + 64 * u, kb - 16) + 4 * kq;
+                xv[u] = *reinterpret_cast<const float4 *>(xr + kk);
+                va[u] = *reinterpret_cast<const float4 *>(a.W.f32 + (size_t)ea * a.W.H + kk);
+                vb[u] = *reinterpret_cast<const float4 *>(a.W.f32 + (size_t)eb * a.W.H + kk);
+            }
+#pragma unroll
+            for (int u = 0; u < RB; u++)
+                asm volatile("" : "+v"(xv[u].x), "+v"(xv[u].y), "+v"(xv[u].z), "+v"(xv[u].w),
+                                  "+v"(va[u].x), "+v"(va[u].y), "+v"(va[u].z), "+v"(va[u].w),
+                                  "+v"(vb[u].x), "+v"(vb[u].y), "+v"(vb[u].z), "+v"(vb[u].w));
+#pragma unroll
+            for (int u = 0; u < RB; u++) {
+                if (k + 64 * u >= kb) break;
+                const double xd[4] = {(double)xv[u].x * tz, (double)xv[u].y * tz, (double)xv[u].z * tz,
+                                      (double)xv[u].w * tz};
+                const double wa[4] = {(double)va[u].x * za, (double)va[u].y * za, (double)va[u].z * za,
+                                      (double)va[u].w * za};
+                const double wb[4] = {(double)vb[u].x * zb, (double)vb[u].y * zb, (double)vb[u].z * zb,
+                                      (double)vb[u].w * zb};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    acc0 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wa[j], acc0, 0, 0, 0);
+                    acc1 = __builtin_amdgcn_mfma_f64_16x16x4f64(xd[j], wb[j], acc1, 0, 0, 0);
+                }
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            red[wave][4 * r + kq][r16] = acc0[r];
+            red[wave][4 * r + kq][16 + r16] = acc1[r];
+        }
+    }
+    __syncthreads();
+    const uint32_t tag = sh_tag;
+    for (int i = tid; i < 16 * 32; i += 256) {
+        const int tt = i >> 5, ee = i & 31;
+        const double s = ((red[0][tt][ee] + red[1][tt][ee]) + red[2][tt][ee]) + red[3][tt][ee];
+        if (t0 + tt < T && e0 + ee < E) {
+            const uint64_t b = __double_as_longlong(s);
+            uint64_t *q = a.pw + (((size_t)ks * T + t0 + tt) * E + e0 + ee) * 2;
+            store_tagged(q, tag, (uint32_t)b);
+            store_tagged(q + 1, tag, (uint32_t)(b >> 32));
+        }
+    }
+
+    // ---- 2. routing of 16 / KS tokens (one wave each), expert tile 0 only ----
+    bool ok = true;
+    const int TPW = 16 / KS;
+    const int t = t0 + ks * TPW + wave;
+    if (blockIdx.z == 0 && wave < TPW && t < T) {
+        constexpr int NW = EPL * FR_MAX_KS * 2;
+        const uint64_t *p[NW];
+        bool want[NW];
+        uint32_t v[NW];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) {
+            const int e = min(lane + WAVE * i, E - 1);
+#pragma unroll
+            for (int k2 = 0; k2 < FR_MAX_KS; k2++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const int n = (i * FR_MAX_KS + k2) * 2 + h;
+                    p[n] = a.pw + (((size_t)min(k2, KS - 1) * T + t) * E + e) * 2 + h;
+                    want[n] = k2 < KS && lane + WAVE * i < E;
+                    v[n] = 0;
+                }
+        }
+        ok = wave_wait<NW>(p, want, tag, v, a.wait_ticks, a.err);
+        if (ok) {
+            float lg[EPL], bl[EPL];
+#pragma unroll
+            for (int i = 0; i < EPL; i++) {
+                double s = 0.0;
+#pragma unroll
+                for (int k2 = 0; k2 < FR_MAX_KS; k2++) {
+                    const int n = (i * FR_MAX_KS + k2) * 2;
+                    const double d = __longlong_as_double((long long)(((uint64_t)v[n + 1] << 32) | v[n]));
+                    if (k2 == 0) s = d;
+                    else if (k2 < KS) s += d;
+                }
+                lg[i] = (lane + WAVE * i < E) ? (float)s : 0.0f;
+                bl[i] = a.bias[min(lane + WAVE * i, E - 1)];
+            }
+            WaveRoute<EPL> R;
+            wave_route<EPL>(lg, bl, E, K, a.softmax != 0, R);
+            if (a.probs) {
+#pragma unroll
+                for (int i = 0; i < EPL; i++) {
+                    const int e = lane + WAVE * i;
+                    if (e < E) a.probs[(size_t)t * E + e] = R.prob[i];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < MAX_K; k++) {
+                if (k < K && lane == k) {
+                    a.idx[(size_t)t * K + k] = R.idx[k];
+                    a.w[(size_t)t * K + k] = (double)R.p[k] * R.inv;
+                    store_tagged(&a.iw[(size_t)t * K + k], tag, (uint32_t)R.idx[k]);
+                }
+            }
+        }
+        if (!ok && lane == 0) sh_fail = 1;
+    }
+
+    // ---- 3. the dispatch, by workgroup 0 ----
+    // After a failed wait it still writes a consistent, empty dispatch (no
+    // slots, every pair unrouted), so the expert kernels behind it do nothing.
+    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+        __syncthreads();
+        const int P = T * K;
+        constexpr int PPT = FR_MAX_P / 256;
+        if (sh_fail == 0) {
+            const uint64_t *p[PPT];
+            bool want[PPT];
+            uint32_t v[PPT];
+#pragma unroll
+            for (int i = 0; i < PPT; i++) {
+                const int q = tid + 256 * i;
+                p[i] = &a.iw[min(q, P - 1)];
+                want[i] = q < P;
+                v[i] = 0;
+            }
+            if (!wave_wait<PPT>(p, want, tag, v, a.wait_ticks, a.err)) sh_fail = 1;
+#pragma unroll
+            for (int i = 0; i < PPT; i++)
+                if (tid + 256 * i < P) pe[tid + 256 * i] = (int)v[i];
+        }
+        for (int e = tid; e < E; e += 256) {
+            cnt[e] = 0;
+            cur[e] = 0;
+        }
+        __syncthreads();
+        const bool good = sh_fail == 0;
+        if (good) {
+            for (int q = tid; q < P; q += 256) {
+                const int e = pe[q];
+                if ((unsigned)e < (unsigned)E && !mask_has(a.mask, e)) atomicAdd(&cnt[e], 1);
+            }
+        }
+        __syncthreads();
+        if (wave == 0) {
+            // exclusive scans of the expert counts and of their row tiles
+            int run = 0, trun = 0;
+            for (int eb = 0; eb < E; eb += WAVE) {
+                const int e = eb + lane;
+                const int c = e < E ? cnt[e] : 0;
+                int tot;
+                const int o = run + wave_excl_scan(c, &tot);
+                if (e < E) {
+                    offs[e] = o;
+                    a.counts[e] = c;
+                    a.offsets[e] = o;
+                }
+                run += tot;
+                if (a.tiles.bm > 0) {
+                    const int nte = (c + a.tiles.bm - 1) / a.tiles.bm;
+                    int ttot;
+                    int tt = trun + wave_excl_scan(nte, &ttot);
+                    for (int m0 = 0; m0 < c && tt < a.tiles.cap; m0 += a.tiles.bm, tt++) {
+                        a.tiles.e[tt] = e;
+                        a.tiles.m0[tt] = m0;
+                    }
+                    trun += ttot;
+                }
+            }
+            if (lane == 0) {
+                offs[E] = run;
+                a.offsets[E] = run;
+                if (a.tiles.bm > 0) *a.tiles.n = min(trun, a.tiles.cap);
+            }
+        }
+        __syncthreads();
+        for (int q = tid; q < P; q += 256) {
+            const int e = good ? pe[q] : -1;
+            if ((unsigned)e < (unsigned)E && !mask_has(a.mask, e)) {
+                const int pos = offs[e] + atomicAdd(&cur[e], 1);
+                a.perm[pos] = q;
+                a.inv[q] = pos;
+            } else {
+                a.inv[q] = -1;
+            }
+        }
+        if (tid == 0) {
+            if (!good) atomicOr(a.err, 1u);
+            // every workgroup has published its partials, so has read the epoch
+            __hip_atomic_store(a.epoch_word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else if (!ok && lane == 0) {
+        atomicOr(a.err, 1u);
+    }
+}
+
 // Number of H slices for T tokens: enough workgroups to spread over the chip,
 // at most ROUTER_MAX_SPLIT, and slices of at least 64 k.
 static int router_split(const qq_moe *m, int T)
@@ -315,6 +620,59 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
     else
         QQ_LAUNCH(ctx, (router_topk_kernel<MAX_E / WAVE>), dim3((T + 3) / 4), dim3(256), 0, part, KS, T,
                   m->E, m->K, m->bias, sm, idx, w, probs);
+    prof_end(ctx);
+    QQ_HIP(ctx, hipGetLastError());
+    return QQ_OK;
+}
+
+bool route_dispatch_supported(const qq_ctx *ctx, const qq_moe *m, int T, const float *x)
+{
+    if (m->router_type != QQ_TYPE_F32 || m->H % 16 != 0 || ((uintptr_t)x & 15) != 0 || m->E > 2 * WAVE)
+        return false;
+    const int KS = router_split(m, T);
+    const size_t wgs = (size_t)((T + 15) / 16) * KS * ((m->E + 31) / 32);
+    // 16 / KS routing waves per workgroup of 4 waves
+    return KS >= 4 && KS <= FR_MAX_KS && 16 % KS == 0 && T * m->K <= FR_MAX_P &&
+           (size_t)KS * T * m->E * 2 <= SYNC_RP_WORDS && (size_t)T * m->K <= SYNC_RI_WORDS &&
+           wgs <= (size_t)ctx->num_cus;
+}
+
+int launch_route_dispatch(qq_ctx *ctx, const qq_moe *m, const float *x, int T, const MaskBits &mask,
+                          int32_t *idx, double *w, float *probs, int32_t *counts, int32_t *offsets,
+                          int32_t *perm, int32_t *inv, const DispatchTiles &tiles)
+{
+    FusedRouteArgs a;
+    a.x = x;
+    a.T = T;
+    a.W.f32 = m->router_f32;
+    a.W.qs = nullptr;
+    a.W.d = nullptr;
+    a.W.H = m->H;
+    a.W.E = m->E;
+    a.W.nb = (m->H + QK - 1) / QK;
+    a.KS = router_split(m, T);
+    a.kchunk = ((m->H + a.KS * 64 - 1) / (a.KS * 64)) * 64;
+    a.bias = m->bias;
+    a.softmax = m->gating == QQ_GATING_SOFTMAX ? 1 : 0;
+    a.K = m->K;
+    a.mask = mask;
+    a.idx = idx;
+    a.w = w;
+    a.probs = probs;
+    a.counts = counts;
+    a.offsets = offsets;
+    a.perm = perm;
+    a.inv = inv;
+    a.tiles = tiles;
+    a.epoch_word = ctx->sync_epoch;
+    a.pw = ctx->sync_rp;
+    a.iw = ctx->sync_ri;
+    a.err = ctx->sync_err;
+    a.wait_ticks = ctx->dec_wait_ticks;
+    const dim3 g((T + 15) / 16, a.KS, (m->E + 31) / 32);
+    prof_begin(ctx, K_ROUTE_DISPATCH);
+    if (m->E <= WAVE) QQ_LAUNCH(ctx, route_dispatch_kernel<1>, g, dim3(256), 0, a);
+    else QQ_LAUNCH(ctx, route_dispatch_kernel<2>, g, dim3(256), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     return QQ_OK;

@@ -382,28 +382,44 @@ size_t stream_work_bytes(const qq_moe *m, int T)
            2 * al256(cap * 4) + 256 + al256(P * m->F * 4) + al256(P * m->H * 4);
 }
 
+// work: counts | offsets | perm | inv | tile e | tile m0 | tile count | act | y
+StreamDispatch stream_dispatch(const qq_moe *m, int T, char *work)
+{
+    const size_t P = (size_t)T * m->K;
+    StreamDispatch d;
+    char *p = work;
+    d.counts = reinterpret_cast<int32_t *>(p);  p += al256((size_t)m->E * 4);
+    d.offsets = reinterpret_cast<int32_t *>(p); p += al256((size_t)(m->E + 1) * 4);
+    d.perm = reinterpret_cast<int32_t *>(p);    p += al256(P * 4);
+    d.inv = reinterpret_cast<int32_t *>(p);     p += al256(P * 4);
+    d.tiles.bm = 16 * stream_mf(m, T);
+    d.tiles.cap = stream_cap(m, T, d.tiles.bm);
+    d.tiles.e = reinterpret_cast<int32_t *>(p); p += al256((size_t)stream_cap(m, T, 16) * 4);
+    d.tiles.m0 = reinterpret_cast<int32_t *>(p);
+    p += al256((size_t)stream_cap(m, T, 16) * 4);
+    d.tiles.n = reinterpret_cast<int32_t *>(p);
+    return d;
+}
+
 int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                      const MaskBits &mask, const int32_t *idx, const double *w, char *work)
+                      const MaskBits &mask, const int32_t *idx, const double *w, char *work,
+                      bool dispatched)
 {
     const size_t P = (size_t)T * m->K;
     const int MF = stream_mf(m, T);
-    const int cap = stream_cap(m, T, 16 * MF);
-    char *p = work;
-    int32_t *counts = reinterpret_cast<int32_t *>(p);  p += al256((size_t)m->E * 4);
-    int32_t *offsets = reinterpret_cast<int32_t *>(p); p += al256((size_t)(m->E + 1) * 4);
-    int32_t *perm = reinterpret_cast<int32_t *>(p);    p += al256(P * 4);
-    int32_t *inv = reinterpret_cast<int32_t *>(p);     p += al256(P * 4);
-    DispatchTiles tiles;
-    tiles.bm = 16 * MF;
-    tiles.cap = cap;
-    tiles.e = reinterpret_cast<int32_t *>(p);          p += al256((size_t)stream_cap(m, T, 16) * 4);
-    tiles.m0 = reinterpret_cast<int32_t *>(p);         p += al256((size_t)stream_cap(m, T, 16) * 4);
-    tiles.n = reinterpret_cast<int32_t *>(p);          p += 256;
+    const StreamDispatch d = stream_dispatch(m, T, work);
+    const int cap = d.tiles.cap;
+    int32_t *counts = d.counts, *offsets = d.offsets, *perm = d.perm, *inv = d.inv;
+    const DispatchTiles &tiles = d.tiles;
+    char *p = work + al256((size_t)m->E * 4) + al256((size_t)(m->E + 1) * 4) + 2 * al256(P * 4) +
+              2 * al256((size_t)stream_cap(m, T, 16) * 4) + 256;
     float *act = reinterpret_cast<float *>(p);         p += al256(P * m->F * 4);
     float *y = reinterpret_cast<float *>(p);
 
-    int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, tiles);
-    if (rc) return rc;
+    if (!dispatched) {
+        const int rc = launch_dispatch(ctx, m, idx, (int)P, mask, counts, offsets, perm, inv, tiles);
+        if (rc) return rc;
+    }
 
     StreamArgs a;
     a.x = x;

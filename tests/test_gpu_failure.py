@@ -1,5 +1,5 @@
-"""Failure path of the batch-1 decode kernel's device-side waits, forced from
-the host (qq_set_wait_limit): with a zero bound every wait gives up at its
+"""Failure path of the device-side waits of the batch-1 decode kernel and of
+the one-launch routing and dispatch of small batches, forced from the host (qq_set_wait_limit): with a zero bound every wait gives up at its
 first poll that misses a word, the kernel still runs to its end, and the call
 either reports the timeout or -- when every wait happened to find its words
 on the first poll -- returns the correct result; never a wrong result without
@@ -250,6 +250,76 @@ def test_host_call_recovers_through_the_multi_launch_path():
         finally:
             ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
         # the decode launches did time out (the epoch moved past their tags)
+        assert (ctx.debug_epoch() - t0) % (1 << 32) >= qq_hip.SYNC_EPOCH_SKIP
+    finally:
+        m.release()
+
+
+def test_batch_routing_zero_wait_bound_fails_loudly_and_recovers():
+    """The one-launch router + top-K + dispatch of a 64-token batch under a
+    zero wait bound: a call that reports the timeout leaves hidden exactly as
+    it was (its dispatch is written empty, so the expert kernels behind it do
+    nothing), one that does not is correct; words left with the failed call's
+    tags are never accepted; the host-pointer call is run again through the
+    multi-launch path and is correct."""
+    import torch
+    print("batch routing wait bound 0, then default", flush=True)
+    ctx = gpu_context()
+    L = full_layer(12)
+    m = upload_layer(ctx, L)
+    T = 64
+    try:
+        x, h0 = synth.activations(35, T, L["H"])
+        ref_h, ref_idx, ref_w, _ = oracle.moe_ffn(L, x, h0)
+        dx = torch.from_numpy(x).cuda()
+        dh = torch.from_numpy(h0).cuda()
+        idx = torch.full((T, L["K"]), -1, dtype=torch.int32, device="cuda")
+        failed = 0
+        fail_e0 = None
+        ctx.set_wait_limit(0)
+        try:
+            for _ in range(3):
+                dh.copy_(torch.from_numpy(h0))
+                torch.cuda.synchronize()
+                e0 = ctx.debug_epoch()
+                m.forward_dev(dx.data_ptr(), dh.data_ptr(), T, idx_ptr=idx.data_ptr())
+                try:
+                    ctx.synchronize()
+                except qq_hip.QQError as e:
+                    assert "timed out" in str(e), e
+                    failed += 1
+                    fail_e0 = e0
+                    got = dh.cpu().numpy()
+                    assert np.array_equal(got.view(np.uint32), h0.view(np.uint32))
+                    assert (ctx.debug_epoch() - e0) % (1 << 32) >= qq_hip.SYNC_EPOCH_SKIP
+                    continue
+                assert ctx.debug_epoch() == (e0 + 1) % (1 << 32)
+                assert np.array_equal(idx.cpu().numpy(), ref_idx)
+                assert rel_l2(moe_delta(dh.cpu().numpy(), h0), moe_delta(ref_h, h0)) < 1e-4
+        finally:
+            ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
+        print("calls that timed out:", failed, "of 3", flush=True)
+        # workgroup 0 polls its token tile's other slices right after
+        # publishing its own, before the later workgroups have published
+        assert failed >= 1
+        for d in (1, 2):
+            ctx.debug_plant_words(fail_e0 + d)
+        dh.copy_(torch.from_numpy(h0))
+        torch.cuda.synchronize()
+        m.forward_dev(dx.data_ptr(), dh.data_ptr(), T, idx_ptr=idx.data_ptr())
+        ctx.synchronize()
+        assert np.array_equal(idx.cpu().numpy(), ref_idx)
+        assert rel_l2(moe_delta(dh.cpu().numpy(), h0), moe_delta(ref_h, h0)) < 1e-4
+        # the host-pointer call under a zero bound: retried without the fused launch
+        t0 = ctx.debug_epoch()
+        ctx.set_wait_limit(0)
+        try:
+            out, oidx, ow, _ = m.forward(x, h0)
+        finally:
+            ctx.set_wait_limit(qq_hip.QQ_WAIT_LIMIT_US_DEFAULT)
+        assert np.array_equal(oidx, ref_idx)
+        assert np.array_equal(ow, ref_w)
+        assert rel_l2(moe_delta(out, h0), moe_delta(ref_h, h0)) < 1e-4
         assert (ctx.debug_epoch() - t0) % (1 << 32) >= qq_hip.SYNC_EPOCH_SKIP
     finally:
         m.release()

@@ -294,6 +294,37 @@ def test_moe_mfma_mask_and_unsupported_shape():
         _check_moe(L2, x2, hid2, tol=TOL_GEMV)
 
 
+@pytest.mark.parametrize("case", [
+    dict(T=37, mask=2),                                              # ragged token tiles, masked experts
+    dict(T=256),                                                     # T K = 1024 pairs, the largest batch
+    dict(H=512, F=96, E=65, K=3, T=20),                              # two experts a lane, ragged
+    dict(H=1024, F=64, E=16, K=2, T=16, bias=None),
+    dict(H=2048, F=768, E=128, K=8, T=128, gating="softmax"),        # 256 workgroups
+    dict(H=2048, F=768, E=128, K=8, T=64, gating="softmax", mask=3),
+])
+def test_moe_batch_one_launch_routing(case):
+    """Small batches whose router, top-K and dispatch run as one launch
+    (workgroups exchange partial logits and expert ids as tagged words):
+    routing bit-exact, the layer within the batch tolerance."""
+    _say("moe one-launch routing", case)
+    case = dict(case)
+    T = case.pop("T")
+    nmask = case.pop("mask", 0)
+    if "H" in case:
+        kw = dict(case)
+        if kw.get("gating") == "softmax":
+            kw.update(bias=None, router_std=0.05)
+        L = synth.moe_layer(91, **kw)
+    else:
+        L = full_layer(2)
+    x, hid = synth.activations(92, T, L["H"])
+    mask = None
+    if nmask:
+        r_idx, _, _ = oracle.moe_route(L, x)
+        mask = {int(e) for e in r_idx[:nmask, 0]}
+    _check_moe(L, x, hid, mask=mask)
+
+
 # ---------------------------------------------------------------- Qwen3-MoE softmax gating
 
 @pytest.mark.parametrize("case", [
