@@ -72,6 +72,7 @@ WORKLOADS = {
     "stack22_prefill": ("stack", 4096, "uniform", "moe_stack22_prefill_4096"),
     "matvec": ("matvec", 1, None, "q8_0_matvec_1024x3072"),
     "qwen3_decode_b1": ("layer", 1, None, "qwen3moe_layer_decode_batch1", "qwen3"),
+    "qwen3_decode_b64": ("layer", 64, None, "qwen3moe_layer_decode_batch64", "qwen3"),
     "qwen3_prefill_2048": ("layer", 2048, None, "qwen3moe_layer_prefill_2048", "qwen3"),
     "lfm2_decode": ("lfm2", 1, "uniform", "lfm2_8b_a1b_token_decode"),
 }

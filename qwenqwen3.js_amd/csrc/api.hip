@@ -21,7 +21,7 @@ static size_t sync_table_words()
 {
     return (size_t)SYNC_REPLICAS * SYNC_REPLICA_WORDS + (size_t)SYNC_LOCAL_TABLES * SYNC_LOCAL_WORDS +
            2 * (size_t)SYNC_H_WORDS + SYNC_P_WORDS + SYNC_ARRIVE_WORDS + 4 * 8 * (size_t)SYNC_X_WORDS +
-           SYNC_RP_WORDS + SYNC_RI_WORDS;
+           2 * (size_t)SYNC_RP_WORDS + SYNC_RI_WORDS;
 }
 
 int set_error(qq_ctx *ctx, const char *fmt, ...)
@@ -309,7 +309,7 @@ int qq_init(int device, qq_ctx **out)
     ctx->sync_arrive = ctx->sync_part + SYNC_P_WORDS;
     ctx->sync_hx = ctx->sync_arrive + SYNC_ARRIVE_WORDS;
     ctx->sync_rp = ctx->sync_hx + 4 * 8 * SYNC_X_WORDS;
-    ctx->sync_ri = ctx->sync_rp + SYNC_RP_WORDS;
+    ctx->sync_ri = ctx->sync_rp + 2 * SYNC_RP_WORDS;   // after the XCD-local and device copies
     // error word and epoch each on a 128-byte line of their own
     ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_ri + SYNC_RI_WORDS);
     ctx->sync_epoch = ctx->sync_err + 32;

@@ -326,10 +326,8 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
 
     const int tid = threadIdx.x;
     const int lane = tid & (WAVE - 1);
-    const int wave = tid / WAVE;
     const int G = gridDim.x;
     const int j = blockIdx.x;
-    const int gx = j % DEC_GROUPS;   // group (XCD)
     const int mi = j / DEC_GROUPS;   // member
     const int M = G / DEC_GROUPS;
     const int NL = STACK ? a.L : 1;

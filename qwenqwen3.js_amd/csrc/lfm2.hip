@@ -189,7 +189,6 @@ __global__ __launch_bounds__(G * WPG * WAVE) void lfm2_mv_kernel(LmArgs a)
     const LmMat M = a.m[mat];
     const int h = lane & 1, rr = (lane >> 1) & (RPW - 1), sl = lane / (2 * RPW);
     const int row = row0 + rr;
-    const bool row_ok = row < M.rows;
     const int rc = min(row, M.rows - 1);
     const int first = wg * SPW + sl;     // this lane's first block of a chunk
     uint4 q[NBW];

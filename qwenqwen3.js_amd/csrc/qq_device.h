@@ -387,6 +387,61 @@ __device__ __forceinline__ size_t bm_index(int mat, int nb, int b, int rows, int
     return ((size_t)mat * nb + b) * rows + r;
 }
 
+// ---- tagged 64-bit exchange words: (tag << 32) | 32 data bits ----
+constexpr uint64_t RF_LOCAL_TICKS = 1000;   // 10 us on an XCD-local table, then the copy
+
+// Bounded wait of one wave for its N words per lane at p[i] (want[i]) to
+// carry `tag`; the low halves go to v[i].  With dev != 0, after
+// RF_LOCAL_TICKS the words are read at p[i] + dev instead (the device-
+// coherent copy).  Returns false when it gave up.
+template <int N>
+__device__ __forceinline__ bool wave_wait(const uint64_t *(&p)[N], const bool (&want)[N], uint32_t tag,
+                                          uint32_t (&v)[N], uint64_t wait_ticks, const uint32_t *err,
+                                          ptrdiff_t dev = 0)
+{
+    bool need[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) need[i] = want[i];
+    const uint64_t t0 = wall_clock64();
+    ptrdiff_t off = 0;
+    while (true) {
+        uint64_t u[N];
+#pragma unroll
+        for (int i = 0; i < N; i++)
+            u[i] = need[i] ? __hip_atomic_load(p[i] + off, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+        bool mine = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            if (!need[i]) continue;
+            if ((uint32_t)(u[i] >> 32) == tag) {
+                need[i] = false;
+                v[i] = (uint32_t)u[i];
+            } else {
+                mine = false;
+            }
+        }
+        if (__all(mine)) return true;
+        const uint64_t dt = wall_clock64() - t0;
+        if (dt >= wait_ticks ||
+            (dt > RF_LOCAL_TICKS && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)))
+            return false;
+        if (dt > RF_LOCAL_TICKS) off = dev;
+        __builtin_amdgcn_s_sleep(1);
+    }
+}
+
+__device__ __forceinline__ void store_tagged(uint64_t *p, uint32_t tag, uint32_t bits)
+{
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The same into the L2 of this XCD only (read there by agent-scope loads of
+// workgroups on the same XCD).
+__device__ __forceinline__ void store_tagged_local(uint64_t *p, uint32_t tag, uint32_t bits)
+{
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 // Exclusive scan over the 64 lanes; *total = sum of all lanes.
 __device__ __forceinline__ int wave_excl_scan(int v, int *total)
 {
@@ -404,8 +459,8 @@ __device__ __forceinline__ int wave_excl_scan(int v, int *total)
 // Sigmoid routing for one token in one wavefront (lfm2-engine.js:420-447).
 // Lane e (+64*i) holds the fp32 logit of expert e.  Every lane returns the
 // same ranked selection: idx[k], unbiased probability p[k] and 1/S with
-// S = 1e-6 + sum_k p[k] accumulated in rank order in binary64.  The argmax
-// order (score desc, index asc) is the order of a stable descending sort.
+// S = 1e-6 + sum_k p[k] accumulated in rank order in binary64.  The ranking
+// is a stable descending sort by selection score (ties to the lower index).
 template <int EPL>
 struct WaveRoute {
     int idx[MAX_K];
@@ -414,12 +469,13 @@ struct WaveRoute {
     float prob[EPL];   // this lane's sigmoid probabilities (expert lane + 64*i)
 };
 
-__device__ __forceinline__ bool rank_before(float av, int ai, float bv, int bi)
-{
-    if (ai == INT_MAX) return false;
-    if (bi == INT_MAX) return true;
-    return (av > bv) || (av == bv && ai < bi);
-}
+// LDS of one wave for wave_route: the sort keys and the selection.
+template <int EPL>
+struct __align__(16) RouteLds {
+    uint64_t key[EPL * WAVE];
+    int idx[MAX_K];
+    float p[MAX_K];
+};
 
 // Softmax gating (Qwen3-MoE, src/qwen3-engine.js:305-321 with softmaxInPlace,
 // src/tensor.js:150-164): probabilities p_e = fp32(fp32(exp(l_e - max)) * (1/S))
@@ -471,9 +527,15 @@ __device__ __forceinline__ void softmax_probs(const float (&logit)[EPL], int E, 
 
 // softmax: Qwen3 gating (bias unused); otherwise LFM2's sigmoid + bias.
 // bias[i] is the selection bias of expert lane + 64 i (any value past E).
+// The rank of each expert is the number of experts whose 64-bit key --
+// order-preserving score bits, then the complemented index -- is larger: a
+// stable descending sort, ties to the lower index (-0 counts as +0).  Every
+// lane counts against all keys at once (LDS broadcast reads), so no chain of
+// cross-lane steps sits on the path.  A wave's LDS accesses complete in
+// order, so its lanes read what its other lanes wrote without a barrier.
 template <int EPL>
 __device__ __forceinline__ void wave_route(const float (&logit)[EPL], const float (&bias)[EPL], int E,
-                                           int K, bool softmax, WaveRoute<EPL> &out)
+                                           int K, bool softmax, WaveRoute<EPL> &out, RouteLds<EPL> &lds)
 {
     const int lane = threadIdx.x & (WAVE - 1);
     float s[EPL];
@@ -493,39 +555,41 @@ __device__ __forceinline__ void wave_route(const float (&logit)[EPL], const floa
             }
         }
     }
-    uint32_t taken = 0;
+    uint64_t key[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane + WAVE * i;
+        const uint32_t u = __float_as_uint(s[i] + 0.0f);
+        const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+        key[i] = e < E ? (((uint64_t)ord << 32) | (uint32_t)~e) : 0;
+        lds.key[e] = key[i];
+    }
+    int rank[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) rank[i] = 0;
+    const int n2 = (E + 1) / 2;
+    for (int u = 0; u < n2; u++) {
+        const ulonglong2 q = reinterpret_cast<const ulonglong2 *>(lds.key)[u];
+#pragma unroll
+        for (int i = 0; i < EPL; i++) rank[i] += (int)(q.x > key[i]) + (int)(q.y > key[i]);
+    }
+#pragma unroll
+    for (int i = 0; i < EPL; i++) {
+        const int e = lane + WAVE * i;
+        if (e < E && rank[i] < K) {
+            lds.idx[rank[i]] = e;
+            lds.p[rank[i]] = out.prob[i];
+        }
+    }
     double sumW = softmax ? 0.0 : 1e-6;
 #pragma unroll
     for (int k = 0; k < MAX_K; k++) {   // fully unrolled: idx/p stay in registers
         out.idx[k] = INT_MAX;
         out.p[k] = 0.0f;
         if (k >= K) continue;
-        float bv = 0.0f, bp = 0.0f;
-        int bi = INT_MAX;
-#pragma unroll
-        for (int i = 0; i < EPL; i++) {
-            const int e = lane + WAVE * i;
-            if (e < E && !((taken >> i) & 1u) && (bi == INT_MAX || s[i] > bv)) {
-                bv = s[i];
-                bi = e;
-                bp = out.prob[i];
-            }
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) {
-            const float ov = __shfl_xor(bv, o, WAVE);
-            const int oi = __shfl_xor(bi, o, WAVE);
-            const float op = __shfl_xor(bp, o, WAVE);
-            if (rank_before(ov, oi, bv, bi)) {
-                bv = ov;
-                bi = oi;
-                bp = op;
-            }
-        }
-        if ((bi & (WAVE - 1)) == lane) taken |= 1u << (bi / WAVE);
-        out.idx[k] = bi;
-        out.p[k] = bp;
-        sumW = sumW + (double)bp;
+        out.idx[k] = lds.idx[k];
+        out.p[k] = lds.p[k];
+        sumW = sumW + (double)out.p[k];
     }
     out.inv = softmax ? (sumW > 0.0 ? 1.0 / sumW : 0.0) : 1.0 / sumW;
 }

@@ -43,7 +43,8 @@ constexpr int SYNC_ARRIVE_WORDS = 256;
 constexpr int SYNC_X_WORDS = 2048;
 constexpr int STACK_MAX_LAYERS = 256;
 // Fused routing and dispatch of a small token batch: the binary64 partial
-// logits [KS][T][E] as two tagged words each, and the expert ids [T][K].
+// logits [KS][T][E] as two tagged words each (an XCD-local and a device-
+// coherent copy), and the expert ids [T][K].
 constexpr int SYNC_RP_WORDS = 2 * 8 * 128 * 128;
 constexpr int SYNC_RI_WORDS = 1024;
 // After a timed-out call the host moves the epoch on by this much: a

@@ -210,6 +210,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const double *__restrict__ part, int KS, int T, int E, int K, const float *__restrict__ bias,
     int softmax, int32_t *__restrict__ idx, double *__restrict__ w, float *__restrict__ probs)
 {
+    __shared__ RouteLds<EPL> rl[4];
     const int lane = threadIdx.x & (WAVE - 1);
     const int t = blockIdx.x * 4 + threadIdx.x / WAVE;
     if (t >= T) return;
@@ -236,7 +237,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 #pragma unroll
     for (int i = 0; i < EPL; i++) bl[i] = bias[min(lane + WAVE * i, E - 1)];
     WaveRoute<EPL> R;
-    wave_route<EPL>(lg, bl, E, K, softmax != 0, R);
+    wave_route<EPL>(lg, bl, E, K, softmax != 0, R, rl[threadIdx.x / WAVE]);
     if (probs) {
 #pragma unroll
         for (int i = 0; i < EPL; i++) {
@@ -255,10 +256,18 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 
 // ---------------------------------------------------------------------------
 // Small token batches: router logits, top-K and the dispatch in one launch.
-// Grid (ceil(T/16), KS, ceil(E/32)) of 256 threads, every workgroup resident.
+// A 1-D grid of 256-thread workgroups, every one resident.  The dispatcher
+// deals workgroups to the 8 XCDs round robin (XCD = blockIdx % 8), and all
+// KS x ceil(E/32) workgroups of a token tile are placed on one XCD
+// (rf_place), so the exchange of the partial logits stays in that XCD's L2.
 //  1. Each workgroup forms the binary64 partial logits of its 16 tokens x 32
 //     experts x H slice on the matrix cores (as router_mfma_kernel) and
-//     publishes each as two tagged words (low and high half).
+//     publishes each as two tagged words (low and high half) into its XCD's
+//     table (L2) and, for a tile whose workgroups did not land on one XCD,
+//     into a device-coherent copy, which the waits fall back to after
+//     RF_LOCAL_TICKS.  The publishing waves are not the routing waves: a wave
+//     that has just stored device-scope words waits for their acknowledgement
+//     at its next load.
 //  2. The workgroups of expert tile 0 then take 16 / KS tokens each, one wave
 //     per token: the KS partials of every expert, added in slice order, the
 //     gating and stable top-K of router_topk_kernel (wave_route); the token's
@@ -285,50 +294,24 @@ struct FusedRouteArgs {
     int32_t *counts, *offsets, *perm, *inv;
     DispatchTiles tiles;
     uint32_t *epoch_word;
-    uint64_t *pw;          // [KS][T][E][2] tagged halves of the partial logits
+    uint64_t *pw;          // [KS][T][E][2] tagged halves of the partial logits, XCD-local copy
+    uint64_t *pwd;         // the same, device-coherent copy
     uint64_t *iw;          // [T][K] tagged expert ids
     uint32_t *err;
     uint64_t wait_ticks;
 };
 
-// Bounded wait of one wave for its N words per lane at p[i] (want[i]) to
-// carry `tag`; the low halves go to v[i].  Returns false when it gave up.
-template <int N>
-__device__ __forceinline__ bool wave_wait(const uint64_t *(&p)[N], const bool (&want)[N], uint32_t tag,
-                                          uint32_t (&v)[N], uint64_t wait_ticks, const uint32_t *err)
+// blockIdx.x -> (token tile, slice, expert tile): the NXY = KS ceil(E/32)
+// workgroups of token tile x take blocks x % 8 + 8 (NXY (x / 8) + j),
+// j < NXY, all on XCD x % 8.  False for the blocks past the tiles.
+__device__ __forceinline__ bool rf_place(int nx, int KS, int nxy, int &x, int &ks, int &z)
 {
-    bool need[N];
-#pragma unroll
-    for (int i = 0; i < N; i++) need[i] = want[i];
-    const uint64_t t0 = wall_clock64();
-    while (true) {
-        uint64_t u[N];
-#pragma unroll
-        for (int i = 0; i < N; i++)
-            u[i] = need[i] ? __hip_atomic_load(p[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
-        bool mine = true;
-#pragma unroll
-        for (int i = 0; i < N; i++) {
-            if (!need[i]) continue;
-            if ((uint32_t)(u[i] >> 32) == tag) {
-                need[i] = false;
-                v[i] = (uint32_t)u[i];
-            } else {
-                mine = false;
-            }
-        }
-        if (__all(mine)) return true;
-        const uint64_t dt = wall_clock64() - t0;
-        if (dt >= wait_ticks ||
-            (dt > 1000 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)))
-            return false;
-        __builtin_amdgcn_s_sleep(1);
-    }
-}
-
-__device__ __forceinline__ void store_tagged(uint64_t *p, uint32_t tag, uint32_t bits)
-{
-    __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int xcd = blockIdx.x & 7, loc = blockIdx.x >> 3;
+    x = xcd + 8 * (loc / nxy);
+    const int j = loc - nxy * (loc / nxy);
+    ks = j % KS;
+    z = j / KS;
+    return x < nx;
 }
 
 constexpr int FR_MAX_KS = 8;
@@ -340,16 +323,26 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
     __shared__ double red[4][16][33];
     __shared__ int cnt[MAX_E], cur[MAX_E], offs[MAX_E + 1];
     __shared__ int pe[FR_MAX_P];
+    __shared__ RouteLds<EPL> rl[4];
     __shared__ uint32_t sh_tag;
     __shared__ int sh_fail;
     const int T = a.T, E = a.W.E, K = a.K, KS = a.KS;
-    const int t0 = blockIdx.x * 16, ks = blockIdx.y, e0 = blockIdx.z * 32;
+    int bx, ks, bz;
+    if (!rf_place((T + 15) / 16, KS, KS * ((E + 31) / 32), bx, ks, bz)) return;
+    const int t0 = bx * 16, e0 = bz * 32;
+    const bool wg0 = bx == 0 && ks == 0 && bz == 0;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), wave = tid / WAVE;
+    const int TPW = 16 / KS;   // routing waves (tokens) per workgroup of expert tile 0
     const uint32_t epoch = __hip_atomic_load(a.epoch_word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         sh_tag = epoch + 1u;
         sh_fail = 0;
     }
+    // the expert biases of the routing waves, loaded now rather than after
+    // their wait
+    float bl[EPL];
+#pragma unroll
+    for (int i = 0; i < EPL; i++) bl[i] = a.bias[min(lane + WAVE * i, E - 1)];
 
     // ---- 1. partial logits of 16 tokens x 32 experts over slice ks ----
     {
@@ -398,24 +391,32 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
             red[wave][4 * r + kq][16 + r16] = acc1[r];
         }
     }
+    // (kept here: not sunk to its use behind the wait)
+#pragma unroll
+    for (int i = 0; i < EPL; i++) asm volatile("" : "+v"(bl[i]));
     __syncthreads();
     const uint32_t tag = sh_tag;
-    for (int i = tid; i < 16 * 32; i += 256) {
-        const int tt = i >> 5, ee = i & 31;
-        const double s = ((red[0][tt][ee] + red[1][tt][ee]) + red[2][tt][ee]) + red[3][tt][ee];
-        if (t0 + tt < T && e0 + ee < E) {
-            const uint64_t b = __double_as_longlong(s);
-            uint64_t *q = a.pw + (((size_t)ks * T + t0 + tt) * E + e0 + ee) * 2;
-            store_tagged(q, tag, (uint32_t)b);
-            store_tagged(q + 1, tag, (uint32_t)(b >> 32));
+    // publishers: the waves that do not route (all four when every wave routes)
+    const int pw0 = (bz == 0 && TPW < 4) ? TPW : 0;
+    if (wave >= pw0) {
+        for (int i = tid - WAVE * pw0; i < 16 * 32; i += WAVE * (4 - pw0)) {
+            const int tt = i >> 5, ee = i & 31;
+            const double s = ((red[0][tt][ee] + red[1][tt][ee]) + red[2][tt][ee]) + red[3][tt][ee];
+            if (t0 + tt < T && e0 + ee < E) {
+                const uint64_t b = __double_as_longlong(s);
+                const size_t o = (((size_t)ks * T + t0 + tt) * E + e0 + ee) * 2;
+                store_tagged_local(a.pw + o, tag, (uint32_t)b);
+                store_tagged_local(a.pw + o + 1, tag, (uint32_t)(b >> 32));
+                store_tagged(a.pwd + o, tag, (uint32_t)b);
+                store_tagged(a.pwd + o + 1, tag, (uint32_t)(b >> 32));
+            }
         }
     }
 
     // ---- 2. routing of 16 / KS tokens (one wave each), expert tile 0 only ----
     bool ok = true;
-    const int TPW = 16 / KS;
     const int t = t0 + ks * TPW + wave;
-    if (blockIdx.z == 0 && wave < TPW && t < T) {
+    if (bz == 0 && wave < TPW && t < T) {
         constexpr int NW = EPL * FR_MAX_KS * 2;
         const uint64_t *p[NW];
         bool want[NW];
@@ -433,9 +434,9 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
                     v[n] = 0;
                 }
         }
-        ok = wave_wait<NW>(p, want, tag, v, a.wait_ticks, a.err);
+        ok = wave_wait<NW>(p, want, tag, v, a.wait_ticks, a.err, a.pwd - a.pw);
         if (ok) {
-            float lg[EPL], bl[EPL];
+            float lg[EPL];
 #pragma unroll
             for (int i = 0; i < EPL; i++) {
                 double s = 0.0;
@@ -447,10 +448,9 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
                     else if (k2 < KS) s += d;
                 }
                 lg[i] = (lane + WAVE * i < E) ? (float)s : 0.0f;
-                bl[i] = a.bias[min(lane + WAVE * i, E - 1)];
             }
             WaveRoute<EPL> R;
-            wave_route<EPL>(lg, bl, E, K, a.softmax != 0, R);
+            wave_route<EPL>(lg, bl, E, K, a.softmax != 0, R, rl[wave]);
             if (a.probs) {
 #pragma unroll
                 for (int i = 0; i < EPL; i++) {
@@ -473,7 +473,7 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
     // ---- 3. the dispatch, by workgroup 0 ----
     // After a failed wait it still writes a consistent, empty dispatch (no
     // slots, every pair unrouted), so the expert kernels behind it do nothing.
-    if (blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0) {
+    if (wg0) {
         __syncthreads();
         const int P = T * K;
         constexpr int PPT = FR_MAX_P / 256;
@@ -666,10 +666,12 @@ int launch_route_dispatch(qq_ctx *ctx, const qq_moe *m, const float *x, int T, c
     a.tiles = tiles;
     a.epoch_word = ctx->sync_epoch;
     a.pw = ctx->sync_rp;
+    a.pwd = ctx->sync_rp + SYNC_RP_WORDS;
     a.iw = ctx->sync_ri;
     a.err = ctx->sync_err;
     a.wait_ticks = ctx->dec_wait_ticks;
-    const dim3 g((T + 15) / 16, a.KS, (m->E + 31) / 32);
+    const int nxy = a.KS * ((m->E + 31) / 32);
+    const dim3 g(8u * (unsigned)(((T + 15) / 16 + 7) / 8) * (unsigned)nxy);
     prof_begin(ctx, K_ROUTE_DISPATCH);
     if (m->E <= WAVE) QQ_LAUNCH(ctx, route_dispatch_kernel<1>, g, dim3(256), 0, a);
     else QQ_LAUNCH(ctx, route_dispatch_kernel<2>, g, dim3(256), 0, a);

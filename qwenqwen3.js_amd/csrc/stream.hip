@@ -4,7 +4,8 @@
 // With ~8 rows per expert (64 tokens, 32 experts, top-4) every weight is used
 // by very few rows, so the layer is bound by streaming the experts' Q8_0
 // weights from HBM once.  A workgroup owns one expert, one tile of 16*MF
-// slots and a group of 128 weight columns; its 4 waves split the reduction
+// slots and a group of weight columns (two halves of 16 NFH: 64 or 112 gate
+// and the same up features, 128 down columns); its 4 waves split the reduction
 // dimension block by block (each streaming its blocks straight into
 // registers, a few blocks ahead, below) and their partial sums are added in
 // wave order through LDS.
@@ -29,7 +30,6 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
 constexpr int ST_THREADS = 256;   // 4 waves split the reduction dimension
-constexpr int ST_NF = 8;          // 16-column fragments per workgroup (128 columns)
 
 struct StreamArgs {
     const float *x;          // [T][H] activations
@@ -82,42 +82,47 @@ __device__ __forceinline__ h8_t int8_to_f16x8(const uint2 q)
 // Operand stream.  Wave w reduces blocks w, w+4, w+8, ... of the reduction
 // dimension.  Every operand of a block goes straight to registers: the
 // lane's 8 activations of each of its MF rows (two float4), its 8 weight
-// bytes of each of the ST_NF fragment columns (uint2) and one fp16 scale per
-// column half: lane l loads column c0[h] + l's, and a fragment's scale is
-// taken from the lane that loaded it (lanes 16t .. 16t+15 hold the columns
-// of fragment t of each half).  Each wave keeps ST_PF blocks in flight: block i + ST_PF is
-// requested as soon as block i's products are done.  (Staged through LDS the
-// stream is held to ~100 KB in flight per CU by the LDS size.)
-// Fragment j: column 16*(j%4) + lane%16 of half j/4; lane l holds row l%16
-// of A and column l%16 of B at k = 8*(l/16) .. 8*(l/16) + 7 of the block.
+// bytes of each of the 2 NFH fragment columns (uint2) and one fp16 scale per
+// 64 columns of a half: load u of lane l reads column c0[h] + 64u + l's, and
+// a fragment's scale is taken from the lane that loaded it (fragment f of a
+// half: load f/4, lanes 16(f%4) .. 16(f%4)+15).  Each wave keeps st_pf
+// blocks in flight: block i + st_pf is requested as soon as block i's
+// products are done.  (Staged through LDS the stream is held to ~100 KB in
+// flight per CU by the LDS size.)
+// Fragment j: column 16*(j%NFH) + lane%16 of half j/NFH; lane l holds row
+// l%16 of A and column l%16 of B at k = 8*(l/16) .. 8*(l/16) + 7 of the block.
 // ---------------------------------------------------------------------------
-template <int MF>
+template <int MF, int NFH>
 struct StBlock {
+    static constexpr int NF = 2 * NFH;      // fragments
+    static constexpr int NS = (NFH + 3) / 4;   // scale loads per column half
     float4 a[MF][2];     // rows 16m + lane%16, k = 8*(lane/16) .. +7
-    uint2 q[ST_NF];      // fragment j's 8 weight bytes
-    uint32_t ds[2];      // scale bits of column c0[h] + lane of half h
+    uint2 q[NF];         // fragment j's 8 weight bytes
+    uint32_t ds[2][NS];  // scale bits of column c0[h] + 64 s + lane of half h
 };
 
-template <int MF>
-constexpr int st_pf() { return MF == 1 ? 3 : 2; }   // blocks in flight per wave
+// blocks in flight per wave: ~12-14 KB of weights either way
+template <int MF, int NFH>
+constexpr int st_pf() { return MF == 1 && NFH == 4 ? 3 : 2; }
 
-template <int MF>
+template <int MF, int NFH>
 struct StSrc {
+    static constexpr int NS = (NFH + 3) / 4;
     const char *abase;          // activation rows (bytes)
     uint32_t arow[MF];          // lane's row 16m + lane%16: byte offset + its k chunk
     const int8_t *qb[2];        // weights of column halves 0 / 1 at the expert's block 0
     const uint16_t *db[2];      // their scales
-    int cb[2];                  // column half h: the lane's column c0[h] + lane%16 (fragment j adds 16*(j%4))
+    int cb[2];                  // column half h: the lane's column c0[h] + lane%16 (fragment f of the half adds 16 f)
     int cmax;                   // last column (loads clamp to it)
-    uint32_t sc[2];             // column of this lane's scale load in half h (clamped)
+    uint32_t sc[2][NS];         // column of this lane's scale load s in half h (clamped)
     uint32_t qk;                // the lane's byte offset within a column's 32 bytes
     uint32_t qstep, dstep;      // one block: rows * 32 bytes, rows scales
     uint32_t okm;               // bit j: fragment j's column in range (else its scale is zero)
 };
 
 // 32-bit offsets from workgroup-uniform bases (one VGPR per address).
-template <int MF>
-__device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int kb)
+template <int MF, int NFH>
+__device__ __forceinline__ void st_load(StBlock<MF, NFH> &b, const StSrc<MF, NFH> &s, int kb)
 {
     const uint32_t ak = (uint32_t)kb * (QK * 4), qk = (uint32_t)kb * s.qstep, dk = (uint32_t)kb * s.dstep;
 #pragma unroll
@@ -129,9 +134,9 @@ __device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int 
     // every weight byte once, so those loads are non-temporal; with more
     // rows the expert's other row tiles read the same bytes through the L2
 #pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const uint32_t c = (uint32_t)min(s.cb[j >> 2] + 16 * (j & 3), s.cmax);
-        const uint2 *src = reinterpret_cast<const uint2 *>(s.qb[j >> 2] + (size_t)(qk + c * QK + s.qk));
+    for (int j = 0; j < 2 * NFH; j++) {
+        const uint32_t c = (uint32_t)min(s.cb[j / NFH] + 16 * (j % NFH), s.cmax);
+        const uint2 *src = reinterpret_cast<const uint2 *>(s.qb[j / NFH] + (size_t)(qk + c * QK + s.qk));
         if constexpr (MF == 1) {
             typedef unsigned int v2u __attribute__((ext_vector_type(2)));
             const v2u v = __builtin_nontemporal_load(reinterpret_cast<const v2u *>(src));
@@ -142,24 +147,28 @@ __device__ __forceinline__ void st_load(StBlock<MF> &b, const StSrc<MF> &s, int 
     }
 #pragma unroll
     for (int h = 0; h < 2; h++)
-        b.ds[h] = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(s.db[h]) +
-                                                      (size_t)(2u * (dk + s.sc[h])));
+#pragma unroll
+        for (int u = 0; u < StSrc<MF, NFH>::NS; u++)
+            b.ds[h][u] = *reinterpret_cast<const uint16_t *>(reinterpret_cast<const char *>(s.db[h]) +
+                                                             (size_t)(2u * (dk + s.sc[h][u])));
 }
 
 // The block's int8 weights enter the MFMA exactly (as fp16 integers); the
 // block's scale is applied to the block's fp32 partial sum:
 //   acc += d * (a_hi * q + a_lo * q).
 // A lane's four outputs of a fragment share one column, hence one scale.
-template <int MF>
-__device__ __forceinline__ void st_block(const StBlock<MF> &b, const StSrc<MF> &s, f4_t (&acc)[MF][ST_NF])
+template <int MF, int NFH>
+__device__ __forceinline__ void st_block(const StBlock<MF, NFH> &b, const StSrc<MF, NFH> &s,
+                                         f4_t (&acc)[MF][2 * NFH])
 {
     h8_t ah[MF], al[MF];
 #pragma unroll
     for (int m = 0; m < MF; m++) split8(b.a[m][0], b.a[m][1], ah[m], al[m]);
     const int l16 = threadIdx.x & 15;
 #pragma unroll
-    for (int j = 0; j < ST_NF; j++) {
-        const uint32_t bits = (uint32_t)__shfl((int)b.ds[j >> 2], 16 * (j & 3) + l16, WAVE);
+    for (int j = 0; j < 2 * NFH; j++) {
+        const int f = j % NFH;
+        const uint32_t bits = (uint32_t)__shfl((int)b.ds[j / NFH][f / 4], 16 * (f & 3) + l16, WAVE);
         const float d = ((s.okm >> j) & 1u) ? (float)__builtin_bit_cast(_Float16, (uint16_t)bits) : 0.0f;
         const h8_t qh = int8_to_f16x8(b.q[j]);
 #pragma unroll
@@ -173,24 +182,25 @@ __device__ __forceinline__ void st_block(const StBlock<MF> &b, const StSrc<MF> &
 }
 
 // Wave w reduces blocks w, w+4, w+8, ... of nb with st_pf blocks in flight.
-template <int MF>
-__device__ __forceinline__ void st_mainloop(const StSrc<MF> &s, int nb, int wave, f4_t (&acc)[MF][ST_NF])
+template <int MF, int NFH>
+__device__ __forceinline__ void st_mainloop(const StSrc<MF, NFH> &s, int nb, int wave,
+                                            f4_t (&acc)[MF][2 * NFH])
 {
-    constexpr int PF = st_pf<MF>();
+    constexpr int PF = st_pf<MF, NFH>();
     const int nblk = (nb - wave + 3) / 4;
-    StBlock<MF> r[PF];
+    StBlock<MF, NFH> r[PF];
 #pragma unroll
     for (int u = 0; u < PF; u++)
-        if (u < nblk) st_load<MF>(r[u], s, wave + 4 * u);
+        if (u < nblk) st_load<MF, NFH>(r[u], s, wave + 4 * u);
     for (int i = 0; i < nblk; i += PF) {
 #pragma unroll
         for (int u = 0; u < PF; u++) {
             if (i + u < nblk) {
-                st_block<MF>(r[u], s, acc);
+                st_block<MF, NFH>(r[u], s, acc);
                 // the refill goes out only after the products, so the
                 // compiler waits for this block alone, not the ones behind it
                 __builtin_amdgcn_sched_barrier(0);
-                if (i + u + PF < nblk) st_load<MF>(r[u], s, wave + 4 * (i + u + PF));
+                if (i + u + PF < nblk) st_load<MF, NFH>(r[u], s, wave + 4 * (i + u + PF));
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -200,8 +210,8 @@ __device__ __forceinline__ void st_mainloop(const StSrc<MF> &s, int nb, int wave
 // Load offsets: activation row r of the tile has byte offset rowoff(r);
 // weight halves start at columns c0[0], c0[1] of a matrix with `rows`
 // columns per block (clamped into range).
-template <int MF, typename RowOff>
-__device__ __forceinline__ void st_offsets(StSrc<MF> &s, RowOff rowoff, const int (&c0)[2],
+template <int MF, int NFH, typename RowOff>
+__device__ __forceinline__ void st_offsets(StSrc<MF, NFH> &s, RowOff rowoff, const int (&c0)[2],
                                            int rows, int lane)
 {
 #pragma unroll
@@ -210,34 +220,39 @@ __device__ __forceinline__ void st_offsets(StSrc<MF> &s, RowOff rowoff, const in
     s.cb[0] = c0[0] + (lane & 15);
     s.cb[1] = c0[1] + (lane & 15);
     s.cmax = rows - 1;
-    s.sc[0] = (uint32_t)min(c0[0] + lane, rows - 1);
-    s.sc[1] = (uint32_t)min(c0[1] + lane, rows - 1);
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int u = 0; u < StSrc<MF, NFH>::NS; u++) s.sc[h][u] = (uint32_t)min(c0[h] + 64 * u + lane, rows - 1);
     s.okm = 0;
 #pragma unroll
-    for (int j = 0; j < ST_NF; j++) s.okm |= (c0[j >> 2] + 16 * (j & 3) + (lane & 15) < rows ? 1u : 0u) << j;
+    for (int j = 0; j < 2 * NFH; j++)
+        s.okm |= (c0[j / NFH] + 16 * (j % NFH) + (lane & 15) < rows ? 1u : 0u) << j;
 }
 
 // Cross-wave sums of fragment row block m: each wave writes its fragments of
-// half 0 to red0 and of half 1 to red1 ([wave][16 rows][64 + 1 columns]).
-template <int MF>
-__device__ __forceinline__ void st_spill(float (*red0)[16][65], float (*red1)[16][65],
-                                         const f4_t (&acc)[MF][ST_NF], int m, int wave, int lane)
+// half 0 to red0 and of half 1 to red1 ([wave][16 rows][16 NFH + 1 columns]).
+template <int MF, int NFH>
+__device__ __forceinline__ void st_spill(float (*red0)[16][16 * NFH + 1], float (*red1)[16][16 * NFH + 1],
+                                         const f4_t (&acc)[MF][2 * NFH], int m, int wave, int lane)
 {
     const int cl = lane & 15, rq = 4 * (lane >> 4);
 #pragma unroll
-    for (int j = 0; j < ST_NF; j++)
+    for (int j = 0; j < 2 * NFH; j++)
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            (j < 4 ? red0 : red1)[wave][rq + r][16 * (j & 3) + cl] = acc[m][j][r];
+            (j < NFH ? red0 : red1)[wave][rq + r][16 * (j % NFH) + cl] = acc[m][j][r];
 }
 
-__device__ __forceinline__ float wave_order_sum(const float (*red)[16][65], int row, int c)
+template <int NFH>
+__device__ __forceinline__ float wave_order_sum(const float (*red)[16][16 * NFH + 1], int row, int c)
 {
     return ((red[0][row][c] + red[1][row][c]) + red[2][row][c]) + red[3][row][c];
 }
 
 // LDS: the cross-wave reduction tiles only
-constexpr int ST_LDS = 2 * 4 * 16 * 65 * 4;
+template <int NFH>
+constexpr int st_lds() { return 2 * 4 * 16 * (16 * NFH + 1) * 4; }
 
 // blockIdx -> (row tile, column group): the dispatcher deals workgroups to
 // the 8 XCDs round robin (XCD x runs blocks x, x+8, ...), and each XCD takes
@@ -257,23 +272,24 @@ __device__ __forceinline__ bool st_item(int n_tiles, int ncg, int &tile, int &cg
 }
 
 // ---------------------------------------------------------------------------
-// gate/up: column half 0 = gate features f0 .. f0+63, half 1 = the same up
-// features.
+// gate/up: column half 0 = gate features f0 .. f0 + 16 NFH - 1, half 1 = the
+// same up features.
 // ---------------------------------------------------------------------------
-template <int MF>
+template <int MF, int NFH>
 __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(StreamArgs a)
 {
-    __shared__ __align__(16) char lds[ST_LDS];
-    const int ncg = (a.F + 63) / 64;
+    constexpr int NC = 16 * NFH;   // features per workgroup
+    __shared__ __align__(16) char lds[st_lds<NFH>()];
+    const int ncg = (a.F + NC - 1) / NC;
     int tile, cg;
     if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
     const int n = min(16 * MF, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
-    const int f0 = cg * 64;
+    const int f0 = cg * NC;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
 
-    StSrc<MF> src;
+    StSrc<MF, NFH> src;
     src.abase = reinterpret_cast<const char *>(a.x);
     const size_t eb = (size_t)e * a.nbH * a.F;     // expert's first block-row
     src.qb[0] = a.gq + eb * QK;
@@ -283,29 +299,29 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
     src.qstep = (uint32_t)a.F * QK;
     src.dstep = (uint32_t)a.F;
     const int c0[2] = {f0, f0};
-    st_offsets<MF>(src, [&](int r) {
+    st_offsets<MF, NFH>(src, [&](int r) {
         return (uint32_t)(a.perm[slot0 + min(r, n - 1)] / a.K) * a.H * 4;
     }, c0, a.F, lane);
 
-    f4_t acc[MF][ST_NF];
+    f4_t acc[MF][2 * NFH];
 #pragma unroll
     for (int m = 0; m < MF; m++)
 #pragma unroll
-        for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(src, a.nbH, wave, acc);
-    float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
-    float (*red1)[16][65] = red0 + 4;
+    st_mainloop<MF, NFH>(src, a.nbH, wave, acc);
+    float (*red0)[16][NC + 1] = reinterpret_cast<float (*)[16][NC + 1]>(lds);
+    float (*red1)[16][NC + 1] = red0 + 4;
 #pragma unroll
     for (int m = 0; m < MF; m++) {
         __syncthreads();
-        st_spill<MF>(red0, red1, acc, m, wave, lane);
+        st_spill<MF, NFH>(red0, red1, acc, m, wave, lane);
         __syncthreads();
-        for (int i = threadIdx.x; i < 16 * 64; i += ST_THREADS) {
-            const int row = i >> 6, c = i & 63;
+        for (int i = threadIdx.x; i < 16 * NC; i += ST_THREADS) {
+            const int row = i / NC, c = i % NC;
             const int f = f0 + c;
             if (16 * m + row < n && f < a.F) {
-                const float g = wave_order_sum(red0, row, c), u = wave_order_sum(red1, row, c);
+                const float g = wave_order_sum<NFH>(red0, row, c), u = wave_order_sum<NFH>(red1, row, c);
                 const double g64 = (double)g;
                 const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
                 a.act[(size_t)(slot0 + 16 * m + row) * a.F + f] = sg * u;
@@ -320,7 +336,8 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 template <int MF>
 __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamArgs a)
 {
-    __shared__ __align__(16) char lds[ST_LDS];
+    constexpr int NFH = 4;
+    __shared__ __align__(16) char lds[st_lds<NFH>()];
     const int ncg = (a.H + 127) / 128;
     int tile, cg;
     if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
@@ -330,7 +347,7 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
     const int h0 = cg * 128;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
 
-    StSrc<MF> src;
+    StSrc<MF, NFH> src;
     src.abase = reinterpret_cast<const char *>(a.act);
     const size_t eb = (size_t)e * a.nbF * a.H;
     src.qb[0] = src.qb[1] = a.dq + eb * QK;
@@ -338,29 +355,29 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
     src.qstep = (uint32_t)a.H * QK;
     src.dstep = (uint32_t)a.H;
     const int c0[2] = {h0, h0 + 64};
-    st_offsets<MF>(src, [&](int r) { return (uint32_t)(slot0 + min(r, n - 1)) * a.F * 4; }, c0,
-                   a.H, lane);
+    st_offsets<MF, NFH>(src, [&](int r) { return (uint32_t)(slot0 + min(r, n - 1)) * a.F * 4; }, c0,
+                        a.H, lane);
 
-    f4_t acc[MF][ST_NF];
+    f4_t acc[MF][2 * NFH];
 #pragma unroll
     for (int m = 0; m < MF; m++)
 #pragma unroll
-        for (int j = 0; j < ST_NF; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
+        for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF>(src, a.nbF, wave, acc);
+    st_mainloop<MF, NFH>(src, a.nbF, wave, acc);
     float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
     float (*red1)[16][65] = red0 + 4;
 #pragma unroll
     for (int m = 0; m < MF; m++) {
         __syncthreads();
-        st_spill<MF>(red0, red1, acc, m, wave, lane);
+        st_spill<MF, NFH>(red0, red1, acc, m, wave, lane);
         __syncthreads();
         for (int i = threadIdx.x; i < 16 * 128; i += ST_THREADS) {
             const int row = i >> 7, c = i & 127;
             const int h = h0 + c;
             if (16 * m + row < n && h < a.H)
                 a.y[(size_t)(slot0 + 16 * m + row) * a.H + h] =
-                    wave_order_sum(c < 64 ? red0 : red1, row, c & 63);
+                    wave_order_sum<NFH>(c < 64 ? red0 : red1, row, c & 63);
         }
     }
 }
@@ -399,6 +416,30 @@ StreamDispatch stream_dispatch(const qq_moe *m, int T, char *work)
     p += al256((size_t)stream_cap(m, T, 16) * 4);
     d.tiles.n = reinterpret_cast<int32_t *>(p);
     return d;
+}
+
+// Gate/up features per column half of a workgroup, 16 NFH.  Each workgroup
+// keeps a fixed number of blocks in flight, so a kernel whose items fill the
+// resident slots (2 per CU) only partly in its last round streams that round
+// at a fraction of the rate.  The wider items are taken where they need
+// fewer item-rounds x width, counting the row tiles of even routing
+// (ceil(T K / 16 / E) per expert, clipped to T K / 16 + E).
+static int stream_gateup_nfh(const qq_ctx *ctx, const qq_moe *m, int T)
+{
+    if (stream_mf(m, T) != 1) return 4;
+    const long slots = 2L * ctx->num_cus;
+    const long per_e = ((long)T * m->K + 16L * m->E - 1) / (16L * m->E);
+    const long tiles = std::min((long)stream_cap(m, T, 16), per_e * m->E);
+    long best = 0, best_cost = 0;
+    for (const int nfh : {4, 7}) {
+        const long items = tiles * ((m->F + 16 * nfh - 1) / (16 * nfh));
+        const long cost = ((items + slots - 1) / slots) * nfh;
+        if (!best || cost < best_cost) {
+            best = nfh;
+            best_cost = cost;
+        }
+    }
+    return (int)best;
 }
 
 int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
@@ -444,13 +485,16 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.nbF = m->F / QK;
 
     // XCD-aware grids (st_item): 8 * ceil(items / 8) workgroups at most
-    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 63) / 64) + 7) / 8);
+    const int nfh = stream_gateup_nfh(ctx, m, T);
+    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 16 * nfh - 1) / (16 * nfh)) + 7) / 8);
     const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8);
     prof_begin(ctx, K_STREAM_GATEUP);
-    if (MF == 1)
-        QQ_LAUNCH(ctx, moe_stream_gateup_kernel<1>, dim3(g1), dim3(ST_THREADS), 0, a);
+    if (MF == 1 && nfh == 7)
+        QQ_LAUNCH(ctx, (moe_stream_gateup_kernel<1, 7>), dim3(g1), dim3(ST_THREADS), 0, a);
+    else if (MF == 1)
+        QQ_LAUNCH(ctx, (moe_stream_gateup_kernel<1, 4>), dim3(g1), dim3(ST_THREADS), 0, a);
     else
-        QQ_LAUNCH(ctx, moe_stream_gateup_kernel<2>, dim3(g1), dim3(ST_THREADS), 0, a);
+        QQ_LAUNCH(ctx, (moe_stream_gateup_kernel<2, 4>), dim3(g1), dim3(ST_THREADS), 0, a);
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_STREAM_DOWN);
