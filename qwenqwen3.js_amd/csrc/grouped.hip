@@ -113,8 +113,8 @@ __global__ __launch_bounds__(DISP_THREADS) void moe_dispatch_kernel(
             const int p = b0 + tid + DISP_THREADS * i;
             if (p >= P) break;
             const int e = ev[i];
-            if ((unsigned)e < (unsigned)E && !mask_has(mask, e)) {
-                const int pos = offs[e] + atomicAdd(&cur[e], 1);
+            const int pos = ((unsigned)e < (unsigned)E && !mask_has(mask, e)) ? offs[e] + atomicAdd(&cur[e], 1) : -1;
+            if ((unsigned)pos < (unsigned)P) {   // (always, for a routed pair)
                 perm[pos] = p;
                 inv[p] = pos;
             } else {

@@ -442,18 +442,22 @@ __device__ __forceinline__ void store_tagged_local(uint64_t *p, uint32_t tag, ui
     __hip_atomic_store(p, ((uint64_t)tag << 32) | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-// Exclusive scan over the 64 lanes; *total = sum of all lanes.
+// Exclusive scan over the 64 lanes; *total = sum of all lanes.  The
+// inclusive scan runs on DPP lane moves (no LDS round trips): within each row
+// of 16 lanes by shifts of 1, 2, 4 and 8 (lanes shifted in from outside the
+// row add 0), then across rows: lane 15 of rows 0 and 2 into rows 1 and 3,
+// and lane 31 into rows 2 and 3.  The whole wave must be active.
 __device__ __forceinline__ int wave_excl_scan(int v, int *total)
 {
-    const int lane = threadIdx.x & (WAVE - 1);
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < WAVE; o <<= 1) {
-        const int u = __shfl_up(incl, o, WAVE);
-        if (lane >= o) incl += u;
-    }
-    *total = __shfl(incl, WAVE - 1, WAVE);
-    return incl - v;
+    int x = v;
+    x += __builtin_amdgcn_update_dpp(0, x, 0x111, 0xf, 0xf, false);   // row_shr:1
+    x += __builtin_amdgcn_update_dpp(0, x, 0x112, 0xf, 0xf, false);   // row_shr:2
+    x += __builtin_amdgcn_update_dpp(0, x, 0x114, 0xf, 0xf, false);   // row_shr:4
+    x += __builtin_amdgcn_update_dpp(0, x, 0x118, 0xf, 0xf, false);   // row_shr:8
+    x += __builtin_amdgcn_update_dpp(0, x, 0x142, 0xa, 0xf, false);   // row_bcast:15
+    x += __builtin_amdgcn_update_dpp(0, x, 0x143, 0xc, 0xf, false);   // row_bcast:31
+    *total = __builtin_amdgcn_readlane(x, WAVE - 1);
+    return x - v;
 }
 
 // Sigmoid routing for one token in one wavefront (lfm2-engine.js:420-447).

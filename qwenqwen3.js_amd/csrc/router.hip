@@ -316,6 +316,7 @@ __device__ __forceinline__ bool rf_place(int nx, int KS, int nxy, int &x, int &k
 
 constexpr int FR_MAX_KS = 8;
 constexpr int FR_MAX_P = 1024;      // T K pairs dispatched by one workgroup
+constexpr int FR_MAX_TILES = FR_MAX_P / 16 + MAX_E;   // row tiles of at least 16 slots
 
 template <int EPL>
 __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
@@ -323,10 +324,15 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
     __shared__ double red[4][16][33];
     __shared__ int cnt[MAX_E], cur[MAX_E], offs[MAX_E + 1];
     __shared__ int pe[FR_MAX_P];
+    __shared__ int tle[FR_MAX_TILES], tlm[FR_MAX_TILES];
+    __shared__ int sh_ntiles;
     __shared__ RouteLds<EPL> rl[4];
     __shared__ uint32_t sh_tag;
     __shared__ int sh_fail;
-    const int T = a.T, E = a.W.E, K = a.K, KS = a.KS;
+    int T = a.T, E = a.W.E, K = a.K, KS = a.KS, softmax = a.softmax;
+    // held in registers: otherwise reloaded from the argument segment (and
+    // waited for) at every use in the routing and dispatch below
+    asm volatile("" : "+s"(T), "+s"(E), "+s"(K), "+s"(KS), "+s"(softmax));
     int bx, ks, bz;
     if (!rf_place((T + 15) / 16, KS, KS * ((E + 31) / 32), bx, ks, bz)) return;
     const int t0 = bx * 16, e0 = bz * 32;
@@ -450,7 +456,7 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
                 lg[i] = (lane + WAVE * i < E) ? (float)s : 0.0f;
             }
             WaveRoute<EPL> R;
-            wave_route<EPL>(lg, bl, E, K, a.softmax != 0, R, rl[wave]);
+            wave_route<EPL>(lg, bl, E, K, softmax != 0, R, rl[wave]);
             if (a.probs) {
 #pragma unroll
                 for (int i = 0; i < EPL; i++) {
@@ -506,42 +512,51 @@ __global__ __launch_bounds__(256) void route_dispatch_kernel(FusedRouteArgs a)
             }
         }
         __syncthreads();
+        // exclusive scans of the expert counts and of their row tiles, into
+        // LDS only: the global copies go out after the last barrier (a
+        // barrier waits for the stores before it)
         if (wave == 0) {
-            // exclusive scans of the expert counts and of their row tiles
             int run = 0, trun = 0;
             for (int eb = 0; eb < E; eb += WAVE) {
                 const int e = eb + lane;
                 const int c = e < E ? cnt[e] : 0;
                 int tot;
                 const int o = run + wave_excl_scan(c, &tot);
-                if (e < E) {
-                    offs[e] = o;
-                    a.counts[e] = c;
-                    a.offsets[e] = o;
-                }
+                if (e < E) offs[e] = o;
                 run += tot;
                 if (a.tiles.bm > 0) {
                     const int nte = (c + a.tiles.bm - 1) / a.tiles.bm;
                     int ttot;
                     int tt = trun + wave_excl_scan(nte, &ttot);
                     for (int m0 = 0; m0 < c && tt < a.tiles.cap; m0 += a.tiles.bm, tt++) {
-                        a.tiles.e[tt] = e;
-                        a.tiles.m0[tt] = m0;
+                        tle[tt] = e;
+                        tlm[tt] = m0;
                     }
                     trun += ttot;
                 }
             }
             if (lane == 0) {
                 offs[E] = run;
-                a.offsets[E] = run;
-                if (a.tiles.bm > 0) *a.tiles.n = min(trun, a.tiles.cap);
+                sh_ntiles = min(trun, a.tiles.cap);
             }
         }
         __syncthreads();
+        for (int e = tid; e <= E; e += 256) {
+            a.offsets[e] = offs[e];
+            if (e < E) a.counts[e] = cnt[e];
+        }
+        if (a.tiles.bm > 0) {
+            const int nt = sh_ntiles;
+            for (int i = tid; i < nt; i += 256) {
+                a.tiles.e[i] = tle[i];
+                a.tiles.m0[i] = tlm[i];
+            }
+            if (tid == 0) *a.tiles.n = nt;
+        }
         for (int q = tid; q < P; q += 256) {
             const int e = good ? pe[q] : -1;
-            if ((unsigned)e < (unsigned)E && !mask_has(a.mask, e)) {
-                const int pos = offs[e] + atomicAdd(&cur[e], 1);
+            const int pos = ((unsigned)e < (unsigned)E && !mask_has(a.mask, e)) ? offs[e] + atomicAdd(&cur[e], 1) : -1;
+            if ((unsigned)pos < (unsigned)P) {   // (always, for a routed pair)
                 a.perm[pos] = q;
                 a.inv[q] = pos;
             } else {
@@ -664,6 +679,7 @@ int launch_route_dispatch(qq_ctx *ctx, const qq_moe *m, const float *x, int T, c
     a.perm = perm;
     a.inv = inv;
     a.tiles = tiles;
+    if (tiles.cap > FR_MAX_TILES) return set_error(ctx, "route_dispatch: %d row tiles, at most %d", tiles.cap, FR_MAX_TILES);
     a.epoch_word = ctx->sync_epoch;
     a.pw = ctx->sync_rp;
     a.pwd = ctx->sync_rp + SYNC_RP_WORDS;
