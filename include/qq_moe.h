@@ -214,20 +214,23 @@ int qq_buffer_read(qq_ctx *ctx, const void *dev, void *host, size_t nbytes);
 int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, float *hidden_dev,
                               int T, const uint8_t *mask, float *record_dev);
 
-/* No reference counterpart.  The workgroups of the batch-1 decode kernel
- * wait on each other through memory (the routing, the h values, the partial
- * sums); every such wait gives up after `microseconds` (default
- * QQ_WAIT_LIMIT_US_DEFAULT, 50 ms), the kernel then finishes with what it
- * has, and the call's error surfaces at the next synchronising call as
- * QQ_E_HIP ("a device-side wait of the decode kernel timed out") rather
- * than the kernel waiting on.  0: a wait gives up at its first poll that
- * misses a word (for tests of that path).
- * qq_moe_forward (host pointers) recovers by itself: when the decode
- * launch's wait times out, the call runs again through the multi-launch
- * path, which needs no co-residency, and returns its result.
+/* No reference counterpart.  The workgroups of the batch-1 decode kernel,
+ * and of the one-launch routing and dispatch of small batches, wait on each
+ * other through memory (the routing, the h values, the partial sums, the
+ * partial logits and expert ids); every such wait gives up after
+ * `microseconds` (default QQ_WAIT_LIMIT_US_DEFAULT, 50 ms), the kernel then
+ * finishes with what it has, and the call's error surfaces at the next
+ * synchronising call as QQ_E_HIP ("a device-side wait ... timed out")
+ * rather than the kernel waiting on.  0: a wait gives up at its first poll
+ * that misses a word (for tests of that path).
+ * qq_moe_forward (host pointers) recovers by itself: when such a launch's
+ * wait times out, the call runs again through the multi-launch path, which
+ * needs no co-residency, and returns its result.
  * What a failed call leaves: each row of hidden holds either its value
- * before the call or its correct new value (a workgroup writes its rows only
- * when all of its waits succeeded); idx/w/probs are not valid.  When the
+ * before the call or its correct new value (a decode workgroup writes its
+ * rows only when all of its waits succeeded; a failed batch routing writes
+ * an empty dispatch, so hidden keeps its old value); idx/w/probs are not
+ * valid.  When the
  * error is read, the host moves the device epoch past every tag the failed
  * launch can have written, so later calls are unaffected by it.  Device-
  * resident state built across calls is invalid after such a call: an LFM2
@@ -237,7 +240,7 @@ int qq_set_wait_limit(qq_ctx *ctx, int microseconds);
 
 /* Test hooks, no reference counterpart (they wait for the stream; not
  * allowed while a capture is open): the device epoch that tags the decode
- * kernel's exchange words (a call uses the tags after it and advances it),
+ * and batch-routing kernels' exchange words (a call uses the tags after it and advances it),
  * and a fill of every exchange table of the context with words carrying
  * `tag`, standing for what a workgroup of a failed call may have left. */
 int qq_debug_epoch(qq_ctx *ctx, uint32_t *epoch);
