@@ -30,25 +30,31 @@ def _dev(torch, a):
     return torch.from_numpy(np.ascontiguousarray(a)).cuda()
 
 
-@pytest.mark.parametrize("T,mfma", [(1, 0), (64, 0), (96, 64)])
-def test_graph_replay_matches_eager(T, mfma):
+@pytest.mark.parametrize("T,mfma,shape", [(1, 0, "small"), (64, 0, "small"), (96, 64, "small"),
+                                          (64, 0, "lfm2")])
+def test_graph_replay_matches_eager(T, mfma, shape):
+    """shape "lfm2": the LFM2-8B-A1B layer, whose 64-token batch routes and
+    dispatches in one launch (8 H slices) and streams 112-feature gate/up
+    items; "small": H=256, F=192, E=8, K=2 (4 H slices at 64 tokens)."""
     import torch
-    _say("graph replay T=%d mfma_min_tokens=%d" % (T, mfma))
+    _say("graph replay T=%d mfma_min_tokens=%d shape=%s" % (T, mfma, shape))
     ctx = gpu_context()
     ctx.set_mfma_min_tokens(mfma)
-    L1 = synth.moe_layer(31, H=256, F=192, E=8, K=2)
-    L2 = synth.moe_layer(32, H=256, F=192, E=8, K=2)
+    dims = dict(H=256, F=192, E=8, K=2) if shape == "small" else {}
+    L1 = synth.moe_layer(31, **dims)
+    L2 = synth.moe_layer(32, **dims)
+    H, K = L1["H"], L1["K"]
     m1, m2 = upload_layer(ctx, L1), upload_layer(ctx, L2)
     try:
-        x, h0 = synth.activations(33, T, 256)
+        x, h0 = synth.activations(33, T, H)
         dx, dh0 = _dev(torch, x), _dev(torch, h0)
         xn = torch.empty_like(dx)
-        idx = torch.empty((2, T, 2), dtype=torch.int32, device="cuda")
+        idx = torch.empty((2, T, K), dtype=torch.int32, device="cuda")
 
         def calls(dh):
             # two layers of a stack: x = rmsnorm(hidden), hidden += MoE(x)
             m1.forward_dev(dx.data_ptr(), dh.data_ptr(), T, idx_ptr=idx[0].data_ptr())
-            ctx.rmsnorm_dev(dh.data_ptr(), None, xn.data_ptr(), T, 256, 1e-5)
+            ctx.rmsnorm_dev(dh.data_ptr(), None, xn.data_ptr(), T, H, 1e-5)
             m2.forward_dev(xn.data_ptr(), dh.data_ptr(), T, idx_ptr=idx[1].data_ptr())
 
         eager_h = dh0.clone()
@@ -88,8 +94,10 @@ def test_graph_replay_matches_eager(T, mfma):
         assert np.array_equal(want_idx[0], ref_idx)
     finally:
         ctx.set_mfma_min_tokens(512)
-        m1.release()
-        m2.release()
+        for m in (m1, m2):
+            for t in m._keep:
+                t.release()
+            m.release()
 
 
 def test_graph_refuses_host_calls_and_double_begin():
