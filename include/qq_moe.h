@@ -217,7 +217,9 @@ int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, 
 /* No reference counterpart.  The workgroups of the batch-1 decode kernel,
  * and of the one-launch routing and dispatch of small batches, wait on each
  * other through memory (the routing, the h values, the partial sums, the
- * partial logits and expert ids); every such wait gives up after
+ * partial logits and expert ids), and the last workgroup of a split item in
+ * the decode-batch kernels reads the other segments' partial sums; every
+ * such wait gives up after
  * `microseconds` (default QQ_WAIT_LIMIT_US_DEFAULT, 50 ms), the kernel then
  * finishes with what it has, and the call's error surfaces at the next
  * synchronising call as QQ_E_HIP ("a device-side wait ... timed out")
@@ -230,7 +232,10 @@ int qq_moe_forward_record_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev, 
  * before the call or its correct new value (a decode workgroup writes its
  * rows only when all of its waits succeeded; a failed batch routing writes
  * an empty dispatch, so hidden keeps its old value); idx/w/probs are not
- * valid.  When the
+ * valid.  (The exception: a split item whose partial-sum read expired --
+ * its segments stored their words before counting themselves in, so this
+ * takes a memory system that lost them -- leaves its rows of hidden
+ * unspecified.)  When the
  * error is read, the host moves the device epoch past every tag the failed
  * launch can have written, so later calls are unaffected by it.  Device-
  * resident state built across calls is invalid after such a call: an LFM2

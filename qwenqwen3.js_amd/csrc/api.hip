@@ -162,7 +162,7 @@ int check_device_error(qq_ctx *ctx, bool staged)
         QQ_HIP(ctx, hipGetLastError());
         QQ_HIP(ctx, hipStreamSynchronize(ctx->stream));
         snprintf(ctx->err, sizeof ctx->err,
-                 "a device-side wait of the decode or fused routing kernel timed out (code %u)", e);
+                 "a device-side wait of the decode, fused routing or split-item exchange timed out (code %u)", e);
         return QQ_E_HIP;
     }
     return QQ_OK;
@@ -292,7 +292,8 @@ int qq_init(int device, qq_ctx **out)
         return check_hip(nullptr, e, "hipEventCreate");
     }
     void *sync = nullptr;
-    const size_t sync_bytes = sync_table_words() * sizeof(uint64_t) + 512;
+    const size_t sync_bytes = sync_table_words() * sizeof(uint64_t) + 512 + SEG_CTR_WORDS * 4 + 256 +
+                              (size_t)ctx->num_cus * SEG_PART_WORDS * 8;
     if ((e = hipMalloc(&sync, sync_bytes)) != hipSuccess || (e = hipMemset(sync, 0, sync_bytes)) != hipSuccess) {
         if (sync) (void)hipFree(sync);
         (void)hipEventDestroy(ctx->ev0);
@@ -313,6 +314,8 @@ int qq_init(int device, qq_ctx **out)
     // error word and epoch each on a 128-byte line of their own
     ctx->sync_err = reinterpret_cast<uint32_t *>(ctx->sync_ri + SYNC_RI_WORDS);
     ctx->sync_epoch = ctx->sync_err + 32;
+    ctx->sync_seg = ctx->sync_err + 128;
+    ctx->seg_part = reinterpret_cast<uint64_t *>(((uintptr_t)(ctx->sync_seg + SEG_CTR_WORDS) + 255) & ~(uintptr_t)255);
     ctx->capturing = 0;
     *out = ctx;
     return QQ_OK;

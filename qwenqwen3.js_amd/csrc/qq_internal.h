@@ -52,6 +52,13 @@ constexpr int SYNC_RI_WORDS = 1024;
 // wrote words tagged with the next call's tags (up to twice the call's layer
 // count past the old epoch), which the next call must not accept.
 constexpr uint32_t SYNC_EPOCH_SKIP = 1024;
+// Split items of the stream kernels, after the error word and the epoch:
+// for each of the two kernels, SEG_CTR_WORDS / 4 32-bit segment counters (one
+// per split item, zero between launches), then its generation and a count of
+// split items done; after them the segments' partial sums as tagged 64-bit
+// words, at most one segment per CU in a launch.
+constexpr int SEG_CTR_WORDS = 4096;
+constexpr int SEG_PART_WORDS = 4096;
 static_assert(SYNC_EPOCH_SKIP >= 2 * STACK_MAX_LAYERS + 2, "epoch skip");
 
 // Expert mask passed by value to kernels (bit e set = expert e skipped).
@@ -150,6 +157,8 @@ struct qq_ctx {
     uint64_t dec_wait_ticks;
     uint32_t *sync_epoch;
     uint64_t *sync_hloc, *sync_hdev, *sync_part, *sync_arrive, *sync_hx, *sync_rp, *sync_ri;
+    uint32_t *sync_seg;   // SEG_CTR_WORDS stream-kernel segment counters and generations
+    uint64_t *seg_part;   // num_cus x SEG_PART_WORDS partial sums
     // device-side waits that timed out on this context so far (counted when
     // the error word is read); device-resident state built across calls (an
     // LFM2 model's conv states and KV cache) is invalid after one

@@ -39,7 +39,15 @@ struct StreamArgs {
     const int32_t *tile_e, *tile_m0, *n_tiles;
     const int8_t *gq, *uq, *dq;
     const uint16_t *gd, *ud, *dd;   // fp16 scale bits
+    uint64_t *part;          // partial sums of split items (st_work), tagged words
+    uint32_t *seg_ctr;       // per split item: segments done (zero between launches)
+    uint32_t *seg_gen;       // [0] generation: a launch's partials carry gen + 1;
+                             // [1] split items done in the launch (zero between launches)
+    uint32_t *err;           // device error word (a bounded wait expired)
+    uint64_t wait_ticks;
     int H, F, K, nbH, nbF;
+    int G;                   // resident workgroups (2 per CU)
+    int tile_cap;            // row tiles the grid is sized for
 };
 
 // 8 consecutive fp32 values -> high and low fp16 halves.  hi is rounded
@@ -181,17 +189,19 @@ __device__ __forceinline__ void st_block(const StBlock<MF, NFH> &b, const StSrc<
     }
 }
 
-// Wave w reduces blocks w, w+4, w+8, ... of nb with st_pf blocks in flight.
+// Wave w reduces blocks kb0 + w, kb0 + w + 4, ... of the nb blocks from kb0
+// on, with st_pf blocks in flight.
 template <int MF, int NFH>
-__device__ __forceinline__ void st_mainloop(const StSrc<MF, NFH> &s, int nb, int wave,
+__device__ __forceinline__ void st_mainloop(const StSrc<MF, NFH> &s, int kb0, int nb, int wave,
                                             f4_t (&acc)[MF][2 * NFH])
 {
     constexpr int PF = st_pf<MF, NFH>();
     const int nblk = (nb - wave + 3) / 4;
+    const int kw = kb0 + wave;
     StBlock<MF, NFH> r[PF];
 #pragma unroll
     for (int u = 0; u < PF; u++)
-        if (u < nblk) st_load<MF, NFH>(r[u], s, wave + 4 * u);
+        if (u < nblk) st_load<MF, NFH>(r[u], s, kw + 4 * u);
     for (int i = 0; i < nblk; i += PF) {
 #pragma unroll
         for (int u = 0; u < PF; u++) {
@@ -200,7 +210,7 @@ __device__ __forceinline__ void st_mainloop(const StSrc<MF, NFH> &s, int nb, int
                 // the refill goes out only after the products, so the
                 // compiler waits for this block alone, not the ones behind it
                 __builtin_amdgcn_sched_barrier(0);
-                if (i + u + PF < nblk) st_load<MF, NFH>(r[u], s, wave + 4 * (i + u + PF));
+                if (i + u + PF < nblk) st_load<MF, NFH>(r[u], s, kw + 4 * (i + u + PF));
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
@@ -254,21 +264,151 @@ __device__ __forceinline__ float wave_order_sum(const float (*red)[16][16 * NFH 
 template <int NFH>
 constexpr int st_lds() { return 2 * 4 * 16 * (16 * NFH + 1) * 4; }
 
-// blockIdx -> (row tile, column group): the dispatcher deals workgroups to
-// the 8 XCDs round robin (XCD x runs blocks x, x+8, ...), and each XCD takes
-// a contiguous run of the real items, row-tile major, so the column groups
-// of a row tile read its activation rows through one L2.  False once past
-// the real items.
-__device__ __forceinline__ bool st_item(int n_tiles, int ncg, int &tile, int &cg)
+// The work of one workgroup among R items (row tile x column group, row-tile
+// major).  Items that fill whole rounds of the G resident workgroups run
+// whole.  A remainder of L < G items would run as a round of its own on L
+// workgroups, each streaming only as fast as its own blocks in flight allow:
+// a tail as long as a full round for a few percent of the work.  Instead each
+// remainder item is split into S segments of the reduction dimension (S L <=
+// G / 2, at least 8 blocks each; the remainder is widened back to the first
+// tile of its first expert, so all rows of an expert are summed the same way
+// whatever their order within the expert) run by S L more workgroups, which store
+// their fp32 partial sums as tagged words (tag = the kernel's generation + 1,
+// new in every launch); the last segment to finish adds them in segment order
+// and applies the epilogue (st_last, st_seg_sum).  The tags stand in for a
+// release / acquire pair, whose device-scope fences would write back the
+// whole L2.
+constexpr int ST_SEG_MAX = 8;   // segments of a split item
+
+struct StWork {
+    int item;         // tile * ncg + column group
+    int seg, nseg;    // segment of the reduction dimension; nseg == 1: whole
+    int li;           // remainder item: counter li, partial slot li * nseg + seg
+    int L;            // remainder items (split when nseg > 1)
+};
+
+__device__ __forceinline__ bool st_work(int R, int G, int nb, int ncg, int bm, const int32_t *tile_m0,
+                                        StWork &w)
 {
-    const int R = n_tiles * ncg;
-    const int per = (R + 7) >> 3;
-    const int x = blockIdx.x & 7, i = blockIdx.x >> 3;
-    const int w = x * per + i;
-    if (i >= per || w >= R) return false;
-    tile = w / ncg;
-    cg = w - tile * ncg;
+    int W = R;                               // items run whole
+    int L = 0, S = 1;
+    if (R % G) {
+        const int t = R / G * G / ncg;      // tile of the first remainder item
+        W = (t - tile_m0[t] / bm) * ncg;
+        L = R - W;
+        S = max(1, min(min(G / (2 * L), nb / 8), ST_SEG_MAX));
+        if (S == 1) W = R;
+    }
+    const int per = (W + 7) >> 3;
+    const int b = blockIdx.x;
+    w.L = L;
+    if (b < 8 * per) {
+        // the dispatcher deals workgroups to the 8 XCDs round robin (one XCD
+        // runs blocks x, x+8, ...); each XCD takes a contiguous run of the
+        // items, so the column groups of a row tile read its activation rows
+        // through one L2
+        const int x = b & 7, i = b >> 3, it = x * per + i;
+        if (it >= W) return false;
+        w.item = it;
+        w.seg = 0;
+        w.nseg = 1;
+        w.li = 0;
+        return true;
+    }
+    const int q = b - 8 * per;
+    if (S == 1 || q >= L * S) return false;
+    w.li = q / S;
+    w.seg = q - w.li * S;
+    w.nseg = S;
+    w.item = W + w.li;
     return true;
+}
+
+// Counts this workgroup's segment of a split item in once its partial sums
+// are stored; true in the workgroup of the last segment to arrive.  That
+// workgroup returns the counter to zero for the next launch.  sh: one int of
+// LDS.
+__device__ __forceinline__ bool st_last(uint32_t *ctr, int nseg, int *sh)
+{
+    wait_vm<0>();   // this wave's tagged stores are out
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int last = old == (uint32_t)nseg - 1u;
+        if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        *sh = last;
+    }
+    __syncthreads();
+    return *sh != 0;
+}
+
+// The last segment's workgroup, after its reduction: counts the item done;
+// the last of the launch's L split items moves the generation on (every
+// segment of the launch read it before its item's counter reached the end).
+__device__ __forceinline__ void st_item_done(uint32_t *gen, int L, uint32_t tag)
+{
+    if (threadIdx.x == 0) {
+        const uint32_t d = __hip_atomic_fetch_add(gen + 1, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == (uint32_t)L - 1u) {
+            __hip_atomic_store(gen + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(gen, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+}
+
+// Sums of a split item's partial sums: the 4 words from offset o[i] of each
+// segment (segments PSZ words apart) into r[i], added in segment order.  All
+// loads go out before the first add; words not yet carrying `tag` are read
+// again (bounded by wait_ticks: false when the wait expired).
+template <int PSZ, int NO>
+__device__ __forceinline__ bool st_seg_sum(const uint64_t *p0, const int (&o)[NO], int nseg, uint32_t tag,
+                                           uint64_t wait_ticks, float (&r)[NO][4])
+{
+    uint64_t v[ST_SEG_MAX][NO][4];
+    uint64_t t0 = 0;
+    for (bool first = true;; first = false) {
+        bool ok = true;
+#pragma unroll
+        for (int sg = 0; sg < ST_SEG_MAX; sg++)
+#pragma unroll
+            for (int i = 0; i < NO; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (sg < nseg)
+                        v[sg][i][j] = __hip_atomic_load(p0 + (size_t)sg * PSZ + o[i] + j, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int sg = 0; sg < ST_SEG_MAX; sg++)
+#pragma unroll
+            for (int i = 0; i < NO; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    if (sg < nseg) ok = ok && (uint32_t)(v[sg][i][j] >> 32) == tag;
+        if (ok) break;
+        if (first) {
+            t0 = wall_clock64();
+        } else if (wall_clock64() - t0 >= wait_ticks) {
+            return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+    }
+#pragma unroll
+    for (int i = 0; i < NO; i++)
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            float x = __uint_as_float((uint32_t)v[0][i][j]);
+#pragma unroll
+            for (int sg = 1; sg < ST_SEG_MAX; sg++)
+                if (sg < nseg) x += __uint_as_float((uint32_t)v[sg][i][j]);
+            r[i][j] = x;
+        }
+    return true;
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u)
+{
+    const double g64 = (double)g;
+    return (float)(g64 * (1.0 / (1.0 + exp(-g64)))) * u;
 }
 
 // ---------------------------------------------------------------------------
@@ -280,9 +420,11 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 {
     constexpr int NC = 16 * NFH;   // features per workgroup
     __shared__ __align__(16) char lds[st_lds<NFH>()];
+    __shared__ int sh_last;
     const int ncg = (a.F + NC - 1) / NC;
-    int tile, cg;
-    if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
+    StWork wk;
+    if (!st_work(min(*a.n_tiles, a.tile_cap) * ncg, a.G, a.nbH, ncg, 16 * MF, a.tile_m0, wk)) return;
+    const int tile = wk.item / ncg, cg = wk.item - tile * ncg;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
     const int n = min(16 * MF, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
@@ -309,9 +451,15 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 #pragma unroll
         for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF, NFH>(src, a.nbH, wave, acc);
+    const int kb0 = wk.seg * a.nbH / wk.nseg, kb1 = (wk.seg + 1) * a.nbH / wk.nseg;
+    const uint32_t tag =
+        wk.nseg > 1 ? __hip_atomic_load(a.seg_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
+    st_mainloop<MF, NFH>(src, kb0, kb1 - kb0, wave, acc);
     float (*red0)[16][NC + 1] = reinterpret_cast<float (*)[16][NC + 1]>(lds);
     float (*red1)[16][NC + 1] = red0 + 4;
+    // split item: partial [16 MF rows][NC gate | NC up] of each segment
+    constexpr int PSZ = 16 * MF * 2 * NC;
+    uint64_t *pp = a.part + (size_t)(wk.li * wk.nseg + wk.seg) * PSZ;
 #pragma unroll
     for (int m = 0; m < MF; m++) {
         __syncthreads();
@@ -320,14 +468,30 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
         for (int i = threadIdx.x; i < 16 * NC; i += ST_THREADS) {
             const int row = i / NC, c = i % NC;
             const int f = f0 + c;
-            if (16 * m + row < n && f < a.F) {
-                const float g = wave_order_sum<NFH>(red0, row, c), u = wave_order_sum<NFH>(red1, row, c);
-                const double g64 = (double)g;
-                const float sg = (float)(g64 * (1.0 / (1.0 + exp(-g64))));
-                a.act[(size_t)(slot0 + 16 * m + row) * a.F + f] = sg * u;
+            const float g = wave_order_sum<NFH>(red0, row, c), u = wave_order_sum<NFH>(red1, row, c);
+            if (wk.nseg > 1) {
+                store_tagged(pp + (16 * m + row) * 2 * NC + c, tag, __float_as_uint(g));
+                store_tagged(pp + (16 * m + row) * 2 * NC + NC + c, tag, __float_as_uint(u));
+            } else if (16 * m + row < n && f < a.F) {
+                a.act[(size_t)(slot0 + 16 * m + row) * a.F + f] = silu_mul(g, u);
             }
         }
     }
+    if (wk.nseg == 1 || !st_last(a.seg_ctr + wk.li, wk.nseg, &sh_last)) return;
+    const uint64_t *p0 = a.part + (size_t)wk.li * wk.nseg * PSZ;
+    constexpr int NC4 = NC / 4;
+    for (int i = threadIdx.x; i < 16 * MF * NC4; i += ST_THREADS) {
+        const int row = i / NC4, c = 4 * (i - row * NC4);
+        if (row >= n) continue;
+        const int o[2] = {row * 2 * NC + c, row * 2 * NC + NC + c};
+        float gu[2][4];
+        if (!st_seg_sum<PSZ, 2>(p0, o, wk.nseg, tag, a.wait_ticks, gu)) atomicOr(a.err, 8u);
+        float *dst = a.act + (size_t)(slot0 + row) * a.F + f0 + c;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (f0 + c + j < a.F) dst[j] = silu_mul(gu[0][j], gu[1][j]);
+    }
+    st_item_done(a.seg_gen, wk.L, tag);
 }
 
 // ---------------------------------------------------------------------------
@@ -338,9 +502,11 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
 {
     constexpr int NFH = 4;
     __shared__ __align__(16) char lds[st_lds<NFH>()];
+    __shared__ int sh_last;
     const int ncg = (a.H + 127) / 128;
-    int tile, cg;
-    if (!st_item(*a.n_tiles, ncg, tile, cg)) return;
+    StWork wk;
+    if (!st_work(min(*a.n_tiles, a.tile_cap) * ncg, a.G, a.nbF, ncg, 16 * MF, a.tile_m0, wk)) return;
+    const int tile = wk.item / ncg, cg = wk.item - tile * ncg;
     const int e = a.tile_e[tile], m0 = a.tile_m0[tile];
     const int n = min(16 * MF, a.counts[e] - m0);
     const int slot0 = a.offsets[e] + m0;
@@ -364,9 +530,15 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
 #pragma unroll
         for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    st_mainloop<MF, NFH>(src, a.nbF, wave, acc);
+    const int kb0 = wk.seg * a.nbF / wk.nseg, kb1 = (wk.seg + 1) * a.nbF / wk.nseg;
+    const uint32_t tag =
+        wk.nseg > 1 ? __hip_atomic_load(a.seg_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
+    st_mainloop<MF, NFH>(src, kb0, kb1 - kb0, wave, acc);
     float (*red0)[16][65] = reinterpret_cast<float (*)[16][65]>(lds);
     float (*red1)[16][65] = red0 + 4;
+    // split item: partial [16 MF rows][128 columns] of each segment
+    constexpr int PSZ = 16 * MF * 128;
+    uint64_t *pp = a.part + (size_t)(wk.li * wk.nseg + wk.seg) * PSZ;
 #pragma unroll
     for (int m = 0; m < MF; m++) {
         __syncthreads();
@@ -375,11 +547,27 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
         for (int i = threadIdx.x; i < 16 * 128; i += ST_THREADS) {
             const int row = i >> 7, c = i & 127;
             const int h = h0 + c;
-            if (16 * m + row < n && h < a.H)
-                a.y[(size_t)(slot0 + 16 * m + row) * a.H + h] =
-                    wave_order_sum<NFH>(c < 64 ? red0 : red1, row, c & 63);
+            const float v = wave_order_sum<NFH>(c < 64 ? red0 : red1, row, c & 63);
+            if (wk.nseg > 1)
+                store_tagged(pp + (16 * m + row) * 128 + c, tag, __float_as_uint(v));
+            else if (16 * m + row < n && h < a.H)
+                a.y[(size_t)(slot0 + 16 * m + row) * a.H + h] = v;
         }
     }
+    if (wk.nseg == 1 || !st_last(a.seg_ctr + wk.li, wk.nseg, &sh_last)) return;
+    const uint64_t *p0 = a.part + (size_t)wk.li * wk.nseg * PSZ;
+    for (int i = threadIdx.x; i < 16 * MF * 32; i += ST_THREADS) {
+        const int row = i >> 5, c = 4 * (i & 31);
+        if (row >= n) continue;
+        const int o[1] = {row * 128 + c};
+        float v[1][4];
+        if (!st_seg_sum<PSZ, 1>(p0, o, wk.nseg, tag, a.wait_ticks, v)) atomicOr(a.err, 8u);
+        float *dst = a.y + (size_t)(slot0 + row) * a.H + h0 + c;
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+            if (h0 + c + j < a.H) dst[j] = v[0][j];
+    }
+    st_item_done(a.seg_gen, wk.L, tag);
 }
 
 // ---------------------------------------------------------------------------
@@ -483,11 +671,24 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.K = m->K;
     a.nbH = m->H / QK;
     a.nbF = m->F / QK;
+    a.part = ctx->seg_part;
+    a.seg_ctr = ctx->sync_seg;
+    a.seg_gen = ctx->sync_seg + SEG_CTR_WORDS / 4;
+    a.err = ctx->sync_err;
+    a.wait_ticks = ctx->dec_wait_ticks;
+    a.G = 2 * ctx->num_cus;
+    a.tile_cap = cap;
 
-    // XCD-aware grids (st_item): 8 * ceil(items / 8) workgroups at most
+    // a split item's partial sums: [16 MF rows][2 x 16 NFH or 128 columns]
+    if (16 * MF * std::max(2 * 16 * stream_gateup_nfh(ctx, m, T), 128) > SEG_PART_WORDS)
+        return set_error(ctx, "stream path: partial sums exceed %d words", SEG_PART_WORDS);
+
+    // grids (st_work): 8 * ceil(items / 8) workgroups for the items of cap
+    // row tiles run whole, and up to G / 2 segment workgroups
     const int nfh = stream_gateup_nfh(ctx, m, T);
-    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 16 * nfh - 1) / (16 * nfh)) + 7) / 8);
-    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8);
+    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 16 * nfh - 1) / (16 * nfh)) + 7) / 8) +
+                        (unsigned)(a.G / 2);
+    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8) + (unsigned)(a.G / 2);
     prof_begin(ctx, K_STREAM_GATEUP);
     if (MF == 1 && nfh == 7)
         QQ_LAUNCH(ctx, (moe_stream_gateup_kernel<1, 7>), dim3(g1), dim3(ST_THREADS), 0, a);
@@ -498,6 +699,8 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     prof_end(ctx);
     QQ_HIP(ctx, hipGetLastError());
     prof_begin(ctx, K_STREAM_DOWN);
+    a.seg_ctr = ctx->sync_seg + SEG_CTR_WORDS / 2;
+    a.seg_gen = ctx->sync_seg + 3 * SEG_CTR_WORDS / 4;
     if (MF == 1)
         QQ_LAUNCH(ctx, moe_stream_down_kernel<1>, dim3(g2), dim3(ST_THREADS), 0, a);
     else

@@ -325,6 +325,56 @@ def test_moe_batch_one_launch_routing(case):
     _check_moe(L, x, hid, mask=mask)
 
 
+@pytest.mark.parametrize("T,hot,tiles", [
+    (64, -1, 33),    # one expert at 18 rows: 16 items past 512 (8 gate/up, 7 down segments)
+    (64, 1, 35),     # 48 items past: 5 segments each
+    (64, 2, 37),     # 80 past: 3 segments
+    (112, 0, 38),    # 96 past: 2 segments
+    (128, 0, 45),    # 208 past: a second round of whole items
+    (200, 0, None),  # 32-row tiles (gate/up items of 64 features)
+    (256, 2, None),
+])
+def test_moe_batch_remainder_items(T, hot, tiles):
+    """Decode batches whose items (row tiles x column groups) overflow the 512
+    resident workgroups of a 256-CU MI355X by a remainder: the remainder items
+    are split along the reduction dimension, each segment's fp32 partial sums
+    added in segment order by the segment that finishes last.  Every row
+    within the batch tolerance; a second input in between and the first input
+    again bit for bit (the segment counters return to zero after each launch).
+    hot: experts 0 .. hot-1 get bias +1 (picked by every token); -1: expert 5
+    gets +0.1 (18 of the 64 tokens)."""
+    _say("moe remainder items", T, hot, tiles)
+    L = dict(full_layer(1))
+    L["bias"] = L["bias"].copy()
+    if hot > 0:
+        L["bias"][:hot] += 1.0
+    elif hot < 0:
+        L["bias"][5] += 0.1
+    x, hid = synth.activations(202, T, 2048)
+    x2, hid2 = synth.activations(203, T, 2048)
+    r_idx, _, _ = oracle.moe_route(L, x)
+    c = np.bincount(r_idx.ravel(), minlength=32)
+    if tiles is not None:
+        assert int(np.sum((c + 15) // 16)) == tiles, c
+    ctx = gpu_context()
+    m = upload_layer(ctx, L)
+    try:
+        outs = [m.forward(xx, hh) for xx, hh in ((x, hid), (x2, hid2), (x, hid))]
+    finally:
+        for t in m._keep:
+            t.release()
+        m.release()
+    for (out, idx, w, probs), xx, hh in zip(outs[:2], (x, x2), (hid, hid2)):
+        r_out, r_idx, r_w, r_probs = oracle.moe_ffn(L, xx, hh)
+        np.testing.assert_array_equal(idx, r_idx)
+        np.testing.assert_array_equal(probs, r_probs)
+        np.testing.assert_array_equal(w, r_w)
+        err = rel_l2(moe_delta(out, hh), moe_delta(r_out, hh))
+        _say("moe rel_l2", err)
+        assert err < TOL_GEMV, err
+    np.testing.assert_array_equal(outs[2][0], outs[0][0])
+
+
 # ---------------------------------------------------------------- Qwen3-MoE softmax gating
 
 @pytest.mark.parametrize("case", [
