@@ -92,7 +92,8 @@ __device__ __forceinline__ _Float16 half_bits(uint16_t b) { return __builtin_bit
 //   B  each wave's raw int8 columns (2 x 32 columns x 32 B), copied as is;
 //      each wave reads back only its own columns and dequantises them in
 //      registers to fp16 w = fp16(q * d);
-//   d  the fp16 scales of the tile's columns (waves 0 and 1, 256 B each).
+//   d  the fp16 scales of the tile's columns (waves 0 and 1, 256 B each; waves
+//      2 and 3 copy them again, unread, so all waves issue 5 copies).
 // The copies run MG_AHEAD blocks ahead through a ring of MG_STAGES stages;
 // one barrier per block.  The reduction index is permuted identically in A
 // and B: lane half h = lane / 32 carries k = 16h + 8s + j in MFMA step s,
@@ -112,7 +113,10 @@ constexpr int MG_STAGES = MG_STAGES_CFG;
 constexpr int MG_AHEAD = MG_AHEAD_CFG;       // blocks copied ahead of the one being read
 constexpr int MG_A = MG_BM * 64;             // A: 128 rows x 64 B
 constexpr int MG_B = 4 * 2 * 1024;           // B: 4 waves x 2 matrices x 32 columns x 32 B
-constexpr int MG_S = 2 * 256;                // scales: 2 x 128 columns x 2 B
+// scales: 2 x 128 columns x 2 B, copied by waves 0 and 1; waves 2 and 3
+// copy the same bytes into the other half, so that every wave issues the
+// same copies per block and waits for the same counts
+constexpr int MG_S = 4 * 256;
 constexpr int MG_STAGE = MG_A + MG_B + MG_S;
 // The copy of block h + MG_AHEAD is issued after the barrier of block h.  A
 // wave may then still be reading stage h (B operands of block h) and stage
@@ -176,18 +180,16 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
     auto issue = [&](int b) {
         const uint32_t so = (uint32_t)(b % MG_STAGES) * MG_STAGE;
         const char *ab = src.abase + (size_t)b * 64;
-        dma16s(src.a0, ab, da0 + so);
-        dma16s(src.a1, ab, da1 + so);
-        dma16s(src.b0, src.bbase0 + (size_t)b * src.bstep, db0 + so);
-        dma16s(src.b1, src.bbase1 + (size_t)b * src.bstep, db1 + so);
-        if (wave < 2) dma4s(src.sc, src.sbase + (size_t)b * src.sstep, ds + so);
+        dma5s(src.a0, ab, da0 + so, src.a1, ab, da1 + so, src.b0, src.bbase0 + (size_t)b * src.bstep, db0 + so,
+              src.b1, src.bbase1 + (size_t)b * src.bstep, db1 + so, src.sc, src.sbase + (size_t)b * src.sstep,
+              ds + so);
     };
-    // per-wave copies per block: 5 (waves 0, 1) or 4.  Wait until block x's
-    // copies landed when blocks up to `upto` have been issued.
-    auto wait_block = [&](int x, int upto) {
-        const int later = min(nb - 1, upto) - x;
-        if (wave < 2) mg_wait<5>(later); else mg_wait<4>(later);
-    };
+    // the wait for the block after the one just issued while MG_AHEAD - 1
+    // more are in flight behind it (5 copies a block per wave)
+    auto wait_steady = [&]() { wait_vm<5 * (MG_AHEAD - 1)>(); };
+    // Wait until block x's copies landed when blocks up to `upto` have been
+    // issued.
+    auto wait_block = [&](int x, int upto) { mg_wait<5>(min(nb - 1, upto) - x); };
     // Operands fetched one block ahead: B dequantised (both matrices, both
     // MFMA steps) and the A fragments of MFMA step 0.
     struct Frag {
@@ -239,6 +241,21 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
     __syncthreads();
     fetch(0, f0);
     int b = 0;
+    // steady state: both copies of an iteration go out and both waits leave
+    // MG_AHEAD - 1 blocks in flight
+    for (; b + 1 + MG_AHEAD < nb; b += 2) {
+        issue(b + MG_AHEAD);
+        wait_steady();
+        __syncthreads();
+        fetch(b + 1, f1);
+        mma(b, f0);
+        issue(b + 1 + MG_AHEAD);
+        wait_steady();
+        __syncthreads();
+        fetch(b + 2, f0);
+        mma(b + 1, f1);
+    }
+    // the last blocks, with waits that count down to zero
     for (; b + 1 < nb; b += 2) {
         // f0 holds block b
         if (b + MG_AHEAD < nb) issue(b + MG_AHEAD);

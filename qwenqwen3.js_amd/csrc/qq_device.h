@@ -124,6 +124,28 @@ __device__ __forceinline__ void dma4s(uint32_t off, const void *base, uint32_t l
                  : "=&s"(save) : "v"(off), "s"(base), "s"(lds) : "memory");
 }
 
+// Four dwordx4 copies and one dword copy (each lane its own 32-bit offset
+// from a wave-uniform base, to LDS M0 + lane * size) in one statement: M0 is
+// saved once and restored once for the five.  A copy reads M0 one wait
+// state after the SALU write that set it.
+__device__ __forceinline__ void dma5s(uint32_t o0, const void *b0, uint32_t l0, uint32_t o1, const void *b1,
+                                      uint32_t l1, uint32_t o2, const void *b2, uint32_t l2, uint32_t o3,
+                                      const void *b3, uint32_t l3, uint32_t o4, const void *b4, uint32_t l4)
+{
+    uint32_t save;
+    asm volatile("s_mov_b32 %0, m0\n\t"
+                 "s_mov_b32 m0, %3\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2\n\t"
+                 "s_mov_b32 m0, %6\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %4, %5\n\t"
+                 "s_mov_b32 m0, %9\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %7, %8\n\t"
+                 "s_mov_b32 m0, %12\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %10, %11\n\t"
+                 "s_mov_b32 m0, %15\n\ts_nop 0\n\tglobal_load_lds_dword %13, %14\n\t"
+                 "s_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "v"(o0), "s"(b0), "s"(l0), "v"(o1), "s"(b1), "s"(l1), "v"(o2), "s"(b2), "s"(l2),
+                   "v"(o3), "s"(b3), "s"(l3), "v"(o4), "s"(b4), "s"(l4)
+                 : "memory");
+}
+
 // Value of lane ^ 1 (resp. lane ^ 2) by a DPP quad permutation: a VALU
 // operation, where __shfl_xor goes through the LDS permute unit.
 __device__ __forceinline__ float xor1_dpp(float v)
