@@ -270,9 +270,11 @@ constexpr int st_lds() { return 2 * 4 * 16 * (16 * NFH + 1) * 4; }
 // workgroups, each streaming only as fast as its own blocks in flight allow:
 // a tail as long as a full round for a few percent of the work.  Instead each
 // remainder item is split into S segments of the reduction dimension (S L <=
-// G / 2, at least 8 blocks each; the remainder is widened back to the first
-// tile of its first expert, so all rows of an expert are summed the same way
-// whatever their order within the expert) run by S L more workgroups, which store
+// G / 2, at least 8 blocks each, and S L within the grid's room past the
+// whole items, which is sized for the most row tiles there can be; the
+// remainder is widened back to the first tile of its first expert, so all
+// rows of an expert are summed the same way whatever their order within the
+// expert) run by S L more workgroups, which store
 // their fp32 partial sums as tagged words (tag = the kernel's generation + 1,
 // new in every launch); the last segment to finish adds them in segment order
 // and applies the epilogue (st_last, st_seg_sum).  The tags stand in for a
@@ -292,12 +294,22 @@ __device__ __forceinline__ bool st_work(int R, int G, int nb, int ncg, int bm, c
 {
     int W = R;                               // items run whole
     int L = 0, S = 1;
-    if (R % G) {
-        const int t = R / G * G / ncg;      // tile of the first remainder item
+    // R mod G by subtraction (R / G is a few rounds at most): the divisions
+    // below sit on every workgroup's way to its first load, so they are
+    // taken only where a split can follow (S >= 2: G >= 4 L, blocks >= 16;
+    // widening the remainder only narrows S)
+    int rem = R;
+    while (rem >= G) rem -= G;
+    if (rem && 4 * rem <= G && nb >= 16) {
+        const int t = (R - rem) / ncg;      // tile of the first remainder item
         W = (t - tile_m0[t] / bm) * ncg;
         L = R - W;
-        S = max(1, min(min(G / (2 * L), nb / 8), ST_SEG_MAX));
-        if (S == 1) W = R;
+        const int room = (int)gridDim.x - 8 * ((W + 7) >> 3);
+        S = max(1, min(min(min(G / (2 * L), nb / 8), ST_SEG_MAX), room / L));
+        if (S == 1) {
+            W = R;
+            L = 0;
+        }
     }
     const int per = (W + 7) >> 3;
     const int b = blockIdx.x;
@@ -451,7 +463,8 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
 #pragma unroll
         for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int kb0 = wk.seg * a.nbH / wk.nseg, kb1 = (wk.seg + 1) * a.nbH / wk.nseg;
+    const int kb0 = wk.nseg > 1 ? wk.seg * a.nbH / wk.nseg : 0;
+    const int kb1 = wk.nseg > 1 ? (wk.seg + 1) * a.nbH / wk.nseg : a.nbH;
     const uint32_t tag =
         wk.nseg > 1 ? __hip_atomic_load(a.seg_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
     st_mainloop<MF, NFH>(src, kb0, kb1 - kb0, wave, acc);
@@ -465,14 +478,16 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_gateup_kernel(Stream
         __syncthreads();
         st_spill<MF, NFH>(red0, red1, acc, m, wave, lane);
         __syncthreads();
-        for (int i = threadIdx.x; i < 16 * NC; i += ST_THREADS) {
+        // the tile's rows only (a split item's last segment reads those alone)
+        const int nr = min(16, n - 16 * m);
+        for (int i = threadIdx.x; i < nr * NC; i += ST_THREADS) {
             const int row = i / NC, c = i % NC;
             const int f = f0 + c;
             const float g = wave_order_sum<NFH>(red0, row, c), u = wave_order_sum<NFH>(red1, row, c);
             if (wk.nseg > 1) {
                 store_tagged(pp + (16 * m + row) * 2 * NC + c, tag, __float_as_uint(g));
                 store_tagged(pp + (16 * m + row) * 2 * NC + NC + c, tag, __float_as_uint(u));
-            } else if (16 * m + row < n && f < a.F) {
+            } else if (f < a.F) {
                 a.act[(size_t)(slot0 + 16 * m + row) * a.F + f] = silu_mul(g, u);
             }
         }
@@ -530,7 +545,8 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
 #pragma unroll
         for (int j = 0; j < 2 * NFH; j++) acc[m][j] = f4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-    const int kb0 = wk.seg * a.nbF / wk.nseg, kb1 = (wk.seg + 1) * a.nbF / wk.nseg;
+    const int kb0 = wk.nseg > 1 ? wk.seg * a.nbF / wk.nseg : 0;
+    const int kb1 = wk.nseg > 1 ? (wk.seg + 1) * a.nbF / wk.nseg : a.nbF;
     const uint32_t tag =
         wk.nseg > 1 ? __hip_atomic_load(a.seg_gen, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1u : 0u;
     st_mainloop<MF, NFH>(src, kb0, kb1 - kb0, wave, acc);
@@ -544,13 +560,15 @@ __global__ __launch_bounds__(ST_THREADS, 2) void moe_stream_down_kernel(StreamAr
         __syncthreads();
         st_spill<MF, NFH>(red0, red1, acc, m, wave, lane);
         __syncthreads();
-        for (int i = threadIdx.x; i < 16 * 128; i += ST_THREADS) {
+        // the tile's rows only (a split item's last segment reads those alone)
+        const int nr = min(16, n - 16 * m);
+        for (int i = threadIdx.x; i < nr * 128; i += ST_THREADS) {
             const int row = i >> 7, c = i & 127;
             const int h = h0 + c;
             const float v = wave_order_sum<NFH>(c < 64 ? red0 : red1, row, c & 63);
             if (wk.nseg > 1)
                 store_tagged(pp + (16 * m + row) * 128 + c, tag, __float_as_uint(v));
-            else if (16 * m + row < n && h < a.H)
+            else if (h < a.H)
                 a.y[(size_t)(slot0 + 16 * m + row) * a.H + h] = v;
         }
     }
@@ -684,11 +702,10 @@ int launch_moe_stream(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
         return set_error(ctx, "stream path: partial sums exceed %d words", SEG_PART_WORDS);
 
     // grids (st_work): 8 * ceil(items / 8) workgroups for the items of cap
-    // row tiles run whole, and up to G / 2 segment workgroups
+    // row tiles; split items' segments take the room past the items there are
     const int nfh = stream_gateup_nfh(ctx, m, T);
-    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 16 * nfh - 1) / (16 * nfh)) + 7) / 8) +
-                        (unsigned)(a.G / 2);
-    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8) + (unsigned)(a.G / 2);
+    const unsigned g1 = 8u * (unsigned)(((size_t)cap * ((m->F + 16 * nfh - 1) / (16 * nfh)) + 7) / 8);
+    const unsigned g2 = 8u * (unsigned)(((size_t)cap * ((m->H + 127) / 128) + 7) / 8);
     prof_begin(ctx, K_STREAM_GATEUP);
     if (MF == 1 && nfh == 7)
         QQ_LAUNCH(ctx, (moe_stream_gateup_kernel<1, 7>), dim3(g1), dim3(ST_THREADS), 0, a);
