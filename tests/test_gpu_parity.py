@@ -325,16 +325,18 @@ def test_moe_batch_one_launch_routing(case):
     _check_moe(L, x, hid, mask=mask)
 
 
-@pytest.mark.parametrize("T,hot,tiles", [
-    (64, -1, 33),    # one expert at 18 rows: 16 items past 512 (8 gate/up, 7 down segments)
-    (64, 1, 35),     # 48 items past: 5 segments each
-    (64, 2, 37),     # 80 past: 3 segments
-    (112, 0, 38),    # 96 past: 2 segments
-    (128, 0, 45),    # 208 past: a second round of whole items
-    (200, 0, None),  # 32-row tiles (gate/up items of 64 features)
-    (256, 2, None),
+@pytest.mark.parametrize("shape,T,hot,tiles", [
+    ("lfm2", 64, -1, 33),    # one expert at 18 rows: 16 items past 512 (8 gate/up, 7 down segments)
+    ("lfm2", 64, 1, 35),     # 48 items past: 5 segments each
+    ("lfm2", 64, 2, 37),     # 80 past: 3 segments
+    ("lfm2", 112, 0, 38),    # 96 past: 2 segments
+    ("lfm2", 128, 0, 45),    # 208 past: a second round of whole items
+    ("lfm2", 200, 0, None),  # 32-row tiles (gate/up items of 64 features)
+    ("lfm2", 256, 2, None),
+    ("qwen3", 19, 0, 89),    # 16-row tiles, 64-feature gate/up items: 48 past, 5 segments
+    ("qwen3", 23, 0, 101),   # down rows of 24 blocks: 80 past, 3 segments
 ])
-def test_moe_batch_remainder_items(T, hot, tiles):
+def test_moe_batch_remainder_items(shape, T, hot, tiles):
     """Decode batches whose items (row tiles x column groups) overflow the 512
     resident workgroups of a 256-CU MI355X by a remainder: the remainder items
     are split along the reduction dimension, each segment's fp32 partial sums
@@ -342,20 +344,27 @@ def test_moe_batch_remainder_items(T, hot, tiles):
     within the batch tolerance; a second input in between and the first input
     again bit for bit (the segment counters return to zero after each launch).
     hot: experts 0 .. hot-1 get bias +1 (picked by every token); -1: expert 5
-    gets +0.1 (18 of the 64 tokens)."""
-    _say("moe remainder items", T, hot, tiles)
-    L = dict(full_layer(1))
-    L["bias"] = L["bias"].copy()
-    if hot > 0:
-        L["bias"][:hot] += 1.0
-    elif hot < 0:
-        L["bias"][5] += 0.1
-    x, hid = synth.activations(202, T, 2048)
+    gets +0.1 (18 of the 64 tokens).  qwen3: the Qwen3-30B-A3B-shaped layer
+    (E=128, K=8, F=768, softmax gating)."""
+    _say("moe remainder items", shape, T, hot, tiles)
+    if shape == "qwen3":
+        L = synth.moe_layer(91, H=2048, F=768, E=128, K=8, bias=None, gating="softmax", router_std=0.05)
+        x, hid = synth.activations(92, T, 2048)
+    else:
+        L = dict(full_layer(1))
+        L["bias"] = L["bias"].copy()
+        if hot > 0:
+            L["bias"][:hot] += 1.0
+        elif hot < 0:
+            L["bias"][5] += 0.1
+        x, hid = synth.activations(202, T, 2048)
     x2, hid2 = synth.activations(203, T, 2048)
     r_idx, _, _ = oracle.moe_route(L, x)
-    c = np.bincount(r_idx.ravel(), minlength=32)
+    E, K = L["E"], L["K"]
+    bm = 16 if T * K <= 16 * E else 32
+    c = np.bincount(r_idx.ravel(), minlength=E)
     if tiles is not None:
-        assert int(np.sum((c + 15) // 16)) == tiles, c
+        assert int(np.sum((c + bm - 1) // bm)) == tiles, c
     ctx = gpu_context()
     m = upload_layer(ctx, L)
     try:
