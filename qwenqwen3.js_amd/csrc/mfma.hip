@@ -177,13 +177,15 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
     for (int st = 0; st < 2; st++) ao[st] = 16 * mg_aslot(lane & 31, 2 * (lane >> 5) + st);
     const int bo = MG_A + (wave * 2) * 1024 + 16 * mg_bslot(lane & 31, lane >> 5);
 
-    auto issue = [&](int b) {
-        const uint32_t so = (uint32_t)(b % MG_STAGES) * MG_STAGE;
+    // (stage st of the ring: block b % MG_STAGES; a literal in the unrolled loop)
+    auto issue_s = [&](int b, int st) {
+        const uint32_t so = (uint32_t)st * MG_STAGE;
         const char *ab = src.abase + (size_t)b * 64;
         dma5s(src.a0, ab, da0 + so, src.a1, ab, da1 + so, src.b0, src.bbase0 + (size_t)b * src.bstep, db0 + so,
               src.b1, src.bbase1 + (size_t)b * src.bstep, db1 + so, src.sc, src.sbase + (size_t)b * src.sstep,
               ds + so);
     };
+    auto issue = [&](int b) { issue_s(b, b % MG_STAGES); };
     // the wait for the block after the one just issued while MG_AHEAD - 1
     // more are in flight behind it (5 copies a block per wave)
     auto wait_steady = [&]() { wait_vm<5 * (MG_AHEAD - 1)>(); };
@@ -196,8 +198,8 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
         h8_t b[2][2];
         h8_t a0[NFR];
     };
-    auto fetch = [&](int b, Frag &f) {
-        const char *st = lds + (b % MG_STAGES) * MG_STAGE;
+    auto fetch_s = [&](int sg, Frag &f) {
+        const char *st = lds + sg * MG_STAGE;
         const uint4 q0 = *reinterpret_cast<const uint4 *>(st + bo);
         const uint4 q1 = *reinterpret_cast<const uint4 *>(st + bo + 1024);
         const _Float16 d0 = *reinterpret_cast<const _Float16 *>(st + sc_off0);
@@ -212,9 +214,10 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
         f.b[1][0] = __builtin_bit_cast(h8_t, lo1);
         f.b[1][1] = __builtin_bit_cast(h8_t, hi1);
     };
+    auto fetch = [&](int b, Frag &f) { fetch_s(b % MG_STAGES, f); };
     // block b's MFMAs; the step-1 A fragments are read here, under step 0's MFMAs
-    auto mma = [&](int b, const Frag &f) {
-        const char *st = lds + (b % MG_STAGES) * MG_STAGE;
+    auto mma_s = [&](int sg, const Frag &f) {
+        const char *st = lds + sg * MG_STAGE;
         h8_t a1[NFR];
 #pragma unroll
         for (int i = 0; i < NFR; i++) a1[i] = *reinterpret_cast<const h8_t *>(st + ao[1] + 2048 * i);
@@ -229,6 +232,7 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
             acc[i][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1[i], f.b[1][1], acc[i][1], 0, 0, 0);
         }
     };
+    auto mma = [&](int b, const Frag &f) { mma_s(b % MG_STAGES, f); };
 
     // Software pipeline: block b+1's B operands and step-0 A fragments are
     // read (and B dequantised) while block b's MFMAs run (two register sets,
@@ -241,8 +245,32 @@ __device__ __forceinline__ void mg_mainloop(const MgSrc &src, int nb, char *lds,
     __syncthreads();
     fetch(0, f0);
     int b = 0;
-    // steady state: both copies of an iteration go out and both waits leave
-    // MG_AHEAD - 1 blocks in flight
+    // steady state: every copy of an iteration goes out and every wait leaves
+    // MG_AHEAD - 1 blocks in flight.  Four blocks an iteration from b = 0, so
+    // the ring stage of each is a literal (no stage arithmetic per block).
+    static_assert(MG_STAGES == 4, "four blocks per steady iteration, one per stage");
+    for (; b + 3 + MG_AHEAD < nb; b += 4) {
+        issue_s(b + MG_AHEAD, MG_AHEAD % 4);
+        wait_steady();
+        __syncthreads();
+        fetch_s(1, f1);
+        mma_s(0, f0);
+        issue_s(b + 1 + MG_AHEAD, (1 + MG_AHEAD) % 4);
+        wait_steady();
+        __syncthreads();
+        fetch_s(2, f0);
+        mma_s(1, f1);
+        issue_s(b + 2 + MG_AHEAD, (2 + MG_AHEAD) % 4);
+        wait_steady();
+        __syncthreads();
+        fetch_s(3, f1);
+        mma_s(2, f0);
+        issue_s(b + 3 + MG_AHEAD, (3 + MG_AHEAD) % 4);
+        wait_steady();
+        __syncthreads();
+        fetch_s(0, f0);
+        mma_s(3, f1);
+    }
     for (; b + 1 + MG_AHEAD < nb; b += 2) {
         issue(b + MG_AHEAD);
         wait_steady();
