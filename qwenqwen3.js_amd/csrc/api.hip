@@ -617,11 +617,16 @@ static size_t forward_scratch(const qq_ctx *ctx, const qq_moe *m, int T)
 
 // x, hidden (and the optional outputs) are device pointers; s holds
 // forward_scratch(ctx, m, T) bytes (256-byte aligned).  Allocates nothing.
+// With norm, x = rmsnorm(hidden) of each chunk is formed first: by the
+// router launch itself on the MFMA path (router_norm_supported), else into
+// xn (T x H floats) and x is ignored.
 static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidden, int T,
-                       const MaskBits &mask, int32_t *idx, double *w, float *probs, char *s)
+                       const MaskBits &mask, int32_t *idx, double *w, float *probs, char *s,
+                       const NormArgs *norm = nullptr, float *xn = nullptr)
 {
     int rc = QQ_OK;
-    if (use_decode(ctx, m, T)) return launch_moe_decode(ctx, m, x, hidden, mask, idx, w, probs);
+    if (use_decode(ctx, m, T))
+        return launch_moe_decode(ctx, m, norm ? hidden : x, hidden, mask, idx, w, probs, norm);
     const size_t Tc = (size_t)(T < T_CHUNK ? T : T_CHUNK);
     double *part = reinterpret_cast<double *>(s);
     int32_t *sidx = reinterpret_cast<int32_t *>(s + align256(router_work_bytes(m, (int)Tc)));
@@ -632,12 +637,16 @@ static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
         int32_t *ci = idx ? idx + (size_t)t0 * m->K : sidx;
         double *cw = w ? w + (size_t)t0 * m->K : sw;
         float *cp = probs ? probs + (size_t)t0 * m->E : nullptr;
-        const float *cx = x + (size_t)t0 * m->H;
+        const float *cx = (norm ? xn : x) + (size_t)t0 * m->H;
         float *ch = hidden + (size_t)t0 * m->H;
         const Path path = chunk_path(ctx, m, tn, cx);
         // on the MFMA path the router launch also writes the fp16 rows
         void *xh = path == PATH_MFMA ? mfma_xh(m, tn, work) : nullptr;
         bool xh_done = false;
+        const bool nfused = norm && path == PATH_MFMA && router_norm_supported(m, ch, norm->w);
+        if (norm && !nfused &&
+            (rc = launch_rmsnorm(ctx, ch, norm->w, xn + (size_t)t0 * m->H, tn, m->H, norm->eps)))
+            return rc;
         if (path == PATH_STREAM && use_route_fused(ctx, m, tn, cx)) {
             const StreamDispatch d = stream_dispatch(m, tn, work);
             if ((rc = launch_route_dispatch(ctx, m, cx, tn, mask, ci, cw, cp, d.counts, d.offsets, d.perm,
@@ -646,7 +655,9 @@ static int forward_run(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidd
             if ((rc = launch_moe_stream(ctx, m, cx, ch, tn, mask, ci, cw, work, true))) return rc;
             continue;
         }
-        if ((rc = launch_router_topk(ctx, m, cx, tn, part, ci, cw, cp, xh, &xh_done))) return rc;
+        if ((rc = launch_router_topk(ctx, m, nfused ? ch : cx, tn, part, ci, cw, cp, xh, &xh_done,
+                                     nfused ? norm : nullptr)))
+            return rc;
         switch (path) {
         case PATH_MFMA: rc = launch_moe_mfma(ctx, m, cx, ch, tn, mask, ci, cw, work, xh_done); break;
         case PATH_STREAM: rc = launch_moe_stream(ctx, m, cx, ch, tn, mask, ci, cw, work); break;
@@ -718,12 +729,13 @@ int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev, con
         // every workgroup of the decode kernel normalises the row itself
         return launch_moe_decode(ctx, m, hidden_dev, hidden_dev, mb, idx_dev, w_dev, probs_dev, &norm);
     }
-    // x = rmsnorm(hidden) at the start of the scratch, then the forward
+    // x = rmsnorm(hidden), chunk by chunk, at the start of the scratch (or
+    // formed by the router launch), then the forward
     const size_t xb = align256((size_t)T * m->H * 4);
     if ((rc = ensure_scratch(ctx, xb + forward_scratch(ctx, m, T)))) return rc;
     float *x = static_cast<float *>(ctx->scratch);
-    if ((rc = launch_rmsnorm(ctx, hidden_dev, norm_w_dev, x, T, m->H, eps))) return rc;
-    return forward_impl(ctx, m, x, hidden_dev, T, mb, idx_dev, w_dev, probs_dev, xb);
+    return forward_run(ctx, m, x, hidden_dev, T, mb, idx_dev, w_dev, probs_dev,
+                       static_cast<char *>(ctx->scratch) + xb, &norm, x);
 }
 
 // ---- MoE stacks ------------------------------------------------------------

@@ -255,10 +255,14 @@ int launch_q8_0_matvec(qq_ctx *ctx, const qq_tensor *t, int mat, const float *x,
 constexpr int ROUTER_MAX_SPLIT = 8;
 size_t router_work_bytes(const qq_moe *m, int T);
 // With xh (T x H fp16) the F32 matrix-core router also stores x rounded to
-// fp16 there and sets *xh_done.
+// fp16 there and sets *xh_done.  With norm, x holds residual rows and the
+// router forms rmsnorm(x) itself, bit-equal to launch_rmsnorm's rows (needs
+// router_norm_supported and xh).
+struct NormArgs;
+bool router_norm_supported(const qq_moe *m, const float *hidden, const float *norm_w);
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
                        int32_t *idx, double *w, float *probs, void *xh = nullptr,
-                       bool *xh_done = nullptr);
+                       bool *xh_done = nullptr, const NormArgs *norm = nullptr);
 // Router, top-K and dispatch of a small batch in one launch (all workgroups
 // resident, tagged-word exchange through the context's sync area); writes
 // what launch_router_topk and launch_dispatch together write.

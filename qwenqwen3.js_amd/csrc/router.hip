@@ -62,14 +62,25 @@ struct RouterW {
 // 16-wide k steps round robin inside the workgroup's slice; the four waves'
 // accumulators are added in wave order.  part[ks][t][e] (binary64).
 // f64 accumulator layout: lane l, element r -> row 4r + l/16, column l%16.
+//
+// NRM: x holds the residual rows, and the workgroup forms x = rmsnorm(row)
+// (src/lfm2-engine.js:251-252) itself as it loads them: out of nw (or unit
+// weights), eps and each token's 1 / sqrt(sum x^2 / H + eps), whose sum of
+// squares is rmsnorm_kernel's own binary64 tree (wave w takes tokens 4w ..
+// 4w + 3; lane l plays thread 64 v + l of the normalising block for v = 0 ..
+// NORM_THREADS / 64 - 1), so logits and fp16 rows equal those of the two
+// launches bit for bit.
 // ---------------------------------------------------------------------------
-template <bool Q8>
+template <bool Q8, bool NRM>
 __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restrict__ x, int T,
                                                           RouterW W, int kchunk,
                                                           double *__restrict__ part,
-                                                          _Float16 *__restrict__ xh)
+                                                          _Float16 *__restrict__ xh,
+                                                          const float *__restrict__ nw, double eps)
 {
+    static_assert(!(Q8 && NRM), "the norm is formed on the F32 router path only");
     __shared__ double red[4][16][33];
+    __shared__ double sinv[16];
     const int t0 = blockIdx.x * 16, ks = blockIdx.y, e0 = blockIdx.z * 32;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int r16 = lane & 15, kq = lane >> 4;
@@ -77,6 +88,60 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
     const double tz = t < T ? 1.0 : 0.0;
     const float *xr = x + (size_t)min(t, T - 1) * W.H;
     const int ka = ks * kchunk, kb = min(W.H, ka + kchunk);
+    double inv = 1.0;
+    if constexpr (NRM) {
+        constexpr int NV = NORM_THREADS / WAVE;
+        constexpr int NJ = 4;   // values 4 x NORM_THREADS of a row per pass of loads
+        for (int i0 = 0; i0 < 4; i0 += 2) {
+            double s[2][NV];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int v = 0; v < NV; v++) s[i][v] = 0.0;
+            // thread 64 v + l adds k = 64 v + l + 512 j for j = 0, 1, ... in
+            // order; past H the term is an exact no-op (s + 0 with s >= +0).
+            // Two tokens' loads of a pass go out together.
+            for (int j0 = 0; j0 < W.H; j0 += NJ * NORM_THREADS) {
+                float q[2][NJ][NV];
+#pragma unroll
+                for (int i = 0; i < 2; i++) {
+                    const float *hr = x + (size_t)min(t0 + 4 * wave + i0 + i, T - 1) * W.H;
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+#pragma unroll
+                        for (int v = 0; v < NV; v++)
+                            q[i][j][v] = hr[min(j0 + j * NORM_THREADS + WAVE * v + lane, W.H - 1)];
+                }
+                // every load above goes out before the first use (a load under
+                // its own bounds branch is waited for inside that branch)
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+#pragma unroll
+                        for (int v = 0; v < NV; v++) asm volatile("" : "+v"(q[i][j][v]));
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < NJ; j++)
+#pragma unroll
+                        for (int v = 0; v < NV; v++) {
+                            const int k = j0 + j * NORM_THREADS + WAVE * v + lane;
+                            const double d = k < W.H ? (double)q[i][j][v] : 0.0;
+                            s[i][v] = fma(d, d, s[i][v]);
+                        }
+            }
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                double r = wave_sum_dpp(s[i][0]);
+#pragma unroll
+                for (int v = 1; v < NV; v++) r = r + wave_sum_dpp(s[i][v]);
+                if (lane == 0) sinv[4 * wave + i0 + i] = rms_inv(r, W.H, eps);
+            }
+        }
+        __syncthreads();
+        inv = sinv[r16];
+    }
 
     d4_t acc0 = {0.0, 0.0, 0.0, 0.0}, acc1 = {0.0, 0.0, 0.0, 0.0};
     auto step = [&](const float4 xv, const double (&wa)[4], const double (&wb)[4]) {
@@ -97,13 +162,14 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
         const int ea = min(e0 + r16, W.E - 1), eb = min(e0 + 16 + r16, W.E - 1);
         const double za = e0 + r16 < W.E ? 1.0 : 0.0, zb = e0 + 16 + r16 < W.E ? 1.0 : 0.0;
         for (; k < kb; k += 64 * RB) {
-            float4 xv[RB], va[RB], vb[RB];
+            float4 xv[RB], va[RB], vb[RB], nv[RB];
 #pragma unroll
             for (int u = 0; u < RB; u++) {
                 const int kk = min(k + 64 * u, kb - 16) + 4 * kq;
                 xv[u] = *reinterpret_cast<const float4 *>(xr + kk);
                 va[u] = *reinterpret_cast<const float4 *>(W.f32 + (size_t)ea * W.H + kk);
                 vb[u] = *reinterpret_cast<const float4 *>(W.f32 + (size_t)eb * W.H + kk);
+                nv[u] = (NRM && nw) ? *reinterpret_cast<const float4 *>(nw + kk) : make_float4(1.0f, 1.0f, 1.0f, 1.0f);
             }
             // keeps the loads above the skip test below (otherwise each is
             // sunk into its step's branch and waited for there)
@@ -112,6 +178,17 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const float *__restric
                 asm volatile("" : "+v"(xv[u].x), "+v"(xv[u].y), "+v"(xv[u].z), "+v"(xv[u].w),
                                   "+v"(va[u].x), "+v"(va[u].y), "+v"(va[u].z), "+v"(va[u].w),
                                   "+v"(vb[u].x), "+v"(vb[u].y), "+v"(vb[u].z), "+v"(vb[u].w));
+            if constexpr (NRM) {
+                // rmsnorm_kernel's out[k] = fp32(w[k] * x[k] * inv)
+#pragma unroll
+                for (int u = 0; u < RB; u++) {
+                    const float4 wv = nv[u];
+                    xv[u].x = (float)((double)wv.x * (double)xv[u].x * inv);
+                    xv[u].y = (float)((double)wv.y * (double)xv[u].y * inv);
+                    xv[u].z = (float)((double)wv.z * (double)xv[u].z * inv);
+                    xv[u].w = (float)((double)wv.w * (double)xv[u].w * inv);
+                }
+            }
 #pragma unroll
             for (int u = 0; u < RB; u++) {
                 if (k + 64 * u >= kb) break;
@@ -589,11 +666,20 @@ size_t router_work_bytes(const qq_moe *m, int T)
     return (size_t)router_split(m, T) * T * m->E * sizeof(double);
 }
 
+bool router_norm_supported(const qq_moe *m, const float *hidden, const float *norm_w)
+{
+    return m->router_type == QQ_TYPE_F32 && m->H % 16 == 0 && ((uintptr_t)hidden & 15) == 0 &&
+           ((uintptr_t)norm_w & 15) == 0;
+}
+
 int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, double *part,
-                       int32_t *idx, double *w, float *probs, void *xh, bool *xh_done)
+                       int32_t *idx, double *w, float *probs, void *xh, bool *xh_done,
+                       const NormArgs *norm)
 {
     if (xh_done) *xh_done = false;
     if (T <= 0) return QQ_OK;
+    if (norm && !(router_norm_supported(m, x, norm->w) && xh && xh_done))
+        return set_error(ctx, "router: the norm is formed only by the F32 matrix-core router with fp16 rows");
     const bool q8 = m->router_type == QQ_TYPE_Q8_0;
     RouterW W;
     W.f32 = m->router_f32;
@@ -609,10 +695,15 @@ int launch_router_topk(qq_ctx *ctx, const qq_moe *m, const float *x, int T, doub
         const int kchunk = ((m->H + KS * 64 - 1) / (KS * 64)) * 64;
         const dim3 g((T + 15) / 16, KS, (m->E + 31) / 32);
         if (q8) {
-            QQ_LAUNCH(ctx, router_mfma_kernel<true>, g, dim3(256), 0, x, T, W, kchunk, part, nullptr);
+            QQ_LAUNCH(ctx, (router_mfma_kernel<true, false>), g, dim3(256), 0, x, T, W, kchunk, part, nullptr,
+                      nullptr, 0.0);
+        } else if (norm) {
+            QQ_LAUNCH(ctx, (router_mfma_kernel<false, true>), g, dim3(256), 0, x, T, W, kchunk, part,
+                      static_cast<_Float16 *>(xh), norm->w, norm->eps);
+            *xh_done = true;
         } else {
-            QQ_LAUNCH(ctx, router_mfma_kernel<false>, g, dim3(256), 0, x, T, W, kchunk, part,
-                      static_cast<_Float16 *>(xh));
+            QQ_LAUNCH(ctx, (router_mfma_kernel<false, false>), g, dim3(256), 0, x, T, W, kchunk, part,
+                      static_cast<_Float16 *>(xh), nullptr, 0.0);
             if (xh && xh_done) *xh_done = true;
         }
     } else {

@@ -40,29 +40,37 @@ def test_rmsnorm_matches_oracle(T, H):
     assert np.max(np.abs(gw - refw) / np.maximum(np.abs(refw), 1e-30)) < 3e-7
 
 
-@pytest.mark.parametrize("T,mfma,weighted,gating", [(1, 0, False, "sigmoid"),
-                                                    (1, 0, True, "sigmoid"),
-                                                    (64, 0, True, "sigmoid"),
-                                                    (96, 64, False, "sigmoid"),
-                                                    (1, 0, True, "softmax")])
-def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating):
+@pytest.mark.parametrize("T,mfma,weighted,gating,H", [(1, 0, False, "sigmoid", 512),
+                                                      (1, 0, True, "sigmoid", 512),
+                                                      (64, 0, True, "sigmoid", 512),
+                                                      (96, 64, False, "sigmoid", 512),
+                                                      (1, 0, True, "softmax", 512),
+                                                      # MFMA chunks: the router forms the norm
+                                                      (97, 64, True, "sigmoid", 800),
+                                                      (600, 64, True, "sigmoid", 2048),
+                                                      (600, 64, False, "softmax", 512),
+                                                      # a 4096-token MFMA chunk, then a 4-token
+                                                      # stream chunk normalised by its own launch
+                                                      (4100, 64, True, "sigmoid", 512)])
+def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating, H):
     """qq_moe_forward_norm_dev == qq_rmsnorm_dev then qq_moe_forward_dev, bit for bit
-    (a single row is normalised inside the decode kernel)."""
+    (a single row is normalised inside the decode kernel, the rows of an MFMA
+    chunk inside its router launch)."""
     import torch
     import synth
     from _util import upload_layer
-    print("fused norm+moe", T, mfma, weighted, gating, flush=True)
+    print("fused norm+moe", T, mfma, weighted, gating, H, flush=True)
     ctx = gpu_context()
     ctx.set_mfma_min_tokens(mfma)
     if gating == "softmax":
-        L = synth.moe_layer(41, H=512, F=256, E=128, K=4, bias=None, gating="softmax")
+        L = synth.moe_layer(41, H=H, F=256, E=128, K=4, bias=None, gating="softmax")
     else:
-        L = synth.moe_layer(41, H=512, F=256, E=16, K=4)
+        L = synth.moe_layer(41, H=H, F=256, E=16, K=4)
     m = upload_layer(ctx, L)
     try:
         rng = np.random.default_rng(T + 7)
-        h0 = (rng.standard_normal((T, 512)) * 2).astype(np.float32)
-        w = rng.uniform(0.5, 1.5, 512).astype(np.float32) if weighted else None
+        h0 = (rng.standard_normal((T, H)) * 2).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, H).astype(np.float32) if weighted else None
         dh0 = torch.from_numpy(h0).cuda()
         dw = torch.from_numpy(w).cuda() if weighted else None
         wp = dw.data_ptr() if weighted else None
@@ -72,7 +80,7 @@ def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating):
         xn = torch.empty_like(dh0)
         torch.cuda.synchronize()
         m.forward_norm_dev(ha.data_ptr(), T, norm_w_ptr=wp, eps=1e-5, idx_ptr=idx_a.data_ptr())
-        ctx.rmsnorm_dev(hb.data_ptr(), wp, xn.data_ptr(), T, 512, 1e-5)
+        ctx.rmsnorm_dev(hb.data_ptr(), wp, xn.data_ptr(), T, H, 1e-5)
         m.forward_dev(xn.data_ptr(), hb.data_ptr(), T, idx_ptr=idx_b.data_ptr())
         ctx.synchronize()
         assert np.array_equal(idx_a.cpu().numpy(), idx_b.cpu().numpy())
