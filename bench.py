@@ -534,7 +534,7 @@ def prefill_leg(torch, ctx, stream, steps, warmup, n_layers=4):
     return out
 
 
-# BASELINE.md's ceilings: (ideal time at the roofline, the north-star target)
+# Per workload: (ideal time at the roofline, the performance target in ms per step)
 LEG_TARGETS = {
     "q8_0_matvec_1024x3072": ("0.42 us per matvec at 8 TB/s (launch bound)", None),
     "moe_layer_decode_batch64": ("47.0 us per step at 8 TB/s", 78.3e-3),
