@@ -51,7 +51,12 @@ def test_rmsnorm_matches_oracle(T, H):
                                                       (600, 64, False, "softmax", 512),
                                                       # a 4096-token MFMA chunk, then a 4-token
                                                       # stream chunk normalised by its own launch
-                                                      (4100, 64, True, "sigmoid", 512)])
+                                                      (4100, 64, True, "sigmoid", 512),
+                                                      # MFMA chunks normalised by their own launch:
+                                                      # a Q8_0 router, norm weights 4 bytes off a
+                                                      # 16-byte boundary
+                                                      (600, 64, True, "q8router", 512),
+                                                      (600, 64, True, "offset_w", 512)])
 def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating, H):
     """qq_moe_forward_norm_dev == qq_rmsnorm_dev then qq_moe_forward_dev, bit for bit
     (a single row is normalised inside the decode kernel, the rows of an MFMA
@@ -64,6 +69,8 @@ def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating, H):
     ctx.set_mfma_min_tokens(mfma)
     if gating == "softmax":
         L = synth.moe_layer(41, H=H, F=256, E=128, K=4, bias=None, gating="softmax")
+    elif gating == "q8router":
+        L = synth.moe_layer(41, H=H, F=256, E=16, K=4, router_type=synth.TYPE_Q8_0)
     else:
         L = synth.moe_layer(41, H=H, F=256, E=16, K=4)
     m = upload_layer(ctx, L)
@@ -72,7 +79,12 @@ def test_fused_norm_moe_matches_two_calls(T, mfma, weighted, gating, H):
         h0 = (rng.standard_normal((T, H)) * 2).astype(np.float32)
         w = rng.uniform(0.5, 1.5, H).astype(np.float32) if weighted else None
         dh0 = torch.from_numpy(h0).cuda()
-        dw = torch.from_numpy(w).cuda() if weighted else None
+        if gating == "offset_w":
+            dwb = torch.zeros(H + 1, dtype=torch.float32, device="cuda")
+            dwb[1:] = torch.from_numpy(w).cuda()
+            dw = dwb[1:]
+        else:
+            dw = torch.from_numpy(w).cuda() if weighted else None
         wp = dw.data_ptr() if weighted else None
         idx_a = torch.empty((T, 4), dtype=torch.int32, device="cuda")
         idx_b = torch.empty_like(idx_a)
