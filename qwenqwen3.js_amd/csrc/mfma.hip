@@ -50,24 +50,19 @@ __global__ __launch_bounds__(256) void cast_f16_kernel(const float4 *__restrict_
 }
 
 // 16 int8 weights of one column (half a Q8_0 block) and the block's fp16
-// scale -> 16 fp16 values w = fp16(q * d), in k order.  Each byte is made
-// offset binary (u = q + 128) and paired with the exponent byte 0x64, so the
-// half 0x64uu is exactly 1024 + u; subtracting 1152 gives q exactly, and the
-// multiply by d is the one rounding.
+// scale -> 16 fp16 values w = fp16(q * d), in k order: q converts exactly
+// (|q| <= 128), and the multiply by d is the one rounding.  Six instructions
+// per four weights (an offset-binary form, bytes paired with the exponent
+// byte 0x64 by v_perm and 1152 subtracted, took seven: 1.5-2 % slower GEMMs).
 __device__ __forceinline__ void dequant16(const uint4 q, const _Float16 d, uint4 &lo, uint4 &hi)
 {
-    const uint32_t w[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u,
-                           q.w ^ 0x80808080u};
-    const h2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
     const h2_t dd = {d, d};
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        // bytes {b0, 0x64, b1, 0x64} and {b2, 0x64, b3, 0x64}
-        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u);
-        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u);
-        const h2_t a = (__builtin_bit_cast(h2_t, p0) + off) * dd;
-        const h2_t b = (__builtin_bit_cast(h2_t, p1) + off) * dd;
+        const h2_t a = __builtin_bit_cast(h2_t, i8pair_f16<0>(w[i])) * dd;
+        const h2_t b = __builtin_bit_cast(h2_t, i8pair_f16<2>(w[i])) * dd;
         o[2 * i] = __builtin_bit_cast(uint32_t, a);
         o[2 * i + 1] = __builtin_bit_cast(uint32_t, b);
     }

@@ -78,6 +78,26 @@ __device__ __forceinline__ double rms_inv(double sumsq, int H, double eps)
     return 1.0 / sqrt(sumsq / (double)H + eps);
 }
 
+// Two int8 values of w (bytes LO, LO + 1) -> two fp16 halves holding the
+// same integers exactly: v_cvt_f16_i16 on a sign-extended byte (SDWA byte
+// select), the second written into the high half with the low half kept.
+template <int LO>
+__device__ __forceinline__ uint32_t i8pair_f16(uint32_t w)
+{
+    static_assert(LO == 0 || LO == 2, "byte pair 0-1 or 2-3");
+    uint32_t o;
+    if constexpr (LO == 0) {
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(o) : "v"(w));
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_1"
+            : "+v"(o) : "v"(w));
+    } else {
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_0 dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(o) : "v"(w));
+        asm("v_cvt_f16_i16_sdwa %0, sext(%1) dst_sel:WORD_1 dst_unused:UNUSED_PRESERVE src0_sel:BYTE_3"
+            : "+v"(o) : "v"(w));
+    }
+    return o;
+}
+
 // LDS byte address of a __shared__ object.
 __device__ __forceinline__ uint32_t lds_u32(const void *p)
 {

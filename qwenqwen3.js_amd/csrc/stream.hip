@@ -69,21 +69,13 @@ __device__ __forceinline__ void split8(const float4 a, const float4 b, h8_t &hi,
 }
 
 // 8 int8 weights (one lane's share of a 16x32 fragment) -> 8 fp16 holding
-// the same integers exactly.  Bytes are made offset binary and paired with
-// the exponent byte 0x64 (half 0x64uu = 1024 + u); subtracting 1152 gives q.
+// the same integers exactly (four conversions per four weights; the
+// offset-binary form, bytes paired with the exponent byte 0x64 and 1152
+// subtracted, took five).
 __device__ __forceinline__ h8_t int8_to_f16x8(const uint2 q)
 {
-    const uint32_t w[2] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u};
-    const h2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
-    uint32_t o[4];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04010400u);
-        const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w[i], 0x04030402u);
-        o[2 * i] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p0) + off);
-        o[2 * i + 1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2_t, p1) + off);
-    }
-    return __builtin_bit_cast(h8_t, make_uint4(o[0], o[1], o[2], o[3]));
+    return __builtin_bit_cast(h8_t, make_uint4(i8pair_f16<0>(q.x), i8pair_f16<2>(q.x), i8pair_f16<0>(q.y),
+                                               i8pair_f16<2>(q.y)));
 }
 
 // ---------------------------------------------------------------------------
