@@ -11,8 +11,11 @@
 //
 //  1. Routing.  Member i forms the binary64 router dots of experts i, i + M,
 //     ... with x (forming x = rmsnorm(hidden) first when asked) and publishes
-//     the fp32 logits in its group's table; every workgroup waits for the E
-//     logits of its own table, takes the sigmoid + bias (or softmax) scores
+//     the fp32 logits in its group's table (with more experts than members,
+//     E > M: workgroup j forms expert j's logit alone and publishes it to the
+//     device-coherent tables, so the router is read once, not once per
+//     group); every workgroup waits for the E logits of its own table (or of
+//     the device-coherent one), takes the sigmoid + bias (or softmax) scores
 //     and ranks the experts itself (stable descending order, ties to the
 //     lower index), so every workgroup holds the same idx[K], p[K], w[K].
 //  2. Gate/up.  Group x owns F blocks [x nbF / 8, (x + 1) nbF / 8) of all K
@@ -71,6 +74,9 @@ struct DecodeArgs {
     int H, F, E, K;
     int nbH, nbF;
     int router_q8;
+    int xr;               // router logits across the grid: workgroup j forms expert j's
+                          // (E > 32, one layer); else member i of each group forms
+                          // experts i, i + M, ... for its group
     int softmax;          // Qwen3-MoE gating
     int nbpH;
     int L;                // layers of a stack launch (1 otherwise)
@@ -270,7 +276,8 @@ constexpr int DEC_MAX_FIN = 3 * DEC_THREADS;   // partial + arrival words read b
 constexpr int DEC_MAX_FIN_STACK = 5 * DEC_THREADS;   // ... by one member of a stack launch
 
 // NBW = blocks of H per wave = ceil(ceil(H/32)/8) in {1, 2, 4, 8}; RE = router
-// experts per member (>= ceil(E/M)); EPL = experts per lane (>= ceil(E/64));
+// experts per member (>= ceil(E/M); 1 with xr, one expert per workgroup);
+// EPL = experts per lane (>= ceil(E/64));
 // PP2: a wave takes two (rank, row half) pairs of down rows (K x halves > 8);
 // STACK: the launch runs a.L layers (ffn_norm folded in) on one residual row.
 //
@@ -311,7 +318,9 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     __shared__ __align__(16) float sh_pr[MAX_K];
     __shared__ double sh_w[MAX_K];
     __shared__ uint32_t sh_mrank;
-    __shared__ __align__(16) uint64_t sh_key[32 * RE];
+    // ranking slots (>= E): 32 RE, or 64 EPL for the xr instantiations (RE = 1)
+    constexpr int SLOTS = (EPL > RE) ? WAVE * EPL : 32 * RE;
+    __shared__ __align__(16) uint64_t sh_key[SLOTS];
     __shared__ float redg[DEC_WAVES][DEC_CCH];
     __shared__ float redu[DEC_WAVES][DEC_CCH];
     __shared__ __align__(16) float hl[DEC_MAX_HW];
@@ -354,12 +363,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
             wv[s] = nw[k];
         }
     }
-    // router rows of this member's experts e = mi + M t (F32 router)
+    // router rows of this member's experts e = mi + M t (F32 router; with
+    // xr, expert j)
     float rw[RE][XPT];
     if (!a.router_q8) {
 #pragma unroll
         for (int t = 0; t < RE; t++) {
-            const int e = min(mi + M * t, a.E - 1);
+            const int e = min(a.xr ? j : mi + M * t, a.E - 1);
 #pragma unroll
             for (int s = 0; s < XPT; s++)
                 rw[t][s] = LAYER0(rf32)[(size_t)e * a.H + min(tid + DEC_THREADS * s, a.H - 1)];
@@ -445,12 +455,12 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
         if (k < XN) xl[k] = xv[s];
     }
     // ---- router dots (lfm2-engine.js:418, tensor.js:469-482): exact products, binary64 sums ----
-    const int re = (A.E > mi) ? (A.E - mi + M - 1) / M : 0;
+    const int re = A.xr ? (j < A.E ? 1 : 0) : (A.E > mi) ? (A.E - mi + M - 1) / M : 0;
 #pragma unroll
     for (int t = 0; t < RE; t++) {
         double acc = 0.0;
         if (A.router_q8) {
-            const int e = min(mi + M * t, A.E - 1);
+            const int e = min(A.xr ? j : mi + M * t, A.E - 1);
 #pragma unroll
             for (int s = 0; s < XPT; s++) {
                 const int k = min(tid + DEC_THREADS * s, A.H - 1);
@@ -472,13 +482,13 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     if (l == 0 && tid == PUB) store_dev(&A.arrive[j], (uint64_t)tag << 32);
     if (tid >= PUB && tid - PUB < re) {
         const int t = tid - PUB;
-        const int e = mi + M * t;
+        const int e = A.xr ? j : mi + M * t;
         double s = rsum[t][0];
 #pragma unroll
         for (int w = 1; w < DEC_WAVES; w++) s = s + rsum[t][w];
         const uint64_t word = tag_word(tag, (float)s);
-        store_local(&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
-        if (gx == 0) {
+        if (!A.xr) store_local(&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + e], word);
+        if (gx == 0 || A.xr) {
             // (stack launches: replicas [0, 8) for even layers, [8, 16) for odd)
             constexpr int NREP = STACK ? SYNC_REPLICAS / 2 : SYNC_REPLICAS;
             const int c0 = STACK ? (l & 1) * NREP : 0;
@@ -495,9 +505,10 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     }
 
     {
-        const uint64_t *pl[1] = {&A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, A.E - 1)]};
         const int rc = STACK ? (l & 1) * (SYNC_REPLICAS / 2) + j % (SYNC_REPLICAS / 2) : j % SYNC_REPLICAS;
         const uint64_t *pd[1] = {&A.rdev[(size_t)rc * SYNC_REPLICA_WORDS + min(tid, A.E - 1)]};
+        // with xr every logit comes from the device-coherent tables
+        const uint64_t *pl[1] = {A.xr ? pd[0] : &A.rloc[(size_t)gx * SYNC_LOCAL_WORDS + min(tid, A.E - 1)]};
         bool want[1] = {tid < A.E};
         float *dst[1] = {&sh_lg[min(tid, EPL * WAVE - 1)]};
         const uint32_t tg[1] = {tag};
@@ -566,7 +577,6 @@ __global__ __launch_bounds__(DEC_THREADS) void moe_decode_kernel(DecodeArgs a)
     // score bits, complemented index), and the top K.  The weights w_k =
     // p_k / S (lfm2-engine.js:444-447; qwen3-engine.js:317-321) follow once
     // the weight loads are out ----
-    constexpr int SLOTS = 32 * RE;   // >= E
     float pr[EPL];
     if (ok && wave == 0) {
         float lg[EPL];
@@ -1027,6 +1037,13 @@ bool stack_decode_supported(const qq_ctx *ctx, const qq_moe *m)
 template <int NBW, bool STACK>
 static void launch_re(qq_ctx *ctx, const DecodeArgs &a, dim3 grid, int re, bool pp2)
 {
+    if constexpr (!STACK) {
+        if (a.xr) {   // one expert per workgroup
+            if (a.E <= 2 * WAVE) launch_t<NBW, 1, 2, STACK>(ctx, a, grid, pp2);
+            else launch_t<NBW, 1, 4, STACK>(ctx, a, grid, pp2);
+            return;
+        }
+    }
     if (re <= 1) launch_t<NBW, 1, 1, STACK>(ctx, a, grid, pp2);
     else if (re <= 2) launch_t<NBW, 2, 1, STACK>(ctx, a, grid, pp2);
     else if (re <= 4) launch_t<NBW, 4, 2, STACK>(ctx, a, grid, pp2);
@@ -1060,6 +1077,7 @@ static void decode_common(qq_ctx *ctx, const qq_moe *m, DecodeArgs &a)
     a.nbH = (m->H + QK - 1) / QK;
     a.nbF = (m->F + QK - 1) / QK;
     a.router_q8 = m->router_type == QQ_TYPE_Q8_0;
+    a.xr = 0;
     a.softmax = m->gating == QQ_GATING_SOFTMAX;
     a.nbpH = m->gate->nbp;
     a.epoch_word = ctx->sync_epoch;
@@ -1112,6 +1130,9 @@ int launch_moe_decode(qq_ctx *ctx, const qq_moe *m, const float *x, float *hidde
     a.out_w = out_w;
     a.out_probs = out_probs;
     a.out_rec = out_rec;
+    // more experts than a group has members: each workgroup forms one logit
+    // (the router is read once, not once per group), exchanged device-wide
+    a.xr = m->E > decode_grid(ctx) / DEC_GROUPS && m->E <= decode_grid(ctx);
     return decode_launch<false>(ctx, m, a);
 }
 
