@@ -154,9 +154,11 @@ int qq_moe_forward_noalloc_dev(qq_ctx *ctx, const qq_moe *m, const float *x_dev,
  *   x = rmsnorm(hidden) * norm_w     (norm_w_dev NULL: unit weight)
  *   hidden += MoE(x)
  * for T rows, with the same routing outputs as qq_moe_forward_dev.  A
- * single row is normalised inside the decode kernel (no separate launch);
- * the result equals qq_rmsnorm_dev followed by qq_moe_forward_dev bit for
- * bit.  Device pointers; enqueued, not waited for. */
+ * single row is normalised inside the decode kernel, and the rows of a chunk
+ * on the fp16 MFMA path inside its router launch (F32 router, hidden_dev and
+ * norm_w_dev 16-byte aligned; no separate launch); the result equals
+ * qq_rmsnorm_dev followed by qq_moe_forward_dev bit for bit.  Device
+ * pointers; enqueued, not waited for. */
 int qq_moe_forward_norm_dev(qq_ctx *ctx, const qq_moe *m, float *hidden_dev,
                             const float *norm_w_dev, double eps, int T, const uint8_t *mask,
                             int32_t *idx_dev, double *w_dev, float *probs_dev);
